@@ -1,0 +1,150 @@
+/*
+ * mote_hip.h: C ABI of libmote_hip.so, the MI355X (gfx950) implementation of
+ * Mote's Q4_0 quantized-linear path, RMSNorm and RoPE.
+ *
+ * Conventions (all of them those of the reference's Rust FFI,
+ * crates/mote-backend-hip/src/ffi.rs:8-13): pointers are untyped device
+ * pointers, streams are opaque `void*` hipStream_t handles, every launch is
+ * asynchronous on the given stream, the caller owns every buffer, and the
+ * return value is an `int` status where 0 means success.
+ *
+ * Symbols marked [reference] keep the exact signature, argument meaning and
+ * status codes of the reference export they replace (file:line cited).
+ * Symbols marked [new] have no counterpart in the reference.
+ */
+#ifndef MOTE_HIP_H
+#define MOTE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- HIP runtime wrappers ------------------------------------------------ */
+/* [reference] crates/mote-backend-hip/src/hipblaslt_shim.cpp:259-324, bound at
+ * crates/mote-backend-hip/src/ffi.rs:42-61.  Raw hipError_t; -1 for a null
+ * out-parameter. */
+int mote_hip_get_device_count(int* count);
+int mote_hip_set_device(int ordinal);
+int mote_hip_malloc(void** pointer, size_t bytes);
+int mote_hip_free(void* pointer);
+int mote_hip_memcpy_host_to_device(void* destination, const void* source, size_t bytes);
+int mote_hip_memcpy_device_to_host(void* destination, const void* source, size_t bytes);
+int mote_hip_stream_create(void** stream);
+int mote_hip_stream_destroy(void* stream);
+int mote_hip_stream_synchronize(void* stream);
+int mote_hip_mem_get_info(size_t* free_bytes, size_t* total_bytes);
+
+/* ---- Q4_0 quantized linear ------------------------------------------------ */
+/* [reference] crates/mote-backend-hip/src/quantized_linear.hip:56-91, bound at
+ * crates/mote-backend-hip/src/ffi.rs:287-326.
+ * output[rows, N] (f16) = input[rows, K] (f16) x weights[N, K]^T (GGML Q4_0,
+ * rows of K/32 blocks of 18 bytes), f32 accumulation, one f16 rounding.
+ * Status: null pointer or K % 32 != 0 -> 1 (hipErrorInvalidValue);
+ * rows == 0 or N == 0 -> 0, nothing launched; rows * N > UINT_MAX -> 9
+ * (hipErrorInvalidConfiguration); K == 0 launches and writes zeros; K >
+ * 2^31 - 1 -> 9; else the launch status.  Output must not alias the inputs. */
+int mote_hip_quantized_linear_q4_0_f16(const void* input, const void* weights, void* output,
+                                       uint64_t rows, uint64_t output_features,
+                                       uint64_t input_features, void* stream);
+
+/* [new] Same as above with an f32 output [rows, N] (the reference oracle's
+ * output type, crates/mote-reference/src/quantized.rs:89-144). */
+int mote_hip_quantized_linear_q4_0_f32(const void* input, const void* weights, void* output,
+                                       uint64_t rows, uint64_t output_features,
+                                       uint64_t input_features, void* stream);
+
+/* [new] Fused gate/up projection: output[rows, N] (f32) =
+ * silu(input . gate^T) * (input . up^T), silu(z) = z / (1 + e^-z); gate and up
+ * are Q4_0 [N, K].  up_weights == NULL means gate_weights is the concatenated
+ * [2N, K] matrix with the gate rows first.  Status codes as above. */
+int mote_hip_q4_0_gate_up_silu_f32(const void* input, const void* gate_weights,
+                                   const void* up_weights, void* output, uint64_t rows,
+                                   uint64_t output_features, uint64_t input_features,
+                                   void* stream);
+
+/* [new] On-device Q4_0 decode of rows x K elements to f32, bit-identical to
+ * dequantize_quantized_row (crates/mote-reference/src/quantized.rs:58-74).
+ * Status: null or K % 32 != 0 -> 1; empty -> 0. */
+int mote_hip_dequantize_q4_0_f32(const void* weights, void* output, uint64_t rows,
+                                 uint64_t input_features, void* stream);
+
+/* ---- Q4_0 dispatch context (per-(M, N, K) plan cache) -------------------- */
+/* [new] Handle pattern of the reference's hipBLASLt plan cache
+ * (crates/mote-backend-hip/src/hipblaslt_shim.cpp:326-408): create / destroy
+ * / last_error, a mutex-guarded map from (M, N, K, op, output type) to the
+ * kernel variant, chosen on first use by a shape heuristic or, with autotune
+ * on, by timing every eligible variant on the caller's stream.  Statuses are
+ * hipError_t values; on failure last_error describes the cause. */
+int mote_q4_0_dispatch_create(void** handle);
+void mote_q4_0_dispatch_destroy(void* handle);
+const char* mote_q4_0_dispatch_last_error(void* handle);
+int mote_q4_0_dispatch_set_autotune(void* handle, int enabled);
+/* Forces one variant by name (NULL or "" clears); tests use it to run every
+ * kernel on the same problem. */
+int mote_q4_0_dispatch_force_variant(void* handle, const char* name);
+int mote_q4_0_dispatch_linear(void* handle, const void* input, const void* weights,
+                              void* output, uint64_t rows, uint64_t output_features,
+                              uint64_t input_features, int output_f16, void* stream);
+int mote_q4_0_dispatch_gate_up_silu(void* handle, const void* input, const void* gate_weights,
+                                    const void* up_weights, void* output, uint64_t rows,
+                                    uint64_t output_features, uint64_t input_features,
+                                    int output_f16, void* stream);
+/* Name of the cached variant for a problem (gate_up_op: 0 linear, 1 gate/up);
+ * hipErrorNotFound (500) when the problem has not run yet. */
+int mote_q4_0_dispatch_plan(void* handle, uint64_t rows, uint64_t output_features,
+                            uint64_t input_features, int gate_up_op, int output_f16,
+                            char* name, size_t capacity);
+int mote_q4_0_variant_count(void);
+const char* mote_q4_0_variant_name(int index);
+
+/* ---- RMSNorm and fused add + RMSNorm -------------------------------------- */
+/* [reference] crates/mote-backend-hip/src/rms_norm.hip:68-98, bound at
+ * crates/mote-backend-hip/src/ffi.rs:120-161.  f16 [rows, hidden] in/out,
+ * f16 weight [hidden], f32 arithmetic.  -1 for null pointers or rows >
+ * UINT32_MAX; rows == 0 or hidden == 0 -> 0 without a launch. */
+int mote_hip_rms_norm_f16(const void* input, const void* weight, void* output, uint64_t rows,
+                          uint64_t hidden_size, float epsilon, void* stream);
+
+/* [reference] crates/mote-backend-hip/src/fused_add_rms_norm.hip:99-138,
+ * bound at crates/mote-backend-hip/src/ffi.rs:163-219.  s = input + residual
+ * in f32; output = f16(s * rsqrt(mean(s^2) + eps) * weight); residual <-
+ * f16(s).  input may alias output; output == residual, a non-finite or
+ * negative epsilon, null pointers or rows > UINT32_MAX -> -1. */
+int mote_hip_fused_add_rms_norm_f16(const void* input, void* residual, const void* weight,
+                                    void* output, uint64_t rows, uint64_t hidden_size,
+                                    float epsilon, void* stream);
+
+/* ---- RoPE ------------------------------------------------------------------ */
+/* [reference] crates/mote-backend-hip/src/rope.hip:99-150, bound at
+ * crates/mote-backend-hip/src/ffi.rs:221-285.  f16 [tokens, heads, head_dim]
+ * in/out (may alias), f32 cos/sin [tokens, rotary_dim / 2]; layout 0 =
+ * half-split (pairs j, j + R/2), 1 = interleaved (2j, 2j + 1); the tail past
+ * rotary_dim is copied.  -1 for null input/output/stream, null cos/sin with
+ * rotary_dim > 0, an unknown layout, an odd or oversized rotary_dim, or
+ * tokens * heads > UINT32_MAX; any zero dimension -> 0 without a launch. */
+int mote_hip_rope_f16(const void* input, const void* cos, const void* sin, void* output,
+                      uint64_t tokens, uint64_t heads, uint64_t head_dim, uint64_t rotary_dim,
+                      uint32_t layout, void* stream);
+
+/* [new] q and k rotated in one launch with the shared cos/sin rows; same
+ * semantics and status codes as mote_hip_rope_f16 applied to each tensor. */
+int mote_hip_rope_qk_f16(const void* q_input, const void* k_input, const void* cos,
+                         const void* sin, void* q_output, void* k_output, uint64_t tokens,
+                         uint64_t q_heads, uint64_t k_heads, uint64_t head_dim,
+                         uint64_t rotary_dim, uint32_t layout, void* stream);
+
+/* [new] cos/sin tables [tokens, rotary_dim / 2] from int64 positions:
+ * inv_j = theta^(-2j / rotary_dim), angle = position * inv_j, computed in
+ * binary64 and rounded to binary32.  -1 for null pointers, an odd rotary_dim
+ * or theta <= 0. */
+int mote_hip_rope_tables_f32(const void* positions, void* cos_out, void* sin_out,
+                             uint64_t tokens, uint64_t rotary_dim, double theta, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOTE_HIP_H */

@@ -1,0 +1,135 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels of the Q4_0 path.
+//
+// GGML Q4_0 block (crates/mote-types/src/lib.rs:49-65, decode at
+// crates/mote-reference/src/quantized.rs:177-201): 18 bytes = a little-endian
+// binary16 scale d followed by 16 bytes; byte j holds element j in its low
+// nibble and element j+16 in its high nibble, value (q - 8) * d.
+//
+// Two consecutive blocks ("a block pair", 36 bytes) start on a 4-byte boundary
+// whenever the row and the matrix base do, so the kernels load a pair as nine
+// dwords (dwordx4 + dwordx4 + dword) and never touch memory byte by byte.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "export.hpp"
+
+namespace mote {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+// 16-byte vector that the compiler may only assume dword aligned.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr uint32_t kBlockElements = 32;
+constexpr uint32_t kBlockBytes = 18;
+constexpr uint32_t kPairBytes = 36;
+
+// ---------------------------------------------------------------------------
+// Nibble unpacking.
+//
+// A nibble n placed in mantissa bits [4, 8) of a binary16 whose exponent field
+// encodes 2^0 (bits 0x3C00) is the exact value 1 + n/64.  One dword of four
+// nibble bytes [b0 b1 b2 b3] therefore yields four packed f16 pairs with one
+// AND-OR (plus a shift) each:
+//   hi02 = ( q       & 0x00F000F0) | 0x3C003C00  -> (H(b0), H(b2))
+//   lo02 = ((q << 4) & 0x00F000F0) | 0x3C003C00  -> (L(b0), L(b2))
+//   lo13 = ((q >> 4) & 0x00F000F0) | 0x3C003C00  -> (L(b1), L(b3))
+//   hi13 = ((q >> 8) & 0x00F000F0) | 0x3C003C00  -> (H(b1), H(b3))
+// where L(bj) is element j (low nibble) and H(bj) element j+16 of the block.
+// With acc = sum_k (1 + n_k/64) x_k accumulated by v_dot2_f32_f16 (the f16
+// products are exact in f32),  sum_k (n_k - 8) x_k = 64 (acc - 1.125 sx)
+// with sx = sum_k x_k over the block.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kNibbleField = 0x00F000F0u;
+constexpr uint32_t kOnePair = 0x3C003C00u;
+
+__device__ __forceinline__ uint32_t nib_hi02(uint32_t q) { return (q & kNibbleField) | kOnePair; }
+__device__ __forceinline__ uint32_t nib_lo02(uint32_t q) { return ((q << 4) & kNibbleField) | kOnePair; }
+__device__ __forceinline__ uint32_t nib_lo13(uint32_t q) { return ((q >> 4) & kNibbleField) | kOnePair; }
+__device__ __forceinline__ uint32_t nib_hi13(uint32_t q) { return ((q >> 8) & kNibbleField) | kOnePair; }
+
+__device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+
+// v_dot2_f32_f16: a.lo*b.lo + a.hi*b.hi + c with f32 accumulation.
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
+}
+
+// Packs the binary16 halves x[a] (low) and x[b] (high) of a register array
+// holding consecutive f16 pairs, with one v_perm_b32.
+template <int A, int B>
+__device__ __forceinline__ uint32_t pick_pair(const uint32_t* x) {
+    constexpr uint32_t lo = (A & 1) ? 0x0302u : 0x0100u;          // bytes of S1
+    constexpr uint32_t hi = (B & 1) ? 0x07060000u : 0x05040000u;  // bytes of S0
+    return __builtin_amdgcn_perm(x[B / 2], x[A / 2], hi | lo);
+}
+
+__device__ __forceinline__ float half_lo_to_float(uint32_t v) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v & 0xffffu)));
+}
+__device__ __forceinline__ float half_hi_to_float(uint32_t v) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v >> 16)));
+}
+
+// Loads the nine dwords of the block pair that starts at `p` (4-byte aligned).
+__device__ __forceinline__ void load_pair(const uint8_t* p, uint32_t (&d)[9]) {
+    const u32x4_a4 a = *reinterpret_cast<const u32x4_a4*>(p);
+    const u32x4_a4 b = *reinterpret_cast<const u32x4_a4*>(p + 16);
+    const uint32_t c = *reinterpret_cast<const uint32_t*>(p + 32);
+    d[0] = a.x; d[1] = a.y; d[2] = a.z; d[3] = a.w;
+    d[4] = b.x; d[5] = b.y; d[6] = b.z; d[7] = b.w;
+    d[8] = c;
+}
+
+// The eight nibble dwords of a pair in unpack order.  Block 0's nibble bytes
+// sit at pair bytes 2..17, so its first dword is assembled from the high half
+// of d0 (bytes 2,3 = elements 0,1) and the low half of d4 (bytes 16,17 =
+// elements 14,15): byte order [e14 e15 e0 e1].  Block 1's nibbles are d5..d8.
+__device__ __forceinline__ uint32_t pair_q0(const uint32_t (&d)[9]) {
+    return __builtin_amdgcn_perm(d[0], d[4], 0x07060100u);  // (d4 & 0xFFFF) | (d0 & 0xFFFF0000)
+}
+
+// Block-local element index of byte position `pos` of nibble dword `w`
+// (w = 0..3 block 0, 4..7 block 1) in the unpack order above.
+__host__ __device__ constexpr int pair_byte_element(int w, int pos) {
+    return (w == 0) ? (pos < 2 ? 14 + pos : pos - 2)
+         : (w < 4)  ? (4 * w - 2 + pos)
+                    : (4 * (w - 4) + pos);
+}
+
+// ---------------------------------------------------------------------------
+// Wave-level reduction with DPP (gfx9 row/bcast controls), result returned
+// uniformly (read from lane 63).
+// ---------------------------------------------------------------------------
+template <int Ctrl, int RowMask = 0xF, int BankMask = 0xF, bool BoundCtrl = true>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+        0, __builtin_bit_cast(int, v), Ctrl, RowMask, BankMask, BoundCtrl));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp<0xB1>(v);        // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);        // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);       // row_half_mirror
+    v += dpp<0x140>(v);       // row_mirror: every lane of a row holds its row sum
+    v += dpp<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3: lane 63 = total
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Output element conversion.
+template <typename T>
+__device__ __forceinline__ T to_out(float v);
+template <>
+__device__ __forceinline__ float to_out<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ _Float16 to_out<_Float16>(float v) { return static_cast<_Float16>(v); }
+
+}  // namespace mote

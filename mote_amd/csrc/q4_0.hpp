@@ -1,0 +1,45 @@
+// Host-side interface between the Q4_0 launch entry points, the dispatch cache
+// and the kernels.  Nothing here is part of the exported C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace mote::q4_0 {
+
+enum class OutType : int { F32 = 0, F16 = 1 };
+
+struct Problem {
+    const void* x;        // f16 [M, K]
+    const void* w;        // Q4_0 [N, K]  (gate rows for the fused op)
+    const void* w_up;     // Q4_0 [N, K]  up rows, fused gate/up only (else null)
+    void* y;              // [M, N] f32 or f16
+    uint32_t M, N, K;
+    OutType out;
+    hipStream_t stream;
+};
+
+enum class Kind : int { Gemv = 0, Mfma = 1, Generic = 2, GateUpMfma = 3, GateUpGeneric = 4 };
+
+struct Variant {
+    const char* name;
+    Kind kind;
+    int p0, p1, p2;       // kernel tile parameters (meaning depends on kind)
+    hipError_t (*launch)(const Problem&);
+};
+
+// Kernel variant tables, defined next to the kernels.
+const Variant* gemv_variants(int* count);
+const Variant* mfma_variants(int* count);
+const Variant* generic_variants(int* count);
+
+// Whether a variant can run the problem (alignment, shape limits).
+bool gemv_supports(const Variant& v, const Problem& p);
+bool mfma_supports(const Variant& v, const Problem& p);
+
+hipError_t launch_zero_fill(void* y, uint64_t count, OutType out, hipStream_t stream);
+hipError_t launch_decode_f32(const void* w, float* out, uint64_t rows, uint64_t cols,
+                             hipStream_t stream);
+
+}  // namespace mote::q4_0

@@ -1,0 +1,401 @@
+// C ABI of the Q4_0 quantized-linear path and its per-(M, N, K) dispatch cache.
+//
+// mote_hip_quantized_linear_q4_0_f16 keeps the signature, argument meaning and
+// status codes of crates/mote-backend-hip/src/quantized_linear.hip:56-91:
+// null pointers or K % 32 != 0 -> hipErrorInvalidValue (1); rows == 0 or N == 0
+// -> 0 without a launch; rows * N > UINT_MAX -> hipErrorInvalidConfiguration
+// (9); K == 0 launches and writes zeros; otherwise the launch status.
+//
+// The dispatch context mirrors the plan cache of the reference's hipBLASLt
+// shim (crates/mote-backend-hip/src/hipblaslt_shim.cpp:43-46, 156-249,
+// 352-408): one mutex-guarded map per handle from the problem key to the
+// chosen kernel variant; on a miss the variant is either picked by the shape
+// heuristic or, with autotuning on, by timing every eligible variant with
+// hipEvents on the caller's stream (each candidate writes the caller's output,
+// which the final launch overwrites).  Later calls only launch.
+#include <hip/hip_runtime.h>
+
+#include "export.hpp"
+
+#include <algorithm>
+#include <climits>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "q4_0.hpp"
+
+namespace mote::q4_0 {
+namespace {
+
+enum class Op : int { Linear = 0, GateUp = 1 };
+
+struct Key {
+    uint32_t m, n, k;
+    int op, out, fast;
+    bool operator<(const Key& o) const {
+        return std::tie(m, n, k, op, out, fast) < std::tie(o.m, o.n, o.k, o.op, o.out, o.fast);
+    }
+};
+
+struct Dispatcher {
+    std::mutex mutex;
+    std::map<Key, const Variant*> plans;
+    bool autotune = false;
+    std::string forced;
+    std::string last_error;
+};
+
+std::vector<const Variant*> all_variants() {
+    std::vector<const Variant*> out;
+    int count = 0;
+    for (auto table : {gemv_variants, mfma_variants, generic_variants}) {
+        const Variant* v = table(&count);
+        for (int i = 0; i < count; ++i) out.push_back(&v[i]);
+    }
+    return out;
+}
+
+const Variant* find_variant(const std::string& name) {
+    for (const Variant* v : all_variants())
+        if (name == v->name) return v;
+    return nullptr;
+}
+
+bool kind_matches(const Variant& v, Op op) {
+    if (op == Op::GateUp) return v.kind == Kind::GateUpMfma || v.kind == Kind::GateUpGeneric;
+    return v.kind == Kind::Gemv || v.kind == Kind::Mfma || v.kind == Kind::Generic;
+}
+
+bool supports(const Variant& v, const Problem& p) {
+    switch (v.kind) {
+        case Kind::Gemv: return gemv_supports(v, p);
+        case Kind::Mfma:
+        case Kind::GateUpMfma: return mfma_supports(v, p);
+        default: return true;
+    }
+}
+
+bool fast_eligible(const Problem& p) {
+    return p.K % 64 == 0 && reinterpret_cast<uintptr_t>(p.w) % 4 == 0 &&
+           reinterpret_cast<uintptr_t>(p.x) % 16 == 0 &&
+           (p.w_up == nullptr || reinterpret_cast<uintptr_t>(p.w_up) % 4 == 0);
+}
+
+// Variants the autotuner may time: the matrix-core kernels only for M >= 64
+// (prefill shapes), the vector-ALU kernels below that.
+std::vector<const Variant*> candidates(const Problem& p, Op op) {
+    std::vector<const Variant*> out;
+    for (const Variant* v : all_variants()) {
+        if (!kind_matches(*v, op) || !supports(*v, p)) continue;
+        const bool generic = v->kind == Kind::Generic || v->kind == Kind::GateUpGeneric;
+        if (generic && fast_eligible(p)) continue;
+        if (v->kind == Kind::Gemv && p.M >= 64) continue;
+        if ((v->kind == Kind::Mfma || v->kind == Kind::GateUpMfma) && p.M < 64) continue;
+        out.push_back(v);
+    }
+    return out;
+}
+
+const Variant* by_name(const char* name) {
+    const Variant* v = find_variant(name);
+    return v;
+}
+
+// Shape heuristic used when autotuning is off.
+const Variant* heuristic(const Problem& p, Op op) {
+    const bool fast = fast_eligible(p);
+    if (op == Op::GateUp) {
+        if (fast && p.M >= 64) return by_name(p.M >= 128 ? "gateup_mfma_m128_n64" : "gateup_mfma_m64_n64");
+        return by_name("gateup_generic");
+    }
+    if (!fast) return by_name("generic");
+    if (p.M >= 64) {
+        // Prefer the largest tile that still gives at least one tile per CU.
+        static const char* const order[] = {"mfma_m128_n128", "mfma_m128_n64", "mfma_m64_n128",
+                                            "mfma_m64_n64"};
+        const Variant* best = nullptr;
+        uint64_t best_tiles = 0;
+        for (const char* name : order) {
+            const Variant* v = by_name(name);
+            const uint64_t tiles = static_cast<uint64_t>((p.M + v->p0 - 1) / v->p0) *
+                                   ((p.N + v->p1 - 1) / v->p1);
+            if (tiles >= 240) return v;
+            if (tiles > best_tiles) {
+                best = v;
+                best_tiles = tiles;
+            }
+        }
+        return best;
+    }
+    if (p.M == 1) {
+        if (p.K >= 8192 && p.N <= 8192) return by_name("gemv_r4_t1_k2");
+        return by_name(p.N >= 8192 ? "gemv_r4_t1_k1" : "gemv_r2_t1_k1");
+    }
+    if (p.M == 2) return by_name("gemv_r4_t2_k1");
+    return by_name("gemv_r4_t4_k1");
+}
+
+hipError_t time_variant(const Variant& v, const Problem& p, float* ms) {
+    hipEvent_t start = nullptr, stop = nullptr;
+    hipError_t err = hipEventCreate(&start);
+    if (err == hipSuccess) err = hipEventCreate(&stop);
+    if (err == hipSuccess) err = v.launch(p);  // warm-up
+    if (err == hipSuccess) err = hipEventRecord(start, p.stream);
+    for (int i = 0; i < 5 && err == hipSuccess; ++i) err = v.launch(p);
+    if (err == hipSuccess) err = hipEventRecord(stop, p.stream);
+    if (err == hipSuccess) err = hipEventSynchronize(stop);
+    if (err == hipSuccess) err = hipEventElapsedTime(ms, start, stop);
+    if (start) (void)hipEventDestroy(start);
+    if (stop) (void)hipEventDestroy(stop);
+    return err;
+}
+
+int fail(Dispatcher* d, hipError_t status, const std::string& message) {
+    if (d) d->last_error = message;
+    return static_cast<int>(status);
+}
+
+int run(Dispatcher& d, const Problem& p, Op op) {
+    std::lock_guard<std::mutex> lock(d.mutex);
+    const Variant* v = nullptr;
+    if (!d.forced.empty()) {
+        v = find_variant(d.forced);
+        if (!v || !kind_matches(*v, op) || !supports(*v, p))
+            return fail(&d, hipErrorInvalidValue,
+                        "forced Q4_0 variant '" + d.forced + "' cannot run this problem");
+    } else {
+        const Key key{p.M, p.N, p.K, static_cast<int>(op), static_cast<int>(p.out),
+                      fast_eligible(p) ? 1 : 0};
+        auto found = d.plans.find(key);
+        if (found == d.plans.end()) {
+            const Variant* chosen = nullptr;
+            if (d.autotune) {
+                float best = 0.0f;
+                for (const Variant* c : candidates(p, op)) {
+                    float ms = 0.0f;
+                    const hipError_t err = time_variant(*c, p, &ms);
+                    if (err != hipSuccess)
+                        return fail(&d, err, std::string("autotuning ") + c->name + " failed");
+                    if (!chosen || ms < best) {
+                        chosen = c;
+                        best = ms;
+                    }
+                }
+            }
+            if (!chosen) chosen = heuristic(p, op);
+            if (!chosen) return fail(&d, hipErrorInvalidValue, "no Q4_0 variant for this problem");
+            found = d.plans.emplace(key, chosen).first;
+        }
+        v = found->second;
+    }
+    const hipError_t err = v->launch(p);
+    if (err != hipSuccess) return fail(&d, err, std::string("launch of ") + v->name + " failed");
+    d.last_error.clear();
+    return 0;
+}
+
+Dispatcher& default_dispatcher() {
+    static Dispatcher* d = [] {
+        auto* x = new Dispatcher();
+        const char* tune = std::getenv("MOTE_Q4_0_AUTOTUNE");
+        x->autotune = tune && tune[0] == '1';
+        const char* forced = std::getenv("MOTE_Q4_0_VARIANT");
+        if (forced) x->forced = forced;
+        return x;
+    }();
+    return *d;
+}
+
+// Argument checks shared by every linear entry point, in the reference order
+// (crates/mote-backend-hip/src/quantized_linear.hip:64-76).  Returns -1 when
+// the caller should go on and launch, otherwise the status to return.
+int check_linear(const void* input, const void* weights, const void* output, uint64_t rows,
+                 uint64_t n, uint64_t k, const void* stream) {
+    if (!input || !weights || !output || !stream) return hipErrorInvalidValue;
+    if (k % 32 != 0) return hipErrorInvalidValue;
+    if (rows == 0 || n == 0) return hipSuccess;
+    if (rows > UINT_MAX || n > UINT_MAX || rows > UINT_MAX / n) return hipErrorInvalidConfiguration;
+    if (k > 0x7fffffffull) return hipErrorInvalidConfiguration;
+    return -1;
+}
+
+int linear(Dispatcher* d, const void* input, const void* weights, void* output, uint64_t rows,
+           uint64_t n, uint64_t k, OutType out, void* stream) {
+    const int pre = check_linear(input, weights, output, rows, n, k, stream);
+    if (pre >= 0) return pre == 0 ? 0 : fail(d, static_cast<hipError_t>(pre), "invalid Q4_0 linear arguments");
+    const auto s = static_cast<hipStream_t>(stream);
+    if (k == 0) return static_cast<int>(launch_zero_fill(output, rows * n, out, s));
+    const Problem p{input, weights, nullptr, output, static_cast<uint32_t>(rows),
+                    static_cast<uint32_t>(n), static_cast<uint32_t>(k), out, s};
+    return run(d ? *d : default_dispatcher(), p, Op::Linear);
+}
+
+int gate_up(Dispatcher* d, const void* input, const void* gate, const void* up, void* output,
+            uint64_t rows, uint64_t n, uint64_t k, OutType out, void* stream) {
+    const int pre = check_linear(input, gate, output, rows, n, k, stream);
+    if (pre >= 0) return pre == 0 ? 0 : fail(d, static_cast<hipError_t>(pre), "invalid Q4_0 gate/up arguments");
+    const auto s = static_cast<hipStream_t>(stream);
+    if (k == 0) return static_cast<int>(launch_zero_fill(output, rows * n, out, s));
+    if (up == nullptr) up = static_cast<const uint8_t*>(gate) + n * (k / 32) * 18;
+    const Problem p{input, gate, up, output, static_cast<uint32_t>(rows), static_cast<uint32_t>(n),
+                    static_cast<uint32_t>(k), out, s};
+    return run(d ? *d : default_dispatcher(), p, Op::GateUp);
+}
+
+}  // namespace
+}  // namespace mote::q4_0
+
+using namespace mote::q4_0;
+
+MOTE_EXPORT int mote_hip_quantized_linear_q4_0_f16(const void* input, const void* weights,
+                                                  void* output, uint64_t rows,
+                                                  uint64_t output_features,
+                                                  uint64_t input_features, void* stream) noexcept {
+    try {
+        return linear(nullptr, input, weights, output, rows, output_features, input_features,
+                      OutType::F16, stream);
+    } catch (...) {
+        return hipErrorUnknown;
+    }
+}
+
+MOTE_EXPORT int mote_hip_quantized_linear_q4_0_f32(const void* input, const void* weights,
+                                                  void* output, uint64_t rows,
+                                                  uint64_t output_features,
+                                                  uint64_t input_features, void* stream) noexcept {
+    try {
+        return linear(nullptr, input, weights, output, rows, output_features, input_features,
+                      OutType::F32, stream);
+    } catch (...) {
+        return hipErrorUnknown;
+    }
+}
+
+MOTE_EXPORT int mote_hip_q4_0_gate_up_silu_f32(const void* input, const void* gate_weights,
+                                              const void* up_weights, void* output,
+                                              uint64_t rows, uint64_t output_features,
+                                              uint64_t input_features, void* stream) noexcept {
+    try {
+        return gate_up(nullptr, input, gate_weights, up_weights, output, rows, output_features,
+                       input_features, OutType::F32, stream);
+    } catch (...) {
+        return hipErrorUnknown;
+    }
+}
+
+MOTE_EXPORT int mote_hip_dequantize_q4_0_f32(const void* weights, void* output, uint64_t rows,
+                                            uint64_t input_features, void* stream) noexcept {
+    if (!weights || !output || !stream) return hipErrorInvalidValue;
+    if (input_features % 32 != 0) return hipErrorInvalidValue;
+    if (rows == 0 || input_features == 0) return hipSuccess;
+    if (rows > (1ull << 40) / input_features) return hipErrorInvalidConfiguration;
+    return static_cast<int>(launch_decode_f32(weights, static_cast<float*>(output), rows,
+                                              input_features, static_cast<hipStream_t>(stream)));
+}
+
+MOTE_EXPORT int mote_q4_0_dispatch_create(void** handle) noexcept {
+    if (!handle) return hipErrorInvalidValue;
+    *handle = nullptr;
+    try {
+        *handle = new mote::q4_0::Dispatcher();
+        return 0;
+    } catch (...) {
+        return hipErrorOutOfMemory;
+    }
+}
+
+MOTE_EXPORT void mote_q4_0_dispatch_destroy(void* handle) noexcept {
+    delete static_cast<mote::q4_0::Dispatcher*>(handle);
+}
+
+MOTE_EXPORT const char* mote_q4_0_dispatch_last_error(void* handle) noexcept {
+    auto* d = static_cast<mote::q4_0::Dispatcher*>(handle);
+    return d ? d->last_error.c_str() : nullptr;
+}
+
+MOTE_EXPORT int mote_q4_0_dispatch_set_autotune(void* handle, int enabled) noexcept {
+    auto* d = static_cast<mote::q4_0::Dispatcher*>(handle);
+    if (!d) return hipErrorInvalidValue;
+    std::lock_guard<std::mutex> lock(d->mutex);
+    d->autotune = enabled != 0;
+    return 0;
+}
+
+MOTE_EXPORT int mote_q4_0_dispatch_force_variant(void* handle, const char* name) noexcept {
+    auto* d = static_cast<mote::q4_0::Dispatcher*>(handle);
+    if (!d) return hipErrorInvalidValue;
+    std::lock_guard<std::mutex> lock(d->mutex);
+    if (name == nullptr || name[0] == '\0') {
+        d->forced.clear();
+        return 0;
+    }
+    if (!find_variant(name)) {
+        d->last_error = std::string("unknown Q4_0 variant '") + name + "'";
+        return hipErrorInvalidValue;
+    }
+    d->forced = name;
+    return 0;
+}
+
+MOTE_EXPORT int mote_q4_0_dispatch_linear(void* handle, const void* input, const void* weights,
+                                         void* output, uint64_t rows, uint64_t output_features,
+                                         uint64_t input_features, int output_f16,
+                                         void* stream) noexcept {
+    auto* d = static_cast<mote::q4_0::Dispatcher*>(handle);
+    if (!d) return hipErrorInvalidValue;
+    try {
+        return linear(d, input, weights, output, rows, output_features, input_features,
+                      output_f16 ? OutType::F16 : OutType::F32, stream);
+    } catch (...) {
+        return fail(d, hipErrorUnknown, "unexpected C++ exception");
+    }
+}
+
+MOTE_EXPORT int mote_q4_0_dispatch_gate_up_silu(void* handle, const void* input,
+                                               const void* gate_weights, const void* up_weights,
+                                               void* output, uint64_t rows,
+                                               uint64_t output_features, uint64_t input_features,
+                                               int output_f16, void* stream) noexcept {
+    auto* d = static_cast<mote::q4_0::Dispatcher*>(handle);
+    if (!d) return hipErrorInvalidValue;
+    try {
+        return gate_up(d, input, gate_weights, up_weights, output, rows, output_features,
+                       input_features, output_f16 ? OutType::F16 : OutType::F32, stream);
+    } catch (...) {
+        return fail(d, hipErrorUnknown, "unexpected C++ exception");
+    }
+}
+
+MOTE_EXPORT int mote_q4_0_dispatch_plan(void* handle, uint64_t rows, uint64_t output_features,
+                                       uint64_t input_features, int gate_up_op, int output_f16,
+                                       char* name, size_t capacity) noexcept {
+    auto* d = static_cast<mote::q4_0::Dispatcher*>(handle);
+    if (!d || !name || capacity == 0) return hipErrorInvalidValue;
+    std::lock_guard<std::mutex> lock(d->mutex);
+    for (const auto& entry : d->plans) {
+        const auto& k = entry.first;
+        if (k.m == rows && k.n == output_features && k.k == input_features &&
+            k.op == gate_up_op && k.out == output_f16) {
+            std::strncpy(name, entry.second->name, capacity - 1);
+            name[capacity - 1] = '\0';
+            return 0;
+        }
+    }
+    name[0] = '\0';
+    return hipErrorNotFound;
+}
+
+MOTE_EXPORT int mote_q4_0_variant_count(void) noexcept {
+    return static_cast<int>(all_variants().size());
+}
+
+MOTE_EXPORT const char* mote_q4_0_variant_name(int index) noexcept {
+    const auto v = all_variants();
+    return (index >= 0 && index < static_cast<int>(v.size())) ? v[static_cast<size_t>(index)]->name
+                                                             : nullptr;
+}

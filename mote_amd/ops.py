@@ -1,0 +1,129 @@
+"""Launch wrappers over the raw C ABI (device pointers as ints, streams as
+:class:`mote_amd.device.Stream`).  Every call enqueues asynchronously and
+raises :class:`mote_amd._ffi.HipError` on a non-zero status."""
+
+from __future__ import annotations
+
+import ctypes
+
+from ._ffi import HipError, check, lib
+
+HALF_SPLIT = 0
+INTERLEAVED = 1
+
+
+def _s(stream) -> int:
+    return stream.handle if hasattr(stream, "handle") else int(stream)
+
+
+def quantized_linear_q4_0_f16(x, w, y, rows, n, k, stream) -> None:
+    check(lib().mote_hip_quantized_linear_q4_0_f16(x, w, y, rows, n, k, _s(stream)), "launch Q4_0 linear kernel")
+
+
+def quantized_linear_q4_0_f32(x, w, y, rows, n, k, stream) -> None:
+    check(lib().mote_hip_quantized_linear_q4_0_f32(x, w, y, rows, n, k, _s(stream)), "launch Q4_0 linear kernel")
+
+
+def q4_0_gate_up_silu_f32(x, w_gate, w_up, y, rows, n, k, stream) -> None:
+    check(
+        lib().mote_hip_q4_0_gate_up_silu_f32(x, w_gate, w_up, y, rows, n, k, _s(stream)),
+        "launch Q4_0 gate/up kernel",
+    )
+
+
+def dequantize_q4_0_f32(w, out, rows, k, stream) -> None:
+    check(lib().mote_hip_dequantize_q4_0_f32(w, out, rows, k, _s(stream)), "launch Q4_0 decode kernel")
+
+
+def rms_norm_f16(x, weight, y, rows, hidden, eps, stream) -> None:
+    check(lib().mote_hip_rms_norm_f16(x, weight, y, rows, hidden, eps, _s(stream)), "launch RMSNorm kernel")
+
+
+def fused_add_rms_norm_f16(x, residual, weight, y, rows, hidden, eps, stream) -> None:
+    check(
+        lib().mote_hip_fused_add_rms_norm_f16(x, residual, weight, y, rows, hidden, eps, _s(stream)),
+        "launch fused add + RMSNorm kernel",
+    )
+
+
+def rope_f16(x, cos, sin, y, tokens, heads, head_dim, rotary_dim, layout, stream) -> None:
+    check(
+        lib().mote_hip_rope_f16(x, cos, sin, y, tokens, heads, head_dim, rotary_dim, layout, _s(stream)),
+        "launch RoPE kernel",
+    )
+
+
+def rope_qk_f16(q, k, cos, sin, q_out, k_out, tokens, q_heads, k_heads, head_dim, rotary_dim, layout, stream) -> None:
+    check(
+        lib().mote_hip_rope_qk_f16(
+            q, k, cos, sin, q_out, k_out, tokens, q_heads, k_heads, head_dim, rotary_dim, layout, _s(stream)
+        ),
+        "launch fused q/k RoPE kernel",
+    )
+
+
+def rope_tables_f32(positions, cos, sin, tokens, rotary_dim, theta, stream) -> None:
+    check(
+        lib().mote_hip_rope_tables_f32(positions, cos, sin, tokens, rotary_dim, float(theta), _s(stream)),
+        "launch RoPE table kernel",
+    )
+
+
+def variant_names() -> list[str]:
+    h = lib()
+    return [h.mote_q4_0_variant_name(i).decode() for i in range(h.mote_q4_0_variant_count())]
+
+
+class Q4_0Dispatch:
+    """A dispatch context: per-(M, N, K) plan cache with optional autotuning."""
+
+    def __init__(self, autotune: bool = False) -> None:
+        handle = ctypes.c_void_p()
+        check(lib().mote_q4_0_dispatch_create(ctypes.byref(handle)), "create Q4_0 dispatch context")
+        self.handle = handle.value
+        if autotune:
+            self.set_autotune(True)
+
+    def _check(self, status: int, operation: str) -> None:
+        if status != 0:
+            msg = lib().mote_q4_0_dispatch_last_error(self.handle)
+            raise HipError(operation, status, msg.decode() if msg else "")
+
+    def set_autotune(self, enabled: bool) -> None:
+        self._check(lib().mote_q4_0_dispatch_set_autotune(self.handle, int(enabled)), "set autotune")
+
+    def force(self, name: str | None) -> None:
+        self._check(
+            lib().mote_q4_0_dispatch_force_variant(self.handle, name.encode() if name else None),
+            "force Q4_0 variant",
+        )
+
+    def linear(self, x, w, y, rows, n, k, stream, f16_out: bool = False) -> None:
+        self._check(
+            lib().mote_q4_0_dispatch_linear(self.handle, x, w, y, rows, n, k, int(f16_out), _s(stream)),
+            "launch Q4_0 linear",
+        )
+
+    def gate_up_silu(self, x, w_gate, w_up, y, rows, n, k, stream, f16_out: bool = False) -> None:
+        self._check(
+            lib().mote_q4_0_dispatch_gate_up_silu(
+                self.handle, x, w_gate, w_up, y, rows, n, k, int(f16_out), _s(stream)
+            ),
+            "launch Q4_0 gate/up",
+        )
+
+    def plan(self, rows, n, k, gate_up: bool = False, f16_out: bool = False) -> str | None:
+        buf = ctypes.create_string_buffer(64)
+        status = lib().mote_q4_0_dispatch_plan(self.handle, rows, n, k, int(gate_up), int(f16_out), buf, 64)
+        return buf.value.decode() if status == 0 else None
+
+    def close(self) -> None:
+        if self.handle:
+            lib().mote_q4_0_dispatch_destroy(self.handle)
+            self.handle = 0
+
+    def __del__(self) -> None:  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,330 @@
+"""GPU parity of the Q4_0 quantized linear against the oracle.
+
+Mirrors crates/mote-backend-hip/tests/quantized_linear.rs (fixture, empty and
+K == 0 cases) and adds the seeded workloads: decode GEMV (M = 1), the skinny
+sweep (M <= 32), the prefill MFMA path (M >= 64) and the fused gate/up.
+Every call goes through the C ABI of libmote_hip.so.
+
+Tolerance (stated by the path's specification): an element passes if
+|y - y64| <= 1e-3 |y64| or |y - y64| <= 2e-3 sqrt(K) max|d| max|x|, y64 being
+the f64-accumulated oracle.  Outputs rounded to f16 get an extra 2^-11 |y64|.
+"""
+
+from __future__ import annotations
+
+import functools
+
+import numpy as np
+import pytest
+
+from helpers import (
+    assert_linear_close,
+    bits_to_f32,
+    f16_bits,
+    q4_0_scales,
+    ref_test_q4_0_inputs,
+    ref_test_q4_0_weights,
+    row_bytes,
+)
+from mote_amd import ops, workloads as wl
+from mote_amd.device import DeviceBuffer
+
+pytestmark = pytest.mark.gpu
+
+F16_REL = 2.0 ** -11
+
+
+@functools.lru_cache(maxsize=None)
+def weights(seed: int, n: int, k: int) -> np.ndarray:
+    return wl.q4_0_weights(seed, n, k)
+
+
+@functools.lru_cache(maxsize=None)
+def normal_x(seed: int, m: int, k: int) -> np.ndarray:
+    return wl.normal_f16(seed, m * k)
+
+
+def run_linear(stream, x_bits, w, m, n, k, f16_out=False, dispatch=None, fn=None, w_offset=0, x_offset=0):
+    """Uploads, launches through the C ABI, synchronises, reads back."""
+    xb = DeviceBuffer(x_bits.nbytes + x_offset)
+    xb.upload(x_bits, offset=x_offset)
+    wb = DeviceBuffer(w.nbytes + w_offset)
+    wb.upload(w, offset=w_offset)
+    out_bytes = m * n * (2 if f16_out else 4)
+    yb = DeviceBuffer(out_bytes)
+    yb.upload(np.full(out_bytes, 0xA5, dtype=np.uint8))  # sentinel: every element must be written
+    args = (xb.ptr + x_offset, wb.ptr + w_offset, yb.ptr, m, n, k)
+    if fn is not None:
+        fn(*args, stream)
+    elif dispatch is not None:
+        dispatch.linear(*args, stream, f16_out=f16_out)
+    elif f16_out:
+        ops.quantized_linear_q4_0_f16(*args, stream)
+    else:
+        ops.quantized_linear_q4_0_f32(*args, stream)
+    stream.synchronize()
+    y = yb.download(np.uint16 if f16_out else np.float32)
+    if f16_out:
+        y = bits_to_f32(y)
+    return y.reshape(m, n)
+
+
+def oracle_f64(oracle, x_bits, w, m, n, k, columns=None):
+    return oracle.quantized_linear_f64(bits_to_f32(x_bits), w, m, n, k, columns)
+
+
+def check_against_oracle(oracle, y, x_bits, w, m, n, k, columns=None, f16_out=False, what="output"):
+    y64 = oracle_f64(oracle, x_bits, w, m, n, k, columns)
+    got = y if columns is None else y[:, columns]
+    max_d = float(np.max(np.abs(q4_0_scales(w, n, k)))) if k else 0.0
+    max_x = float(np.max(np.abs(bits_to_f32(x_bits)))) if x_bits.size else 0.0
+    assert_linear_close(got, y64, k, max_d, max_x, extra_rel=F16_REL if f16_out else 0.0, what=what)
+
+
+def sample_columns(n: int, count: int = 256, seed: int = 7) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    cols = np.unique(np.concatenate([[0, n - 1], rng.choice(n, size=min(count, n), replace=False)]))
+    return cols.astype(np.uint64)
+
+
+# --- the reference's own fixture ----------------------------------------------
+
+def test_reference_fixture_matches_cpu_oracle(stream, oracle):
+    """crates/mote-backend-hip/tests/quantized_linear.rs:13-62: M=3, N=5, K=64,
+    F16 output, tolerance max(0.01, 0.002 |e|) against f16(oracle f32)."""
+    m, n, k = 3, 5, 64
+    x = ref_test_q4_0_inputs(m, k)
+    w = ref_test_q4_0_weights(n, k)
+    wb = DeviceBuffer.from_array(w)
+    assert bytes(wb.download(np.uint8)) == bytes(w)  # stored verbatim
+    y = run_linear(stream, x, w, m, n, k, f16_out=True)
+    expected = oracle.quantized_linear_f32(bits_to_f32(x), w, oracle.Q4_0, m, n, k).reshape(m, n)
+    expected = expected.astype(np.float16).astype(np.float32)
+    tol = np.maximum(0.01, np.abs(expected) * 0.002)
+    assert np.all(np.abs(y - expected) <= tol), (y, expected)
+    check_against_oracle(oracle, y, x, w, m, n, k, f16_out=True)
+
+
+def test_empty_outputs_return_without_a_launch(stream):
+    """crates/mote-backend-hip/tests/quantized_linear.rs:124-140."""
+    w = ref_test_q4_0_weights(2, 32)
+    wb = DeviceBuffer.from_array(w)
+    xb = DeviceBuffer(0)
+    yb = DeviceBuffer(0)
+    for fn in (ops.quantized_linear_q4_0_f16, ops.quantized_linear_q4_0_f32):
+        fn(xb.ptr, wb.ptr, yb.ptr, 0, 2, 32, stream)
+        fn(xb.ptr, wb.ptr, yb.ptr, 3, 0, 32, stream)
+    stream.synchronize()
+
+
+def test_zero_input_features_writes_zeros(stream):
+    """crates/mote-backend-hip/tests/quantized_linear.rs:142-158: K == 0 with
+    M, N > 0 launches and writes zeros."""
+    for f16_out in (True, False):
+        y = run_linear(stream, np.zeros(0, np.uint16), np.zeros(0, np.uint8), 3, 2, 0, f16_out=f16_out)
+        assert np.array_equal(y, np.zeros((3, 2), np.float32))
+        assert not np.signbit(y).any()
+
+
+# --- seeded workloads -------------------------------------------------------------
+
+def test_decode_gemv_4096x4096_uniform_activations(stream, oracle):
+    m, k, n = 1, 4096, 4096
+    x = wl.uniform_f16(wl.seed_for(0, 0), m * k)
+    w = weights(wl.seed_for(0, 1), n, k)
+    y = run_linear(stream, x, w, m, n, k)
+    check_against_oracle(oracle, y, x, w, m, n, k)
+
+
+@pytest.mark.parametrize("k,n", [(4096, 14336), (14336, 4096)], ids=["up_gate", "down"])
+def test_decode_gemv_llama_mlp_shapes(stream, oracle, k, n):
+    m = 1
+    x = normal_x(wl.seed_for(1, 0), m, k)
+    w = weights(wl.seed_for(1, 1), n, k)
+    y = run_linear(stream, x, w, m, n, k)
+    check_against_oracle(oracle, y, x, w, m, n, k)
+    y16 = run_linear(stream, x, w, m, n, k, f16_out=True)
+    check_against_oracle(oracle, y16, x, w, m, n, k, f16_out=True, what="f16 output")
+
+
+@pytest.mark.parametrize("n", [4096, 6144, 14336])
+@pytest.mark.parametrize("m", [2, 4, 8, 16, 32])
+def test_skinny_sweep(stream, oracle, m, n):
+    k = 4096
+    x = normal_x(wl.seed_for(2, 0), m, k)
+    w = weights(wl.seed_for(2, 1), n, k)
+    y = run_linear(stream, x, w, m, n, k)
+    check_against_oracle(oracle, y, x, w, m, n, k, columns=sample_columns(n))
+
+
+@pytest.mark.parametrize("m", [64, 256, 512])
+def test_prefill_mfma(stream, oracle, m):
+    k, n = 4096, 14336
+    x = normal_x(wl.seed_for(4, 0), m, k)
+    w = weights(wl.seed_for(4, 1), n, k)
+    y = run_linear(stream, x, w, m, n, k)
+    check_against_oracle(oracle, y, x, w, m, n, k, columns=sample_columns(n, 128))
+
+
+@pytest.mark.parametrize("m", [64, 256, 512])
+def test_fused_gate_up_silu(stream, oracle, m):
+    k, n = 4096, 14336
+    x = normal_x(wl.seed_for(4, 0), m, k)
+    wg = weights(wl.seed_for(4, 1), n, k)
+    wu = weights(wl.seed_for(4, 2), n, k)
+    xb, gb, ub = DeviceBuffer.from_array(x), DeviceBuffer.from_array(wg), DeviceBuffer.from_array(wu)
+    yb = DeviceBuffer(m * n * 4)
+    ops.q4_0_gate_up_silu_f32(xb.ptr, gb.ptr, ub.ptr, yb.ptr, m, n, k, stream)
+    # concatenated [2N, K] form with up == NULL
+    cat = DeviceBuffer.from_array(np.concatenate([wg, wu]))
+    yc = DeviceBuffer(m * n * 4)
+    ops.q4_0_gate_up_silu_f32(xb.ptr, cat.ptr, None, yc.ptr, m, n, k, stream)
+    stream.synchronize()
+    y = yb.download(np.float32).reshape(m, n)
+    assert np.array_equal(y, yc.download(np.float32).reshape(m, n))
+    cols = sample_columns(n, 96)
+    y64 = oracle.gate_up_silu_f64(bits_to_f32(x), wg, wu, m, n, k, cols)
+    g64 = oracle.quantized_linear_f64(bits_to_f32(x), wg, m, n, k, cols)
+    u64 = oracle.quantized_linear_f64(bits_to_f32(x), wu, m, n, k, cols)
+    max_d = float(max(np.abs(q4_0_scales(wg, n, k)).max(), np.abs(q4_0_scales(wu, n, k)).max()))
+    max_x = float(np.abs(bits_to_f32(x)).max())
+    # silu(g) u: propagate the linear bound of g and u through the product
+    # (|d silu/dg| <= 1.1): |dy| <= 1.1 |u| tol_g + |silu(g)| tol_u.
+    from helpers import linear_tolerance
+
+    silu = g64 / (1.0 + np.exp(-g64))
+    tol = 1.1 * np.abs(u64) * linear_tolerance(g64, k, max_d, max_x) + np.abs(silu) * linear_tolerance(
+        u64, k, max_d, max_x
+    )
+    err = np.abs(y[:, cols] - y64)
+    assert np.all(err <= np.maximum(tol, 1e-3 * np.abs(y64))), float(np.max(err - tol))
+
+
+# --- every kernel variant, ragged and misaligned shapes ------------------------------
+
+def _variants(prefix):
+    return [v for v in ops.variant_names() if v.startswith(prefix)]
+
+
+@pytest.mark.parametrize("variant", _variants("gemv_") + ["generic"])
+def test_every_vector_variant(stream, oracle, variant):
+    d = ops.Q4_0Dispatch()
+    d.force(variant)
+    for m, n, k in [(1, 257, 1024), (5, 61, 4480), (3, 130, 64)]:
+        x = normal_x(wl.seed_for(9, m), m, k)
+        w = weights(wl.seed_for(9, 100 + n), n, k)
+        y = run_linear(stream, x, w, m, n, k, dispatch=d)
+        check_against_oracle(oracle, y, x, w, m, n, k, what=f"{variant} {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("variant", _variants("mfma_"))
+def test_every_mfma_variant(stream, oracle, variant):
+    d = ops.Q4_0Dispatch()
+    d.force(variant)
+    for m, n, k in [(70, 200, 512), (130, 67, 1024), (64, 128, 64)]:
+        x = normal_x(wl.seed_for(10, m), m, k)
+        w = weights(wl.seed_for(10, 100 + n), n, k)
+        y = run_linear(stream, x, w, m, n, k, dispatch=d)
+        check_against_oracle(oracle, y, x, w, m, n, k, what=f"{variant} {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("variant", _variants("gateup_"))
+def test_every_gate_up_variant(stream, oracle, variant):
+    d = ops.Q4_0Dispatch()
+    d.force(variant)
+    m, n, k = 70, 100, 512
+    x = normal_x(wl.seed_for(11, 0), m, k)
+    wg, wu = weights(wl.seed_for(11, 1), n, k), weights(wl.seed_for(11, 2), n, k)
+    xb, gb, ub = DeviceBuffer.from_array(x), DeviceBuffer.from_array(wg), DeviceBuffer.from_array(wu)
+    yb = DeviceBuffer(m * n * 4)
+    d.gate_up_silu(xb.ptr, gb.ptr, ub.ptr, yb.ptr, m, n, k, stream)
+    stream.synchronize()
+    y = yb.download(np.float32).reshape(m, n)
+    y64 = oracle.gate_up_silu_f64(bits_to_f32(x), wg, wu, m, n, k)
+    assert np.all(np.abs(y - y64) <= np.maximum(2e-2, 2e-3 * np.abs(y64))), float(np.max(np.abs(y - y64)))
+
+
+@pytest.mark.parametrize(
+    "m,n,k,w_offset,x_offset",
+    [(7, 13, 96, 0, 0), (2, 33, 4096, 2, 0), (1, 40, 1024, 0, 2), (65, 50, 512, 2, 0), (9, 1, 32, 0, 0)],
+    ids=["k96", "w_misaligned", "x_misaligned", "prefill_w_misaligned", "k32_n1"],
+)
+def test_ragged_and_misaligned(stream, oracle, m, n, k, w_offset, x_offset):
+    x = normal_x(wl.seed_for(12, m), m, k)
+    w = weights(wl.seed_for(12, n), n, k)
+    y = run_linear(stream, x, w, m, n, k, w_offset=w_offset, x_offset=x_offset)
+    check_against_oracle(oracle, y, x, w, m, n, k)
+
+
+# --- bit-exact decode ----------------------------------------------------------------
+
+def _all_scale_weights(k: int) -> np.ndarray:
+    """One block per binary16 scale pattern (all 65536), nibble bytes covering
+    every low and high nibble value at every position."""
+    blocks = 65536
+    out = np.empty((blocks, 18), dtype=np.uint8)
+    out[:, 0:2] = np.arange(blocks, dtype="<u2").view(np.uint8).reshape(blocks, 2)
+    j = np.arange(16)
+    b = np.arange(blocks)[:, None]
+    out[:, 2:] = ((j + b) % 16 | (((15 - j) + 3 * b) % 16) << 4).astype(np.uint8)
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("k,offset", [(4096, 0), (4096, 2), (32, 0)], ids=["pairs", "misaligned", "k32"])
+def test_decode_is_bit_exact_for_every_scale(stream, oracle, k, offset):
+    w = _all_scale_weights(k)
+    rows = w.size // row_bytes(k)
+    wb = DeviceBuffer(w.nbytes + offset)
+    wb.upload(w, offset=offset)
+    ob = DeviceBuffer(rows * k * 4)
+    ops.dequantize_q4_0_f32(wb.ptr + offset, ob.ptr, rows, k, stream)
+    stream.synchronize()
+    got = ob.download(np.float32).reshape(rows, k)
+    rb = row_bytes(k)
+    want = np.stack([oracle.dequantize_row(w[r * rb:(r + 1) * rb], oracle.Q4_0, k) for r in range(rows)])
+    gn, wn = np.isnan(got), np.isnan(want)
+    assert np.array_equal(gn, wn)
+    assert np.array_equal(got[~gn].view(np.uint32), want[~wn].view(np.uint32))
+
+
+# --- size-independent properties at full size ------------------------------------------
+
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 14336), (1, 14336, 4096), (8, 4096, 14336), (256, 4096, 14336)])
+def test_exact_properties_at_full_size(stream, m, k, n):
+    """Doubling x doubles y, negating every scale negates y, and zeroing the
+    scales of one K block equals zeroing those 32 activations: all exact in
+    the kernels' f32 arithmetic, so compared bit for bit.  Repeated runs are
+    bitwise identical (no atomics)."""
+    x = normal_x(wl.seed_for(1, 0), m, k)
+    w = weights(wl.seed_for(1, 1), n, k)
+    y = run_linear(stream, x, w, m, n, k)
+    assert np.array_equal(y, run_linear(stream, x, w, m, n, k)), "non-deterministic"
+    x2 = f16_bits(bits_to_f32(x) * 2.0)
+    assert np.array_equal(run_linear(stream, x2, w, m, n, k), 2.0 * y)
+    wneg = w.copy().reshape(n, k // 32, 18)
+    wneg[:, :, 1] ^= 0x80
+    yneg = run_linear(stream, x, wneg.reshape(-1), m, n, k)
+    if m < 64:
+        assert np.array_equal(yneg, -y)
+    else:
+        # The matrix cores' f32 accumulation is not symmetric under negation
+        # (measured: 1-ulp differences), so the MFMA path is held to 4 ulps.
+        ulp = np.spacing(np.abs(y).astype(np.float32))
+        assert np.all(np.abs(yneg + y) <= 4 * ulp)
+    blk = 5
+    wz = w.copy().reshape(n, k // 32, 18)
+    wz[:, blk, 0:2] = 0
+    xz = x.copy().reshape(m, k)
+    xz[:, 32 * blk:32 * blk + 32] = 0
+    assert np.array_equal(run_linear(stream, x, wz.reshape(-1), m, n, k), run_linear(stream, xz.reshape(-1), w, m, n, k))
+
+
+def test_autotuned_dispatch_caches_a_plan(stream, oracle):
+    m, k, n = 1, 4096, 4096
+    d = ops.Q4_0Dispatch(autotune=True)
+    x = normal_x(wl.seed_for(1, 0), m, k)
+    w = weights(wl.seed_for(0, 1), n, k)
+    assert d.plan(m, n, k) is None
+    y = run_linear(stream, x, w, m, n, k, dispatch=d)
+    assert d.plan(m, n, k) in ops.variant_names()
+    check_against_oracle(oracle, y, x, w, m, n, k)
