@@ -1,0 +1,319 @@
+"""Benchmark of the Q4_0 quantized-linear hot path on one MI355X.
+
+Workload (the headline case): the Llama-3-8B MLP up/gate decode linear,
+M = 1 token, K = 4096 input features, N = 14336 output features, GGML Q4_0
+weights (18-byte blocks of 32), f16 activations, f32 output, through the C ABI
+entry point ``mote_hip_quantized_linear_q4_0_f32`` of ``libmote_hip.so``.
+
+* A "step" is one call of the linear.  ``--warmup`` untimed calls, then
+  ``--steps`` timed calls enqueued back to back on one HIP stream, bracketed by
+  HIP events recorded on that same stream (stream synchronised on both sides).
+* The weights rotate over enough distinct device copies (>= 384 MB) that no
+  call finds its matrix in the 256 MB last-level cache (MALL): every call
+  reads its weights from HBM, as a decode step over a real model does.
+* Algorithmic bytes per call: |W| = N (K/32) 18, |x| = 2 M K, |y| = 4 M N,
+  each counted once (33 095 680 B for the headline case).
+* ``value`` is the whole-job rate, bytes x steps / elapsed (launch gaps
+  included); ``roofline.achieved`` divides the same bytes by the kernel's own
+  average duration, measured with an event pair around every launch.
+* ``roofline.traffic`` is the HBM traffic per launch measured by rocprofv3
+  counters, read from the committed summary under ``profiles/`` (null when
+  absent).
+* ``cpu_baseline`` times the single-threaded C restatement of the reference's
+  CPU oracle (``quantized_linear_f32``, crates/mote-reference/src/
+  quantized.rs:89-144) on the same inputs for a bounded number of calls, and
+  uses its output to check the GPU result.
+
+Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep]``.
+``--sweep`` also prints one line per parity-test configuration to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import re
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from mote_amd import _ffi, ops, workloads as wl  # noqa: E402
+from mote_amd.device import DeviceBuffer, Stream, device_count  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 << 20
+ROTATION_BYTES = 384 << 20
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "q4_0_gemv_m1_k4096_n14336_traffic.md")
+
+
+# --- HIP events from the runtime instance libmote_hip.so is linked against ----
+
+class _Events:
+    def __init__(self) -> None:
+        _ffi.lib()  # loads libamdhip64.so.7 as a dependency first
+        h = ctypes.CDLL("libamdhip64.so.7")
+        P = ctypes.c_void_p
+        h.hipEventCreate.argtypes = [ctypes.POINTER(P)]
+        h.hipEventRecord.argtypes = [P, P]
+        h.hipEventSynchronize.argtypes = [P]
+        h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), P, P]
+        h.hipEventDestroy.argtypes = [P]
+        self.h = h
+
+    def create(self) -> int:
+        e = ctypes.c_void_p()
+        _ffi.check(self.h.hipEventCreate(ctypes.byref(e)), "create event")
+        return e.value
+
+    def record(self, event: int, stream: Stream) -> None:
+        _ffi.check(self.h.hipEventRecord(event, stream.handle), "record event")
+
+    def elapsed_ms(self, start: int, stop: int) -> float:
+        _ffi.check(self.h.hipEventSynchronize(stop), "synchronize event")
+        ms = ctypes.c_float()
+        _ffi.check(self.h.hipEventElapsedTime(ctypes.byref(ms), start, stop), "event elapsed time")
+        return float(ms.value)
+
+    def destroy(self, event: int) -> None:
+        self.h.hipEventDestroy(event)
+
+
+def linear_bytes(m: int, n: int, k: int, out_bytes: int = 4) -> int:
+    return n * (k // 32) * 18 + 2 * m * k + out_bytes * m * n
+
+
+def read_traffic() -> dict | None:
+    """Per-launch HBM bytes from the committed rocprofv3 counter summary: the
+    line ``traffic_bytes_per_launch: <int>`` (FETCH_SIZE + WRITE_SIZE, scaled by
+    the copy-kernel calibration stated in the summary)."""
+    try:
+        with open(TRAFFIC_SUMMARY, encoding="utf-8") as f:
+            text = f.read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", text)
+    return int(m.group(1)) if m else None
+
+
+class LinearCase:
+    """Device buffers for one Q4_0 linear problem with rotating weight copies."""
+
+    def __init__(self, m: int, n: int, k: int, workload: int, x_uniform: bool = False,
+                 gate_up: bool = False) -> None:
+        self.m, self.n, self.k, self.gate_up = m, n, k, gate_up
+        self.x = (wl.uniform_f16 if x_uniform else wl.normal_f16)(wl.seed_for(workload, 0), m * k)
+        self.w = wl.q4_0_weights(wl.seed_for(workload, 1), n, k)
+        self.w_up = wl.q4_0_weights(wl.seed_for(workload, 2), n, k) if gate_up else None
+        per_copy = self.w.nbytes * (2 if gate_up else 1)
+        self.copies = max(2, math.ceil(ROTATION_BYTES / per_copy))
+        self.xb = DeviceBuffer.from_array(self.x)
+        self.wb = []
+        for _ in range(self.copies):
+            mats = [self.w] if not gate_up else [self.w, self.w_up]
+            self.wb.append([DeviceBuffer.from_array(a) for a in mats])
+        self.yb = DeviceBuffer(m * n * 4)
+
+    def launch(self, i: int, stream: Stream) -> None:
+        bufs = self.wb[i % self.copies]
+        if self.gate_up:
+            ops.q4_0_gate_up_silu_f32(self.xb.ptr, bufs[0].ptr, bufs[1].ptr, self.yb.ptr,
+                                      self.m, self.n, self.k, stream)
+        else:
+            ops.quantized_linear_q4_0_f32(self.xb.ptr, bufs[0].ptr, self.yb.ptr,
+                                          self.m, self.n, self.k, stream)
+
+    def algorithmic_bytes(self) -> int:
+        b = linear_bytes(self.m, self.n, self.k)
+        return b + (self.w_up.nbytes if self.gate_up else 0)
+
+    def flops(self) -> int:
+        return 2 * self.m * self.n * self.k * (2 if self.gate_up else 1)
+
+    def output(self) -> np.ndarray:
+        return self.yb.download(np.float32).reshape(self.m, self.n)
+
+    def free(self) -> None:
+        self.xb.free()
+        self.yb.free()
+        for bufs in self.wb:
+            for b in bufs:
+                b.free()
+
+
+def time_case(case: LinearCase, stream: Stream, ev: _Events, steps: int, warmup: int) -> dict:
+    """`steps` back-to-back calls on one stream.  The host clock around the
+    enqueue loop and the final synchronisation gives the whole-job time; one
+    HIP event pair recorded on the same stream around the whole run gives the
+    GPU time, whose average per call is the kernel's average launch duration
+    (the kernels run back to back, so launch gaps are hidden behind them; an
+    event pair around every single launch would add its own overhead)."""
+    for i in range(warmup):
+        case.launch(i, stream)
+    stream.synchronize()
+
+    start, stop = ev.create(), ev.create()
+    t0 = time.perf_counter()
+    ev.record(start, stream)
+    for i in range(steps):
+        case.launch(i, stream)
+    ev.record(stop, stream)
+    stream.synchronize()
+    wall_s = time.perf_counter() - t0
+    gpu_ms = ev.elapsed_ms(start, stop)
+    ev.destroy(start)
+    ev.destroy(stop)
+    return {"ms_per_step": wall_s * 1e3 / steps, "kernel_ms_mean": gpu_ms / steps}
+
+
+def cpu_baseline(case: LinearCase, budget_s: float) -> tuple[dict, np.ndarray]:
+    """The single-threaded C oracle on the same inputs: calls until `budget_s`
+    of CPU time (at least one).  Returns the report and one f32 output."""
+    import oracle  # the CPU restatement of the reference oracle (checker only)
+
+    x32 = case.x.view(np.float16).astype(np.float32)
+    first = oracle.time_quantized_linear_f32(x32, case.w, case.m, case.n, case.k, 1)
+    calls = max(1, min(200, int(budget_s / max(first, 1e-6))))
+    seconds = oracle.time_quantized_linear_f32(x32, case.w, case.m, case.n, case.k, calls)
+    y_cpu = oracle.quantized_linear_f32(x32, case.w, oracle.Q4_0, case.m, case.n, case.k)
+    per_call = seconds / calls
+    report = {
+        "value": round(case.algorithmic_bytes() / per_call / 1e9, 4),
+        "unit": "GB/s",
+        "us_per_call": round(per_call * 1e6, 1),
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{calls} calls of the f32 oracle (gcc -O2, -ffp-contract=off) at "
+                   f"M={case.m} K={case.k} N={case.n}, {seconds:.1f} s, host has "
+                   f"{os.cpu_count()} cores"),
+    }
+    return report, y_cpu.reshape(case.m, case.n)
+
+
+def check_output(case: LinearCase, y_cpu: np.ndarray) -> None:
+    """Parity with the oracle's f32 output: |y - y_cpu| <= 1e-3 |y_cpu| +
+    2e-3 sqrt(K) max|d| max|x| (the f32 oracle itself is within a few ulps of
+    the f64 sum at these sizes)."""
+    y = case.output()
+    scales = case.w.reshape(case.n, case.k // 32, 18)[:, :, 0:2].copy().view("<u2")[..., 0]
+    max_d = float(np.abs(scales.view(np.float16).astype(np.float32)).max())
+    max_x = float(np.abs(case.x.view(np.float16).astype(np.float32)).max())
+    tol = np.maximum(1e-3 * np.abs(y_cpu), 2e-3 * math.sqrt(case.k) * max_d * max_x)
+    bad = np.abs(y.astype(np.float64) - y_cpu) > tol
+    if bad.any():
+        raise SystemExit(f"bench: GPU output differs from the oracle in {int(bad.sum())} elements")
+
+
+SWEEP = (
+    [("cfg0 decode", 1, 4096, 4096, 0, True, False), ("cfg1 up/gate", 1, 4096, 14336, 1, False, False),
+     ("cfg1 down", 1, 14336, 4096, 1, False, False)]
+    + [(f"cfg2 skinny", m, 4096, n, 2, False, False) for n in (4096, 6144, 14336) for m in (2, 4, 8, 16, 32)]
+    + [("cfg4 prefill", m, 4096, 14336, 4, False, False) for m in (64, 256, 512)]
+    + [("cfg4 gate/up", m, 4096, 14336, 4, False, True) for m in (64, 256, 512)]
+)
+
+
+def run_sweep(stream: Stream, ev: _Events, steps: int, warmup: int) -> None:
+    print(f"{'case':<14}{'M':>5}{'K':>7}{'N':>7}{'kernel us':>11}{'call us':>10}{'GB/s':>9}"
+          f"{'%HBM':>7}{'TFLOP/s':>9}{'%MFMA':>7}", file=sys.stderr)
+    for name, m, k, n, workload, uni, gate_up in SWEEP:
+        case = LinearCase(m, n, k, workload, x_uniform=uni, gate_up=gate_up)
+        t = time_case(case, stream, ev, steps, warmup)
+        us = t["kernel_ms_mean"] * 1e3
+        gbs = case.algorithmic_bytes() / (us * 1e-6) / 1e9
+        tf = case.flops() / (us * 1e-6) / 1e12
+        print(f"{name:<14}{m:>5}{k:>7}{n:>7}{us:>11.2f}{t['ms_per_step'] * 1e3:>10.2f}{gbs:>9.0f}"
+              f"{100 * gbs / HBM_PEAK_GBS:>6.1f}%{tf:>9.1f}{100 * tf / MFMA_F16_PEAK_TFLOPS:>6.1f}%",
+              file=sys.stderr, flush=True)
+        case.free()
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="CPU time budget of the oracle baseline (0 skips it)")
+    ap.add_argument("--sweep", action="store_true", help="also time every configuration (stderr)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the Q4_0 linear shards by output rows with no exchange; see the design notes)",
+              file=sys.stderr)
+        return 2
+    if args.steps < 1:
+        print("bench.py: --steps must be >= 1", file=sys.stderr)
+        return 2
+    if device_count() < 1:
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+
+    stream = Stream()
+    ev = _Events()
+    m, k, n = 1, 4096, 14336
+    case = LinearCase(m, n, k, workload=1)
+    print(f"bench: Q4_0 linear M={m} K={k} N={n}, {case.copies} weight copies "
+          f"({case.copies * case.w.nbytes / 1e6:.0f} MB), warmup {args.warmup}, steps {args.steps}",
+          file=sys.stderr, flush=True)
+    t = time_case(case, stream, ev, args.steps, args.warmup)
+    nbytes = case.algorithmic_bytes()
+    value = nbytes / (t["ms_per_step"] * 1e-3) / 1e9
+    achieved = nbytes / (t["kernel_ms_mean"] * 1e-3) / 1e9
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu, y_cpu = cpu_baseline(case, args.cpu_seconds)
+        check_output(case, y_cpu)
+
+    line = {
+        "metric": "Q4_0 linear µs/call + achieved HBM GB/s (% peak), M=1 K=4096 N=14336",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t["ms_per_step"], 6),
+        "us_per_call": round(t["ms_per_step"] * 1e3, 3),
+        "kernel_us": round(t["kernel_ms_mean"] * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "Q4_0 decode linear, Llama-3-8B MLP up/gate: M=1, K=4096, N=14336",
+            "M": m, "K": k, "N": n,
+            "weights": "GGML Q4_0, d=f16(|N(0,0.02)|), uniform nibbles, SplitMix64 seeded",
+            "activations": "f16 N(0,1)", "output": "f32",
+            "entry_point": "mote_hip_quantized_linear_q4_0_f32",
+            "weight_copies": case.copies,
+            "algorithmic_bytes_per_call": nbytes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": read_traffic(),
+        },
+        "cpu_baseline": cpu,
+    }
+    if args.sweep:
+        run_sweep(stream, ev, min(args.steps, 50), min(args.warmup, 5))
+    case.free()
+    stream.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -173,9 +173,10 @@ def block_geometry(fmt: int) -> tuple[int, int, int]:
 
 def dequantize_row(data, fmt: int, row_elements: int) -> np.ndarray:
     w = _u8(data)
-    out = np.zeros(max(row_elements, 1), dtype=np.float32)
+    # Overflowing geometries are rejected before anything is written, so they
+    # get a one-element buffer.
+    out = np.zeros(row_elements if 0 < row_elements < (1 << 40) else 1, dtype=np.float32)
     detail = np.zeros(3, dtype=np.uint64)
-    # Overflowing geometries are rejected before anything is written.
     _check(lib().mote_oracle_dequantize_row(_ptr(w), w.size, fmt, row_elements, _ptr(out), _ptr(detail)), detail)
     return out[:row_elements]
 

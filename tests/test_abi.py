@@ -1,0 +1,182 @@
+"""CPU tests of the C ABI of libmote_hip.so (no GPU needed, nothing launched).
+
+* The library loads and exports exactly the symbols include/mote_hip.h
+  declares.
+* Every argument rejection and every empty-problem early return of the
+  reference's shims happens before any device work, so their status codes are
+  checked here with stand-in pointers that are never dereferenced
+  (crates/mote-backend-hip/src/quantized_linear.hip:64-76, rms_norm.hip:75-83,
+  fused_add_rms_norm.hip:107-122, rope.hip:109-130, hipblaslt_shim.cpp:259-324).
+* The dispatch context's host-side state (variants, forcing, plan lookup).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mote_hip.h")
+
+FAKE = 0x10000  # stand-in device pointer: every call below returns before using it
+STREAM = 0x20000
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from mote_amd import _ffi
+
+    if not os.path.exists(_ffi.LIBRARY):
+        from mote_amd import build
+
+        build.build()
+    return _ffi.lib()
+
+
+def declared_symbols() -> set[str]:
+    with open(HEADER, encoding="utf-8") as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(mote_\w+)\s*\(", text))
+
+
+def test_exports_match_header(lib):
+    from mote_amd import _ffi
+
+    declared = declared_symbols()
+    out = subprocess.run(["nm", "-D", "--defined-only", _ffi.LIBRARY], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert declared, "no declarations parsed"
+    assert declared == exported, (sorted(declared - exported), sorted(exported - declared))
+    assert declared == set(_ffi.SIGNATURES), "ctypes signature table out of sync with the header"
+    for name in declared:
+        assert getattr(lib, name) is not None
+
+
+def test_q4_0_linear_status_codes(lib):
+    for fn in (lib.mote_hip_quantized_linear_q4_0_f16, lib.mote_hip_quantized_linear_q4_0_f32):
+        assert fn(None, FAKE, FAKE, 1, 1, 32, STREAM) == 1
+        assert fn(FAKE, None, FAKE, 1, 1, 32, STREAM) == 1
+        assert fn(FAKE, FAKE, None, 1, 1, 32, STREAM) == 1
+        assert fn(FAKE, FAKE, FAKE, 1, 1, 32, None) == 1
+        assert fn(FAKE, FAKE, FAKE, 1, 1, 33, STREAM) == 1  # K % 32 != 0
+        assert fn(FAKE, FAKE, FAKE, 0, 5, 32, STREAM) == 0   # empty: no launch
+        assert fn(FAKE, FAKE, FAKE, 5, 0, 32, STREAM) == 0
+        assert fn(FAKE, FAKE, FAKE, 0, 5, 33, STREAM) == 1   # K checked before emptiness
+        assert fn(FAKE, FAKE, FAKE, 1 << 32, 1, 32, STREAM) == 9
+        assert fn(FAKE, FAKE, FAKE, 65536, 65536, 32, STREAM) == 9  # rows * N > UINT_MAX
+        assert fn(FAKE, FAKE, FAKE, 1, 1, 1 << 31, STREAM) == 9
+
+
+def test_gate_up_and_decode_status_codes(lib):
+    g = lib.mote_hip_q4_0_gate_up_silu_f32
+    assert g(None, FAKE, FAKE, FAKE, 1, 1, 32, STREAM) == 1
+    assert g(FAKE, FAKE, None, FAKE, 1, 1, 48, STREAM) == 1
+    assert g(FAKE, FAKE, None, FAKE, 0, 1, 32, STREAM) == 0
+    d = lib.mote_hip_dequantize_q4_0_f32
+    assert d(None, FAKE, 1, 32, STREAM) == 1
+    assert d(FAKE, FAKE, 1, 31, STREAM) == 1
+    assert d(FAKE, FAKE, 0, 32, STREAM) == 0
+    assert d(FAKE, FAKE, 4, 0, STREAM) == 0
+
+
+def test_norm_status_codes(lib):
+    r = lib.mote_hip_rms_norm_f16
+    assert r(None, FAKE, FAKE, 1, 8, 1e-6, STREAM) == -1
+    assert r(FAKE, FAKE, FAKE, 1, 8, 1e-6, None) == -1
+    assert r(FAKE, FAKE, FAKE, 0, 8, 1e-6, STREAM) == 0
+    assert r(FAKE, FAKE, FAKE, 3, 0, 1e-6, STREAM) == 0
+    assert r(FAKE, FAKE, FAKE, 1 << 32, 8, 1e-6, STREAM) == -1
+    f = lib.mote_hip_fused_add_rms_norm_f16
+    assert f(FAKE, FAKE + 64, FAKE, FAKE + 64, 1, 8, 1e-6, STREAM) == -1  # output == residual
+    for eps in (-1e-6, float("nan"), float("inf")):
+        assert f(FAKE, FAKE + 64, FAKE, FAKE + 128, 1, 8, eps, STREAM) == -1
+    assert f(FAKE, FAKE + 64, FAKE, FAKE + 128, 0, 8, 1e-6, STREAM) == 0
+    assert f(None, FAKE + 64, FAKE, FAKE + 128, 1, 8, 1e-6, STREAM) == -1
+
+
+def test_rope_status_codes(lib):
+    r = lib.mote_hip_rope_f16
+    assert r(FAKE, FAKE, FAKE, FAKE, 2, 3, 8, 7, 0, STREAM) == -1
+    assert r(FAKE, FAKE, FAKE, FAKE, 2, 3, 8, 10, 0, STREAM) == -1
+    assert r(FAKE, FAKE, FAKE, FAKE, 2, 3, 8, 8, 2, STREAM) == -1
+    assert r(FAKE, None, FAKE, FAKE, 2, 3, 8, 8, 0, STREAM) == -1
+    assert r(None, FAKE, FAKE, FAKE, 2, 3, 8, 8, 0, STREAM) == -1
+    assert r(FAKE, FAKE, FAKE, FAKE, 2, 3, 8, 8, 0, None) == -1
+    assert r(FAKE, FAKE, FAKE, FAKE, 0, 3, 8, 8, 0, STREAM) == 0
+    assert r(FAKE, FAKE, FAKE, FAKE, 2, 0, 8, 8, 0, STREAM) == 0
+    assert r(FAKE, FAKE, FAKE, FAKE, 1 << 31, 1 << 31, 8, 8, 0, STREAM) == -1
+    qk = lib.mote_hip_rope_qk_f16
+    assert qk(FAKE, None, FAKE, FAKE, FAKE, None, 2, 4, 1, 8, 8, 0, STREAM) == -1  # k heads but no k
+    assert qk(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 4, 1, 8, 9, 0, STREAM) == -1
+    assert qk(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0, 4, 1, 8, 8, 0, STREAM) == 0
+    assert qk(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 0, 0, 8, 8, 0, STREAM) == 0
+    t = lib.mote_hip_rope_tables_f32
+    assert t(FAKE, FAKE, FAKE, 4, 7, 10000.0, STREAM) == -1
+    assert t(FAKE, FAKE, FAKE, 4, 8, 0.0, STREAM) == -1
+    assert t(FAKE, FAKE, FAKE, 4, 8, float("nan"), STREAM) == -1
+    assert t(None, FAKE, FAKE, 4, 8, 10000.0, STREAM) == -1
+    assert t(FAKE, FAKE, FAKE, 0, 8, 10000.0, STREAM) == 0
+
+
+def test_runtime_wrappers_reject_null_out_parameters(lib):
+    assert lib.mote_hip_get_device_count(None) == -1
+    assert lib.mote_hip_malloc(None, 16) == -1
+    assert lib.mote_hip_stream_create(None) == -1
+    assert lib.mote_hip_mem_get_info(None, None) == -1
+
+
+def test_dispatch_context_host_state(lib):
+    names = [lib.mote_q4_0_variant_name(i).decode() for i in range(lib.mote_q4_0_variant_count())]
+    assert len(names) == len(set(names)) and "generic" in names and "gateup_generic" in names
+    assert lib.mote_q4_0_variant_name(-1) is None
+    assert lib.mote_q4_0_variant_name(len(names)) is None
+    h = ctypes.c_void_p()
+    assert lib.mote_q4_0_dispatch_create(ctypes.byref(h)) == 0 and h.value
+    try:
+        assert lib.mote_q4_0_dispatch_force_variant(h, b"no_such_kernel") == 1
+        assert b"no_such_kernel" in lib.mote_q4_0_dispatch_last_error(h)
+        assert lib.mote_q4_0_dispatch_force_variant(h, names[0].encode()) == 0
+        assert lib.mote_q4_0_dispatch_force_variant(h, None) == 0
+        assert lib.mote_q4_0_dispatch_set_autotune(h, 1) == 0
+        buf = ctypes.create_string_buffer(64)
+        assert lib.mote_q4_0_dispatch_plan(h, 1, 4096, 4096, 0, 0, buf, 64) == 500  # nothing cached
+        # argument errors surface through last_error without touching a device
+        assert lib.mote_q4_0_dispatch_linear(h, None, FAKE, FAKE, 1, 1, 32, 0, STREAM) == 1
+        assert lib.mote_q4_0_dispatch_last_error(h) != b""
+        assert lib.mote_q4_0_dispatch_linear(h, FAKE, FAKE, FAKE, 0, 1, 32, 0, STREAM) == 0
+        assert lib.mote_q4_0_dispatch_gate_up_silu(h, FAKE, FAKE, None, FAKE, 1, 1, 40, 0, STREAM) == 1
+    finally:
+        lib.mote_q4_0_dispatch_destroy(h)
+    assert lib.mote_q4_0_dispatch_create(None) == 1
+    assert lib.mote_q4_0_dispatch_linear(None, FAKE, FAKE, FAKE, 1, 1, 32, 0, STREAM) == 1
+    assert lib.mote_q4_0_dispatch_set_autotune(None, 1) == 1
+
+
+def test_python_wrappers_raise_hip_error(lib):
+    from mote_amd import HipError, ops
+
+    with pytest.raises(HipError) as e:
+        ops.quantized_linear_q4_0_f32(FAKE, FAKE, FAKE, 1, 1, 33, STREAM)
+    assert e.value.status == 1 and "Q4_0" in str(e.value)
+    with pytest.raises(HipError):
+        ops.rope_f16(FAKE, FAKE, FAKE, FAKE, 2, 3, 8, 7, ops.HALF_SPLIT, STREAM)
+    d = ops.Q4_0Dispatch()
+    with pytest.raises(HipError) as e:
+        d.force("no_such_kernel")
+    assert "no_such_kernel" in str(e.value)
+    d.close()
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from mote_amd import _ffi
+
+    monkeypatch.setattr(_ffi, "_lib", None)
+    monkeypatch.setattr(_ffi, "LIBRARY", str(tmp_path / "absent.so"))
+    with pytest.raises(_ffi.LibraryNotBuilt):
+        _ffi.lib()

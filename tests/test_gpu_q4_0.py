@@ -308,9 +308,11 @@ def test_exact_properties_at_full_size(stream, m, k, n):
         assert np.array_equal(yneg, -y)
     else:
         # The matrix cores' f32 accumulation is not symmetric under negation
-        # (measured: 1-ulp differences), so the MFMA path is held to 4 ulps.
-        ulp = np.spacing(np.abs(y).astype(np.float32))
-        assert np.all(np.abs(yneg + y) <= 4 * ulp)
+        # (measured: differences of a few ulps of the partial sums, which can
+        # exceed the result's own ulp after cancellation), so the MFMA path is
+        # held to 2^-20 of the accumulation scale sqrt(K) max|d| max|x| * 8.
+        scale = 8 * np.sqrt(k) * float(np.abs(q4_0_scales(w, n, k)).max()) * float(np.abs(bits_to_f32(x)).max())
+        assert np.all(np.abs(yneg + y) <= 2.0 ** -20 * scale)
     blk = 5
     wz = w.copy().reshape(n, k // 32, 18)
     wz[:, blk, 0:2] = 0
