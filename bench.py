@@ -6,16 +6,22 @@ weights (18-byte blocks of 32), f16 activations, f32 output, through the C ABI
 entry point ``mote_hip_quantized_linear_q4_0_f32`` of ``libmote_hip.so``.
 
 * A "step" is one call of the linear.  ``--warmup`` untimed calls, then
-  ``--steps`` timed calls enqueued back to back on one HIP stream, bracketed by
-  HIP events recorded on that same stream (stream synchronised on both sides).
+  ``--steps`` calls captured once into a HIP graph (stream capture of the C-ABI
+  calls) and replayed three times, bracketed by HIP events recorded on the
+  launch stream and by the host clock (stream synchronised on both sides).
+  The graph issues the kernels back to back with no host work in between, as
+  a decode loop captured in a graph does; the eager rate (one Python ctypes
+  call per step, bounded by the host for kernels this short) is reported
+  beside it.
 * The weights rotate over enough distinct device copies (>= 384 MB) that no
   call finds its matrix in the 256 MB last-level cache (MALL): every call
   reads its weights from HBM, as a decode step over a real model does.
 * Algorithmic bytes per call: |W| = N (K/32) 18, |x| = 2 M K, |y| = 4 M N,
   each counted once (33 095 680 B for the headline case).
-* ``value`` is the whole-job rate, bytes x steps / elapsed (launch gaps
-  included); ``roofline.achieved`` divides the same bytes by the kernel's own
-  average duration, measured with an event pair around every launch.
+* ``value`` is the whole-job rate, bytes x calls / host time of the replays;
+  ``roofline.achieved`` divides the same bytes by the average launch duration
+  from the events (the kernels run back to back, so this agrees with the
+  kernel durations of a rocprofv3 kernel trace).
 * ``roofline.traffic`` is the HBM traffic per launch measured by rocprofv3
   counters, read from the committed summary under ``profiles/`` (null when
   absent).
@@ -54,9 +60,14 @@ ROTATION_BYTES = 384 << 20
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "q4_0_gemv_m1_k4096_n14336_traffic.md")
 
 
-# --- HIP events from the runtime instance libmote_hip.so is linked against ----
+# --- HIP events and graphs from the runtime libmote_hip.so is linked against ---
 
-class _Events:
+class _Hip:
+    """hipEvent / hipGraph entry points of the libamdhip64.so.7 instance that
+    libmote_hip.so loaded (the same runtime, so its streams are valid here)."""
+
+    CAPTURE_THREAD_LOCAL = 1
+
     def __init__(self) -> None:
         _ffi.lib()  # loads libamdhip64.so.7 as a dependency first
         h = ctypes.CDLL("libamdhip64.so.7")
@@ -66,6 +77,12 @@ class _Events:
         h.hipEventSynchronize.argtypes = [P]
         h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), P, P]
         h.hipEventDestroy.argtypes = [P]
+        h.hipStreamBeginCapture.argtypes = [P, ctypes.c_int]
+        h.hipStreamEndCapture.argtypes = [P, ctypes.POINTER(P)]
+        h.hipGraphInstantiate.argtypes = [ctypes.POINTER(P), P, P, P, ctypes.c_size_t]
+        h.hipGraphLaunch.argtypes = [P, P]
+        h.hipGraphExecDestroy.argtypes = [P]
+        h.hipGraphDestroy.argtypes = [P]
         self.h = h
 
     def create(self) -> int:
@@ -84,6 +101,28 @@ class _Events:
 
     def destroy(self, event: int) -> None:
         self.h.hipEventDestroy(event)
+
+    def capture(self, stream: Stream, body) -> int:
+        """Records the launches `body()` enqueues on `stream` into an
+        executable graph (nothing runs during capture)."""
+        _ffi.check(self.h.hipStreamBeginCapture(stream.handle, self.CAPTURE_THREAD_LOCAL), "begin capture")
+        try:
+            body()
+        finally:
+            graph = ctypes.c_void_p()
+            status = self.h.hipStreamEndCapture(stream.handle, ctypes.byref(graph))
+        _ffi.check(status, "end capture")
+        exe = ctypes.c_void_p()
+        status = self.h.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0)
+        self.h.hipGraphDestroy(graph)
+        _ffi.check(status, "instantiate graph")
+        return exe.value
+
+    def launch_graph(self, exe: int, stream: Stream) -> None:
+        _ffi.check(self.h.hipGraphLaunch(exe, stream.handle), "launch graph")
+
+    def destroy_graph(self, exe: int) -> None:
+        self.h.hipGraphExecDestroy(exe)
 
 
 def linear_bytes(m: int, n: int, k: int, out_bytes: int = 4) -> int:
@@ -148,29 +187,56 @@ class LinearCase:
                 b.free()
 
 
-def time_case(case: LinearCase, stream: Stream, ev: _Events, steps: int, warmup: int) -> dict:
-    """`steps` back-to-back calls on one stream.  The host clock around the
-    enqueue loop and the final synchronisation gives the whole-job time; one
-    HIP event pair recorded on the same stream around the whole run gives the
-    GPU time, whose average per call is the kernel's average launch duration
-    (the kernels run back to back, so launch gaps are hidden behind them; an
-    event pair around every single launch would add its own overhead)."""
+def time_case(case: LinearCase, stream: Stream, hip: _Hip, steps: int, warmup: int,
+              replays: int = 3) -> dict:
+    """`steps` calls back to back, issued two ways.
+
+    * graph: the `steps` C-ABI calls are captured once into a HIP graph, which
+      is then replayed; the kernels run back to back with no host work between
+      them.  An event pair on the launch stream around the replays gives the
+      average kernel launch duration (it agrees with rocprofv3's kernel trace),
+      and the host clock around the same replays the whole-job rate.
+    * eager: each call enqueued from Python through ctypes; for kernels of a
+      few microseconds this rate is bounded by the host, and is reported for
+      reference only.
+    """
     for i in range(warmup):
         case.launch(i, stream)
     stream.synchronize()
 
-    start, stop = ev.create(), ev.create()
+    start, stop = hip.create(), hip.create()
+    hip.record(start, stream)
     t0 = time.perf_counter()
-    ev.record(start, stream)
     for i in range(steps):
         case.launch(i, stream)
-    ev.record(stop, stream)
+    hip.record(stop, stream)
     stream.synchronize()
-    wall_s = time.perf_counter() - t0
-    gpu_ms = ev.elapsed_ms(start, stop)
-    ev.destroy(start)
-    ev.destroy(stop)
-    return {"ms_per_step": wall_s * 1e3 / steps, "kernel_ms_mean": gpu_ms / steps}
+    eager_wall_s = time.perf_counter() - t0
+    eager_gpu_ms = hip.elapsed_ms(start, stop)
+
+    exe = hip.capture(stream, lambda: [case.launch(i, stream) for i in range(steps)])
+    try:
+        hip.launch_graph(exe, stream)  # warm-up replay
+        stream.synchronize()
+        t0 = time.perf_counter()
+        hip.record(start, stream)
+        for _ in range(replays):
+            hip.launch_graph(exe, stream)
+        hip.record(stop, stream)
+        stream.synchronize()
+        wall_s = time.perf_counter() - t0
+        gpu_ms = hip.elapsed_ms(start, stop)
+    finally:
+        hip.destroy_graph(exe)
+        hip.destroy(start)
+        hip.destroy(stop)
+    calls = steps * replays
+    return {
+        "ms_per_step": wall_s * 1e3 / calls,
+        "kernel_ms_mean": gpu_ms / calls,
+        "eager_ms_per_step": eager_wall_s * 1e3 / steps,
+        "eager_gpu_ms_per_step": eager_gpu_ms / steps,
+    }
 
 
 def cpu_baseline(case: LinearCase, budget_s: float) -> tuple[dict, np.ndarray]:
@@ -211,6 +277,24 @@ def check_output(case: LinearCase, y_cpu: np.ndarray) -> None:
         raise SystemExit(f"bench: GPU output differs from the oracle in {int(bad.sum())} elements")
 
 
+def profile_run(case: LinearCase, stream: Stream, hip: _Hip) -> int:
+    """Copy one weight matrix device to device (reads and writes |W| bytes:
+    the runtime's copy kernel calibrates the HBM byte counters), then run the
+    headline linear 20 times on rotating weight copies."""
+    dst = DeviceBuffer(case.w.nbytes)
+    h = hip.h
+    h.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    _ffi.check(h.hipMemcpy(dst.ptr, case.wb[0][0].ptr, case.w.nbytes, 3), "device-to-device copy")
+    for i in range(20):
+        case.launch(i + 1, stream)
+    stream.synchronize()
+    print(f"profile run: copied {case.w.nbytes} bytes, 20 linear calls", file=sys.stderr)
+    dst.free()
+    case.free()
+    stream.close()
+    return 0
+
+
 SWEEP = (
     [("cfg0 decode", 1, 4096, 4096, 0, True, False), ("cfg1 up/gate", 1, 4096, 14336, 1, False, False),
      ("cfg1 down", 1, 14336, 4096, 1, False, False)]
@@ -220,16 +304,16 @@ SWEEP = (
 )
 
 
-def run_sweep(stream: Stream, ev: _Events, steps: int, warmup: int) -> None:
-    print(f"{'case':<14}{'M':>5}{'K':>7}{'N':>7}{'kernel us':>11}{'call us':>10}{'GB/s':>9}"
+def run_sweep(stream: Stream, hip: _Hip, steps: int, warmup: int) -> None:
+    print(f"{'case':<14}{'M':>5}{'K':>7}{'N':>7}{'kernel us':>11}{'eager us':>10}{'GB/s':>9}"
           f"{'%HBM':>7}{'TFLOP/s':>9}{'%MFMA':>7}", file=sys.stderr)
     for name, m, k, n, workload, uni, gate_up in SWEEP:
         case = LinearCase(m, n, k, workload, x_uniform=uni, gate_up=gate_up)
-        t = time_case(case, stream, ev, steps, warmup)
+        t = time_case(case, stream, hip, steps, warmup)
         us = t["kernel_ms_mean"] * 1e3
         gbs = case.algorithmic_bytes() / (us * 1e-6) / 1e9
         tf = case.flops() / (us * 1e-6) / 1e12
-        print(f"{name:<14}{m:>5}{k:>7}{n:>7}{us:>11.2f}{t['ms_per_step'] * 1e3:>10.2f}{gbs:>9.0f}"
+        print(f"{name:<14}{m:>5}{k:>7}{n:>7}{us:>11.2f}{t['eager_ms_per_step'] * 1e3:>10.2f}{gbs:>9.0f}"
               f"{100 * gbs / HBM_PEAK_GBS:>6.1f}%{tf:>9.1f}{100 * tf / MFMA_F16_PEAK_TFLOPS:>6.1f}%",
               file=sys.stderr, flush=True)
         case.free()
@@ -243,6 +327,10 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU time budget of the oracle baseline (0 skips it)")
     ap.add_argument("--sweep", action="store_true", help="also time every configuration (stderr)")
+    ap.add_argument("--profile-run", action="store_true",
+                    help="for rocprofv3 counter passes: one device-to-device copy of one weight "
+                         "matrix (the calibration kernel of known size), then 20 calls of the "
+                         "headline linear; prints no result line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -257,13 +345,15 @@ def main() -> int:
         return 1
 
     stream = Stream()
-    ev = _Events()
+    hip = _Hip()
     m, k, n = 1, 4096, 14336
     case = LinearCase(m, n, k, workload=1)
+    if args.profile_run:
+        return profile_run(case, stream, hip)
     print(f"bench: Q4_0 linear M={m} K={k} N={n}, {case.copies} weight copies "
           f"({case.copies * case.w.nbytes / 1e6:.0f} MB), warmup {args.warmup}, steps {args.steps}",
           file=sys.stderr, flush=True)
-    t = time_case(case, stream, ev, args.steps, args.warmup)
+    t = time_case(case, stream, hip, args.steps, args.warmup)
     nbytes = case.algorithmic_bytes()
     value = nbytes / (t["ms_per_step"] * 1e-3) / 1e9
     achieved = nbytes / (t["kernel_ms_mean"] * 1e-3) / 1e9
@@ -283,6 +373,8 @@ def main() -> int:
         "ms_per_step": round(t["ms_per_step"], 6),
         "us_per_call": round(t["ms_per_step"] * 1e3, 3),
         "kernel_us": round(t["kernel_ms_mean"] * 1e3, 3),
+        "eager_us_per_call": round(t["eager_ms_per_step"] * 1e3, 3),
+        "issue": "HIP graph of `steps` captured C-ABI calls, replayed 3 times",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -308,7 +400,7 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     if args.sweep:
-        run_sweep(stream, ev, min(args.steps, 50), min(args.warmup, 5))
+        run_sweep(stream, hip, min(args.steps, 50), min(args.warmup, 5))
     case.free()
     stream.close()
     print(json.dumps(line), flush=True)

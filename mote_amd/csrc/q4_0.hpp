@@ -20,7 +20,8 @@ struct Problem {
     hipStream_t stream;
 };
 
-enum class Kind : int { Gemv = 0, Mfma = 1, Generic = 2, GateUpMfma = 3, GateUpGeneric = 4 };
+enum class Kind : int { Gemv = 0, Mfma = 1, Generic = 2, GateUpMfma = 3, GateUpGeneric = 4, GemvRows = 5,
+                        GemvStream = 6 };
 
 struct Variant {
     const char* name;
@@ -31,11 +32,15 @@ struct Variant {
 
 // Kernel variant tables, defined next to the kernels.
 const Variant* gemv_variants(int* count);
+const Variant* gemv_rows_variants(int* count);
+const Variant* gemv_stream_variants(int* count);
 const Variant* mfma_variants(int* count);
 const Variant* generic_variants(int* count);
 
 // Whether a variant can run the problem (alignment, shape limits).
 bool gemv_supports(const Variant& v, const Problem& p);
+bool gemv_rows_supports(const Variant& v, const Problem& p);
+bool gemv_stream_supports(const Variant& v, const Problem& p);
 bool mfma_supports(const Variant& v, const Problem& p);
 
 hipError_t launch_zero_fill(void* y, uint64_t count, OutType out, hipStream_t stream);

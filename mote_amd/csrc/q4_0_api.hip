@@ -19,6 +19,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -53,7 +54,8 @@ struct Dispatcher {
 std::vector<const Variant*> all_variants() {
     std::vector<const Variant*> out;
     int count = 0;
-    for (auto table : {gemv_variants, mfma_variants, generic_variants}) {
+    for (auto table : {gemv_stream_variants, gemv_rows_variants, gemv_variants, mfma_variants,
+                       generic_variants}) {
         const Variant* v = table(&count);
         for (int i = 0; i < count; ++i) out.push_back(&v[i]);
     }
@@ -68,12 +70,15 @@ const Variant* find_variant(const std::string& name) {
 
 bool kind_matches(const Variant& v, Op op) {
     if (op == Op::GateUp) return v.kind == Kind::GateUpMfma || v.kind == Kind::GateUpGeneric;
-    return v.kind == Kind::Gemv || v.kind == Kind::Mfma || v.kind == Kind::Generic;
+    return v.kind == Kind::Gemv || v.kind == Kind::GemvRows || v.kind == Kind::GemvStream ||
+           v.kind == Kind::Mfma || v.kind == Kind::Generic;
 }
 
 bool supports(const Variant& v, const Problem& p) {
     switch (v.kind) {
         case Kind::Gemv: return gemv_supports(v, p);
+        case Kind::GemvRows: return gemv_rows_supports(v, p);
+        case Kind::GemvStream: return gemv_stream_supports(v, p);
         case Kind::Mfma:
         case Kind::GateUpMfma: return mfma_supports(v, p);
         default: return true;
@@ -94,7 +99,9 @@ std::vector<const Variant*> candidates(const Problem& p, Op op) {
         if (!kind_matches(*v, op) || !supports(*v, p)) continue;
         const bool generic = v->kind == Kind::Generic || v->kind == Kind::GateUpGeneric;
         if (generic && fast_eligible(p)) continue;
-        if (v->kind == Kind::Gemv && p.M >= 64) continue;
+        const bool vector_alu = v->kind == Kind::Gemv || v->kind == Kind::GemvRows ||
+                                v->kind == Kind::GemvStream;
+        if (vector_alu && p.M >= 64) continue;
         if ((v->kind == Kind::Mfma || v->kind == Kind::GateUpMfma) && p.M < 64) continue;
         out.push_back(v);
     }
@@ -133,6 +140,17 @@ const Variant* heuristic(const Problem& p, Op op) {
         return best;
     }
     if (p.M == 1) {
+        // Measured on MI355X (graph replays, weights rotated past the MALL):
+        // the persistent pipelined GEMV wins for K <= 4096, the row-streaming
+        // GEMV with KS K-slice waves above that.
+        const Variant* st = by_name("stream_d1_g2");
+        if (st && gemv_stream_supports(*st, p)) return st;
+        uint32_t ks = 1;
+        while (ks < 8 && p.K > 4096u * ks) ks *= 2;
+        char name[32];
+        std::snprintf(name, sizeof name, "rows_r4_k%u", ks);
+        const Variant* rows = by_name(name);
+        if (rows && gemv_rows_supports(*rows, p)) return rows;
         if (p.K >= 8192 && p.N <= 8192) return by_name("gemv_r4_t1_k2");
         return by_name(p.N >= 8192 ? "gemv_r4_t1_k1" : "gemv_r2_t1_k1");
     }

@@ -217,6 +217,47 @@ def test_every_vector_variant(stream, oracle, variant):
         check_against_oracle(oracle, y, x, w, m, n, k, what=f"{variant} {m}x{n}x{k}")
 
 
+def _rows_shapes(variant):
+    """M = 1 shapes a row-streaming variant rows_r<R>_k<KS> can run: ragged N,
+    idle lanes (K below 4096 KS) and a row exactly filling the K slices."""
+    ks = int(variant.split("_k")[1])
+    shapes = []
+    for n, k in [(257, 1024), (130, 64), (61, 4480), (1000, 14336), (67, 28672), (33, 4096 * ks)]:
+        if k <= 4096 * ks and (k // 64) * 144 <= 65536:
+            shapes.append((1, n, k))
+    return shapes
+
+
+@pytest.mark.parametrize("variant", _variants("rows_"))
+def test_every_rows_variant(stream, oracle, variant):
+    d = ops.Q4_0Dispatch()
+    d.force(variant)
+    for m, n, k in _rows_shapes(variant):
+        x = normal_x(wl.seed_for(9, k), m, k)
+        w = weights(wl.seed_for(9, 100 + n), n, k)
+        y = run_linear(stream, x, w, m, n, k, dispatch=d)
+        check_against_oracle(oracle, y, x, w, m, n, k, what=f"{variant} {m}x{n}x{k}")
+        y16 = run_linear(stream, x, w, m, n, k, dispatch=d, f16_out=True)
+        check_against_oracle(oracle, y16, x, w, m, n, k, f16_out=True, what=f"{variant} f16 {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("variant", _variants("stream_"))
+def test_every_stream_variant(stream, oracle, variant):
+    """Persistent pipelined GEMV: N below one workgroup, ragged N, idle lanes
+    (K < 4096), and N = 140001 at K = 64, where waves own more than 64 rows
+    and flush their register-held sums mid-loop."""
+    d = ops.Q4_0Dispatch()
+    d.force(variant)
+    for m, n, k in [(1, 1, 64), (1, 7, 4096), (1, 257, 1024), (1, 130, 64), (1, 140001, 64), (1, 14336, 4096)]:
+        x = normal_x(wl.seed_for(13, k), m, k)
+        w = weights(wl.seed_for(13, 100 + n), n, k)
+        y = run_linear(stream, x, w, m, n, k, dispatch=d)
+        cols = None if n < 2000 else sample_columns(n, 512)
+        check_against_oracle(oracle, y, x, w, m, n, k, columns=cols, what=f"{variant} {m}x{n}x{k}")
+    y16 = run_linear(stream, x, w, m, n, k, dispatch=d, f16_out=True)
+    check_against_oracle(oracle, y16, x, w, m, n, k, columns=cols, f16_out=True, what=f"{variant} f16")
+
+
 @pytest.mark.parametrize("variant", _variants("mfma_"))
 def test_every_mfma_variant(stream, oracle, variant):
     d = ops.Q4_0Dispatch()
