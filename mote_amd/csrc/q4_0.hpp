@@ -21,7 +21,7 @@ struct Problem {
 };
 
 enum class Kind : int { Gemv = 0, Mfma = 1, Generic = 2, GateUpMfma = 3, GateUpGeneric = 4, GemvRows = 5,
-                        GemvStream = 6 };
+                        GemvStream = 6, SkinnyMfma = 7 };
 
 struct Variant {
     const char* name;
@@ -34,6 +34,7 @@ struct Variant {
 const Variant* gemv_variants(int* count);
 const Variant* gemv_rows_variants(int* count);
 const Variant* gemv_stream_variants(int* count);
+const Variant* skinny_mfma_variants(int* count);
 const Variant* mfma_variants(int* count);
 const Variant* generic_variants(int* count);
 
@@ -41,6 +42,7 @@ const Variant* generic_variants(int* count);
 bool gemv_supports(const Variant& v, const Problem& p);
 bool gemv_rows_supports(const Variant& v, const Problem& p);
 bool gemv_stream_supports(const Variant& v, const Problem& p);
+bool skinny_mfma_supports(const Variant& v, const Problem& p);
 bool mfma_supports(const Variant& v, const Problem& p);
 
 hipError_t launch_zero_fill(void* y, uint64_t count, OutType out, hipStream_t stream);

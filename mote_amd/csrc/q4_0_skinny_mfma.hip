@@ -1,0 +1,282 @@
+// Q4_0 skinny GEMM (2 <= M <= 64) on the CDNA4 matrix cores.
+//
+// Computes y[m, n] = sum_k x[m, k] * w[n, k] for f16 x [M, K] and GGML Q4_0
+// w [N, K], the operation of crates/mote-backend-hip/src/
+// quantized_linear.hip:13-52 (oracle crates/mote-reference/src/
+// quantized.rs:89-144).  With a handful of tokens the vector-ALU dot products
+// cost M K N / 2 v_dot2 operations and bound the kernel; here the products run
+// on v_mfma_f32_16x16x32_f16 and the vector ALUs only dequantise, so the
+// weight stream from HBM stays the bound up to 16 tokens per token tile.
+//
+// Mapping:
+//  * a workgroup is KS waves; wave kw owns the K slice of STEPS x 4 block pairs
+//    starting at pair 4 STEPS kw, and keeps the activations of its slice for
+//    the workgroup's tokens in registers for the whole kernel;
+//  * the workgroups walk (16-row tile, token group) items persistently, a
+//    token group being MT 16-token tiles that share each dequantised weight
+//    operand (a workgroup keeps one token group for the whole kernel); per
+//    item and step, lane (i, g) = (lane % 16, lane / 16) loads block pair
+//    4 (STEPS kw + s) + g of row i of the tile (36 bytes, the same dword-
+//    aligned load as the GEMV), dequantises it in registers to binary16
+//    (q - 8) * d (exact q - 8 from the 1024 + q exponent trick, one rounding
+//    of the product), and feeds the 8 MFMAs of the step: MFMA t takes nibble
+//    dword t of every lane's pair, so one MFMA spans the same 8 positions of
+//    the 4 pairs of its lane groups, and the activation operand holds x at
+//    exactly those positions (any consistent order of k is exact for a dot);
+//  * the KS partial 16 x 16 tiles meet in LDS and are summed in a fixed order
+//    (deterministic), then written as f32 or f16.
+//
+// The next item's weight loads are issued before the current item's MFMAs.
+#include "common.hpp"
+#include "q4_0.hpp"
+
+#include <type_traits>
+
+namespace mote::q4_0 {
+namespace {
+
+__device__ __forceinline__ uint32_t pick(const uint32_t* x, int a, int b) {
+    const uint32_t lo = (a & 1) ? 0x0302u : 0x0100u;
+    const uint32_t hi = (b & 1) ? 0x07060000u : 0x05040000u;
+    return __builtin_amdgcn_perm(x[b >> 1], x[a >> 1], hi | lo);
+}
+
+// (q - 8) * d for the 8 nibbles of nibble dword q, in the order
+// [b0.lo, b2.lo, b1.lo, b3.lo, b0.hi, b2.hi, b1.hi, b3.hi].  `one` holds
+// binary16 1024 in both halves (0x64006400) in a VGPR: gfx9-family VOP3 instructions take no literal, so with
+// the constant in a register each mask-and-insert is one v_and_or_b32 (mask in
+// an SGPR) instead of an AND and an OR.
+__device__ __forceinline__ f16x8 dequant8(uint32_t q, f16x2 d, uint32_t one) {
+    const f16x2 bias = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+    const f16x2 l02 = (as_h2((q & 0x000F000Fu) | one) + bias) * d;
+    const f16x2 l13 = (as_h2(((q >> 8) & 0x000F000Fu) | one) + bias) * d;
+    const f16x2 h02 = (as_h2(((q >> 4) & 0x000F000Fu) | one) + bias) * d;
+    const f16x2 h13 = (as_h2(((q >> 12) & 0x000F000Fu) | one) + bias) * d;
+    return f16x8{l02.x, l02.y, l13.x, l13.y, h02.x, h02.y, h13.x, h13.y};
+}
+
+template <int KS, int STEPS, int MT, int D, int RT, typename OutT>
+__global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __restrict__ x,
+                                                             const uint8_t* __restrict__ w,
+                                                             OutT* __restrict__ y, uint32_t M,
+                                                             uint32_t N, uint32_t K,
+                                                             uint32_t token_groups, uint32_t items,
+                                                             uint32_t groups_per_xcd) {
+    __shared__ float part[KS][RT * MT][16][17];
+
+    const int tid = static_cast<int>(threadIdx.x);
+    const int kw = tid >> 6;
+    const int lane = tid & 63;
+    const int li = lane & 15;  // row of the A operand, token of the B operand
+    const int lg = lane >> 4;  // lane group: which of the step's 4 pairs
+    const uint32_t npairs = K >> 6;
+    const size_t row_bytes = static_cast<size_t>(npairs) * kPairBytes;
+    const uint32_t groups = gridDim.x;
+    // XCD-aware order: workgroups of one XCD take consecutive items, so the
+    // token tiles of a row tile read its weights through the same L2.
+    const uint32_t first = (blockIdx.x % 8u) * groups_per_xcd + blockIdx.x / 8u;
+
+    // Item -> (row tile, token group of MT 16-token tiles).  The grid size is
+    // a multiple of token_groups, so a workgroup keeps one token group.
+    auto rows_of = [&](uint32_t item) { return (item / token_groups) * (16u * RT); };
+    const uint32_t tok0 = (first % token_groups) * (16u * MT);
+
+    // Weight loads of one item: RT row tiles x STEPS pairs per lane.
+    auto load_item = [&](uint32_t item, uint32_t (&raw)[RT * STEPS][9]) {
+        const uint32_t it = min(item, items - 1);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const uint32_t n = min(rows_of(it) + 16u * rt + static_cast<uint32_t>(li), N - 1);
+            const uint8_t* row = w + static_cast<size_t>(n) * row_bytes;
+#pragma unroll
+            for (int s = 0; s < STEPS; ++s) {
+                const uint32_t p = (static_cast<uint32_t>(kw) * STEPS + s) * 4u + static_cast<uint32_t>(lg);
+                load_pair(row + static_cast<size_t>(p) * kPairBytes, raw[rt * STEPS + s]);
+            }
+        }
+    };
+
+    // The first item's weights, then the activations (reused by every item).
+    uint32_t buf0[RT * STEPS][9];
+    load_item(first, buf0);
+    // Activations of this wave's K slice for the workgroup's MT token tiles.
+    f16x8 xb[MT][STEPS][8];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const uint32_t m = tok0 + 16u * mt + static_cast<uint32_t>(li);
+        const bool live = m < M;
+        const uint16_t* xrow = x + static_cast<size_t>(min(m, M - 1)) * K;
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+            const uint32_t p = (static_cast<uint32_t>(kw) * STEPS + s) * 4u + static_cast<uint32_t>(lg);
+            uint32_t xr[32];
+            const u32x4* src = reinterpret_cast<const u32x4*>(xrow + static_cast<size_t>(p) * 64);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const u32x4 v = src[c];
+                xr[4 * c + 0] = live ? v.x : 0u; xr[4 * c + 1] = live ? v.y : 0u;
+                xr[4 * c + 2] = live ? v.z : 0u; xr[4 * c + 3] = live ? v.w : 0u;
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int base = t < 4 ? 0 : 32;
+                const int e0 = base + pair_byte_element(t, 0), e1 = base + pair_byte_element(t, 1);
+                const int e2 = base + pair_byte_element(t, 2), e3 = base + pair_byte_element(t, 3);
+                const f16x2 a = as_h2(pick(xr, e0, e2)), b = as_h2(pick(xr, e1, e3));
+                const f16x2 c = as_h2(pick(xr, e0 + 16, e2 + 16)), d = as_h2(pick(xr, e1 + 16, e3 + 16));
+                xb[mt][s][t] = f16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+            }
+        }
+    }
+    uint32_t one;
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(one));
+
+
+    // One item: dequantise + MFMA from `buf`, refill `buf` with item `next`
+    // right after its last use (so the refill overlaps the reduction and the
+    // other buffer's item), then reduce the KS partial tiles and store.
+    auto process = [&](uint32_t it, uint32_t (&buf)[RT * STEPS][9], uint32_t next, auto refill) {
+        f32x4 acc[RT][MT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+            uint32_t q[RT][8];
+            f16x2 d0[RT], d1[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const uint32_t (&c)[9] = buf[rt * STEPS + s];
+                q[rt][0] = pair_q0(c);
+                q[rt][1] = c[1]; q[rt][2] = c[2]; q[rt][3] = c[3];
+                q[rt][4] = c[5]; q[rt][5] = c[6]; q[rt][6] = c[7]; q[rt][7] = c[8];
+                d0[rt] = as_h2(__builtin_amdgcn_perm(c[0], c[0], 0x01000100u));
+                d1[rt] = as_h2(__builtin_amdgcn_perm(c[4], c[4], 0x03020302u));
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const f16x8 a = dequant8(q[rt][t], t < 4 ? d0[rt] : d1[rt], one);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+                        acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xb[mt][s][t], acc[rt][mt], 0, 0, 0);
+                }
+            }
+        }
+        if constexpr (decltype(refill)::value) load_item(next, buf);
+
+        // lane holds rows 4 lg + r, token li of each (row tile, token tile)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) part[kw][rt * MT + mt][4 * lg + r][li] = acc[rt][mt][r];
+        __syncthreads();
+        for (int o = tid; o < 256 * RT * MT; o += KS * 64) {
+            const int row = o & 15, tok = (o >> 4) & 15, tile = o >> 8;
+            const int rt = tile / MT, mt = tile % MT;
+            float sum = part[0][tile][row][tok];
+#pragma unroll
+            for (int k = 1; k < KS; ++k) sum += part[k][tile][row][tok];
+            const uint32_t n = rows_of(it) + 16u * rt + static_cast<uint32_t>(row);
+            const uint32_t m = tok0 + 16u * mt + static_cast<uint32_t>(tok);
+            if (n < N && m < M) y[static_cast<size_t>(m) * N + n] = to_out<OutT>(sum);
+        }
+        __syncthreads();
+    };
+
+    uint32_t item = first;
+    if constexpr (D == 1) {
+        for (; item < items; item += groups) {
+            // Copying the buffer waits for this item only; the next item's
+            // loads then run under this item's arithmetic.
+            uint32_t cur[RT * STEPS][9];
+#pragma unroll
+            for (int s = 0; s < RT * STEPS; ++s)
+#pragma unroll
+                for (int i = 0; i < 9; ++i) cur[s][i] = buf0[s][i];
+            load_item(item + groups, buf0);
+            process(item, cur, item, std::false_type{});
+        }
+    } else {
+        uint32_t buf1[RT * STEPS][9];
+        load_item(item + groups, buf1);
+        for (; item < items; item += 2 * groups) {
+            process(item, buf0, item + 2 * groups, std::true_type{});
+            if (item + groups < items)  // uniform
+                process(item + groups, buf1, item + 3 * groups, std::true_type{});
+        }
+    }
+}
+
+template <int KS, int STEPS, int MT, int D, int G, int RT>
+hipError_t launch_skinny(const Problem& p) {
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        return n;
+    }();
+    const uint32_t row_tiles = (p.N + 16 * RT - 1) / (16 * RT);
+    const uint32_t token_groups = (p.M + 16 * MT - 1) / (16 * MT);
+    const uint64_t items64 = static_cast<uint64_t>(row_tiles) * token_groups;
+    if (items64 > 0x7fffffffull) return hipErrorInvalidConfiguration;
+    const uint32_t items = static_cast<uint32_t>(items64);
+    // Whole XCD rounds (8 groups) that are also a multiple of token_groups, so
+    // every workgroup keeps one token group; extra groups find no item.
+    uint32_t a = 8u, b = token_groups;
+    while (b != 0) { const uint32_t t = a % b; a = b; b = t; }
+    const uint32_t unit = 8u / a * token_groups;  // lcm(8, token_groups)
+    uint32_t groups = static_cast<uint32_t>(cus) * G;
+    if (groups > items) groups = items;
+    groups = (groups + unit - 1) / unit * unit;
+    const uint32_t per_xcd = groups / 8u;
+    const dim3 grid(groups), block(KS * 64);
+    if (p.out == OutType::F32) {
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, float>), grid, block, 0, p.stream,
+                           static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
+                           static_cast<float*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
+    } else {
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, _Float16>), grid, block, 0, p.stream,
+                           static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
+                           static_cast<_Float16*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
+    }
+    return hipGetLastError();
+}
+
+#define MOTE_SKINNY(KS, STEPS, MT, D, G, RT)                                                     \
+    Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d" #D "_g" #G "_r" #RT, Kind::SkinnyMfma, KS, \
+            STEPS, MT, &launch_skinny<KS, STEPS, MT, D, G, RT>}
+
+const Variant kSkinny[] = {
+    MOTE_SKINNY(16, 1, 1, 1, 1, 1), MOTE_SKINNY(16, 1, 1, 2, 1, 1), MOTE_SKINNY(16, 1, 2, 1, 1, 1),
+    MOTE_SKINNY(16, 1, 2, 2, 1, 1), MOTE_SKINNY(16, 1, 1, 2, 2, 1), MOTE_SKINNY(16, 1, 1, 2, 1, 2),
+    MOTE_SKINNY(8, 2, 1, 1, 1, 1), MOTE_SKINNY(8, 2, 1, 2, 1, 1), MOTE_SKINNY(8, 2, 1, 2, 2, 1),
+    MOTE_SKINNY(8, 1, 1, 1, 1, 1), MOTE_SKINNY(8, 1, 2, 1, 1, 1), MOTE_SKINNY(8, 1, 1, 2, 1, 1),
+    MOTE_SKINNY(4, 2, 1, 1, 1, 1), MOTE_SKINNY(4, 1, 1, 1, 1, 1), MOTE_SKINNY(4, 1, 1, 2, 1, 1),
+    MOTE_SKINNY(16, 2, 1, 1, 1, 1),
+};
+
+#undef MOTE_SKINNY
+
+}  // namespace
+
+const Variant* skinny_mfma_variants(int* count) {
+    *count = static_cast<int>(sizeof(kSkinny) / sizeof(kSkinny[0]));
+    return kSkinny;
+}
+
+// K exactly KS * STEPS * 256 (each wave one K slice of whole steps), x 16-byte
+// and w dword aligned, at most 64 tokens (MT token tiles per pass, RT row
+// tiles per item).
+bool skinny_mfma_supports(const Variant& v, const Problem& p) {
+    const uint32_t span = static_cast<uint32_t>(v.p0) * static_cast<uint32_t>(v.p1) * 256u;
+    return p.M >= 1 && p.M <= 64 && p.K == span && reinterpret_cast<uintptr_t>(p.w) % 4 == 0 &&
+           reinterpret_cast<uintptr_t>(p.x) % 16 == 0;
+}
+
+}  // namespace mote::q4_0

@@ -258,6 +258,29 @@ def test_every_stream_variant(stream, oracle, variant):
     check_against_oracle(oracle, y16, x, w, m, n, k, columns=cols, f16_out=True, what=f"{variant} f16")
 
 
+def _skinny_k(variant):
+    ks, rest = variant.split("_mfma_k")[1].split("_s")
+    return int(ks) * int(rest.split("_t")[0]) * 256
+
+
+@pytest.mark.parametrize("variant", _variants("skinny_mfma_"))
+def test_every_skinny_mfma_variant(stream, oracle, variant):
+    """Matrix-core skinny GEMM: tokens padded inside a 16-token tile (M = 2, 5),
+    exactly one and two tiles (16, 32), one token over (17, 33), the 64-token
+    maximum, N ragged against the 16-row tiles, f32 and f16 outputs."""
+    d = ops.Q4_0Dispatch()
+    d.force(variant)
+    k = _skinny_k(variant)
+    for m, n in [(2, 100), (5, 33), (16, 16), (17, 130), (32, 61), (33, 7), (64, 80), (3, 4096)]:
+        x = normal_x(wl.seed_for(14, m), m, k)
+        w = weights(wl.seed_for(14, 100 + n), n, k)
+        y = run_linear(stream, x, w, m, n, k, dispatch=d)
+        cols = None if n < 1000 else sample_columns(n, 256)
+        check_against_oracle(oracle, y, x, w, m, n, k, columns=cols, what=f"{variant} {m}x{n}x{k}")
+    y16 = run_linear(stream, x, w, m, n, k, dispatch=d, f16_out=True)
+    check_against_oracle(oracle, y16, x, w, m, n, k, columns=cols, f16_out=True, what=f"{variant} f16")
+
+
 @pytest.mark.parametrize("variant", _variants("mfma_"))
 def test_every_mfma_variant(stream, oracle, variant):
     d = ops.Q4_0Dispatch()
@@ -330,7 +353,8 @@ def test_decode_is_bit_exact_for_every_scale(stream, oracle, k, offset):
 
 # --- size-independent properties at full size ------------------------------------------
 
-@pytest.mark.parametrize("m,k,n", [(1, 4096, 14336), (1, 14336, 4096), (8, 4096, 14336), (256, 4096, 14336)])
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 14336), (1, 14336, 4096), (2, 4096, 4096), (8, 4096, 14336),
+                                   (256, 4096, 14336)])
 def test_exact_properties_at_full_size(stream, m, k, n):
     """Doubling x doubles y, negating every scale negates y, and zeroing the
     scales of one K block equals zeroing those 32 activations: all exact in
@@ -338,14 +362,16 @@ def test_exact_properties_at_full_size(stream, m, k, n):
     bitwise identical (no atomics)."""
     x = normal_x(wl.seed_for(1, 0), m, k)
     w = weights(wl.seed_for(1, 1), n, k)
-    y = run_linear(stream, x, w, m, n, k)
-    assert np.array_equal(y, run_linear(stream, x, w, m, n, k)), "non-deterministic"
+    d = ops.Q4_0Dispatch()
+    y = run_linear(stream, x, w, m, n, k, dispatch=d)
+    matrix_cores = "mfma" in d.plan(m, n, k)
+    assert np.array_equal(y, run_linear(stream, x, w, m, n, k, dispatch=d)), "non-deterministic"
     x2 = f16_bits(bits_to_f32(x) * 2.0)
-    assert np.array_equal(run_linear(stream, x2, w, m, n, k), 2.0 * y)
+    assert np.array_equal(run_linear(stream, x2, w, m, n, k, dispatch=d), 2.0 * y)
     wneg = w.copy().reshape(n, k // 32, 18)
     wneg[:, :, 1] ^= 0x80
-    yneg = run_linear(stream, x, wneg.reshape(-1), m, n, k)
-    if m < 64:
+    yneg = run_linear(stream, x, wneg.reshape(-1), m, n, k, dispatch=d)
+    if not matrix_cores:
         assert np.array_equal(yneg, -y)
     else:
         # The matrix cores' f32 accumulation is not symmetric under negation
@@ -359,7 +385,8 @@ def test_exact_properties_at_full_size(stream, m, k, n):
     wz[:, blk, 0:2] = 0
     xz = x.copy().reshape(m, k)
     xz[:, 32 * blk:32 * blk + 32] = 0
-    assert np.array_equal(run_linear(stream, x, wz.reshape(-1), m, n, k), run_linear(stream, xz.reshape(-1), w, m, n, k))
+    assert np.array_equal(run_linear(stream, x, wz.reshape(-1), m, n, k, dispatch=d),
+                          run_linear(stream, xz.reshape(-1), w, m, n, k, dispatch=d))
 
 
 def test_autotuned_dispatch_caches_a_plan(stream, oracle):
