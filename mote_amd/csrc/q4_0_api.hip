@@ -119,7 +119,7 @@ const Variant* by_name(const char* name) {
 const Variant* heuristic(const Problem& p, Op op) {
     const bool fast = fast_eligible(p);
     if (op == Op::GateUp) {
-        if (fast && p.M >= 64) return by_name(p.M >= 128 ? "gateup_mfma_m128_n64" : "gateup_mfma_m64_n64");
+        if (fast && p.M >= 64) return by_name(p.M >= 128 ? "gateup_mfma_m128_n64_p1" : "gateup_mfma_m64_n64_p1");
         return by_name("gateup_generic");
     }
     if (!fast) return by_name("generic");
@@ -129,8 +129,8 @@ const Variant* heuristic(const Problem& p, Op op) {
     }
     if (p.M >= 64) {
         // Prefer the largest tile that still gives at least one tile per CU.
-        static const char* const order[] = {"mfma_m128_n128", "mfma_m128_n64", "mfma_m64_n128",
-                                            "mfma_m64_n64"};
+        static const char* const order[] = {"mfma_m128_n128_p1", "mfma_m128_n64_p1", "mfma_m64_n128_p1",
+                                            "mfma_m64_n64_p1"};
         const Variant* best = nullptr;
         uint64_t best_tiles = 0;
         for (const char* name : order) {

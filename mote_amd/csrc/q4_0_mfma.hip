@@ -89,7 +89,7 @@ __device__ __forceinline__ void block_groups(const uint32_t (&d)[5], int blk, ui
     }
 }
 
-template <int BM, int BN, bool GATE_UP, typename OutT>
+template <int BM, int BN, bool GATE_UP, int PF, typename OutT>
 __global__ __launch_bounds__(256) void mfma_kernel(const uint16_t* __restrict__ x,
                                                    const uint8_t* __restrict__ wg,
                                                    const uint8_t* __restrict__ wu,
@@ -150,23 +150,29 @@ __global__ __launch_bounds__(256) void mfma_kernel(const uint16_t* __restrict__ 
         woff[j] = row * kRowBytes + wblk[j] * 64;
     }
 
-    u32x4 xreg[T::kXChunks];
-    uint32_t wreg[NW][T::kWItems][5];
+    // A ring of PF register stages: the global loads of step k are issued PF
+    // steps before step k is written to LDS, so their HBM latency hides
+    // behind PF steps of matrix-core work.  Steps past the end are clamped
+    // to the last one (a re-read), which keeps every load unconditional and
+    // the wait counts exact.
+    u32x4 xreg[PF][T::kXChunks];
+    uint32_t wreg[PF][NW][T::kWItems][5];
 
-    auto load_stage = [&](uint32_t kp) {
+    auto load_stage = [&](uint32_t kp, int r) {
+        kp = min(kp, npairs - 1);
 #pragma unroll
         for (int j = 0; j < T::kXChunks; ++j)
-            xreg[j] = *reinterpret_cast<const u32x4*>(xptr[j] + static_cast<size_t>(kp) * 64);
+            xreg[r][j] = *reinterpret_cast<const u32x4*>(xptr[j] + static_cast<size_t>(kp) * 64);
 #pragma unroll
         for (int s = 0; s < NW; ++s)
 #pragma unroll
             for (int j = 0; j < T::kWItems; ++j)
-                if (wlive[j]) load_block(wptr[s][j] + static_cast<size_t>(kp) * kPairBytes, wblk[j], wreg[s][j]);
+                if (wlive[j]) load_block(wptr[s][j] + static_cast<size_t>(kp) * kPairBytes, wblk[j], wreg[r][s][j]);
     };
-    auto store_stage = [&](int buf) {
+    auto store_stage = [&](int buf, int r) {
 #pragma unroll
         for (int j = 0; j < T::kXChunks; ++j) {
-            const u32x4 v = xreg[j];
+            const u32x4 v = xreg[r][j];
             u32x2 a, b;
             a.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);  // (x0, x2)
             a.y = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);  // (x1, x3)
@@ -181,7 +187,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(const uint16_t* __restrict__ 
             for (int j = 0; j < T::kWItems; ++j) {
                 if (!wlive[j]) continue;
                 uint32_t g[4], scale;
-                block_groups(wreg[s][j], wblk[j], g, scale);
+                block_groups(wreg[r][s][j], wblk[j], g, scale);
                 u32x4 out[4];
                 dequant_block(g, scale, out);
                 u32x4* dst = reinterpret_cast<u32x4*>(&ws[s][buf][woff[j]]);
@@ -202,14 +208,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(const uint16_t* __restrict__ 
     const int a_base = (wm * (BM / 2) + lrow) * kRowBytes + lgrp * 16;
     const int b_base = (wn * (BN / 2) + lrow) * kRowBytes + lgrp * 16;
 
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
-
-    for (uint32_t kp = 0; kp < npairs; ++kp) {
-        const int buf = static_cast<int>(kp & 1u);
-        const bool more = kp + 1 < npairs;
-        if (more) load_stage(kp + 1);
+    auto mma_step = [&](int buf) {
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
             f16x8 a[TM];
@@ -228,8 +227,33 @@ __global__ __launch_bounds__(256) void mfma_kernel(const uint16_t* __restrict__ 
                 }
             }
         }
-        if (more) store_stage(buf ^ 1);
-        __syncthreads();
+    };
+
+    // Prologue: steps 0 .. PF-1 in flight, step 0 in LDS, step PF loading.
+#pragma unroll
+    for (int r = 0; r < PF; ++r) load_stage(static_cast<uint32_t>(r), r);
+    store_stage(0, 0);
+    load_stage(PF, 0);
+    __syncthreads();
+
+    // Iteration k: write step k + 1 (ring slot (k + 1) % PF) to the other LDS
+    // buffer, refill that slot with step k + 1 + PF, multiply step k.  The
+    // loop is unrolled by PF so ring slots are compile-time constants.
+    for (uint32_t kp = 0; kp < npairs; kp += PF) {
+#pragma unroll
+        for (int d = 0; d < PF; ++d) {
+            const uint32_t k = kp + static_cast<uint32_t>(d);
+            if (k < npairs) {  // uniform
+                const int buf = static_cast<int>(k & 1u);
+                const int slot = (d + 1) % PF;
+                if (k + 1 < npairs) {
+                    store_stage(buf ^ 1, slot);
+                    load_stage(k + 1 + PF, slot);
+                }
+                mma_step(buf);
+                __syncthreads();
+            }
+        }
     }
 
     // Epilogue: lane holds rows 4*lgrp .. 4*lgrp+3, column lrow of each tile.
@@ -249,7 +273,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(const uint16_t* __restrict__ 
     }
 }
 
-template <int BM, int BN, bool GATE_UP>
+template <int BM, int BN, bool GATE_UP, int PF>
 hipError_t launch_mfma(const Problem& p) {
     const uint32_t m_tiles = (p.M + BM - 1) / BM;
     const uint32_t n_tiles = (p.N + BN - 1) / BN;
@@ -262,21 +286,23 @@ hipError_t launch_mfma(const Problem& p) {
     const auto* wg = static_cast<const uint8_t*>(p.w);
     const auto* wu = static_cast<const uint8_t*>(p.w_up);
     if (p.out == OutType::F32) {
-        hipLaunchKernelGGL((mfma_kernel<BM, BN, GATE_UP, float>), grid, block, 0, p.stream, x, wg, wu,
+        hipLaunchKernelGGL((mfma_kernel<BM, BN, GATE_UP, PF, float>), grid, block, 0, p.stream, x, wg, wu,
                            static_cast<float*>(p.y), p.M, p.N, p.K, m_tiles, total, per_xcd);
     } else {
-        hipLaunchKernelGGL((mfma_kernel<BM, BN, GATE_UP, _Float16>), grid, block, 0, p.stream, x, wg,
+        hipLaunchKernelGGL((mfma_kernel<BM, BN, GATE_UP, PF, _Float16>), grid, block, 0, p.stream, x, wg,
                            wu, static_cast<_Float16*>(p.y), p.M, p.N, p.K, m_tiles, total, per_xcd);
     }
     return hipGetLastError();
 }
 
-#define MOTE_MFMA(BM, BN)                                                                  \
-    Variant{"mfma_m" #BM "_n" #BN, Kind::Mfma, BM, BN, 0, &launch_mfma<BM, BN, false>}, \
-    Variant{"gateup_mfma_m" #BM "_n" #BN, Kind::GateUpMfma, BM, BN, 0, &launch_mfma<BM, BN, true>}
+#define MOTE_MFMA(BM, BN, PF)                                                                   \
+    Variant{"mfma_m" #BM "_n" #BN "_p" #PF, Kind::Mfma, BM, BN, PF, &launch_mfma<BM, BN, false, PF>}, \
+    Variant{"gateup_mfma_m" #BM "_n" #BN "_p" #PF, Kind::GateUpMfma, BM, BN, PF,                    \
+            &launch_mfma<BM, BN, true, PF>}
 
 const Variant kMfma[] = {
-    MOTE_MFMA(64, 64), MOTE_MFMA(128, 64), MOTE_MFMA(64, 128), MOTE_MFMA(128, 128),
+    MOTE_MFMA(64, 64, 1), MOTE_MFMA(128, 64, 1), MOTE_MFMA(64, 128, 1), MOTE_MFMA(128, 128, 1),
+    MOTE_MFMA(128, 64, 3), MOTE_MFMA(128, 128, 2),
 };
 
 #undef MOTE_MFMA
