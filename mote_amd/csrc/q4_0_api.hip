@@ -110,6 +110,17 @@ std::vector<const Variant*> candidates(const Problem& p, Op op) {
     return out;
 }
 
+int device_cus() {
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        return n;
+    }();
+    return cus;
+}
+
 const Variant* by_name(const char* name) {
     const Variant* v = find_variant(name);
     return v;
@@ -147,13 +158,23 @@ const Variant* heuristic(const Problem& p, Op op) {
     }
     if (p.M == 1) {
         // Measured on MI355X (graph replays, weights rotated past the MALL):
-        // the persistent pipelined GEMV wins for K <= 4096, the row-streaming
-        // GEMV with KS K-slice waves above that.
-        const Variant* st = by_name("stream_d1_g2");
+        // the persistent pipelined GEMV, with rows split over S waves for
+        // K > 4096 (4096 x 14336: 7.3 us; 14336 x 4096: 8.0 us, against
+        // 9.9 us for the row-streaming GEMV).  Two workgroups per CU pay off
+        // once every row group then still owns at least two rows.
+        uint32_t split = 1;
+        while (split < 4 && p.K > 4096u * split) split *= 2;
+        const uint64_t row_groups_g2 = static_cast<uint64_t>(device_cus()) * 2u * (8u / split);
+        const unsigned g = p.N >= 2u * row_groups_g2 ? 2u : 1u;
+        char name[32];
+        if (split == 1)
+            std::snprintf(name, sizeof name, "stream_d1_g%u", g);
+        else
+            std::snprintf(name, sizeof name, "stream_s%u_d1_g%u", split, g);
+        const Variant* st = by_name(name);
         if (st && gemv_stream_supports(*st, p)) return st;
         uint32_t ks = 1;
         while (ks < 8 && p.K > 4096u * ks) ks *= 2;
-        char name[32];
         std::snprintf(name, sizeof name, "rows_r4_k%u", ks);
         const Variant* rows = by_name(name);
         if (rows && gemv_rows_supports(*rows, p)) return rows;

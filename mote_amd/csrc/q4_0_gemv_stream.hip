@@ -5,14 +5,16 @@
 // quantized_linear.hip:13-52 (oracle crates/mote-reference/src/
 // quantized.rs:89-144) at rows == 1.
 //
-// The grid is G workgroups of 8 waves per CU.  Lane l owns block pair l (64
-// elements, 36 bytes) of every row; wave g of the grid walks rows g, g + W,
-// g + 2W, ... (W waves in the grid), so at any moment the waves of the whole
-// chip read neighbouring rows and the request front sweeps the matrix once,
-// in order.  Each wave keeps D rows in flight: it computes row j while the
-// loads of rows j + 1 .. j + D - 1 are outstanding and issues row j + D right
-// after, so the nibble arithmetic of early rows overlaps the HBM stream of
-// later ones instead of piling up after the last byte arrives.
+// The grid is G workgroups of 8 waves per CU.  Lane l owns block pairs l,
+// l + 64, ..., l + 64 (P - 1) (64 elements, 36 bytes each) of every row, so
+// K <= 4096 P; wave g of the grid walks rows g, g + W, g + 2W, ... (W waves
+// in the grid), so at any moment the waves of the whole chip read
+// neighbouring rows and the request front sweeps the matrix once, in order.
+// Each wave issues the loads of row j + D before it computes row j, so D rows
+// are in flight behind the nibble arithmetic instead of the arithmetic
+// piling up after the last byte arrives.  D = 1 measures fastest: a deeper
+// front spreads the chip's outstanding requests over more of the matrix and
+// lowers the achieved HBM rate, also for a pure read of the same pattern.
 //
 // x is staged once per workgroup through LDS (coalesced 16-byte loads, one
 // 144-byte slot per 128-byte pair chunk so the per-lane reads hit distinct
@@ -79,46 +81,79 @@ __device__ __forceinline__ float pair_dot(const uint32_t (&raw)[9], const XPair&
     return __builtin_fmaf(d1, __builtin_fmaf(lo1, 16.0f, hi1), acc);
 }
 
-template <int D, typename OutT>
+template <int P, int S, int D, typename OutT>
 __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint16_t* __restrict__ x,
                                                                      const uint8_t* __restrict__ w,
                                                                      OutT* __restrict__ y, uint32_t N,
-                                                                     uint32_t K, uint32_t total_waves) {
+                                                                     uint32_t K, uint32_t total_groups) {
+    constexpr int kGroups = kStreamWaves / S;  // row groups per workgroup
     extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
     const int tid = static_cast<int>(threadIdx.x);
     const int wave = tid >> 6;
     const int lane = tid & 63;
+    const int slice = wave % S;
     const uint32_t npairs = K >> 6;
     const size_t row_bytes = static_cast<size_t>(npairs) * kPairBytes;
-    const uint32_t p = min(static_cast<uint32_t>(lane), npairs - 1);  // idle lanes: clamped, dropped
-    const bool active = static_cast<uint32_t>(lane) < npairs;
-    const uint32_t g = blockIdx.x * kStreamWaves + static_cast<uint32_t>(wave);
-    // rows g, g + W, ...: count, and the last one (prefetches past it re-read
-    // it, an L2 hit, so every load is unconditional and vmcnt stays exact)
-    const uint32_t nrows = g < N ? (N - 1 - g) / total_waves + 1 : 0;
-    const uint32_t last = g < N ? g + (nrows - 1) * total_waves : N - 1;
-    const uint8_t* wl = w + static_cast<size_t>(p) * kPairBytes;
-
-    // x chunk load first, then the first D rows.
-    const uint32_t xchunks = npairs * 8;
-    const uint32_t xc = min(static_cast<uint32_t>(tid), xchunks - 1);
-    const u32x4 xreg = reinterpret_cast<const u32x4*>(x)[xc];
-    __builtin_amdgcn_sched_barrier(0);
-    uint32_t buf[D][9];
+    // The S waves of a row group split each row into S slices of `span`
+    // pairs; lane l of slice s owns pairs s*span + l + 64i (i < P).  Idle
+    // slots are clamped to the last pair (a cached re-read) and dropped.
+    const uint32_t span = (npairs + S - 1) / S;
+    uint32_t pc[P], keep[P];
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-        const uint32_t r = min(g + static_cast<uint32_t>(d) * total_waves, last);
-        load_pair(wl + static_cast<size_t>(r) * row_bytes, buf[d]);
+    for (int i = 0; i < P; ++i) {
+        const uint32_t off = static_cast<uint32_t>(lane + 64 * i);
+        const uint32_t pi = static_cast<uint32_t>(slice) * span + off;
+        pc[i] = min(pi, npairs - 1);
+        keep[i] = (off < span && pi < npairs) ? 0xFFFFFFFFu : 0u;  // bit mask: NaN-safe, branch-free drop
     }
-    *reinterpret_cast<u32x4*>(xs + (xc >> 3) * kSlot + (xc & 7) * 16) = xreg;
+    const uint32_t g = blockIdx.x * kGroups + static_cast<uint32_t>(wave / S);
+    // rows g, g + T, ... (T row groups in the grid): count, and the last one
+    // (prefetches past it re-read it, an L2 hit, so every load is
+    // unconditional and vmcnt stays exact)
+    const uint32_t nrows = g < N ? (N - 1 - g) / total_groups + 1 : 0;
+    const uint32_t last = g < N ? g + (nrows - 1) * total_groups : N - 1;
+    // Split rows reduce across waves through LDS behind barriers, so every
+    // wave of the workgroup runs the trip count of its first row group (the
+    // largest); the others compute clamped rows and store nothing.
+    const uint32_t g0 = blockIdx.x * kGroups;
+    const uint32_t trips = S == 1 ? nrows : (g0 < N ? (N - 1 - g0) / total_groups + 1 : 0);
+    auto load_row = [&](uint32_t jj, uint32_t (&b)[P][9]) {
+        const uint8_t* row = w + static_cast<size_t>(min(g + jj * total_groups, last)) * row_bytes;
+#pragma unroll
+        for (int i = 0; i < P; ++i) load_pair(row + static_cast<size_t>(pc[i]) * kPairBytes, b[i]);
+    };
+
+    // x chunk loads first (P S 16-byte chunks per thread), then the first D
+    // rows, and only then the LDS stores of x, so no row load waits for x.
+    constexpr int XC = P * S;
+    const uint32_t xchunks = npairs * 8;
+    u32x4 xreg[XC];
+    uint32_t xc[XC];
+#pragma unroll
+    for (int c = 0; c < XC; ++c) {
+        xc[c] = min(static_cast<uint32_t>(tid + kStreamThreads * c), xchunks - 1);
+        xreg[c] = reinterpret_cast<const u32x4*>(x)[xc[c]];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Ring of D + 1 row buffers: row j + D is issued before row j is
+    // computed, so D rows stay in flight behind the arithmetic.
+    constexpr int R = D + 1;
+    uint32_t buf[R][P][9];
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_row(static_cast<uint32_t>(d), buf[d]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < XC; ++c)
+        *reinterpret_cast<u32x4*>(xs + (xc[c] >> 3) * kSlot + (xc[c] & 7) * 16) = xreg[c];
     __syncthreads();
 
-    XPair xv;
-    {
+    XPair xv[P];
+#pragma unroll
+    for (int s = 0; s < P; ++s) {
         uint32_t xr[32];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const u32x4 v = *reinterpret_cast<const u32x4*>(xs + p * kSlot + i * 16);
+            const u32x4 v = *reinterpret_cast<const u32x4*>(xs + pc[s] * kSlot + i * 16);
             xr[4 * i + 0] = v.x; xr[4 * i + 1] = v.y; xr[4 * i + 2] = v.z; xr[4 * i + 3] = v.w;
         }
         float s0 = 0.0f, s1 = 0.0f;
@@ -127,8 +162,8 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
             s0 = dot2(xr[i], kOnePair, s0);
             s1 = dot2(xr[16 + i], kOnePair, s1);
         }
-        xv.c0 = (-8.0f / kTwo20) * s0;
-        xv.c1 = (-8.0f / kTwo20) * s1;
+        xv[s].c0 = (-8.0f / kTwo20) * s0;
+        xv[s].c1 = (-8.0f / kTwo20) * s1;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             const int base = (q < 4) ? 0 : 32;
@@ -136,40 +171,58 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
             const int e1 = base + pair_byte_element(q, 1);
             const int e2 = base + pair_byte_element(q, 2);
             const int e3 = base + pair_byte_element(q, 3);
-            xv.xp[4 * q + 0] = pick(xr, e0 + 16, e2 + 16);  // hi02
-            xv.xp[4 * q + 1] = pick(xr, e0, e2);            // lo02
-            xv.xp[4 * q + 2] = pick(xr, e1, e3);            // lo13
-            xv.xp[4 * q + 3] = pick(xr, e1 + 16, e3 + 16);  // hi13
+            xv[s].xp[4 * q + 0] = pick(xr, e0 + 16, e2 + 16);  // hi02
+            xv[s].xp[4 * q + 1] = pick(xr, e0, e2);            // lo02
+            xv[s].xp[4 * q + 2] = pick(xr, e1, e3);            // lo13
+            xv[s].xp[4 * q + 3] = pick(xr, e1 + 16, e3 + 16);  // hi13
         }
     }
 
     // Row sums stay in registers (lane j % 64 holds row j of this wave) and
     // are stored every 64 rows and at the end, so no store sits between the
-    // pipelined loads.  The loop runs at least once (a wave without rows
-    // computes clamped rows and stores nothing), which keeps the first D
-    // loads ahead of the x barrier.
+    // pipelined loads.  Split rows first add the S slice sums through LDS
+    // (after the x area).  The loop runs at least once and is unrolled by the
+    // ring size, so slots are compile-time registers; steps past the last row
+    // compute clamped rows and store nothing.
+    float* red = reinterpret_cast<float*>(xs + static_cast<size_t>(npairs) * kSlot);
+    auto flush = [&](float v, uint32_t first, uint32_t count) {
+        if constexpr (S > 1) {
+            red[wave * 64 + lane] = v;
+            __syncthreads();
+            if (slice == 0) {
+#pragma unroll
+                for (int t = 1; t < S; ++t) v += red[(wave + t) * 64 + lane];
+            }
+            __syncthreads();
+            if (slice != 0) return;
+        }
+        if (static_cast<uint32_t>(lane) < count)
+            y[g + (first + static_cast<uint32_t>(lane)) * total_groups] = to_out<OutT>(kTwo20 * v);
+    };
     float mine = 0.0f;
     uint32_t j = 0;
     do {
 #pragma unroll
-        for (int d = 0; d < D; ++d) {
-            const uint32_t jj = j + static_cast<uint32_t>(d);
-            const float s = wave_sum(active ? pair_dot(buf[d], xv) : 0.0f);
-            mine = (jj < nrows && static_cast<uint32_t>(lane) == (jj & 63u)) ? s : mine;
-            const uint32_t r = min(g + (jj + D) * total_waves, last);
-            load_pair(wl + static_cast<size_t>(r) * row_bytes, buf[d]);
-            if ((jj & 63u) == 63u && jj < nrows) {  // uniform: flush a full slot set
-                y[g + (jj - 63u + static_cast<uint32_t>(lane)) * total_waves] = to_out<OutT>(kTwo20 * mine);
-            }
+        for (int u = 0; u < R; ++u) {
+            const uint32_t jj = j + static_cast<uint32_t>(u);
+            load_row(jj + D, buf[(u + D) % R]);
+            __builtin_amdgcn_sched_barrier(0);
+            float part = 0.0f;
+#pragma unroll
+            for (int i = 0; i < P; ++i)
+                part += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pair_dot(buf[u][i], xv[i])) & keep[i]);
+            const float s = wave_sum(part);
+            mine = (jj < trips && static_cast<uint32_t>(lane) == (jj & 63u)) ? s : mine;
+            if ((jj & 63u) == 63u && jj < trips)  // uniform over the workgroup
+                flush(mine, jj - 63u, nrows > jj - 63u ? min(nrows - (jj - 63u), 64u) : 0u);
         }
-        j += D;
-    } while (j < nrows);
-    const uint32_t base = nrows & ~63u;
-    if (static_cast<uint32_t>(lane) < nrows - base)
-        y[g + (base + static_cast<uint32_t>(lane)) * total_waves] = to_out<OutT>(kTwo20 * mine);
+        j += R;
+    } while (j < trips);
+    const uint32_t base = trips & ~63u;
+    if (base < trips) flush(mine, base, nrows > base ? nrows - base : 0u);
 }
 
-template <int D, int G>
+template <int P, int S, int D, int G>
 hipError_t launch_gemv_stream(const Problem& p) {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -178,34 +231,48 @@ hipError_t launch_gemv_stream(const Problem& p) {
             n = 256;
         return n;
     }();
+    constexpr uint32_t kGroups = kStreamWaves / S;
     uint32_t groups = static_cast<uint32_t>(cus) * G;
-    const uint32_t need = (p.N + kStreamWaves - 1) / kStreamWaves;  // no idle workgroups
+    const uint32_t need = (p.N + kGroups - 1) / kGroups;  // no idle workgroups
     if (groups > need) groups = need;
-    const uint32_t total_waves = groups * kStreamWaves;
-    const size_t lds = static_cast<size_t>(p.K / 64) * kSlot;
+    const uint32_t total_groups = groups * kGroups;
+    const size_t lds = static_cast<size_t>(p.K / 64) * kSlot + (S > 1 ? kStreamThreads * sizeof(float) : 0);
     const dim3 grid(groups), block(kStreamThreads);
     if (p.out == OutType::F32) {
-        hipLaunchKernelGGL((gemv_stream_kernel<D, float>), grid, block, lds, p.stream,
+        hipLaunchKernelGGL((gemv_stream_kernel<P, S, D, float>), grid, block, lds, p.stream,
                            static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
-                           static_cast<float*>(p.y), p.N, p.K, total_waves);
+                           static_cast<float*>(p.y), p.N, p.K, total_groups);
     } else {
-        hipLaunchKernelGGL((gemv_stream_kernel<D, _Float16>), grid, block, lds, p.stream,
+        hipLaunchKernelGGL((gemv_stream_kernel<P, S, D, _Float16>), grid, block, lds, p.stream,
                            static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
-                           static_cast<_Float16*>(p.y), p.N, p.K, total_waves);
+                           static_cast<_Float16*>(p.y), p.N, p.K, total_groups);
     }
     return hipGetLastError();
 }
 
+// p0 = 64-pair capacity of a row (K <= 4096 p0), p1 = rows in flight,
+// p2 = workgroups per CU.
 #define MOTE_STREAM(D, G) \
-    Variant{"stream_d" #D "_g" #G, Kind::GemvStream, D, G, 1, &launch_gemv_stream<D, G>}
+    Variant{"stream_d" #D "_g" #G, Kind::GemvStream, 1, D, G, &launch_gemv_stream<1, 1, D, G>}
+#define MOTE_STREAM_P(P, D, G) \
+    Variant{"stream_p" #P "_d" #D "_g" #G, Kind::GemvStream, P, D, G, &launch_gemv_stream<P, 1, D, G>}
+#define MOTE_STREAM_S(S, D, G) \
+    Variant{"stream_s" #S "_d" #D "_g" #G, Kind::GemvStream, S, D, G, &launch_gemv_stream<1, S, D, G>}
 
 const Variant kStream[] = {
     MOTE_STREAM(1, 1), MOTE_STREAM(2, 1), MOTE_STREAM(3, 1), MOTE_STREAM(4, 1),
     MOTE_STREAM(1, 2), MOTE_STREAM(2, 2), MOTE_STREAM(3, 2), MOTE_STREAM(4, 2),
     MOTE_STREAM(2, 3), MOTE_STREAM(2, 4),
+    MOTE_STREAM_P(2, 1, 1), MOTE_STREAM_P(2, 1, 2), MOTE_STREAM_P(2, 2, 1),
+    MOTE_STREAM_P(3, 1, 1), MOTE_STREAM_P(3, 2, 1),
+    MOTE_STREAM_P(4, 1, 1),
+    MOTE_STREAM_S(2, 1, 1), MOTE_STREAM_S(2, 1, 2), MOTE_STREAM_S(4, 1, 1), MOTE_STREAM_S(4, 1, 2),
+    MOTE_STREAM_S(4, 2, 1), MOTE_STREAM_S(4, 2, 2),
 };
 
 #undef MOTE_STREAM
+#undef MOTE_STREAM_P
+#undef MOTE_STREAM_S
 
 }  // namespace
 
@@ -214,11 +281,10 @@ const Variant* gemv_stream_variants(int* count) {
     return kStream;
 }
 
-// One token, K a multiple of 64 and at most 4096 (one pair per lane), x 16-byte
-// and w dword aligned.
+// One token, K a multiple of 64 and at most 4096 per pair slot of a lane, x
+// 16-byte and w dword aligned.
 bool gemv_stream_supports(const Variant& v, const Problem& p) {
-    (void)v;
-    return p.M == 1 && p.K % 64 == 0 && p.K > 0 && p.K <= 4096 &&
+    return p.M == 1 && p.K % 64 == 0 && p.K > 0 && p.K <= 4096u * static_cast<uint32_t>(v.p0) &&
            reinterpret_cast<uintptr_t>(p.w) % 4 == 0 && reinterpret_cast<uintptr_t>(p.x) % 16 == 0;
 }
 

@@ -245,10 +245,21 @@ def test_every_rows_variant(stream, oracle, variant):
 def test_every_stream_variant(stream, oracle, variant):
     """Persistent pipelined GEMV: N below one workgroup, ragged N, idle lanes
     (K < 4096), and N = 140001 at K = 64, where waves own more than 64 rows
-    and flush their register-held sums mid-loop."""
+    and flush their register-held sums mid-loop.  Variants with P pair slots
+    per lane, or rows split over S waves, also run K filling all of the P S
+    64-pair slots, K one pair past P S - 1 slots, and the 14336 -> 4096 down
+    projection where it fits."""
     d = ops.Q4_0Dispatch()
     d.force(variant)
-    for m, n, k in [(1, 1, 64), (1, 7, 4096), (1, 257, 1024), (1, 130, 64), (1, 140001, 64), (1, 14336, 4096)]:
+    slots = int(variant.split("_p")[1].split("_")[0]) if "_p" in variant else 1
+    slots *= int(variant.split("_s")[1].split("_")[0]) if "_s" in variant else 1
+    shapes = [(1, 1, 64), (1, 7, 4096), (1, 257, 1024), (1, 130, 64), (1, 140001, 64)]
+    if slots > 1:
+        shapes += [(1, 61, 4096 * slots), (1, 1000, 4096 * (slots - 1) + 64)]
+        if 14336 <= 4096 * slots:
+            shapes.append((1, 4096, 14336))
+    shapes.append((1, 14336, 4096))
+    for m, n, k in shapes:
         x = normal_x(wl.seed_for(13, k), m, k)
         w = weights(wl.seed_for(13, 100 + n), n, k)
         y = run_linear(stream, x, w, m, n, k, dispatch=d)
