@@ -28,6 +28,7 @@ struct Variant {
     Kind kind;
     int p0, p1, p2;       // kernel tile parameters (meaning depends on kind)
     hipError_t (*launch)(const Problem&);
+    int tokens = 0;       // exact M the variant requires (0: any M it supports)
 };
 
 // Kernel variant tables, defined next to the kernels.

@@ -56,6 +56,30 @@ struct XPair {
 //   sum x (n - 8) = 2^20 (16 a_lo + a_hi)   with a_hi started at -8 * 2^-20 sum x,
 // five VALU operations per nibble dword instead of a mask, shift and OR per
 // nibble pair.
+// The 32 masked nibble operands of a pair, in the order of XPair::xp, and
+// the two block scales; shared by every token of a row.
+struct Unpacked {
+    uint32_t u[32];
+    float d0, d1;
+};
+
+__device__ __forceinline__ void pair_unpack(const uint32_t (&raw)[9], Unpacked& o) {
+    uint32_t q[8];
+    q[0] = pair_q0(raw);
+    q[1] = raw[1]; q[2] = raw[2]; q[3] = raw[3];
+    q[4] = raw[5]; q[5] = raw[6]; q[6] = raw[7]; q[7] = raw[8];
+    o.d0 = half_lo_to_float(raw[0]);
+    o.d1 = half_hi_to_float(raw[4]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t a = q[i], a8 = a >> 8;
+        o.u[4 * i + 0] = a & kSubHi;
+        o.u[4 * i + 1] = a & kSubLo;
+        o.u[4 * i + 2] = a8 & kSubLo;
+        o.u[4 * i + 3] = a8 & kSubHi;
+    }
+}
+
 __device__ __forceinline__ float pair_dot(const uint32_t (&raw)[9], const XPair& x) {
     uint32_t q[8];
     q[0] = pair_q0(raw);
@@ -81,7 +105,25 @@ __device__ __forceinline__ float pair_dot(const uint32_t (&raw)[9], const XPair&
     return __builtin_fmaf(d1, __builtin_fmaf(lo1, 16.0f, hi1), acc);
 }
 
-template <int P, int S, int D, typename OutT>
+// The same sum from operands unpacked once for several tokens.
+__device__ __forceinline__ float pair_dot(const Unpacked& w, const XPair& x) {
+    float lo0 = 0.0f, hi0 = x.c0, lo1 = 0.0f, hi1 = x.c1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        hi0 = dot2(w.u[4 * i + 0], x.xp[4 * i + 0], hi0);
+        lo0 = dot2(w.u[4 * i + 1], x.xp[4 * i + 1], lo0);
+        lo0 = dot2(w.u[4 * i + 2], x.xp[4 * i + 2], lo0);
+        hi0 = dot2(w.u[4 * i + 3], x.xp[4 * i + 3], hi0);
+        hi1 = dot2(w.u[16 + 4 * i + 0], x.xp[16 + 4 * i + 0], hi1);
+        lo1 = dot2(w.u[16 + 4 * i + 1], x.xp[16 + 4 * i + 1], lo1);
+        lo1 = dot2(w.u[16 + 4 * i + 2], x.xp[16 + 4 * i + 2], lo1);
+        hi1 = dot2(w.u[16 + 4 * i + 3], x.xp[16 + 4 * i + 3], hi1);
+    }
+    const float acc = w.d0 * __builtin_fmaf(lo0, 16.0f, hi0);
+    return __builtin_fmaf(w.d1, __builtin_fmaf(lo1, 16.0f, hi1), acc);
+}
+
+template <int P, int S, int D, int MT, bool LAG, typename OutT>
 __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint16_t* __restrict__ x,
                                                                      const uint8_t* __restrict__ w,
                                                                      OutT* __restrict__ y, uint32_t N,
@@ -123,10 +165,12 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
         for (int i = 0; i < P; ++i) load_pair(row + static_cast<size_t>(pc[i]) * kPairBytes, b[i]);
     };
 
-    // x chunk loads first (P S 16-byte chunks per thread), then the first D
-    // rows, and only then the LDS stores of x, so no row load waits for x.
-    constexpr int XC = P * S;
-    const uint32_t xchunks = npairs * 8;
+    // x chunk loads first (P S MT 16-byte chunks per thread; chunk c of the
+    // [MT, K] activations is token c / (8 npairs), pair (c / 8) % npairs),
+    // then the first D rows, and only then the LDS stores of x, so no row
+    // load waits for x.
+    constexpr int XC = P * S * MT;
+    const uint32_t xchunks = npairs * 8 * MT;
     u32x4 xreg[XC];
     uint32_t xc[XC];
 #pragma unroll
@@ -136,7 +180,9 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
     }
     __builtin_amdgcn_sched_barrier(0);
     // Ring of D + 1 row buffers: row j + D is issued before row j is
-    // computed, so D rows stay in flight behind the arithmetic.
+    // computed, so D rows stay in flight behind the arithmetic (with LAG the
+    // wave then waits for row j + 1 before issuing more; without it, D + 1
+    // rows are in flight while it waits).
     constexpr int R = D + 1;
     uint32_t buf[R][P][9];
 #pragma unroll
@@ -147,13 +193,16 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
         *reinterpret_cast<u32x4*>(xs + (xc[c] >> 3) * kSlot + (xc[c] & 7) * 16) = xreg[c];
     __syncthreads();
 
-    XPair xv[P];
+    XPair xv[MT][P];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
 #pragma unroll
     for (int s = 0; s < P; ++s) {
         uint32_t xr[32];
+        const uint8_t* slot = xs + (static_cast<size_t>(m) * npairs + pc[s]) * kSlot;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const u32x4 v = *reinterpret_cast<const u32x4*>(xs + pc[s] * kSlot + i * 16);
+            const u32x4 v = *reinterpret_cast<const u32x4*>(slot + i * 16);
             xr[4 * i + 0] = v.x; xr[4 * i + 1] = v.y; xr[4 * i + 2] = v.z; xr[4 * i + 3] = v.w;
         }
         float s0 = 0.0f, s1 = 0.0f;
@@ -162,8 +211,8 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
             s0 = dot2(xr[i], kOnePair, s0);
             s1 = dot2(xr[16 + i], kOnePair, s1);
         }
-        xv[s].c0 = (-8.0f / kTwo20) * s0;
-        xv[s].c1 = (-8.0f / kTwo20) * s1;
+        xv[m][s].c0 = (-8.0f / kTwo20) * s0;
+        xv[m][s].c1 = (-8.0f / kTwo20) * s1;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             const int base = (q < 4) ? 0 : 32;
@@ -171,10 +220,10 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
             const int e1 = base + pair_byte_element(q, 1);
             const int e2 = base + pair_byte_element(q, 2);
             const int e3 = base + pair_byte_element(q, 3);
-            xv[s].xp[4 * q + 0] = pick(xr, e0 + 16, e2 + 16);  // hi02
-            xv[s].xp[4 * q + 1] = pick(xr, e0, e2);            // lo02
-            xv[s].xp[4 * q + 2] = pick(xr, e1, e3);            // lo13
-            xv[s].xp[4 * q + 3] = pick(xr, e1 + 16, e3 + 16);  // hi13
+            xv[m][s].xp[4 * q + 0] = pick(xr, e0 + 16, e2 + 16);  // hi02
+            xv[m][s].xp[4 * q + 1] = pick(xr, e0, e2);            // lo02
+            xv[m][s].xp[4 * q + 2] = pick(xr, e1, e3);            // lo13
+            xv[m][s].xp[4 * q + 3] = pick(xr, e1 + 16, e3 + 16);  // hi13
         }
     }
 
@@ -184,22 +233,28 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
     // (after the x area).  The loop runs at least once and is unrolled by the
     // ring size, so slots are compile-time registers; steps past the last row
     // compute clamped rows and store nothing.
-    float* red = reinterpret_cast<float*>(xs + static_cast<size_t>(npairs) * kSlot);
-    auto flush = [&](float v, uint32_t first, uint32_t count) {
-        if constexpr (S > 1) {
-            red[wave * 64 + lane] = v;
-            __syncthreads();
-            if (slice == 0) {
+    float* red = reinterpret_cast<float*>(xs + static_cast<size_t>(npairs) * MT * kSlot);
+    auto flush = [&](const float (&v)[MT], uint32_t first, uint32_t count) {
 #pragma unroll
-                for (int t = 1; t < S; ++t) v += red[(wave + t) * 64 + lane];
+        for (int m = 0; m < MT; ++m) {
+            float t = v[m];
+            if constexpr (S > 1) {
+                red[wave * 64 + lane] = t;
+                __syncthreads();
+                if (slice == 0) {
+#pragma unroll
+                    for (int r = 1; r < S; ++r) t += red[(wave + r) * 64 + lane];
+                }
+                __syncthreads();
             }
-            __syncthreads();
-            if (slice != 0) return;
+            if (slice == 0 && static_cast<uint32_t>(lane) < count)
+                y[static_cast<size_t>(m) * N + g + (first + static_cast<uint32_t>(lane)) * total_groups] =
+                    to_out<OutT>(kTwo20 * t);
         }
-        if (static_cast<uint32_t>(lane) < count)
-            y[g + (first + static_cast<uint32_t>(lane)) * total_groups] = to_out<OutT>(kTwo20 * v);
     };
-    float mine = 0.0f;
+    float mine[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) mine[m] = 0.0f;
     uint32_t j = 0;
     do {
 #pragma unroll
@@ -207,14 +262,35 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
             const uint32_t jj = j + static_cast<uint32_t>(u);
             load_row(jj + D, buf[(u + D) % R]);
             __builtin_amdgcn_sched_barrier(0);
-            float part = 0.0f;
+            float part[MT];
 #pragma unroll
-            for (int i = 0; i < P; ++i)
-                part += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pair_dot(buf[u][i], xv[i])) & keep[i]);
-            const float s = wave_sum(part);
-            mine = (jj < trips && static_cast<uint32_t>(lane) == (jj & 63u)) ? s : mine;
+            for (int m = 0; m < MT; ++m) part[m] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                if constexpr (MT == 1) {  // masks feed the dot chains directly: fewer live registers
+                    part[0] += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pair_dot(buf[u][i], xv[0][i])) & keep[i]);
+                } else {
+                    Unpacked wu;
+                    pair_unpack(buf[u][i], wu);
+#pragma unroll
+                    for (int m = 0; m < MT; ++m)
+                        part[m] += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pair_dot(wu, xv[m][i])) & keep[i]);
+                }
+            }
+            const bool mine_lane = jj < trips && static_cast<uint32_t>(lane) == (jj & 63u);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const float s = wave_sum(part[m]);
+                mine[m] = mine_lane ? s : mine[m];
+            }
             if ((jj & 63u) == 63u && jj < trips)  // uniform over the workgroup
                 flush(mine, jj - 63u, nrows > jj - 63u ? min(nrows - (jj - 63u), 64u) : 0u);
+            if constexpr (LAG) {
+                // Row j + 1 arrives before row j + 1 + D is issued: D rows in
+                // flight at any time, never D + 1.
+                constexpr int kLater = 9 * P * (D - 1);  // loads of rows j + 2 .. j + D
+                __builtin_amdgcn_s_waitcnt((kLater & 0xF) | ((kLater >> 4) << 14) | 0x0F70);
+            }
         }
         j += R;
     } while (j < trips);
@@ -222,7 +298,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
     if (base < trips) flush(mine, base, nrows > base ? nrows - base : 0u);
 }
 
-template <int P, int S, int D, int G>
+template <int P, int S, int D, int G, int MT = 1, bool LAG = true>
 hipError_t launch_gemv_stream(const Problem& p) {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -236,14 +312,14 @@ hipError_t launch_gemv_stream(const Problem& p) {
     const uint32_t need = (p.N + kGroups - 1) / kGroups;  // no idle workgroups
     if (groups > need) groups = need;
     const uint32_t total_groups = groups * kGroups;
-    const size_t lds = static_cast<size_t>(p.K / 64) * kSlot + (S > 1 ? kStreamThreads * sizeof(float) : 0);
+    const size_t lds = static_cast<size_t>(p.K / 64) * MT * kSlot + (S > 1 ? kStreamThreads * sizeof(float) : 0);
     const dim3 grid(groups), block(kStreamThreads);
     if (p.out == OutType::F32) {
-        hipLaunchKernelGGL((gemv_stream_kernel<P, S, D, float>), grid, block, lds, p.stream,
+        hipLaunchKernelGGL((gemv_stream_kernel<P, S, D, MT, LAG, float>), grid, block, lds, p.stream,
                            static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<float*>(p.y), p.N, p.K, total_groups);
     } else {
-        hipLaunchKernelGGL((gemv_stream_kernel<P, S, D, _Float16>), grid, block, lds, p.stream,
+        hipLaunchKernelGGL((gemv_stream_kernel<P, S, D, MT, LAG, _Float16>), grid, block, lds, p.stream,
                            static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<_Float16*>(p.y), p.N, p.K, total_groups);
     }
@@ -254,25 +330,42 @@ hipError_t launch_gemv_stream(const Problem& p) {
 // p2 = workgroups per CU.
 #define MOTE_STREAM(D, G) \
     Variant{"stream_d" #D "_g" #G, Kind::GemvStream, 1, D, G, &launch_gemv_stream<1, 1, D, G>}
+#define MOTE_STREAM_Q(D, G) \
+    Variant{"stream_d" #D "q_g" #G, Kind::GemvStream, 1, D, G, &launch_gemv_stream<1, 1, D, G, 1, false>}
 #define MOTE_STREAM_P(P, D, G) \
     Variant{"stream_p" #P "_d" #D "_g" #G, Kind::GemvStream, P, D, G, &launch_gemv_stream<P, 1, D, G>}
 #define MOTE_STREAM_S(S, D, G) \
     Variant{"stream_s" #S "_d" #D "_g" #G, Kind::GemvStream, S, D, G, &launch_gemv_stream<1, S, D, G>}
+#define MOTE_STREAM_SQ(S, D, G)                                              \
+    Variant{"stream_s" #S "_d" #D "q_g" #G, Kind::GemvStream, S, D, G,       \
+            &launch_gemv_stream<1, S, D, G, 1, false>}
+#define MOTE_STREAM_M(MT, D, G)                                                          \
+    Variant{"stream_m" #MT "_d" #D "_g" #G, Kind::GemvStream, 1, D, G,                  \
+            &launch_gemv_stream<1, 1, D, G, MT>, MT}
+#define MOTE_STREAM_MQ(MT, D, G)                                                         \
+    Variant{"stream_m" #MT "_d" #D "q_g" #G, Kind::GemvStream, 1, D, G,                 \
+            &launch_gemv_stream<1, 1, D, G, MT, false>, MT}
 
+// "q" variants queue row j + 1 + D while waiting for row j + 1.
 const Variant kStream[] = {
-    MOTE_STREAM(1, 1), MOTE_STREAM(2, 1), MOTE_STREAM(3, 1), MOTE_STREAM(4, 1),
-    MOTE_STREAM(1, 2), MOTE_STREAM(2, 2), MOTE_STREAM(3, 2), MOTE_STREAM(4, 2),
-    MOTE_STREAM(2, 3), MOTE_STREAM(2, 4),
-    MOTE_STREAM_P(2, 1, 1), MOTE_STREAM_P(2, 1, 2), MOTE_STREAM_P(2, 2, 1),
-    MOTE_STREAM_P(3, 1, 1), MOTE_STREAM_P(3, 2, 1),
-    MOTE_STREAM_P(4, 1, 1),
+    MOTE_STREAM(1, 1), MOTE_STREAM(2, 1), MOTE_STREAM(3, 1),
+    MOTE_STREAM(1, 2), MOTE_STREAM(2, 2),
+    MOTE_STREAM_Q(1, 1), MOTE_STREAM_Q(1, 2), MOTE_STREAM_Q(2, 1),
+    MOTE_STREAM_P(2, 1, 1), MOTE_STREAM_P(2, 1, 2),
+    MOTE_STREAM_P(3, 1, 1), MOTE_STREAM_P(4, 1, 1),
     MOTE_STREAM_S(2, 1, 1), MOTE_STREAM_S(2, 1, 2), MOTE_STREAM_S(4, 1, 1), MOTE_STREAM_S(4, 1, 2),
-    MOTE_STREAM_S(4, 2, 1), MOTE_STREAM_S(4, 2, 2),
+    MOTE_STREAM_S(4, 2, 2), MOTE_STREAM_SQ(4, 1, 2), MOTE_STREAM_SQ(2, 1, 2), MOTE_STREAM_SQ(4, 1, 1),
+    MOTE_STREAM_M(2, 1, 1), MOTE_STREAM_M(3, 1, 1), MOTE_STREAM_M(4, 1, 1),
+    MOTE_STREAM_MQ(2, 1, 1), MOTE_STREAM_MQ(2, 1, 2),
 };
 
 #undef MOTE_STREAM
 #undef MOTE_STREAM_P
 #undef MOTE_STREAM_S
+#undef MOTE_STREAM_M
+#undef MOTE_STREAM_Q
+#undef MOTE_STREAM_SQ
+#undef MOTE_STREAM_MQ
 
 }  // namespace
 
@@ -281,10 +374,11 @@ const Variant* gemv_stream_variants(int* count) {
     return kStream;
 }
 
-// One token, K a multiple of 64 and at most 4096 per pair slot of a lane, x
-// 16-byte and w dword aligned.
+// One token (or exactly the variant's token count), K a multiple of 64 and at
+// most 4096 per 64-pair slot of a row, x 16-byte and w dword aligned.
 bool gemv_stream_supports(const Variant& v, const Problem& p) {
-    return p.M == 1 && p.K % 64 == 0 && p.K > 0 && p.K <= 4096u * static_cast<uint32_t>(v.p0) &&
+    const uint32_t tokens = v.tokens > 0 ? static_cast<uint32_t>(v.tokens) : 1u;
+    return p.M == tokens && p.K % 64 == 0 && p.K > 0 && p.K <= 4096u * static_cast<uint32_t>(v.p0) &&
            reinterpret_cast<uintptr_t>(p.w) % 4 == 0 && reinterpret_cast<uintptr_t>(p.x) % 16 == 0;
 }
 

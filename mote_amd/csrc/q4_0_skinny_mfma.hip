@@ -55,7 +55,7 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t q, f16x2 d, uint32_t one) {
     return f16x8{l02.x, l02.y, l13.x, l13.y, h02.x, h02.y, h13.x, h13.y};
 }
 
-template <int KS, int STEPS, int MT, int D, int RT, typename OutT>
+template <int KS, int STEPS, int MT, int D, int RT, bool TR, typename OutT>
 __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __restrict__ x,
                                                              const uint8_t* __restrict__ w,
                                                              OutT* __restrict__ y, uint32_t M,
@@ -63,6 +63,12 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
                                                              uint32_t token_groups, uint32_t items,
                                                              uint32_t groups_per_xcd) {
     __shared__ float part[KS][RT * MT][16][17];
+    // Transposed loads: wave-private staging of the raw pairs, [row tile][row]
+    // [pair of the slice], rows padded by one dword so the 16 rows read by an
+    // MFMA operand fall on distinct banks.
+    constexpr int kSlicePairs = STEPS * 4;
+    constexpr int kStageRow = kSlicePairs * kPairBytes + 4;
+    __shared__ __attribute__((aligned(16))) uint8_t stage[TR ? KS * RT * 16 * kStageRow : 4];
 
     const int tid = static_cast<int>(threadIdx.x);
     const int kw = tid >> 6;
@@ -81,19 +87,51 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     auto rows_of = [&](uint32_t item) { return (item / token_groups) * (16u * RT); };
     const uint32_t tok0 = (first % token_groups) * (16u * MT);
 
-    // Weight loads of one item: RT row tiles x STEPS pairs per lane.
+    // Weight loads of one item: RT row tiles x STEPS pairs per lane.  Direct
+    // mapping: lane (li, lg) loads the pair it feeds to the MFMAs, so one
+    // instruction spans 16 rows.  Transposed mapping (TR): lane l loads pair
+    // l % (4 STEPS) of the wave's slice in row s (16 / STEPS) + l / (4 STEPS),
+    // so one instruction spans 16 / STEPS rows of 4 STEPS neighbouring pairs,
+    // and the pairs reach their MFMA lanes through the wave's LDS stage.
+    constexpr int kRowsPerLoad = 16 / STEPS;
     auto load_item = [&](uint32_t item, uint32_t (&raw)[RT * STEPS][9]) {
         const uint32_t it = min(item, items - 1);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
-            const uint32_t n = min(rows_of(it) + 16u * rt + static_cast<uint32_t>(li), N - 1);
-            const uint8_t* row = w + static_cast<size_t>(n) * row_bytes;
 #pragma unroll
             for (int s = 0; s < STEPS; ++s) {
-                const uint32_t p = (static_cast<uint32_t>(kw) * STEPS + s) * 4u + static_cast<uint32_t>(lg);
-                load_pair(row + static_cast<size_t>(p) * kPairBytes, raw[rt * STEPS + s]);
+                uint32_t r, p;
+                if constexpr (TR) {
+                    r = static_cast<uint32_t>(s * kRowsPerLoad + lane / kSlicePairs);
+                    p = static_cast<uint32_t>(kw * kSlicePairs + lane % kSlicePairs);
+                } else {
+                    r = static_cast<uint32_t>(li);
+                    p = (static_cast<uint32_t>(kw) * STEPS + s) * 4u + static_cast<uint32_t>(lg);
+                }
+                const uint32_t n = min(rows_of(it) + 16u * rt + r, N - 1);
+                load_pair(w + static_cast<size_t>(n) * row_bytes + static_cast<size_t>(p) * kPairBytes,
+                          raw[rt * STEPS + s]);
             }
         }
+    };
+    uint8_t* my_stage = stage + (TR ? kw * RT * 16 * kStageRow : 0);
+    auto stage_item = [&](const uint32_t (&raw)[RT * STEPS][9]) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int s = 0; s < STEPS; ++s) {
+                const int r = s * kRowsPerLoad + lane / kSlicePairs;
+                uint32_t* dst = reinterpret_cast<uint32_t*>(my_stage + (rt * 16 + r) * kStageRow +
+                                                            (lane % kSlicePairs) * kPairBytes);
+#pragma unroll
+                for (int i = 0; i < 9; ++i) dst[i] = raw[rt * STEPS + s][i];
+            }
+    };
+    auto staged_pair = [&](int rt, int s, uint32_t (&c)[9]) {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(my_stage + (rt * 16 + li) * kStageRow +
+                                                                (4 * s + lg) * kPairBytes);
+#pragma unroll
+        for (int i = 0; i < 9; ++i) c[i] = src[i];
     };
 
     // The first item's weights, then the activations (reused by every item).
@@ -136,6 +174,13 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     // right after its last use (so the refill overlaps the reduction and the
     // other buffer's item), then reduce the KS partial tiles and store.
     auto process = [&](uint32_t it, uint32_t (&buf)[RT * STEPS][9], uint32_t next, auto refill) {
+        if constexpr (TR) {
+            // LDS operations of a wave complete in order: the stage is read
+            // back below, and rewritten by the next item only after this
+            // item's reads.
+            stage_item(buf);
+            if constexpr (decltype(refill)::value) load_item(next, buf);
+        }
         f32x4 acc[RT][MT];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
@@ -147,7 +192,13 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
             f16x2 d0[RT], d1[RT];
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
-                const uint32_t (&c)[9] = buf[rt * STEPS + s];
+                uint32_t c[9];
+                if constexpr (TR) {
+                    staged_pair(rt, s, c);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 9; ++i) c[i] = buf[rt * STEPS + s][i];
+                }
                 q[rt][0] = pair_q0(c);
                 q[rt][1] = c[1]; q[rt][2] = c[2]; q[rt][3] = c[3];
                 q[rt][4] = c[5]; q[rt][5] = c[6]; q[rt][6] = c[7]; q[rt][7] = c[8];
@@ -165,7 +216,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
                 }
             }
         }
-        if constexpr (decltype(refill)::value) load_item(next, buf);
+        if constexpr (!TR && decltype(refill)::value) load_item(next, buf);
 
         // lane holds rows 4 lg + r, token li of each (row tile, token tile)
 #pragma unroll
@@ -189,7 +240,11 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     };
 
     uint32_t item = first;
-    if constexpr (D == 1) {
+    if constexpr (TR && D == 1) {
+        // The stage frees the registers as soon as an item is written to LDS,
+        // so one register buffer already keeps the next item in flight.
+        for (; item < items; item += groups) process(item, buf0, item + groups, std::true_type{});
+    } else if constexpr (D == 1) {
         for (; item < items; item += groups) {
             // Copying the buffer waits for this item only; the next item's
             // loads then run under this item's arithmetic.
@@ -212,7 +267,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     }
 }
 
-template <int KS, int STEPS, int MT, int D, int G, int RT>
+template <int KS, int STEPS, int MT, int D, int G, int RT, bool TR = false>
 hipError_t launch_skinny(const Problem& p) {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -237,11 +292,11 @@ hipError_t launch_skinny(const Problem& p) {
     const uint32_t per_xcd = groups / 8u;
     const dim3 grid(groups), block(KS * 64);
     if (p.out == OutType::F32) {
-        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, float>), grid, block, 0, p.stream,
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float>), grid, block, 0, p.stream,
                            static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<float*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
     } else {
-        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, _Float16>), grid, block, 0, p.stream,
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, _Float16>), grid, block, 0, p.stream,
                            static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<_Float16*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
     }
@@ -251,6 +306,9 @@ hipError_t launch_skinny(const Problem& p) {
 #define MOTE_SKINNY(KS, STEPS, MT, D, G, RT)                                                     \
     Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d" #D "_g" #G "_r" #RT, Kind::SkinnyMfma, KS, \
             STEPS, MT, &launch_skinny<KS, STEPS, MT, D, G, RT>}
+#define MOTE_SKINNY_TR(KS, STEPS, MT, D, G)                                                       \
+    Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d" #D "_g" #G "_r1_tr", Kind::SkinnyMfma, KS, \
+            STEPS, MT, &launch_skinny<KS, STEPS, MT, D, G, 1, true>}
 
 const Variant kSkinny[] = {
     MOTE_SKINNY(16, 1, 1, 1, 1, 1), MOTE_SKINNY(16, 1, 1, 2, 1, 1), MOTE_SKINNY(16, 1, 2, 1, 1, 1),
@@ -259,9 +317,14 @@ const Variant kSkinny[] = {
     MOTE_SKINNY(8, 1, 1, 1, 1, 1), MOTE_SKINNY(8, 1, 2, 1, 1, 1), MOTE_SKINNY(8, 1, 1, 2, 1, 1),
     MOTE_SKINNY(4, 2, 1, 1, 1, 1), MOTE_SKINNY(4, 1, 1, 1, 1, 1), MOTE_SKINNY(4, 1, 1, 2, 1, 1),
     MOTE_SKINNY(16, 2, 1, 1, 1, 1),
+    MOTE_SKINNY_TR(4, 4, 1, 1, 1), MOTE_SKINNY_TR(4, 4, 1, 1, 2), MOTE_SKINNY_TR(4, 4, 1, 2, 1),
+    MOTE_SKINNY_TR(4, 4, 1, 2, 2), MOTE_SKINNY_TR(8, 2, 1, 1, 1), MOTE_SKINNY_TR(8, 2, 1, 1, 2),
+    MOTE_SKINNY_TR(8, 2, 2, 1, 1), MOTE_SKINNY_TR(8, 2, 2, 2, 1), MOTE_SKINNY_TR(4, 2, 1, 1, 1),
+    MOTE_SKINNY_TR(4, 2, 2, 1, 1),
 };
 
 #undef MOTE_SKINNY
+#undef MOTE_SKINNY_TR
 
 }  // namespace
 

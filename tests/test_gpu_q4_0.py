@@ -248,17 +248,20 @@ def test_every_stream_variant(stream, oracle, variant):
     and flush their register-held sums mid-loop.  Variants with P pair slots
     per lane, or rows split over S waves, also run K filling all of the P S
     64-pair slots, K one pair past P S - 1 slots, and the 14336 -> 4096 down
-    projection where it fits."""
+    projection where it fits.  Multi-token variants run every shape with
+    their M."""
     d = ops.Q4_0Dispatch()
     d.force(variant)
     slots = int(variant.split("_p")[1].split("_")[0]) if "_p" in variant else 1
     slots *= int(variant.split("_s")[1].split("_")[0]) if "_s" in variant else 1
-    shapes = [(1, 1, 64), (1, 7, 4096), (1, 257, 1024), (1, 130, 64), (1, 140001, 64)]
+    tokens = int(variant.split("_m")[1].split("_")[0]) if "_m" in variant else 1
+    shapes = [(1, 64), (7, 4096), (257, 1024), (130, 64), (140001, 64)]
     if slots > 1:
-        shapes += [(1, 61, 4096 * slots), (1, 1000, 4096 * (slots - 1) + 64)]
+        shapes += [(61, 4096 * slots), (1000, 4096 * (slots - 1) + 64)]
         if 14336 <= 4096 * slots:
-            shapes.append((1, 4096, 14336))
-    shapes.append((1, 14336, 4096))
+            shapes.append((4096, 14336))
+    shapes.append((14336, 4096))
+    shapes = [(tokens, n, k) for n, k in shapes]
     for m, n, k in shapes:
         x = normal_x(wl.seed_for(13, k), m, k)
         w = weights(wl.seed_for(13, 100 + n), n, k)
