@@ -288,7 +288,8 @@ def profile_run(case: LinearCase, stream: Stream, hip: _Hip) -> int:
     for i in range(20):
         case.launch(i + 1, stream)
     stream.synchronize()
-    print(f"profile run: copied {case.w.nbytes} bytes, 20 linear calls", file=sys.stderr)
+    print(f"profile run: copied {case.w.nbytes} bytes, 20 calls of M={case.m} K={case.k} N={case.n}"
+          f"{' gate/up' if case.gate_up else ''}", file=sys.stderr)
     dst.free()
     case.free()
     stream.close()
@@ -331,6 +332,10 @@ def main() -> int:
                     help="for rocprofv3 counter passes: one device-to-device copy of one weight "
                          "matrix (the calibration kernel of known size), then 20 calls of the "
                          "headline linear; prints no result line")
+    ap.add_argument("--profile-shape", default=None, metavar="M,K,N",
+                    help="with --profile-run: profile this linear shape instead of the headline")
+    ap.add_argument("--profile-gate-up", action="store_true",
+                    help="with --profile-run: profile the fused gate/up SiLU-mul of the shape")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -347,9 +352,15 @@ def main() -> int:
     stream = Stream()
     hip = _Hip()
     m, k, n = 1, 4096, 14336
-    case = LinearCase(m, n, k, workload=1)
     if args.profile_run:
+        if args.profile_shape:
+            pm, pk, pn = (int(v) for v in args.profile_shape.split(","))
+            case = LinearCase(pm, pn, pk, workload=4 if pm >= 64 else (2 if pm > 1 else 1),
+                              gate_up=args.profile_gate_up)
+        else:
+            case = LinearCase(m, n, k, workload=1)
         return profile_run(case, stream, hip)
+    case = LinearCase(m, n, k, workload=1)
     print(f"bench: Q4_0 linear M={m} K={k} N={n}, {case.copies} weight copies "
           f"({case.copies * case.w.nbytes / 1e6:.0f} MB), warmup {args.warmup}, steps {args.steps}",
           file=sys.stderr, flush=True)

@@ -168,9 +168,9 @@ const Variant* heuristic(const Problem& p, Op op) {
         const unsigned g = p.N >= 2u * row_groups_g2 ? 2u : 1u;
         char name[32];
         if (split == 1)
-            std::snprintf(name, sizeof name, "stream_d1q_g%u", g);
+            std::snprintf(name, sizeof name, "stream_d1_g%u", g);
         else
-            std::snprintf(name, sizeof name, "stream_s%u_d1q_g%u", split, g);
+            std::snprintf(name, sizeof name, "stream_s%u_d1_g%u", split, g);
         const Variant* st = by_name(name);
         if (st && gemv_stream_supports(*st, p)) return st;
         uint32_t ks = 1;
