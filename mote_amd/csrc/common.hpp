@@ -104,6 +104,37 @@ __host__ __device__ constexpr int pair_byte_element(int w, int pos) {
                     : (4 * (w - 4) + pos);
 }
 
+// (q - 8) * d for the 8 nibbles of nibble dword q, in the order
+// [b0.lo, b2.lo, b1.lo, b3.lo, b0.hi, b2.hi, b1.hi, b3.hi].  A low nibble
+// masked into the mantissa of binary16 1024 (0x6400, ulp 1) reads 1024 + n; a
+// high nibble left in place (bits 4-7) and masked into binary16 64 (0x5400,
+// ulp 1/16) reads 64 + n, so one shift (by 8, for bytes 1 and 3) serves all
+// four nibble pairs; adding -1032 or -72 gives n - 8 exactly and the multiply
+// by d rounds once.  `c1024` and `c64` hold those constants in both halves in
+// VGPRs: gfx9-family VOP3 instructions take no literal, so with the constant in
+// a register each mask-and-insert is one v_and_or_b32 (mask in an SGPR).
+__device__ __forceinline__ f16x8 dequant8(uint32_t q, f16x2 d, uint32_t c1024, uint32_t c64) {
+    const f16x2 bias_lo = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+    const f16x2 bias_hi = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
+    const uint32_t q8 = q >> 8;
+    const f16x2 l02 = (as_h2((q & 0x000F000Fu) | c1024) + bias_lo) * d;
+    const f16x2 l13 = (as_h2((q8 & 0x000F000Fu) | c1024) + bias_lo) * d;
+    const f16x2 h02 = (as_h2((q & 0x00F000F0u) | c64) + bias_hi) * d;
+    const f16x2 h13 = (as_h2((q8 & 0x00F000F0u) | c64) + bias_hi) * d;
+    return f16x8{l02.x, l02.y, l13.x, l13.y, h02.x, h02.y, h13.x, h13.y};
+}
+
+// The two VGPR constants of dequant8.
+struct DequantConsts {
+    uint32_t c1024, c64;
+};
+__device__ __forceinline__ DequantConsts dequant_consts() {
+    DequantConsts c;
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(c.c1024));
+    asm("v_mov_b32 %0, 0x54005400" : "=v"(c.c64));
+    return c;
+}
+
 // ---------------------------------------------------------------------------
 // Wave-level reduction with DPP (gfx9 row/bcast controls), result returned
 // uniformly (read from lane 63).

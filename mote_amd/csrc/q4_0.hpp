@@ -37,6 +37,7 @@ const Variant* gemv_rows_variants(int* count);
 const Variant* gemv_stream_variants(int* count);
 const Variant* skinny_mfma_variants(int* count);
 const Variant* mfma_variants(int* count);
+const Variant* prefill_variants(int* count);
 const Variant* generic_variants(int* count);
 
 // Whether a variant can run the problem (alignment, shape limits).

@@ -1,0 +1,262 @@
+// Q4_0 prefill-shaped linear (M >= 64) on the CDNA4 matrix cores with the
+// weights staged in LDS as raw Q4_0 bytes, plus the fused gate/up variant.
+//
+//   y[m, n] = sum_k x[m, k] * w[n, k]                                (linear)
+//   y[m, n] = silu(sum_k x w_gate[n, k]) * (sum_k x w_up[n, k])       (gate/up)
+//
+// The linear is the operation of crates/mote-backend-hip/src/
+// quantized_linear.hip:13-52 (oracle crates/mote-reference/src/quantized.rs:
+// 89-144); the fused gate/up has no counterpart in the reference.
+//
+// One 256-thread workgroup computes a BM x BN output tile with 2 x 2 waves,
+// each wave a (BM/2) x (BN/2) grid of 16x16 v_mfma_f32_16x16x32_f16 tiles.
+// K advances one Q4_0 block pair (64 elements) per step through a
+// double-buffered LDS stage, one barrier per step:
+//  * activations: BM rows x 64 f16 copied from HBM, stored in the k order of
+//    the nibble unpacking (below), rows padded to 144 bytes so the 16 rows of
+//    an MFMA operand fall on distinct banks;
+//  * weights: BN rows x 36 bytes, the block pair's bytes re-aligned so every
+//    nibble dword is dword aligned: [d0 | d1 << 16][block 0 nibble dwords 0-3]
+//    [block 1 nibble dwords 0-3].  36 bytes per row and step, against 128 for
+//    dequantised f16: the LDS traffic of the weight operand drops by 3.5x and
+//    each wave dequantises the operands it feeds to its own MFMAs, in registers,
+//    (q - 8) * d exactly as the skinny kernel does (exact q - 8 from the
+//    1024 + q and 64 + q exponent tricks, one binary16 rounding of the
+//    product).
+// A 32-element block is split into four k groups g = 0..3: nibble bytes
+// 4g..4g+3, elements [4g, 4g+2, 4g+1, 4g+3, 16+4g, 16+4g+2, 16+4g+1,
+// 16+4g+3]; MFMA lane group g (lanes 16g..16g+15) takes group g of both
+// operands, so activations and weights agree on k.
+#include "common.hpp"
+#include "q4_0.hpp"
+
+namespace mote::q4_0 {
+namespace {
+
+constexpr int kXRow = 144;  // LDS bytes per activation row and step (128 + 16 padding)
+constexpr int kWRow = 36;   // LDS bytes per weight row and step (9 dwords)
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+template <int BM, int BN, bool GATE_UP, typename OutT>
+__global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict__ x,
+                                                      const uint8_t* __restrict__ wg,
+                                                      const uint8_t* __restrict__ wu,
+                                                      OutT* __restrict__ y, uint32_t M, uint32_t N,
+                                                      uint32_t K, uint32_t m_tiles, uint32_t total,
+                                                      uint32_t per_xcd) {
+    constexpr int NW = GATE_UP ? 2 : 1;
+    constexpr int TM = BM / 32;               // 16-row MFMA tiles per wave along M
+    constexpr int TN = BN / 32;               // along N
+    constexpr int XC = BM * 8 / 256;          // 16-byte activation chunks per thread and step
+    constexpr int WI = (BN + 255) / 256;      // weight rows per thread and step (per matrix)
+    static_assert(BM % 32 == 0 && BN % 32 == 0 && XC >= 1, "tile shape");
+
+    __shared__ __attribute__((aligned(16))) uint8_t xs[2][BM * kXRow];
+    __shared__ __attribute__((aligned(16))) uint8_t ws[NW][2][BN * kWRow];
+
+    const uint32_t logical = (blockIdx.x % 8u) * per_xcd + blockIdx.x / 8u;
+    if (logical >= total) return;
+    const uint32_t tile_n = logical / m_tiles;
+    const uint32_t tile_m = logical - tile_n * m_tiles;
+    const uint32_t m0 = tile_m * BM;
+    const uint32_t n0 = tile_n * BN;
+
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const uint32_t npairs = K >> 6;
+    const size_t row_bytes = static_cast<size_t>(npairs) * kPairBytes;
+    const uint8_t* wsrc[NW] = {wg};
+    if constexpr (GATE_UP) wsrc[1] = wu;
+
+    // Activation chunks: thread c of the tile copies 16 bytes (8 halves) of
+    // row c / 8; chunk c % 8 holds elements 8 (c % 4) .. + 7 of block (c % 8) / 4.
+    const uint16_t* xptr[XC];
+    int xoff[XC];
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+        const int c = tid + 256 * j;
+        const int row = c >> 3, chunk = c & 7;
+        const uint32_t m = min(m0 + row, M - 1);
+        xptr[j] = x + static_cast<size_t>(m) * K + chunk * 8;
+        const int blk = chunk >> 2, kin = (chunk & 3) * 8;
+        xoff[j] = row * kXRow + blk * 64 + ((kin & 15) >> 2) * 16 + (kin >= 16 ? 8 : 0);
+    }
+    // Weight rows: thread t copies the step's block pair of rows t, t + 256, ...
+    const uint8_t* wptr[NW][WI];
+    bool wlive[WI];
+#pragma unroll
+    for (int j = 0; j < WI; ++j) {
+        const int row = tid + 256 * j;
+        wlive[j] = row < BN;
+        const uint32_t n = min(n0 + static_cast<uint32_t>(wlive[j] ? row : 0), N - 1);
+#pragma unroll
+        for (int s = 0; s < NW; ++s) wptr[s][j] = wsrc[s] + static_cast<size_t>(n) * row_bytes;
+    }
+
+    u32x4 xreg[XC];
+    uint32_t wreg[NW][WI][9];
+    auto load_stage = [&](uint32_t kp) {
+        kp = min(kp, npairs - 1);  // past the end: a cached re-read, never used
+#pragma unroll
+        for (int j = 0; j < XC; ++j)
+            xreg[j] = *reinterpret_cast<const u32x4*>(xptr[j] + static_cast<size_t>(kp) * 64);
+#pragma unroll
+        for (int s = 0; s < NW; ++s)
+#pragma unroll
+            for (int j = 0; j < WI; ++j)
+                if (wlive[j]) load_pair(wptr[s][j] + static_cast<size_t>(kp) * kPairBytes, wreg[s][j]);
+    };
+    auto store_stage = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < XC; ++j) {
+            const u32x4 v = xreg[j];
+            u32x2 a, b;
+            a.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);  // (x0, x2)
+            a.y = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);  // (x1, x3)
+            b.x = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);  // (x4, x6)
+            b.y = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);  // (x5, x7)
+            *reinterpret_cast<u32x2*>(&xs[buf][xoff[j]]) = a;
+            *reinterpret_cast<u32x2*>(&xs[buf][xoff[j] + 16]) = b;
+        }
+#pragma unroll
+        for (int s = 0; s < NW; ++s)
+#pragma unroll
+            for (int j = 0; j < WI; ++j) {
+                if (!wlive[j]) continue;
+                const uint32_t (&d)[9] = wreg[s][j];
+                uint32_t* dst = reinterpret_cast<uint32_t*>(&ws[s][buf][(tid + 256 * j) * kWRow]);
+                dst[0] = __builtin_amdgcn_perm(d[4], d[0], 0x07060100u);  // d0 (bytes 0-1) | d1 (bytes 18-19)
+                dst[1] = __builtin_amdgcn_perm(d[1], d[0], 0x05040302u);  // block 0 nibble bytes 0-3
+                dst[2] = __builtin_amdgcn_perm(d[2], d[1], 0x05040302u);
+                dst[3] = __builtin_amdgcn_perm(d[3], d[2], 0x05040302u);
+                dst[4] = __builtin_amdgcn_perm(d[4], d[3], 0x05040302u);
+                dst[5] = d[5]; dst[6] = d[6]; dst[7] = d[7]; dst[8] = d[8];
+            }
+    };
+
+    f32x4 acc[NW][TM][TN];
+#pragma unroll
+    for (int s = 0; s < NW; ++s)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[s][i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const DequantConsts dq = dequant_consts();
+    const int lrow = lane & 15;
+    const int lgrp = lane >> 4;
+    const int a_base = (wm * (BM / 2) + lrow) * kXRow + lgrp * 16;
+    const int b_base = (wn * (BN / 2) + lrow) * kWRow;
+
+    auto mma_step = [&](int buf) {
+        uint32_t scales[NW][TN];
+#pragma unroll
+        for (int s = 0; s < NW; ++s)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                scales[s][j] = *reinterpret_cast<const uint32_t*>(&ws[s][buf][b_base + j * 16 * kWRow]);
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+            f16x8 a[TM];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+                a[i] = *reinterpret_cast<const f16x8*>(&xs[buf][a_base + i * 16 * kXRow + blk * 64]);
+#pragma unroll
+            for (int s = 0; s < NW; ++s) {
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const uint32_t q = *reinterpret_cast<const uint32_t*>(
+                        &ws[s][buf][b_base + j * 16 * kWRow + 4 + blk * 16 + lgrp * 4]);
+                    const f16x2 d = as_h2(__builtin_amdgcn_perm(scales[s][j], scales[s][j],
+                                                                blk ? 0x03020302u : 0x01000100u));
+                    const f16x8 b = dequant8(q, d, dq.c1024, dq.c64);
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+                        acc[s][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b, acc[s][i][j], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // Step k: write step k + 1 (loaded during step k - 1) to the other LDS
+    // buffer, issue the loads of step k + 2, multiply step k, barrier.
+    load_stage(0);
+    store_stage(0);
+    load_stage(1);
+    __syncthreads();
+    for (uint32_t kp = 0; kp < npairs; ++kp) {
+        const int buf = static_cast<int>(kp & 1u);
+        if (kp + 1 < npairs) {  // uniform
+            store_stage(buf ^ 1);
+            load_stage(kp + 2);
+        }
+        mma_step(buf);
+        __syncthreads();
+    }
+
+    // Epilogue: lane holds rows 4*lgrp .. 4*lgrp+3, column lrow of each tile.
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const uint32_t n = n0 + wn * (BN / 2) + j * 16 + lrow;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t m = m0 + wm * (BM / 2) + i * 16 + lgrp * 4 + r;
+                float v = acc[0][i][j][r];
+                if constexpr (GATE_UP) v = silu(v) * acc[NW - 1][i][j][r];
+                if (m < M && n < N) y[static_cast<size_t>(m) * N + n] = to_out<OutT>(v);
+            }
+        }
+    }
+}
+
+template <int BM, int BN, bool GATE_UP>
+hipError_t launch_prefill(const Problem& p) {
+    const uint32_t m_tiles = (p.M + BM - 1) / BM;
+    const uint32_t n_tiles = (p.N + BN - 1) / BN;
+    const uint64_t total64 = static_cast<uint64_t>(m_tiles) * n_tiles;
+    if (total64 > 0x7fffffffull) return hipErrorInvalidConfiguration;
+    const uint32_t total = static_cast<uint32_t>(total64);
+    const uint32_t per_xcd = (total + 7u) / 8u;
+    const dim3 grid(per_xcd * 8u), block(256);
+    const auto* x = static_cast<const uint16_t*>(p.x);
+    const auto* wg = static_cast<const uint8_t*>(p.w);
+    const auto* wu = static_cast<const uint8_t*>(p.w_up);
+    if (p.out == OutType::F32) {
+        hipLaunchKernelGGL((prefill_kernel<BM, BN, GATE_UP, float>), grid, block, 0, p.stream, x, wg, wu,
+                           static_cast<float*>(p.y), p.M, p.N, p.K, m_tiles, total, per_xcd);
+    } else {
+        hipLaunchKernelGGL((prefill_kernel<BM, BN, GATE_UP, _Float16>), grid, block, 0, p.stream, x, wg,
+                           wu, static_cast<_Float16*>(p.y), p.M, p.N, p.K, m_tiles, total, per_xcd);
+    }
+    return hipGetLastError();
+}
+
+#define MOTE_PREFILL(BM, BN)                                                                      \
+    Variant{"mfma_r_m" #BM "_n" #BN, Kind::Mfma, BM, BN, 1, &launch_prefill<BM, BN, false>}
+#define MOTE_PREFILL_GU(BM, BN)                                                                   \
+    Variant{"gateup_mfma_r_m" #BM "_n" #BN, Kind::GateUpMfma, BM, BN, 1, &launch_prefill<BM, BN, true>}
+
+// 128 x 224 tiles: N = 14336 splits into 64 of them, so M = 512 makes exactly
+// one tile per CU of a 256-CU MI355X.
+const Variant kPrefill[] = {
+    MOTE_PREFILL(128, 256), MOTE_PREFILL(128, 128), MOTE_PREFILL(64, 256), MOTE_PREFILL(256, 128),
+    MOTE_PREFILL(64, 128), MOTE_PREFILL(128, 224), MOTE_PREFILL(64, 224),
+    MOTE_PREFILL_GU(128, 128), MOTE_PREFILL_GU(64, 128), MOTE_PREFILL_GU(128, 64), MOTE_PREFILL_GU(64, 64),
+};
+
+#undef MOTE_PREFILL
+#undef MOTE_PREFILL_GU
+
+}  // namespace
+
+const Variant* prefill_variants(int* count) {
+    *count = static_cast<int>(sizeof(kPrefill) / sizeof(kPrefill[0]));
+    return kPrefill;
+}
+
+}  // namespace mote::q4_0

@@ -18,8 +18,8 @@
 //    item and step, lane (i, g) = (lane % 16, lane / 16) loads block pair
 //    4 (STEPS kw + s) + g of row i of the tile (36 bytes, the same dword-
 //    aligned load as the GEMV), dequantises it in registers to binary16
-//    (q - 8) * d (exact q - 8 from the 1024 + q exponent trick, one rounding
-//    of the product), and feeds the 8 MFMAs of the step: MFMA t takes nibble
+//    (q - 8) * d (exact q - 8 from the 1024 + q and 64 + q exponent tricks,
+//    one rounding of the product), and feeds the 8 MFMAs of the step: MFMA t takes nibble
 //    dword t of every lane's pair, so one MFMA spans the same 8 positions of
 //    the 4 pairs of its lane groups, and the activation operand holds x at
 //    exactly those positions (any consistent order of k is exact for a dot);
@@ -39,20 +39,6 @@ __device__ __forceinline__ uint32_t pick(const uint32_t* x, int a, int b) {
     const uint32_t lo = (a & 1) ? 0x0302u : 0x0100u;
     const uint32_t hi = (b & 1) ? 0x07060000u : 0x05040000u;
     return __builtin_amdgcn_perm(x[b >> 1], x[a >> 1], hi | lo);
-}
-
-// (q - 8) * d for the 8 nibbles of nibble dword q, in the order
-// [b0.lo, b2.lo, b1.lo, b3.lo, b0.hi, b2.hi, b1.hi, b3.hi].  `one` holds
-// binary16 1024 in both halves (0x64006400) in a VGPR: gfx9-family VOP3 instructions take no literal, so with
-// the constant in a register each mask-and-insert is one v_and_or_b32 (mask in
-// an SGPR) instead of an AND and an OR.
-__device__ __forceinline__ f16x8 dequant8(uint32_t q, f16x2 d, uint32_t one) {
-    const f16x2 bias = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
-    const f16x2 l02 = (as_h2((q & 0x000F000Fu) | one) + bias) * d;
-    const f16x2 l13 = (as_h2(((q >> 8) & 0x000F000Fu) | one) + bias) * d;
-    const f16x2 h02 = (as_h2(((q >> 4) & 0x000F000Fu) | one) + bias) * d;
-    const f16x2 h13 = (as_h2(((q >> 12) & 0x000F000Fu) | one) + bias) * d;
-    return f16x8{l02.x, l02.y, l13.x, l13.y, h02.x, h02.y, h13.x, h13.y};
 }
 
 template <int KS, int STEPS, int MT, int D, int RT, bool TR, typename OutT>
@@ -166,8 +152,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
             }
         }
     }
-    uint32_t one;
-    asm("v_mov_b32 %0, 0x64006400" : "=v"(one));
+    const DequantConsts dq = dequant_consts();
 
 
     // One item: dequantise + MFMA from `buf`, refill `buf` with item `next`
@@ -209,7 +194,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
             for (int t = 0; t < 8; ++t) {
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt) {
-                    const f16x8 a = dequant8(q[rt][t], t < 4 ? d0[rt] : d1[rt], one);
+                    const f16x8 a = dequant8(q[rt][t], t < 4 ? d0[rt] : d1[rt], dq.c1024, dq.c64);
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
                         acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xb[mt][s][t], acc[rt][mt], 0, 0, 0);
