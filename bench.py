@@ -297,16 +297,16 @@ def profile_run(case: LinearCase, stream: Stream, hip: _Hip) -> int:
 
 
 SWEEP = (
-    [("cfg0 decode", 1, 4096, 4096, 0, True, False), ("cfg1 up/gate", 1, 4096, 14336, 1, False, False),
-     ("cfg1 down", 1, 14336, 4096, 1, False, False)]
-    + [(f"cfg2 skinny", m, 4096, n, 2, False, False) for n in (4096, 6144, 14336) for m in (2, 4, 8, 16, 32)]
-    + [("cfg4 prefill", m, 4096, 14336, 4, False, False) for m in (64, 256, 512)]
-    + [("cfg4 gate/up", m, 4096, 14336, 4, False, True) for m in (64, 256, 512)]
+    [("decode", 1, 4096, 4096, 0, True, False), ("mlp up/gate", 1, 4096, 14336, 1, False, False),
+     ("mlp down", 1, 14336, 4096, 1, False, False)]
+    + [("skinny", m, 4096, n, 2, False, False) for n in (4096, 6144, 14336) for m in (2, 4, 8, 16, 32)]
+    + [("prefill", m, 4096, 14336, 4, False, False) for m in (64, 256, 512)]
+    + [("fused gate/up", m, 4096, 14336, 4, False, True) for m in (64, 256, 512)]
 )
 
 
 def run_sweep(stream: Stream, hip: _Hip, steps: int, warmup: int) -> None:
-    print(f"{'case':<14}{'M':>5}{'K':>7}{'N':>7}{'kernel us':>11}{'eager us':>10}{'GB/s':>9}"
+    print(f"{'case':<15}{'M':>5}{'K':>7}{'N':>7}{'kernel us':>11}{'eager us':>10}{'GB/s':>9}"
           f"{'%HBM':>7}{'TFLOP/s':>9}{'%MFMA':>7}", file=sys.stderr)
     for name, m, k, n, workload, uni, gate_up in SWEEP:
         case = LinearCase(m, n, k, workload, x_uniform=uni, gate_up=gate_up)
@@ -314,7 +314,7 @@ def run_sweep(stream: Stream, hip: _Hip, steps: int, warmup: int) -> None:
         us = t["kernel_ms_mean"] * 1e3
         gbs = case.algorithmic_bytes() / (us * 1e-6) / 1e9
         tf = case.flops() / (us * 1e-6) / 1e12
-        print(f"{name:<14}{m:>5}{k:>7}{n:>7}{us:>11.2f}{t['eager_ms_per_step'] * 1e3:>10.2f}{gbs:>9.0f}"
+        print(f"{name:<15}{m:>5}{k:>7}{n:>7}{us:>11.2f}{t['eager_ms_per_step'] * 1e3:>10.2f}{gbs:>9.0f}"
               f"{100 * gbs / HBM_PEAK_GBS:>6.1f}%{tf:>9.1f}{100 * tf / MFMA_F16_PEAK_TFLOPS:>6.1f}%",
               file=sys.stderr, flush=True)
         case.free()
