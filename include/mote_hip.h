@@ -65,6 +65,18 @@ int mote_hip_q4_0_gate_up_silu_f32(const void* input, const void* gate_weights,
                                    uint64_t output_features, uint64_t input_features,
                                    void* stream);
 
+/* [new] Q8_0 weight-only linear, the next format of the path: the reference
+ * decodes Q8_0 in its oracle (crates/mote-reference/src/quantized.rs:191-195,
+ * 34-byte blocks: f16 scale + 32 int8, value v * d) but has no HIP kernel for
+ * it.  Weights are raw GGML Q8_0 bytes [N, K] (2-byte aligned at least);
+ * arguments, outputs and status codes as for the Q4_0 entry points above. */
+int mote_hip_quantized_linear_q8_0_f16(const void* input, const void* weights, void* output,
+                                       uint64_t rows, uint64_t output_features,
+                                       uint64_t input_features, void* stream);
+int mote_hip_quantized_linear_q8_0_f32(const void* input, const void* weights, void* output,
+                                       uint64_t rows, uint64_t output_features,
+                                       uint64_t input_features, void* stream);
+
 /* [new] On-device Q4_0 decode of rows x K elements to f32, bit-identical to
  * dequantize_quantized_row (crates/mote-reference/src/quantized.rs:58-74).
  * Status: null or K % 32 != 0 -> 1; empty -> 0. */
@@ -92,8 +104,12 @@ int mote_q4_0_dispatch_gate_up_silu(void* handle, const void* input, const void*
                                     const void* up_weights, void* output, uint64_t rows,
                                     uint64_t output_features, uint64_t input_features,
                                     int output_f16, void* stream);
-/* Name of the cached variant for a problem (gate_up_op: 0 linear, 1 gate/up);
- * hipErrorNotFound (500) when the problem has not run yet. */
+/* The Q8_0 linear through the same context (its own plans and variants). */
+int mote_q4_0_dispatch_linear_q8_0(void* handle, const void* input, const void* weights,
+                                   void* output, uint64_t rows, uint64_t output_features,
+                                   uint64_t input_features, int output_f16, void* stream);
+/* Name of the cached variant for a problem (gate_up_op: 0 linear, 1 gate/up,
+ * 2 Q8_0 linear); hipErrorNotFound (500) when the problem has not run yet. */
 int mote_q4_0_dispatch_plan(void* handle, uint64_t rows, uint64_t output_features,
                             uint64_t input_features, int gate_up_op, int output_f16,
                             char* name, size_t capacity);

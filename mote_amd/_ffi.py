@@ -48,6 +48,8 @@ SIGNATURES = {
     "mote_hip_mem_get_info": (_I, [ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
     "mote_hip_quantized_linear_q4_0_f16": (_I, [_P, _P, _P, _U64, _U64, _U64, _P]),
     "mote_hip_quantized_linear_q4_0_f32": (_I, [_P, _P, _P, _U64, _U64, _U64, _P]),
+    "mote_hip_quantized_linear_q8_0_f16": (_I, [_P, _P, _P, _U64, _U64, _U64, _P]),
+    "mote_hip_quantized_linear_q8_0_f32": (_I, [_P, _P, _P, _U64, _U64, _U64, _P]),
     "mote_hip_q4_0_gate_up_silu_f32": (_I, [_P, _P, _P, _P, _U64, _U64, _U64, _P]),
     "mote_hip_dequantize_q4_0_f32": (_I, [_P, _P, _U64, _U64, _P]),
     "mote_q4_0_dispatch_create": (_I, [ctypes.POINTER(_P)]),
@@ -56,6 +58,7 @@ SIGNATURES = {
     "mote_q4_0_dispatch_set_autotune": (_I, [_P, _I]),
     "mote_q4_0_dispatch_force_variant": (_I, [_P, ctypes.c_char_p]),
     "mote_q4_0_dispatch_linear": (_I, [_P, _P, _P, _P, _U64, _U64, _U64, _I, _P]),
+    "mote_q4_0_dispatch_linear_q8_0": (_I, [_P, _P, _P, _P, _U64, _U64, _U64, _I, _P]),
     "mote_q4_0_dispatch_gate_up_silu": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _U64, _I, _P]),
     "mote_q4_0_dispatch_plan": (_I, [_P, _U64, _U64, _U64, _I, _I, ctypes.c_char_p, _SZ]),
     "mote_q4_0_variant_count": (_I, []),

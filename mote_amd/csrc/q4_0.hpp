@@ -12,7 +12,7 @@ enum class OutType : int { F32 = 0, F16 = 1 };
 
 struct Problem {
     const void* x;        // f16 [M, K]
-    const void* w;        // Q4_0 [N, K]  (gate rows for the fused op)
+    const void* w;        // Q4_0 [N, K] (Q8_0 for the Q8_0 linear; gate rows for the fused op)
     const void* w_up;     // Q4_0 [N, K]  up rows, fused gate/up only (else null)
     void* y;              // [M, N] f32 or f16
     uint32_t M, N, K;
@@ -21,7 +21,7 @@ struct Problem {
 };
 
 enum class Kind : int { Gemv = 0, Mfma = 1, Generic = 2, GateUpMfma = 3, GateUpGeneric = 4, GemvRows = 5,
-                        GemvStream = 6, SkinnyMfma = 7 };
+                        GemvStream = 6, SkinnyMfma = 7, Q8Stream = 8, Q8Generic = 9 };
 
 struct Variant {
     const char* name;

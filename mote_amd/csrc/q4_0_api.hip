@@ -33,7 +33,7 @@
 namespace mote::q4_0 {
 namespace {
 
-enum class Op : int { Linear = 0, GateUp = 1 };
+enum class Op : int { Linear = 0, GateUp = 1, LinearQ8 = 2 };
 
 struct Key {
     uint32_t m, n, k;
@@ -70,6 +70,7 @@ const Variant* find_variant(const std::string& name) {
 
 bool kind_matches(const Variant& v, Op op) {
     if (op == Op::GateUp) return v.kind == Kind::GateUpMfma || v.kind == Kind::GateUpGeneric;
+    if (op == Op::LinearQ8) return v.kind == Kind::Q8Stream || v.kind == Kind::Q8Generic;
     return v.kind == Kind::Gemv || v.kind == Kind::GemvRows || v.kind == Kind::GemvStream ||
            v.kind == Kind::SkinnyMfma || v.kind == Kind::Mfma || v.kind == Kind::Generic;
 }
@@ -78,7 +79,8 @@ bool supports(const Variant& v, const Problem& p) {
     switch (v.kind) {
         case Kind::Gemv: return gemv_supports(v, p);
         case Kind::GemvRows: return gemv_rows_supports(v, p);
-        case Kind::GemvStream: return gemv_stream_supports(v, p);
+        case Kind::GemvStream:
+        case Kind::Q8Stream: return gemv_stream_supports(v, p);
         case Kind::SkinnyMfma: return skinny_mfma_supports(v, p);
         case Kind::Mfma:
         case Kind::GateUpMfma: return mfma_supports(v, p);
@@ -101,7 +103,7 @@ std::vector<const Variant*> candidates(const Problem& p, Op op) {
         const bool generic = v->kind == Kind::Generic || v->kind == Kind::GateUpGeneric;
         if (generic && fast_eligible(p)) continue;
         const bool vector_alu = v->kind == Kind::Gemv || v->kind == Kind::GemvRows ||
-                                v->kind == Kind::GemvStream;
+                                v->kind == Kind::GemvStream || v->kind == Kind::Q8Stream;
         if (vector_alu && p.M >= 64) continue;
         if (v->kind == Kind::SkinnyMfma && p.M > 64) continue;
         if ((v->kind == Kind::Mfma || v->kind == Kind::GateUpMfma) && p.M < 64) continue;
@@ -129,6 +131,26 @@ const Variant* by_name(const char* name) {
 // Shape heuristic used when autotuning is off.
 const Variant* heuristic(const Problem& p, Op op) {
     const bool fast = fast_eligible(p);
+    if (op == Op::LinearQ8) {
+        // The streaming GEMV over Q8_0 pairs for 1, 2 or 4 tokens (rows split
+        // over S waves above K = 4096; one workgroup per CU measured fastest
+        // for Q8_0's 68-byte pairs at every Llama shape), the generic kernel
+        // otherwise.
+        if (fast && (p.M == 1 || p.M == 2 || p.M == 4)) {
+            uint32_t split = 1;
+            while (split < 4 && p.K > 4096u * split) split *= 2;
+            char name[32];
+            if (p.M > 1)
+                std::snprintf(name, sizeof name, "q8_stream_m%u_d1q_g1", p.M);
+            else if (split == 1)
+                std::snprintf(name, sizeof name, "q8_stream_d1_g1");
+            else
+                std::snprintf(name, sizeof name, "q8_stream_s%u_d1_g1", split);
+            const Variant* v = by_name(name);
+            if (v && gemv_stream_supports(*v, p)) return v;
+        }
+        return by_name("q8_generic");
+    }
     if (op == Op::GateUp) {
         // Raw Q4_0 weights staged in LDS (measured on MI355X at N = 14336,
         // K = 4096: 1.4x-1.8x faster than dequantised f16 weight tiles).
@@ -297,14 +319,14 @@ int check_linear(const void* input, const void* weights, const void* output, uin
 }
 
 int linear(Dispatcher* d, const void* input, const void* weights, void* output, uint64_t rows,
-           uint64_t n, uint64_t k, OutType out, void* stream) {
+           uint64_t n, uint64_t k, OutType out, void* stream, Op op = Op::Linear) {
     const int pre = check_linear(input, weights, output, rows, n, k, stream);
-    if (pre >= 0) return pre == 0 ? 0 : fail(d, static_cast<hipError_t>(pre), "invalid Q4_0 linear arguments");
+    if (pre >= 0) return pre == 0 ? 0 : fail(d, static_cast<hipError_t>(pre), "invalid quantized linear arguments");
     const auto s = static_cast<hipStream_t>(stream);
     if (k == 0) return static_cast<int>(launch_zero_fill(output, rows * n, out, s));
     const Problem p{input, weights, nullptr, output, static_cast<uint32_t>(rows),
                     static_cast<uint32_t>(n), static_cast<uint32_t>(k), out, s};
-    return run(d ? *d : default_dispatcher(), p, Op::Linear);
+    return run(d ? *d : default_dispatcher(), p, op);
 }
 
 int gate_up(Dispatcher* d, const void* input, const void* gate, const void* up, void* output,
@@ -343,6 +365,30 @@ MOTE_EXPORT int mote_hip_quantized_linear_q4_0_f32(const void* input, const void
     try {
         return linear(nullptr, input, weights, output, rows, output_features, input_features,
                       OutType::F32, stream);
+    } catch (...) {
+        return hipErrorUnknown;
+    }
+}
+
+MOTE_EXPORT int mote_hip_quantized_linear_q8_0_f16(const void* input, const void* weights,
+                                                  void* output, uint64_t rows,
+                                                  uint64_t output_features,
+                                                  uint64_t input_features, void* stream) noexcept {
+    try {
+        return linear(nullptr, input, weights, output, rows, output_features, input_features,
+                      OutType::F16, stream, Op::LinearQ8);
+    } catch (...) {
+        return hipErrorUnknown;
+    }
+}
+
+MOTE_EXPORT int mote_hip_quantized_linear_q8_0_f32(const void* input, const void* weights,
+                                                  void* output, uint64_t rows,
+                                                  uint64_t output_features,
+                                                  uint64_t input_features, void* stream) noexcept {
+    try {
+        return linear(nullptr, input, weights, output, rows, output_features, input_features,
+                      OutType::F32, stream, Op::LinearQ8);
     } catch (...) {
         return hipErrorUnknown;
     }
@@ -423,6 +469,20 @@ MOTE_EXPORT int mote_q4_0_dispatch_linear(void* handle, const void* input, const
     try {
         return linear(d, input, weights, output, rows, output_features, input_features,
                       output_f16 ? OutType::F16 : OutType::F32, stream);
+    } catch (...) {
+        return fail(d, hipErrorUnknown, "unexpected C++ exception");
+    }
+}
+
+MOTE_EXPORT int mote_q4_0_dispatch_linear_q8_0(void* handle, const void* input, const void* weights,
+                                              void* output, uint64_t rows, uint64_t output_features,
+                                              uint64_t input_features, int output_f16,
+                                              void* stream) noexcept {
+    auto* d = static_cast<mote::q4_0::Dispatcher*>(handle);
+    if (!d) return hipErrorInvalidValue;
+    try {
+        return linear(d, input, weights, output, rows, output_features, input_features,
+                      output_f16 ? OutType::F16 : OutType::F32, stream, Op::LinearQ8);
     } catch (...) {
         return fail(d, hipErrorUnknown, "unexpected C++ exception");
     }

@@ -1,26 +1,29 @@
-// Q4_0 decode GEMV (M = 1) for gfx950: persistent, software-pipelined waves.
+// Decode GEMV (M = 1, and 2-4 tokens) for gfx950 over GGML Q4_0 and Q8_0
+// weights: persistent, software-pipelined waves.
 //
-// Computes y[n] = sum_k x[k] * w[n, k] for f16 x [K] and GGML Q4_0 w [N, K]
-// (K <= 4096), the operation of crates/mote-backend-hip/src/
+// Computes y[m, n] = sum_k x[m, k] * w[n, k] for f16 x [M, K] and quantized
+// w [N, K], the operation of crates/mote-backend-hip/src/
 // quantized_linear.hip:13-52 (oracle crates/mote-reference/src/
-// quantized.rs:89-144) at rows == 1.
+// quantized.rs:89-144; Q8_0 decode at :191-195).
 //
-// The grid is G workgroups of 8 waves per CU.  Lane l owns block pairs l,
-// l + 64, ..., l + 64 (P - 1) (64 elements, 36 bytes each) of every row, so
-// K <= 4096 P; wave g of the grid walks rows g, g + W, g + 2W, ... (W waves
-// in the grid), so at any moment the waves of the whole chip read
-// neighbouring rows and the request front sweeps the matrix once, in order.
-// Each wave issues the loads of row j + D before it computes row j, so D rows
-// are in flight behind the nibble arithmetic instead of the arithmetic
-// piling up after the last byte arrives.  D = 1 measures fastest: a deeper
-// front spreads the chip's outstanding requests over more of the matrix and
-// lowers the achieved HBM rate, also for a pure read of the same pattern.
+// The grid is G workgroups of 8 waves per CU.  A row group of S waves owns
+// one row at a time; lane l of slice s owns block pairs s*span + l + 64 i
+// (i < P, 64 elements each) of the row, so K <= 4096 P S.  Row group g walks
+// rows g, g + T, g + 2T, ... (T groups in the grid), so at any moment the
+// waves of the whole chip read neighbouring rows and the request front
+// sweeps the matrix once, in order.  Each wave issues the loads of row j + D
+// before it computes row j, so D rows are in flight behind the arithmetic
+// instead of the arithmetic piling up after the last byte arrives.  D = 1
+// measures fastest: a deeper front spreads the chip's outstanding requests
+// over more of the matrix and lowers the achieved HBM rate, also for a pure
+// read of the same pattern.
 //
 // x is staged once per workgroup through LDS (coalesced 16-byte loads, one
 // 144-byte slot per 128-byte pair chunk so the per-lane reads hit distinct
-// banks) and kept in registers, permuted into the nibble-unpack order; the
-// nibbles are multiplied as binary16 subnormals (pair_dot), then a DPP wave
-// sum and an exact rescale by 2^20.
+// banks) and kept in registers, permuted into the order the weight operands
+// take it; the quantized values are multiplied as binary16 subnormals (the
+// format policies FmtQ4 and FmtQ8 below), then a DPP wave sum and an exact
+// power-of-two rescale.
 #include "common.hpp"
 #include "q4_0.hpp"
 
@@ -32,7 +35,6 @@ constexpr int kStreamThreads = kStreamWaves * kWave;
 constexpr uint32_t kSlot = 144;
 constexpr uint32_t kSubLo = 0x000F000Fu;  // low nibbles of bytes 0 and 2: n * 2^-24
 constexpr uint32_t kSubHi = 0x00F000F0u;  // high nibbles of bytes 0 and 2: n * 2^-20
-constexpr float kTwo20 = 1048576.0f;
 
 __device__ __forceinline__ uint32_t pick(const uint32_t* x, int a, int b) {
     const uint32_t lo = (a & 1) ? 0x0302u : 0x0100u;
@@ -42,88 +44,192 @@ __device__ __forceinline__ uint32_t pick(const uint32_t* x, int a, int b) {
 
 struct XPair {
     uint32_t xp[32];
-    float c0, c1;  // -8 * 2^-20 * (sum of the block's 32 activations)
+    float c0, c1;  // start values of the two blocks' sums (format's kStart times sum of x)
 };
 
-// sum_k x_k (n_k - 8) d of the two blocks of a pair, divided by 2^20.
-//
-// Nibbles are read as binary16 subnormals, with no carrier term and no shift
-// for bytes 0 and 2 of a dword: q & 0x000F000F holds (n_b0, n_b2) * 2^-24 and
-// q & 0x00F000F0 holds (n_b0, n_b2) * 2^-20 (the high nibbles); bytes 1 and 3
-// take one shift by 8.  Each such value times an f16 activation is exact in
-// f32 (v_dot2_f32_f16 honours f16 subnormals: the kernels run with f16
-// denormals enabled), so per block
-//   sum x (n - 8) = 2^20 (16 a_lo + a_hi)   with a_hi started at -8 * 2^-20 sum x,
-// five VALU operations per nibble dword instead of a mask, shift and OR per
-// nibble pair.
-// The 32 masked nibble operands of a pair, in the order of XPair::xp, and
-// the two block scales; shared by every token of a row.
+// Operands of a pair unpacked once and shared by every token of a row.
 struct Unpacked {
     uint32_t u[32];
     float d0, d1;
 };
 
-__device__ __forceinline__ void pair_unpack(const uint32_t (&raw)[9], Unpacked& o) {
-    uint32_t q[8];
-    q[0] = pair_q0(raw);
-    q[1] = raw[1]; q[2] = raw[2]; q[3] = raw[3];
-    q[4] = raw[5]; q[5] = raw[6]; q[6] = raw[7]; q[7] = raw[8];
-    o.d0 = half_lo_to_float(raw[0]);
-    o.d1 = half_hi_to_float(raw[4]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t a = q[i], a8 = a >> 8;
-        o.u[4 * i + 0] = a & kSubHi;
-        o.u[4 * i + 1] = a & kSubLo;
-        o.u[4 * i + 2] = a8 & kSubLo;
-        o.u[4 * i + 3] = a8 & kSubHi;
-    }
-}
+// ---------------------------------------------------------------------------
+// GGML Q4_0: a pair is two 18-byte blocks (36 bytes, 9 dwords), value
+// (n - 8) d.  Nibbles are read as binary16 subnormals, with no carrier term
+// and no shift for bytes 0 and 2 of a dword: q & 0x000F000F holds (n_b0,
+// n_b2) * 2^-24 and q & 0x00F000F0 holds (n_b0, n_b2) * 2^-20 (the high
+// nibbles); bytes 1 and 3 take one shift by 8.  Each such value times an f16
+// activation is exact in f32 (v_dot2_f32_f16 honours f16 subnormals: the
+// kernels run with f16 denormals enabled), so per block
+//   sum x (n - 8) = 2^20 (16 a_lo + a_hi)   with a_hi started at -8 * 2^-20 sum x,
+// five VALU operations per nibble dword instead of a mask, shift and OR per
+// nibble pair.
+// ---------------------------------------------------------------------------
+struct FmtQ4 {
+    static constexpr uint32_t kPairBytes = 36;
+    static constexpr int kDwords = 9;
+    static constexpr float kFinal = 1048576.0f;           // 2^20
+    static constexpr float kStart = -8.0f / 1048576.0f;   // times the block's sum of x
 
-__device__ __forceinline__ float pair_dot(const uint32_t (&raw)[9], const XPair& x) {
-    uint32_t q[8];
-    q[0] = pair_q0(raw);
-    q[1] = raw[1]; q[2] = raw[2]; q[3] = raw[3];
-    q[4] = raw[5]; q[5] = raw[6]; q[6] = raw[7]; q[7] = raw[8];
-    const float d0 = half_lo_to_float(raw[0]);
-    const float d1 = half_hi_to_float(raw[4]);
-    float lo0 = 0.0f, hi0 = x.c0, lo1 = 0.0f, hi1 = x.c1;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t a = q[i], b = q[4 + i];
-        const uint32_t a8 = a >> 8, b8 = b >> 8;
-        hi0 = dot2(a & kSubHi, x.xp[4 * i + 0], hi0);
-        lo0 = dot2(a & kSubLo, x.xp[4 * i + 1], lo0);
-        lo0 = dot2(a8 & kSubLo, x.xp[4 * i + 2], lo0);
-        hi0 = dot2(a8 & kSubHi, x.xp[4 * i + 3], hi0);
-        hi1 = dot2(b & kSubHi, x.xp[16 + 4 * i + 0], hi1);
-        lo1 = dot2(b & kSubLo, x.xp[16 + 4 * i + 1], lo1);
-        lo1 = dot2(b8 & kSubLo, x.xp[16 + 4 * i + 2], lo1);
-        hi1 = dot2(b8 & kSubHi, x.xp[16 + 4 * i + 3], hi1);
-    }
-    const float acc = d0 * __builtin_fmaf(lo0, 16.0f, hi0);
-    return __builtin_fmaf(d1, __builtin_fmaf(lo1, 16.0f, hi1), acc);
-}
+    __device__ static void load(const uint8_t* p, uint32_t (&d)[kDwords]) { load_pair(p, d); }
 
-// The same sum from operands unpacked once for several tokens.
-__device__ __forceinline__ float pair_dot(const Unpacked& w, const XPair& x) {
-    float lo0 = 0.0f, hi0 = x.c0, lo1 = 0.0f, hi1 = x.c1;
+    // x of the pair (64 halves in xr) in the order the nibble operands take it.
+    __device__ static void order_x(const uint32_t (&xr)[32], XPair& xv) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        hi0 = dot2(w.u[4 * i + 0], x.xp[4 * i + 0], hi0);
-        lo0 = dot2(w.u[4 * i + 1], x.xp[4 * i + 1], lo0);
-        lo0 = dot2(w.u[4 * i + 2], x.xp[4 * i + 2], lo0);
-        hi0 = dot2(w.u[4 * i + 3], x.xp[4 * i + 3], hi0);
-        hi1 = dot2(w.u[16 + 4 * i + 0], x.xp[16 + 4 * i + 0], hi1);
-        lo1 = dot2(w.u[16 + 4 * i + 1], x.xp[16 + 4 * i + 1], lo1);
-        lo1 = dot2(w.u[16 + 4 * i + 2], x.xp[16 + 4 * i + 2], lo1);
-        hi1 = dot2(w.u[16 + 4 * i + 3], x.xp[16 + 4 * i + 3], hi1);
+        for (int q = 0; q < 8; ++q) {
+            const int base = (q < 4) ? 0 : 32;
+            const int e0 = base + pair_byte_element(q, 0);
+            const int e1 = base + pair_byte_element(q, 1);
+            const int e2 = base + pair_byte_element(q, 2);
+            const int e3 = base + pair_byte_element(q, 3);
+            xv.xp[4 * q + 0] = pick(xr, e0 + 16, e2 + 16);  // hi02
+            xv.xp[4 * q + 1] = pick(xr, e0, e2);            // lo02
+            xv.xp[4 * q + 2] = pick(xr, e1, e3);            // lo13
+            xv.xp[4 * q + 3] = pick(xr, e1 + 16, e3 + 16);  // hi13
+        }
     }
-    const float acc = w.d0 * __builtin_fmaf(lo0, 16.0f, hi0);
-    return __builtin_fmaf(w.d1, __builtin_fmaf(lo1, 16.0f, hi1), acc);
-}
 
-template <int P, int S, int D, int MT, bool LAG, typename OutT>
+    // sum_k x_k (n_k - 8) d of the two blocks of a pair, divided by 2^20.
+    __device__ static float dot(const uint32_t (&raw)[kDwords], const XPair& x) {
+        uint32_t q[8];
+        q[0] = pair_q0(raw);
+        q[1] = raw[1]; q[2] = raw[2]; q[3] = raw[3];
+        q[4] = raw[5]; q[5] = raw[6]; q[6] = raw[7]; q[7] = raw[8];
+        const float d0 = half_lo_to_float(raw[0]);
+        const float d1 = half_hi_to_float(raw[4]);
+        float lo0 = 0.0f, hi0 = x.c0, lo1 = 0.0f, hi1 = x.c1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t a = q[i], b = q[4 + i];
+            const uint32_t a8 = a >> 8, b8 = b >> 8;
+            hi0 = dot2(a & kSubHi, x.xp[4 * i + 0], hi0);
+            lo0 = dot2(a & kSubLo, x.xp[4 * i + 1], lo0);
+            lo0 = dot2(a8 & kSubLo, x.xp[4 * i + 2], lo0);
+            hi0 = dot2(a8 & kSubHi, x.xp[4 * i + 3], hi0);
+            hi1 = dot2(b & kSubHi, x.xp[16 + 4 * i + 0], hi1);
+            lo1 = dot2(b & kSubLo, x.xp[16 + 4 * i + 1], lo1);
+            lo1 = dot2(b8 & kSubLo, x.xp[16 + 4 * i + 2], lo1);
+            hi1 = dot2(b8 & kSubHi, x.xp[16 + 4 * i + 3], hi1);
+        }
+        const float acc = d0 * __builtin_fmaf(lo0, 16.0f, hi0);
+        return __builtin_fmaf(d1, __builtin_fmaf(lo1, 16.0f, hi1), acc);
+    }
+
+    // The 32 masked nibble operands in the order of XPair::xp, and the scales.
+    __device__ static void unpack(const uint32_t (&raw)[kDwords], Unpacked& o) {
+        uint32_t q[8];
+        q[0] = pair_q0(raw);
+        q[1] = raw[1]; q[2] = raw[2]; q[3] = raw[3];
+        q[4] = raw[5]; q[5] = raw[6]; q[6] = raw[7]; q[7] = raw[8];
+        o.d0 = half_lo_to_float(raw[0]);
+        o.d1 = half_hi_to_float(raw[4]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t a = q[i], a8 = a >> 8;
+            o.u[4 * i + 0] = a & kSubHi;
+            o.u[4 * i + 1] = a & kSubLo;
+            o.u[4 * i + 2] = a8 & kSubLo;
+            o.u[4 * i + 3] = a8 & kSubHi;
+        }
+    }
+
+    __device__ static float dot(const Unpacked& w, const XPair& x) {
+        float lo0 = 0.0f, hi0 = x.c0, lo1 = 0.0f, hi1 = x.c1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            hi0 = dot2(w.u[4 * i + 0], x.xp[4 * i + 0], hi0);
+            lo0 = dot2(w.u[4 * i + 1], x.xp[4 * i + 1], lo0);
+            lo0 = dot2(w.u[4 * i + 2], x.xp[4 * i + 2], lo0);
+            hi0 = dot2(w.u[4 * i + 3], x.xp[4 * i + 3], hi0);
+            hi1 = dot2(w.u[16 + 4 * i + 0], x.xp[16 + 4 * i + 0], hi1);
+            lo1 = dot2(w.u[16 + 4 * i + 1], x.xp[16 + 4 * i + 1], lo1);
+            lo1 = dot2(w.u[16 + 4 * i + 2], x.xp[16 + 4 * i + 2], lo1);
+            hi1 = dot2(w.u[16 + 4 * i + 3], x.xp[16 + 4 * i + 3], hi1);
+        }
+        const float acc = w.d0 * __builtin_fmaf(lo0, 16.0f, hi0);
+        return __builtin_fmaf(w.d1, __builtin_fmaf(lo1, 16.0f, hi1), acc);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// GGML Q8_0 (crates/mote-reference/src/quantized.rs:191-195): a block is an
+// f16 scale d and 32 two's-complement bytes, value v d; a pair is 68 bytes
+// (17 dwords, dword aligned whenever the row is).  Block 0's bytes start at
+// pair byte 2, so its dwords are re-aligned with one v_perm each.  XOR 0x80
+// turns every byte into u = v + 128; u & 0x00FF00FF read as binary16 is
+// (u_b0, u_b2) * 2^-24 exactly (a subnormal), and one shift by 8 gives bytes
+// 1 and 3: each product with an f16 activation is exact in f32, so per block
+//   sum x v = 2^24 a   with a started at -128 * 2^-24 sum x.
+// ---------------------------------------------------------------------------
+struct FmtQ8 {
+    static constexpr uint32_t kPairBytes = 68;
+    static constexpr int kDwords = 17;
+    static constexpr float kFinal = 16777216.0f;            // 2^24
+    static constexpr float kStart = -128.0f / 16777216.0f;  // times the block's sum of x
+
+    __device__ static void load(const uint8_t* p, uint32_t (&d)[kDwords]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4_a4 v = *reinterpret_cast<const u32x4_a4*>(p + 16 * i);
+            d[4 * i + 0] = v.x; d[4 * i + 1] = v.y; d[4 * i + 2] = v.z; d[4 * i + 3] = v.w;
+        }
+        d[16] = *reinterpret_cast<const uint32_t*>(p + 64);
+    }
+
+    // Dword i of the pair's 64 bytes (elements 4i .. 4i + 3) takes x as
+    // (x[4i], x[4i + 2]) for bytes 0 and 2 and (x[4i + 1], x[4i + 3]) for 1, 3.
+    __device__ static void order_x(const uint32_t (&xr)[32], XPair& xv) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            xv.xp[2 * i + 0] = pick(xr, 4 * i, 4 * i + 2);
+            xv.xp[2 * i + 1] = pick(xr, 4 * i + 1, 4 * i + 3);
+        }
+    }
+
+    __device__ static uint32_t bytes(const uint32_t (&raw)[kDwords], int i) {
+        // block 0: pair bytes 2 + 4i .. 5 + 4i; block 1: dwords 9 .. 16
+        return i < 8 ? __builtin_amdgcn_perm(raw[i + 1], raw[i], 0x05040302u) : raw[i + 1];
+    }
+
+    __device__ static float dot(const uint32_t (&raw)[kDwords], const XPair& x) {
+        float a0 = x.c0, a1 = x.c1;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t u = bytes(raw, i) ^ 0x80808080u;
+            const uint32_t w = bytes(raw, 8 + i) ^ 0x80808080u;
+            a0 = dot2(u & 0x00FF00FFu, x.xp[2 * i + 0], a0);
+            a0 = dot2((u >> 8) & 0x00FF00FFu, x.xp[2 * i + 1], a0);
+            a1 = dot2(w & 0x00FF00FFu, x.xp[16 + 2 * i + 0], a1);
+            a1 = dot2((w >> 8) & 0x00FF00FFu, x.xp[16 + 2 * i + 1], a1);
+        }
+        const float d0 = half_lo_to_float(raw[0]);
+        const float d1 = half_hi_to_float(raw[8]);
+        return __builtin_fmaf(d1, a1, d0 * a0);
+    }
+
+    __device__ static void unpack(const uint32_t (&raw)[kDwords], Unpacked& o) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t u = bytes(raw, i) ^ 0x80808080u;
+            o.u[2 * i + 0] = u & 0x00FF00FFu;
+            o.u[2 * i + 1] = (u >> 8) & 0x00FF00FFu;
+        }
+        o.d0 = half_lo_to_float(raw[0]);
+        o.d1 = half_hi_to_float(raw[8]);
+    }
+
+    __device__ static float dot(const Unpacked& w, const XPair& x) {
+        float a0 = x.c0, a1 = x.c1;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            a0 = dot2(w.u[i], x.xp[i], a0);
+            a1 = dot2(w.u[16 + i], x.xp[16 + i], a1);
+        }
+        return __builtin_fmaf(w.d1, a1, w.d0 * a0);
+    }
+};
+
+template <class F, int P, int S, int D, int MT, bool LAG, typename OutT>
 __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint16_t* __restrict__ x,
                                                                      const uint8_t* __restrict__ w,
                                                                      OutT* __restrict__ y, uint32_t N,
@@ -135,7 +241,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
     const int lane = tid & 63;
     const int slice = wave % S;
     const uint32_t npairs = K >> 6;
-    const size_t row_bytes = static_cast<size_t>(npairs) * kPairBytes;
+    const size_t row_bytes = static_cast<size_t>(npairs) * F::kPairBytes;
     // The S waves of a row group split each row into S slices of `span`
     // pairs; lane l of slice s owns pairs s*span + l + 64i (i < P).  Idle
     // slots are clamped to the last pair (a cached re-read) and dropped.
@@ -159,10 +265,10 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
     // largest); the others compute clamped rows and store nothing.
     const uint32_t g0 = blockIdx.x * kGroups;
     const uint32_t trips = S == 1 ? nrows : (g0 < N ? (N - 1 - g0) / total_groups + 1 : 0);
-    auto load_row = [&](uint32_t jj, uint32_t (&b)[P][9]) {
+    auto load_row = [&](uint32_t jj, uint32_t (&b)[P][F::kDwords]) {
         const uint8_t* row = w + static_cast<size_t>(min(g + jj * total_groups, last)) * row_bytes;
 #pragma unroll
-        for (int i = 0; i < P; ++i) load_pair(row + static_cast<size_t>(pc[i]) * kPairBytes, b[i]);
+        for (int i = 0; i < P; ++i) F::load(row + static_cast<size_t>(pc[i]) * F::kPairBytes, b[i]);
     };
 
     // x chunk loads first (P S MT 16-byte chunks per thread; chunk c of the
@@ -184,7 +290,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
     // wave then waits for row j + 1 before issuing more; without it, D + 1
     // rows are in flight while it waits).
     constexpr int R = D + 1;
-    uint32_t buf[R][P][9];
+    uint32_t buf[R][P][F::kDwords];
 #pragma unroll
     for (int d = 0; d < D; ++d) load_row(static_cast<uint32_t>(d), buf[d]);
     __builtin_amdgcn_sched_barrier(0);
@@ -211,20 +317,9 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
             s0 = dot2(xr[i], kOnePair, s0);
             s1 = dot2(xr[16 + i], kOnePair, s1);
         }
-        xv[m][s].c0 = (-8.0f / kTwo20) * s0;
-        xv[m][s].c1 = (-8.0f / kTwo20) * s1;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int base = (q < 4) ? 0 : 32;
-            const int e0 = base + pair_byte_element(q, 0);
-            const int e1 = base + pair_byte_element(q, 1);
-            const int e2 = base + pair_byte_element(q, 2);
-            const int e3 = base + pair_byte_element(q, 3);
-            xv[m][s].xp[4 * q + 0] = pick(xr, e0 + 16, e2 + 16);  // hi02
-            xv[m][s].xp[4 * q + 1] = pick(xr, e0, e2);            // lo02
-            xv[m][s].xp[4 * q + 2] = pick(xr, e1, e3);            // lo13
-            xv[m][s].xp[4 * q + 3] = pick(xr, e1 + 16, e3 + 16);  // hi13
-        }
+        xv[m][s].c0 = F::kStart * s0;
+        xv[m][s].c1 = F::kStart * s1;
+        F::order_x(xr, xv[m][s]);
     }
 
     // Row sums stay in registers (lane j % 64 holds row j of this wave) and
@@ -249,7 +344,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
             }
             if (slice == 0 && static_cast<uint32_t>(lane) < count)
                 y[static_cast<size_t>(m) * N + g + (first + static_cast<uint32_t>(lane)) * total_groups] =
-                    to_out<OutT>(kTwo20 * t);
+                    to_out<OutT>(F::kFinal * t);
         }
     };
     float mine[MT];
@@ -268,13 +363,13 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
 #pragma unroll
             for (int i = 0; i < P; ++i) {
                 if constexpr (MT == 1) {  // masks feed the dot chains directly: fewer live registers
-                    part[0] += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pair_dot(buf[u][i], xv[0][i])) & keep[i]);
+                    part[0] += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, F::dot(buf[u][i], xv[0][i])) & keep[i]);
                 } else {
                     Unpacked wu;
-                    pair_unpack(buf[u][i], wu);
+                    F::unpack(buf[u][i], wu);
 #pragma unroll
                     for (int m = 0; m < MT; ++m)
-                        part[m] += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pair_dot(wu, xv[m][i])) & keep[i]);
+                        part[m] += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, F::dot(wu, xv[m][i])) & keep[i]);
                 }
             }
             const bool mine_lane = jj < trips && static_cast<uint32_t>(lane) == (jj & 63u);
@@ -298,7 +393,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
     if (base < trips) flush(mine, base, nrows > base ? nrows - base : 0u);
 }
 
-template <int P, int S, int D, int G, int MT = 1, bool LAG = true>
+template <int P, int S, int D, int G, int MT = 1, bool LAG = true, class F = FmtQ4>
 hipError_t launch_gemv_stream(const Problem& p) {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -315,11 +410,11 @@ hipError_t launch_gemv_stream(const Problem& p) {
     const size_t lds = static_cast<size_t>(p.K / 64) * MT * kSlot + (S > 1 ? kStreamThreads * sizeof(float) : 0);
     const dim3 grid(groups), block(kStreamThreads);
     if (p.out == OutType::F32) {
-        hipLaunchKernelGGL((gemv_stream_kernel<P, S, D, MT, LAG, float>), grid, block, lds, p.stream,
+        hipLaunchKernelGGL((gemv_stream_kernel<F, P, S, D, MT, LAG, float>), grid, block, lds, p.stream,
                            static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<float*>(p.y), p.N, p.K, total_groups);
     } else {
-        hipLaunchKernelGGL((gemv_stream_kernel<P, S, D, MT, LAG, _Float16>), grid, block, lds, p.stream,
+        hipLaunchKernelGGL((gemv_stream_kernel<F, P, S, D, MT, LAG, _Float16>), grid, block, lds, p.stream,
                            static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<_Float16*>(p.y), p.N, p.K, total_groups);
     }
@@ -342,6 +437,11 @@ hipError_t launch_gemv_stream(const Problem& p) {
 #define MOTE_STREAM_M(MT, D, G)                                                          \
     Variant{"stream_m" #MT "_d" #D "_g" #G, Kind::GemvStream, 1, D, G,                  \
             &launch_gemv_stream<1, 1, D, G, MT>, MT}
+#define MOTE_Q8(NAME, S, G) \
+    Variant{"q8_stream_" NAME, Kind::Q8Stream, S, 1, G, &launch_gemv_stream<1, S, 1, G, 1, true, FmtQ8>}
+#define MOTE_Q8_M(MT, G)                                                             \
+    Variant{"q8_stream_m" #MT "_d1q_g" #G, Kind::Q8Stream, 1, 1, G,                \
+            &launch_gemv_stream<1, 1, 1, G, MT, false, FmtQ8>, MT}
 #define MOTE_STREAM_MQ(MT, D, G)                                                         \
     Variant{"stream_m" #MT "_d" #D "q_g" #G, Kind::GemvStream, 1, D, G,                 \
             &launch_gemv_stream<1, 1, D, G, MT, false>, MT}
@@ -357,6 +457,8 @@ const Variant kStream[] = {
     MOTE_STREAM_S(4, 2, 2), MOTE_STREAM_SQ(4, 1, 2), MOTE_STREAM_SQ(2, 1, 2), MOTE_STREAM_SQ(4, 1, 1),
     MOTE_STREAM_M(2, 1, 1), MOTE_STREAM_M(3, 1, 1), MOTE_STREAM_M(4, 1, 1),
     MOTE_STREAM_MQ(2, 1, 1), MOTE_STREAM_MQ(2, 1, 2),
+    MOTE_Q8("d1_g1", 1, 1), MOTE_Q8("d1_g2", 1, 2), MOTE_Q8("s2_d1_g1", 2, 1), MOTE_Q8("s2_d1_g2", 2, 2),
+    MOTE_Q8("s4_d1_g1", 4, 1), MOTE_Q8("s4_d1_g2", 4, 2), MOTE_Q8_M(2, 1), MOTE_Q8_M(4, 1),
 };
 
 #undef MOTE_STREAM
@@ -366,6 +468,8 @@ const Variant kStream[] = {
 #undef MOTE_STREAM_Q
 #undef MOTE_STREAM_SQ
 #undef MOTE_STREAM_MQ
+#undef MOTE_Q8
+#undef MOTE_Q8_M
 
 }  // namespace
 

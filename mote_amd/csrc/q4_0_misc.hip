@@ -1,6 +1,7 @@
 // Q4_0 support kernels: the alignment-agnostic fallback linear, the on-device
 // block decoder and the K == 0 zero fill.
 //
+//  * q8_generic_kernel: the same for Q8_0 weights (34-byte blocks).
 //  * generic_kernel: any K % 32 == 0 and any 2-byte-aligned pointers (the
 //    Q4_0 storage alignment of crates/mote-types/src/lib.rs:67-73).  One wave
 //    per weight row, lanes over 32-element blocks, the decode of
@@ -86,9 +87,54 @@ hipError_t launch_generic(const Problem& p) {
     return hipGetLastError();
 }
 
+// Q8_0 (crates/mote-reference/src/quantized.rs:191-195): 34-byte blocks, an f16
+// scale and 32 two's-complement bytes, value v d.  Same mapping as the Q4_0
+// generic kernel: one wave per weight row, lanes over blocks, f32 arithmetic.
+template <typename OutT>
+__global__ __launch_bounds__(256) void q8_generic_kernel(const uint16_t* __restrict__ x,
+                                                         const uint8_t* __restrict__ w,
+                                                         OutT* __restrict__ y, uint32_t M,
+                                                         uint32_t N, uint32_t K) {
+    constexpr uint32_t kQ8BlockBytes = 34;
+    const uint32_t n = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    if (n >= N) return;
+    const uint32_t blocks = K / kBlockElements;
+    const uint8_t* row = w + static_cast<size_t>(n) * blocks * kQ8BlockBytes;
+    for (uint32_t m = blockIdx.y; m < M; m += gridDim.y) {
+        const uint16_t* xr = x + static_cast<size_t>(m) * K;
+        float acc = 0.0f;
+        for (uint32_t b = lane; b < blocks; b += kWave) {
+            const uint8_t* blk = row + static_cast<size_t>(b) * kQ8BlockBytes;
+            const float d = load_half(blk);
+            for (int j = 0; j < 32; ++j) {
+                const float xv = static_cast<float>(__builtin_bit_cast(_Float16, xr[32 * b + j]));
+                acc = __builtin_fmaf(xv, static_cast<float>(static_cast<int8_t>(blk[2 + j])) * d, acc);
+            }
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) y[static_cast<size_t>(m) * N + n] = to_out<OutT>(acc);
+    }
+}
+
+hipError_t launch_q8_generic(const Problem& p) {
+    const dim3 grid((p.N + 3) / 4, min(p.M, 1024u)), block(256);
+    if (p.out == OutType::F32) {
+        hipLaunchKernelGGL((q8_generic_kernel<float>), grid, block, 0, p.stream,
+                           static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
+                           static_cast<float*>(p.y), p.M, p.N, p.K);
+    } else {
+        hipLaunchKernelGGL((q8_generic_kernel<_Float16>), grid, block, 0, p.stream,
+                           static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
+                           static_cast<_Float16*>(p.y), p.M, p.N, p.K);
+    }
+    return hipGetLastError();
+}
+
 const Variant kGeneric[] = {
     Variant{"generic", Kind::Generic, 0, 0, 0, &launch_generic<false>},
     Variant{"gateup_generic", Kind::GateUpGeneric, 0, 0, 0, &launch_generic<true>},
+    Variant{"q8_generic", Kind::Q8Generic, 0, 0, 0, &launch_q8_generic},
 };
 
 // One thread per block pair; same unpack as the GEMV kernel.

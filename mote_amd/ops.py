@@ -24,6 +24,14 @@ def quantized_linear_q4_0_f32(x, w, y, rows, n, k, stream) -> None:
     check(lib().mote_hip_quantized_linear_q4_0_f32(x, w, y, rows, n, k, _s(stream)), "launch Q4_0 linear kernel")
 
 
+def quantized_linear_q8_0_f16(x, w, y, rows, n, k, stream) -> None:
+    check(lib().mote_hip_quantized_linear_q8_0_f16(x, w, y, rows, n, k, _s(stream)), "launch Q8_0 linear kernel")
+
+
+def quantized_linear_q8_0_f32(x, w, y, rows, n, k, stream) -> None:
+    check(lib().mote_hip_quantized_linear_q8_0_f32(x, w, y, rows, n, k, _s(stream)), "launch Q8_0 linear kernel")
+
+
 def q4_0_gate_up_silu_f32(x, w_gate, w_up, y, rows, n, k, stream) -> None:
     check(
         lib().mote_hip_q4_0_gate_up_silu_f32(x, w_gate, w_up, y, rows, n, k, _s(stream)),
@@ -104,6 +112,12 @@ class Q4_0Dispatch:
             "launch Q4_0 linear",
         )
 
+    def linear_q8_0(self, x, w, y, rows, n, k, stream, f16_out: bool = False) -> None:
+        self._check(
+            lib().mote_q4_0_dispatch_linear_q8_0(self.handle, x, w, y, rows, n, k, int(f16_out), _s(stream)),
+            "launch Q8_0 linear",
+        )
+
     def gate_up_silu(self, x, w_gate, w_up, y, rows, n, k, stream, f16_out: bool = False) -> None:
         self._check(
             lib().mote_q4_0_dispatch_gate_up_silu(
@@ -112,9 +126,10 @@ class Q4_0Dispatch:
             "launch Q4_0 gate/up",
         )
 
-    def plan(self, rows, n, k, gate_up: bool = False, f16_out: bool = False) -> str | None:
+    def plan(self, rows, n, k, gate_up: bool = False, f16_out: bool = False, q8_0: bool = False) -> str | None:
         buf = ctypes.create_string_buffer(64)
-        status = lib().mote_q4_0_dispatch_plan(self.handle, rows, n, k, int(gate_up), int(f16_out), buf, 64)
+        op = 2 if q8_0 else int(gate_up)
+        status = lib().mote_q4_0_dispatch_plan(self.handle, rows, n, k, op, int(f16_out), buf, 64)
         return buf.value.decode() if status == 0 else None
 
     def close(self) -> None:

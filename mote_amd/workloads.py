@@ -31,6 +31,7 @@ BASE_SEED = 20261201
 
 Q4_0_BLOCK_ELEMENTS = 32
 Q4_0_BLOCK_BYTES = 18
+Q8_0_BLOCK_BYTES = 34
 
 
 def seed_for(workload: int, tensor: int) -> int:
@@ -81,6 +82,21 @@ def q4_0_weights(seed: int, rows: int, cols: int, std: float = 0.02) -> np.ndarr
     return out.reshape(-1)
 
 
+def q8_0_weights(seed: int, rows: int, cols: int, std: float = 0.02) -> np.ndarray:
+    """GGML Q8_0 bytes for a ``[rows, cols]`` matrix: per 32-element block an
+    f16 scale ``|N(0, std)|`` and 32 uniform two's-complement bytes."""
+    if cols % Q4_0_BLOCK_ELEMENTS:
+        raise ValueError("cols must be a multiple of 32")
+    blocks = rows * (cols // Q4_0_BLOCK_ELEMENTS)
+    draws = splitmix64(seed, 6 * blocks).reshape(blocks, 6) if blocks else np.zeros((0, 6), np.uint64)
+    u = uniform01(draws[:, :2])
+    d = np.abs(std * _box_muller(u[:, 0], u[:, 1])).astype(np.float16).view(np.uint16)
+    out = np.empty((blocks, Q8_0_BLOCK_BYTES), dtype=np.uint8)
+    out[:, 0:2] = d.astype("<u2").view(np.uint8).reshape(blocks, 2)
+    out[:, 2:34] = np.ascontiguousarray(draws[:, 2:6]).astype("<u8").view(np.uint8).reshape(blocks, 32)
+    return out.reshape(-1)
+
+
 def positions(seed: int, count: int, high: int = 8191) -> np.ndarray:
     """Uniform integers in ``[0, high]`` by rejection sampling on 13-bit draws."""
     bits = int(high).bit_length()
@@ -106,6 +122,10 @@ def rope_tables(positions_: np.ndarray, rotary_dim: int, theta: float) -> tuple[
     inv = np.power(float(theta), -(2.0 * i) / float(rotary_dim))
     angle = positions_.astype(np.float64)[:, None] * inv[None, :]
     return np.cos(angle).astype(np.float32), np.sin(angle).astype(np.float32)
+
+
+def q8_0_row_bytes(cols: int) -> int:
+    return (cols // Q4_0_BLOCK_ELEMENTS) * Q8_0_BLOCK_BYTES
 
 
 def q4_0_row_bytes(cols: int) -> int:
