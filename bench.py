@@ -143,13 +143,13 @@ def read_traffic() -> dict | None:
 
 
 class LinearCase:
-    """Device buffers for one Q4_0 linear problem with rotating weight copies."""
+    """Device buffers for one Q4_0 (or Q8_0) linear problem with rotating weight copies."""
 
     def __init__(self, m: int, n: int, k: int, workload: int, x_uniform: bool = False,
-                 gate_up: bool = False) -> None:
-        self.m, self.n, self.k, self.gate_up = m, n, k, gate_up
+                 gate_up: bool = False, q8_0: bool = False) -> None:
+        self.m, self.n, self.k, self.gate_up, self.q8_0 = m, n, k, gate_up, q8_0
         self.x = (wl.uniform_f16 if x_uniform else wl.normal_f16)(wl.seed_for(workload, 0), m * k)
-        self.w = wl.q4_0_weights(wl.seed_for(workload, 1), n, k)
+        self.w = (wl.q8_0_weights if q8_0 else wl.q4_0_weights)(wl.seed_for(workload, 1), n, k)
         self.w_up = wl.q4_0_weights(wl.seed_for(workload, 2), n, k) if gate_up else None
         per_copy = self.w.nbytes * (2 if gate_up else 1)
         self.copies = max(2, math.ceil(ROTATION_BYTES / per_copy))
@@ -165,11 +165,16 @@ class LinearCase:
         if self.gate_up:
             ops.q4_0_gate_up_silu_f32(self.xb.ptr, bufs[0].ptr, bufs[1].ptr, self.yb.ptr,
                                       self.m, self.n, self.k, stream)
+        elif self.q8_0:
+            ops.quantized_linear_q8_0_f32(self.xb.ptr, bufs[0].ptr, self.yb.ptr,
+                                          self.m, self.n, self.k, stream)
         else:
             ops.quantized_linear_q4_0_f32(self.xb.ptr, bufs[0].ptr, self.yb.ptr,
                                           self.m, self.n, self.k, stream)
 
     def algorithmic_bytes(self) -> int:
+        if self.q8_0:
+            return self.w.nbytes + 2 * self.m * self.k + 4 * self.m * self.n
         b = linear_bytes(self.m, self.n, self.k)
         return b + (self.w_up.nbytes if self.gate_up else 0)
 
@@ -302,14 +307,17 @@ SWEEP = (
     + [("skinny", m, 4096, n, 2, False, False) for n in (4096, 6144, 14336) for m in (2, 4, 8, 16, 32)]
     + [("prefill", m, 4096, 14336, 4, False, False) for m in (64, 256, 512)]
     + [("fused gate/up", m, 4096, 14336, 4, False, True) for m in (64, 256, 512)]
+    + [("q8_0 decode", 1, 4096, 4096, 5, False, "q8"), ("q8_0 up/gate", 1, 4096, 14336, 5, False, "q8"),
+       ("q8_0 down", 1, 14336, 4096, 5, False, "q8"), ("q8_0 2 tok", 2, 4096, 14336, 5, False, "q8"),
+       ("q8_0 4 tok", 4, 4096, 14336, 5, False, "q8")]
 )
 
 
 def run_sweep(stream: Stream, hip: _Hip, steps: int, warmup: int) -> None:
     print(f"{'case':<15}{'M':>5}{'K':>7}{'N':>7}{'kernel us':>11}{'eager us':>10}{'GB/s':>9}"
           f"{'%HBM':>7}{'TFLOP/s':>9}{'%MFMA':>7}", file=sys.stderr)
-    for name, m, k, n, workload, uni, gate_up in SWEEP:
-        case = LinearCase(m, n, k, workload, x_uniform=uni, gate_up=gate_up)
+    for name, m, k, n, workload, uni, kind in SWEEP:
+        case = LinearCase(m, n, k, workload, x_uniform=uni, gate_up=kind is True, q8_0=kind == "q8")
         t = time_case(case, stream, hip, steps, warmup)
         us = t["kernel_ms_mean"] * 1e3
         gbs = case.algorithmic_bytes() / (us * 1e-6) / 1e9
