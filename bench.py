@@ -313,6 +313,59 @@ SWEEP = (
 )
 
 
+class NormRopeCase:
+    """RMSNorm, fused add + RMSNorm or q/k RoPE on the decoder-step shape: 32
+    tokens, hidden 4096 (f16, eps 1e-5, weight f16(1 + 0.1 N(0,1))); RoPE on 32
+    query and 8 KV heads of head_dim 128, theta 500000, rotate-half layout,
+    positions uniform in [0, 8191].  Algorithmic bytes: every input and output
+    element once (RMSNorm 532 480 B, fused add + RMSNorm 1 056 768 B with the
+    residual read and written back, RoPE 671 744 B)."""
+
+    TOKENS, HIDDEN, QH, KH, HD = 32, 4096, 32, 8, 128
+
+    def __init__(self, kind: str) -> None:
+        self.kind = kind
+        t, h = self.TOKENS, self.HIDDEN
+        self.bufs = []
+        def buf(arr):
+            b = DeviceBuffer.from_array(arr)
+            self.bufs.append(b)
+            return b
+        if kind in ("rmsnorm", "fused add+rmsnorm"):
+            self.x = buf(wl.normal_f16(wl.seed_for(3, 0), t * h))
+            self.res = buf(wl.normal_f16(wl.seed_for(3, 2), t * h))
+            self.w = buf(wl.normal_f16(wl.seed_for(3, 1), h, mean=1.0, std=0.1))
+            self.y = buf(np.zeros(t * h, np.uint16))
+            self.nbytes = (2 * t * h + h) * 2 + (2 * t * h * 2 if kind != "rmsnorm" else 0)
+        else:
+            pos = wl.positions(wl.seed_for(3, 3), t)
+            cos, sin = wl.rope_tables(pos, self.HD, 500000.0)
+            self.q = buf(wl.normal_f16(wl.seed_for(3, 4), t * self.QH * self.HD))
+            self.k = buf(wl.normal_f16(wl.seed_for(3, 5), t * self.KH * self.HD))
+            self.cos, self.sin = buf(cos), buf(sin)
+            self.qo = buf(np.zeros(t * self.QH * self.HD, np.uint16))
+            self.ko = buf(np.zeros(t * self.KH * self.HD, np.uint16))
+            self.nbytes = 2 * t * (self.QH + self.KH) * self.HD * 2 + 2 * cos.nbytes
+        self.m, self.n, self.k_dim = t, h, 0
+
+    def launch(self, i: int, stream: Stream) -> None:
+        t, h = self.TOKENS, self.HIDDEN
+        if self.kind == "rmsnorm":
+            ops.rms_norm_f16(self.x.ptr, self.w.ptr, self.y.ptr, t, h, 1e-5, stream)
+        elif self.kind == "fused add+rmsnorm":
+            ops.fused_add_rms_norm_f16(self.x.ptr, self.res.ptr, self.w.ptr, self.y.ptr, t, h, 1e-5, stream)
+        else:
+            ops.rope_qk_f16(self.q.ptr, self.k.ptr, self.cos.ptr, self.sin.ptr, self.qo.ptr, self.ko.ptr,
+                            t, self.QH, self.KH, self.HD, self.HD, 0, stream)
+
+    def algorithmic_bytes(self) -> int:
+        return self.nbytes
+
+    def free(self) -> None:
+        for b in self.bufs:
+            b.free()
+
+
 def run_sweep(stream: Stream, hip: _Hip, steps: int, warmup: int) -> None:
     print(f"{'case':<15}{'M':>5}{'K':>7}{'N':>7}{'kernel us':>11}{'eager us':>10}{'GB/s':>9}"
           f"{'%HBM':>7}{'TFLOP/s':>9}{'%MFMA':>7}", file=sys.stderr)
@@ -325,6 +378,14 @@ def run_sweep(stream: Stream, hip: _Hip, steps: int, warmup: int) -> None:
         print(f"{name:<15}{m:>5}{k:>7}{n:>7}{us:>11.2f}{t['eager_ms_per_step'] * 1e3:>10.2f}{gbs:>9.0f}"
               f"{100 * gbs / HBM_PEAK_GBS:>6.1f}%{tf:>9.1f}{100 * tf / MFMA_F16_PEAK_TFLOPS:>6.1f}%",
               file=sys.stderr, flush=True)
+        case.free()
+    for kind in ("rmsnorm", "fused add+rmsnorm", "rope q+k"):
+        case = NormRopeCase(kind)
+        t = time_case(case, stream, hip, steps, warmup)
+        us = t["kernel_ms_mean"] * 1e3
+        gbs = case.algorithmic_bytes() / (us * 1e-6) / 1e9
+        print(f"{kind:<15}{case.TOKENS:>5}{0:>7}{case.HIDDEN:>7}{us:>11.2f}{t['eager_ms_per_step'] * 1e3:>10.2f}"
+              f"{gbs:>9.0f}{100 * gbs / HBM_PEAK_GBS:>6.1f}%{0.0:>9.1f}{0.0:>6.1f}%", file=sys.stderr, flush=True)
         case.free()
 
 
