@@ -41,14 +41,17 @@ __device__ __forceinline__ uint32_t pick(const uint32_t* x, int a, int b) {
     return __builtin_amdgcn_perm(x[b >> 1], x[a >> 1], hi | lo);
 }
 
-template <int KS, int STEPS, int MT, int D, int RT, bool TR, typename OutT>
+template <int KS, int STEPS, int MT, int D, int RT, bool TR, typename OutT, int LAZY = 0>
 __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __restrict__ x,
                                                              const uint8_t* __restrict__ w,
                                                              OutT* __restrict__ y, uint32_t M,
                                                              uint32_t N, uint32_t K,
                                                              uint32_t token_groups, uint32_t items,
                                                              uint32_t groups_per_xcd) {
-    __shared__ float part[KS][RT * MT][16][17];
+    // LAZY > 0: a workgroup owns at most LAZY items and its waves reduce them
+    // all at the end, behind one barrier, instead of once per item.
+    constexpr int kParts = (LAZY > 0 ? LAZY : 1) * RT * MT;
+    __shared__ float part[KS][kParts][16][17];
     // Transposed loads: wave-private staging of the raw pairs, [row tile][row]
     // [pair of the slice], rows padded by one dword so the 16 rows read by an
     // MFMA operand fall on distinct banks.
@@ -158,19 +161,9 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     // One item: dequantise + MFMA from `buf`, refill `buf` with item `next`
     // right after its last use (so the refill overlaps the reduction and the
     // other buffer's item), then reduce the KS partial tiles and store.
-    auto process = [&](uint32_t it, uint32_t (&buf)[RT * STEPS][9], uint32_t next, auto refill) {
-        if constexpr (TR) {
-            // LDS operations of a wave complete in order: the stage is read
-            // back below, and rewritten by the next item only after this
-            // item's reads.
-            stage_item(buf);
-            if constexpr (decltype(refill)::value) load_item(next, buf);
-        }
-        f32x4 acc[RT][MT];
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // Dequantise + MFMA one item (staged in LDS with TR, else from `buf`)
+    // into `acc`.
+    auto mma_item = [&](const uint32_t (&buf)[RT * STEPS][9], f32x4 (&acc)[RT][MT]) {
 #pragma unroll
         for (int s = 0; s < STEPS; ++s) {
             uint32_t q[RT][8];
@@ -201,6 +194,22 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
                 }
             }
         }
+    };
+
+    auto process = [&](uint32_t it, uint32_t (&buf)[RT * STEPS][9], uint32_t next, auto refill) {
+        if constexpr (TR) {
+            // LDS operations of a wave complete in order: the stage is read
+            // back below, and rewritten by the next item only after this
+            // item's reads.
+            stage_item(buf);
+            if constexpr (decltype(refill)::value) load_item(next, buf);
+        }
+        f32x4 acc[RT][MT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        mma_item(buf, acc);
         if constexpr (!TR && decltype(refill)::value) load_item(next, buf);
 
         // lane holds rows 4 lg + r, token li of each (row tile, token tile)
@@ -225,7 +234,49 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     };
 
     uint32_t item = first;
-    if constexpr (TR && D == 1) {
+    if constexpr (LAZY > 0) {
+        // Each wave streams its slice of every item of the workgroup with the
+        // next item's loads in flight, independently of the other waves; the
+        // partial tiles stay in registers until all items are done.
+        f32x4 accs[LAZY][RT][MT];
+#pragma unroll
+        for (int i = 0; i < LAZY; ++i)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) accs[i][rt][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < LAZY; ++i) {
+            const uint32_t it = first + static_cast<uint32_t>(i) * groups;
+            if (it < items) {  // uniform over the workgroup
+                stage_item(buf0);
+                load_item(it + groups, buf0);
+                mma_item(buf0, accs[i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < LAZY; ++i)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        part[kw][(i * RT + rt) * MT + mt][4 * lg + r][li] = accs[i][rt][mt][r];
+        __syncthreads();
+        for (int o = tid; o < 256 * kParts; o += KS * 64) {
+            const int row = o & 15, tok = (o >> 4) & 15, tile = o >> 8;
+            const int i = tile / (RT * MT), rt = (tile / MT) % RT, mt = tile % MT;
+            const uint32_t it = first + static_cast<uint32_t>(i) * groups;
+            if (it >= items) continue;
+            float sum = part[0][tile][row][tok];
+#pragma unroll
+            for (int k = 1; k < KS; ++k) sum += part[k][tile][row][tok];
+            const uint32_t n = rows_of(it) + 16u * rt + static_cast<uint32_t>(row);
+            const uint32_t m = tok0 + 16u * mt + static_cast<uint32_t>(tok);
+            if (n < N && m < M) y[static_cast<size_t>(m) * N + n] = to_out<OutT>(sum);
+        }
+    } else if constexpr (TR && D == 1) {
         // The stage frees the registers as soon as an item is written to LDS,
         // so one register buffer already keeps the next item in flight.
         for (; item < items; item += groups) process(item, buf0, item + groups, std::true_type{});
@@ -252,7 +303,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     }
 }
 
-template <int KS, int STEPS, int MT, int D, int G, int RT, bool TR = false>
+template <int KS, int STEPS, int MT, int D, int G, int RT, bool TR = false, int LAZY = 0>
 hipError_t launch_skinny(const Problem& p) {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -273,15 +324,16 @@ hipError_t launch_skinny(const Problem& p) {
     const uint32_t unit = 8u / a * token_groups;  // lcm(8, token_groups)
     uint32_t groups = static_cast<uint32_t>(cus) * G;
     if (groups > items) groups = items;
+    if (LAZY > 0 && groups < (items + LAZY - 1) / LAZY) groups = (items + LAZY - 1) / LAZY;  // <= LAZY items each
     groups = (groups + unit - 1) / unit * unit;
     const uint32_t per_xcd = groups / 8u;
     const dim3 grid(groups), block(KS * 64);
     if (p.out == OutType::F32) {
-        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float>), grid, block, 0, p.stream,
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float, LAZY>), grid, block, 0, p.stream,
                            static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<float*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
     } else {
-        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, _Float16>), grid, block, 0, p.stream,
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, _Float16, LAZY>), grid, block, 0, p.stream,
                            static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<_Float16*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
     }
@@ -291,6 +343,9 @@ hipError_t launch_skinny(const Problem& p) {
 #define MOTE_SKINNY(KS, STEPS, MT, D, G, RT)                                                     \
     Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d" #D "_g" #G "_r" #RT, Kind::SkinnyMfma, KS, \
             STEPS, MT, &launch_skinny<KS, STEPS, MT, D, G, RT>}
+#define MOTE_SKINNY_TRL(KS, STEPS, MT, G, L)                                                      \
+    Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d1_g" #G "_r1_tr_l" #L, Kind::SkinnyMfma, KS, \
+            STEPS, MT, &launch_skinny<KS, STEPS, MT, 1, G, 1, true, L>}
 #define MOTE_SKINNY_TR(KS, STEPS, MT, D, G)                                                       \
     Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d" #D "_g" #G "_r1_tr", Kind::SkinnyMfma, KS, \
             STEPS, MT, &launch_skinny<KS, STEPS, MT, D, G, 1, true>}
@@ -306,10 +361,13 @@ const Variant kSkinny[] = {
     MOTE_SKINNY_TR(4, 4, 1, 2, 2), MOTE_SKINNY_TR(8, 2, 1, 1, 1), MOTE_SKINNY_TR(8, 2, 1, 1, 2),
     MOTE_SKINNY_TR(8, 2, 2, 1, 1), MOTE_SKINNY_TR(8, 2, 2, 2, 1), MOTE_SKINNY_TR(4, 2, 1, 1, 1),
     MOTE_SKINNY_TR(4, 2, 2, 1, 1),
+    MOTE_SKINNY_TRL(8, 2, 1, 1, 4), MOTE_SKINNY_TRL(8, 2, 1, 1, 8), MOTE_SKINNY_TRL(8, 2, 2, 1, 4),
+    MOTE_SKINNY_TRL(4, 4, 1, 1, 4), MOTE_SKINNY_TRL(8, 2, 1, 2, 4),
 };
 
 #undef MOTE_SKINNY
 #undef MOTE_SKINNY_TR
+#undef MOTE_SKINNY_TRL
 
 }  // namespace
 
