@@ -128,6 +128,22 @@ const Variant* by_name(const char* name) {
     return v;
 }
 
+// Skinny GEMM (3 <= M <= 64, K = 4096) on the matrix cores, measured on
+// MI355X: one 16-token tile per workgroup with transposed loads; when a
+// workgroup owns 2-8 of the (16-row, token-tile) items its waves reduce them
+// once at the end (deferred reduction: 5-25 % faster than a reduction per
+// item); with one item, or more than 8, the per-item kernels.  Null when the
+// K slicing does not fit.
+const Variant* skinny_heuristic(const Problem& p) {
+    const uint64_t items = static_cast<uint64_t>((p.N + 15) / 16) * ((p.M + 15) / 16);
+    const uint64_t per_group = (items + device_cus() - 1) / static_cast<uint64_t>(device_cus());
+    const char* name = p.M <= 32 ? "skinny_mfma_k8_s2_t1_d1_g1_r1_tr" : "skinny_mfma_k8_s2_t2_d2_g1_r1_tr";
+    if (per_group >= 2 && per_group <= 4) name = "skinny_mfma_k8_s2_t1_d1_g1_r1_tr_l4";
+    if (per_group > 4 && per_group <= 8) name = "skinny_mfma_k8_s2_t1_d1_g1_r1_tr_l8";
+    const Variant* v = by_name(name);
+    return v && skinny_mfma_supports(*v, p) ? v : nullptr;
+}
+
 // Shape heuristic used when autotuning is off.
 const Variant* heuristic(const Problem& p, Op op) {
     const bool fast = fast_eligible(p);
@@ -159,8 +175,9 @@ const Variant* heuristic(const Problem& p, Op op) {
     }
     if (!fast) return by_name("generic");
     if (p.M == 64) {
-        const Variant* v = by_name("skinny_mfma_k16_s1_t2_d2_g1_r1");
-        if (v && skinny_mfma_supports(*v, p)) return v;
+        // 64 tokens still run as a skinny GEMM (faster than the prefill tiles).
+        const Variant* v = skinny_heuristic(p);
+        if (v) return v;
     }
     if (p.M >= 64) {
         // Prefer the largest tile that still gives about one tile per CU
@@ -212,25 +229,14 @@ const Variant* heuristic(const Problem& p, Op op) {
     // per workgroup up to 16 tokens, double-buffered items above, two token
     // tiles per workgroup above 32 tokens.
     // Two tokens: the vector-ALU streaming GEMV over both tokens at once
-    // (4096 x 14336: 9.2 us against 11.9 us on the matrix cores).  From 3 to
-    // 32 tokens: 8-wave K slices with transposed (row-contiguous) weight
-    // loads, 5-12% faster than the direct mapping.
+    // (4096 x 14336: 9.2 us against 11.9 us on the matrix cores).  From 3
+    // tokens: the skinny GEMM of skinny_heuristic, then any skinny variant
+    // whose K slicing fits, then the vector-ALU GEMV.
     if (p.M == 2) {
         const Variant* v = by_name("stream_m2_d1q_g1");
         if (v && gemv_stream_supports(*v, p)) return v;
     }
-    if (p.M <= 32) {
-        // Workgroups that own three or more 16-row items reduce them once at
-        // the end (deferred reduction: 5-14 % faster at N = 14336); with
-        // fewer items per workgroup the per-item reduction is as fast.
-        const uint64_t items = static_cast<uint64_t>((p.N + 15) / 16) * ((p.M + 15) / 16);
-        const uint64_t per_group = (items + device_cus() - 1) / static_cast<uint64_t>(device_cus());
-        const char* name = p.M <= 16 ? "skinny_mfma_k8_s2_t1_d1_g1_r1_tr" : "skinny_mfma_k8_s2_t2_d1_g1_r1_tr";
-        if (per_group >= 3 && per_group <= 4) name = "skinny_mfma_k8_s2_t1_d1_g1_r1_tr_l4";
-        if (per_group > 4 && per_group <= 8) name = "skinny_mfma_k8_s2_t1_d1_g1_r1_tr_l8";
-        const Variant* v = by_name(name);
-        if (v && skinny_mfma_supports(*v, p)) return v;
-    }
+    if (const Variant* v = skinny_heuristic(p)) return v;
     const char* suffix = p.M <= 16 ? "_t1_d1_g1_r1" : p.M <= 32 ? "_t1_d2_g1_r1" : "_t2_d2_g1_r1";
     for (const char* name : {"skinny_mfma_k16_s1", "skinny_mfma_k8_s2", "skinny_mfma_k16_s2",
                              "skinny_mfma_k8_s1", "skinny_mfma_k4_s2", "skinny_mfma_k4_s1"}) {
