@@ -389,6 +389,55 @@ def run_sweep(stream: Stream, hip: _Hip, steps: int, warmup: int) -> None:
         case.free()
 
 
+def run_comparator(steps: int = 40) -> int:
+    """Comparator for the prefill path: the vendor library's dense f16 GEMM
+    (torch.matmul, i.e. hipBLASLt on ROCm) at M in {64, 256, 512}, K = 4096,
+    N = 14336, with the weights already in f16 (117 MB per matrix, rotated over
+    4 copies so every call reads HBM), captured in a graph; plus the time to
+    write and re-read one f16 weight matrix, the extra cost a
+    dequantise-then-GEMM path pays per call.  Runs in its own process: it
+    loads torch's HIP runtime and never this library."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    k, n = 4096, 14336
+    print(f"{'comparator':<22}{'M':>5}{'K':>7}{'N':>7}{'kernel us':>11}{'TFLOP/s':>9}{'%MFMA':>7}",
+          file=sys.stderr)
+    for m in (64, 256, 512):
+        x = torch.randn(m, k, device=dev, dtype=torch.float16)
+        ws = [torch.randn(n, k, device=dev, dtype=torch.float16) for _ in range(4)]
+        side = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                y = x @ ws[0].t()
+            side.synchronize()
+            with torch.cuda.graph(graph, stream=side):
+                for i in range(steps):
+                    y = x @ ws[i % 4].t()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        tf = 2 * m * n * k / (us * 1e-6) / 1e12
+        print(f"{'f16 GEMM (library)':<22}{m:>5}{k:>7}{n:>7}{us:>11.2f}{tf:>9.1f}"
+              f"{100 * tf / MFMA_F16_PEAK_TFLOPS:>6.1f}%", file=sys.stderr, flush=True)
+        del graph, y
+    e0.record()
+    for i in range(10):
+        ws[(i + 1) % 4].copy_(ws[i % 4])
+    e1.record()
+    torch.cuda.synchronize()
+    print(f"f16 weight matrix write + read ({2 * n * k * 2 / 1e6:.0f} MB): "
+          f"{e0.elapsed_time(e1) * 1e3 / 10:.2f} us", file=sys.stderr, flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -405,7 +454,12 @@ def main() -> int:
                     help="with --profile-run: profile this linear shape instead of the headline")
     ap.add_argument("--profile-gate-up", action="store_true",
                     help="with --profile-run: profile the fused gate/up SiLU-mul of the shape")
+    ap.add_argument("--comparator", action="store_true",
+                    help="time the vendor library's dense f16 GEMM at the prefill shapes (needs torch; "
+                         "stderr table, no result line)")
     args = ap.parse_args()
+    if args.comparator:
+        return run_comparator()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the Q4_0 linear shards by output rows with no exchange; see the design notes)",
