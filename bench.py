@@ -390,13 +390,14 @@ def run_sweep(stream: Stream, hip: _Hip, steps: int, warmup: int) -> None:
 
 
 def run_comparator(steps: int = 40) -> int:
-    """Comparator for the prefill path: the vendor library's dense f16 GEMM
-    (torch.matmul, i.e. hipBLASLt on ROCm) at M in {64, 256, 512}, K = 4096,
-    N = 14336, with the weights already in f16 (117 MB per matrix, rotated over
-    4 copies so every call reads HBM), captured in a graph; plus the time to
-    write and re-read one f16 weight matrix, the extra cost a
-    dequantise-then-GEMM path pays per call.  Runs in its own process: it
-    loads torch's HIP runtime and never this library."""
+    """Comparators from the vendor libraries, through torch.  Prefill: the
+    dense f16 GEMM (torch.matmul, i.e. hipBLASLt on ROCm) at M in {64, 256,
+    512}, K = 4096, N = 14336, with the weights already in f16 (117 MB per
+    matrix, rotated over 4 copies so every call reads HBM), captured in a
+    graph; plus the time to write and re-read one f16 weight matrix, the extra
+    cost a dequantise-then-GEMM path pays per call.  Decode: a plain read of
+    the headline's 33 095 680 bytes by the library's reduction kernel.  Runs
+    in its own process: it loads torch's HIP runtime and never this library."""
     import torch
 
     dev = torch.device("cuda:0")
@@ -435,6 +436,31 @@ def run_comparator(steps: int = 40) -> int:
     torch.cuda.synchronize()
     print(f"f16 weight matrix write + read ({2 * n * k * 2 / 1e6:.0f} MB): "
           f"{e0.elapsed_time(e1) * 1e3 / 10:.2f} us", file=sys.stderr, flush=True)
+    del ws
+    # The decode headline's byte count read by the library's own reduction
+    # (amax over int32 words), 13 rotated copies, graph-captured.
+    words = linear_bytes(1, n, k) // 4
+    bufs = [torch.randint(0, 1 << 30, (words,), device=dev, dtype=torch.int32) for _ in range(13)]
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        for b in bufs:
+            r = b.amax()
+        side.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(steps * 5):
+                r = bufs[i % 13].amax()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (steps * 5)
+    gbs = words * 4 / (us * 1e-6) / 1e9
+    print(f"read of {words * 4} B (library amax reduction): {us:.2f} us, {gbs:.0f} GB/s, "
+          f"{100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak", file=sys.stderr, flush=True)
     return 0
 
 
