@@ -367,25 +367,42 @@ class NormRopeCase:
 
 
 def run_sweep(stream: Stream, hip: _Hip, steps: int, warmup: int) -> None:
+    """One line per configuration; the last column is the kernel variant the
+    library's shape heuristic plans for it (the one the default entry points
+    launch)."""
     print(f"{'case':<15}{'M':>5}{'K':>7}{'N':>7}{'kernel us':>11}{'eager us':>10}{'GB/s':>9}"
-          f"{'%HBM':>7}{'TFLOP/s':>9}{'%MFMA':>7}", file=sys.stderr)
+          f"{'%HBM':>7}{'TFLOP/s':>9}{'%MFMA':>7}  kernel", file=sys.stderr)
+    planner = ops.Q4_0Dispatch()  # no autotuning: the default entry points' heuristic
     for name, m, k, n, workload, uni, kind in SWEEP:
         case = LinearCase(m, n, k, workload, x_uniform=uni, gate_up=kind is True, q8_0=kind == "q8")
         t = time_case(case, stream, hip, steps, warmup)
         us = t["kernel_ms_mean"] * 1e3
+        w = case.wb[0]
+        if kind is True:
+            planner.gate_up_silu(case.xb.ptr, w[0].ptr, w[1].ptr, case.yb.ptr, m, n, k, stream)
+        elif kind == "q8":
+            planner.linear_q8_0(case.xb.ptr, w[0].ptr, case.yb.ptr, m, n, k, stream)
+        else:
+            planner.linear(case.xb.ptr, w[0].ptr, case.yb.ptr, m, n, k, stream)
+        stream.synchronize()
+        variant = planner.plan(m, n, k, gate_up=kind is True, q8_0=kind == "q8")
         gbs = case.algorithmic_bytes() / (us * 1e-6) / 1e9
         tf = case.flops() / (us * 1e-6) / 1e12
         print(f"{name:<15}{m:>5}{k:>7}{n:>7}{us:>11.2f}{t['eager_ms_per_step'] * 1e3:>10.2f}{gbs:>9.0f}"
-              f"{100 * gbs / HBM_PEAK_GBS:>6.1f}%{tf:>9.1f}{100 * tf / MFMA_F16_PEAK_TFLOPS:>6.1f}%",
+              f"{100 * gbs / HBM_PEAK_GBS:>6.1f}%{tf:>9.1f}{100 * tf / MFMA_F16_PEAK_TFLOPS:>6.1f}%  {variant}",
               file=sys.stderr, flush=True)
         case.free()
+    planner.close()
+    entry = {"rmsnorm": "mote_hip_rms_norm_f16", "fused add+rmsnorm": "mote_hip_fused_add_rms_norm_f16",
+             "rope q+k": "mote_hip_rope_qk_f16"}
     for kind in ("rmsnorm", "fused add+rmsnorm", "rope q+k"):
         case = NormRopeCase(kind)
         t = time_case(case, stream, hip, steps, warmup)
         us = t["kernel_ms_mean"] * 1e3
         gbs = case.algorithmic_bytes() / (us * 1e-6) / 1e9
         print(f"{kind:<15}{case.TOKENS:>5}{0:>7}{case.HIDDEN:>7}{us:>11.2f}{t['eager_ms_per_step'] * 1e3:>10.2f}"
-              f"{gbs:>9.0f}{100 * gbs / HBM_PEAK_GBS:>6.1f}%{0.0:>9.1f}{0.0:>6.1f}%", file=sys.stderr, flush=True)
+              f"{gbs:>9.0f}{100 * gbs / HBM_PEAK_GBS:>6.1f}%{0.0:>9.1f}{0.0:>6.1f}%  {entry[kind]}",
+              file=sys.stderr, flush=True)
         case.free()
 
 

@@ -128,18 +128,31 @@ const Variant* by_name(const char* name) {
     return v;
 }
 
-// Skinny GEMM (3 <= M <= 64, K = 4096) on the matrix cores, measured on
-// MI355X: one 16-token tile per workgroup with transposed loads; when a
-// workgroup owns 2-8 of the (16-row, token-tile) items its waves reduce them
-// once at the end (deferred reduction: 5-25 % faster than a reduction per
-// item); with one item, or more than 8, the per-item kernels.  Null when the
-// K slicing does not fit.
+// Skinny GEMM (3 <= M <= 64, K = 4096) on the matrix cores, transposed weight
+// loads; null when the K slicing does not fit.  Measured on MI355X (graph
+// replays, weights rotated past the MALL): one (16-row, 16-token) item per
+// step of a workgroup, with the reduction deferred over up to 4 items (16
+// waves, one K step each) or 8 items (8 waves, two steps); past 8 items per
+// workgroup with more than 16 tokens, both token tiles in one item.  Above 4
+// tokens the activations are loaded whole lines per instruction and
+// redistributed through LDS (16 x 4096 x 14336: 11.8 us against 12.3 us;
+// 32 x 4096 x 14336: 15.7 against 16.9 us; 16 x 4096 x 4096: 6.8 against
+// 8.0 us); up to 4 tokens the direct loads are level or faster, and with at
+// most one item per workgroup 8 waves of two steps without the deferred
+// reduction are fastest (4 x 4096 x 4096: 5.7 us against 6.1 us).
 const Variant* skinny_heuristic(const Problem& p) {
     const uint64_t items = static_cast<uint64_t>((p.N + 15) / 16) * ((p.M + 15) / 16);
     const uint64_t per_group = (items + device_cus() - 1) / static_cast<uint64_t>(device_cus());
-    const char* name = p.M <= 32 ? "skinny_mfma_k8_s2_t1_d1_g1_r1_tr" : "skinny_mfma_k8_s2_t2_d2_g1_r1_tr";
-    if (per_group >= 2 && per_group <= 4) name = "skinny_mfma_k8_s2_t1_d1_g1_r1_tr_l4";
-    if (per_group > 4 && per_group <= 8) name = "skinny_mfma_k8_s2_t1_d1_g1_r1_tr_l8";
+    const bool xc = p.M > 4;
+    const char* name;
+    if (per_group <= 1 && !xc)
+        name = "skinny_mfma_k8_s2_t1_d1_g1_r1_tr";
+    else if (per_group <= 4)
+        name = xc ? "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c" : "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4";
+    else if (per_group <= 8 || p.M <= 16)
+        name = xc ? "skinny_mfma_k8_s2_t1_d1_g1_r1_tr_l8_c" : "skinny_mfma_k8_s2_t1_d1_g1_r1_tr_l8";
+    else
+        name = "skinny_mfma_k16_s1_t2_d2_g1_r1_tr_c";
     const Variant* v = by_name(name);
     return v && skinny_mfma_supports(*v, p) ? v : nullptr;
 }

@@ -41,23 +41,41 @@ __device__ __forceinline__ uint32_t pick(const uint32_t* x, int a, int b) {
     return __builtin_amdgcn_perm(x[b >> 1], x[a >> 1], hi | lo);
 }
 
-template <int KS, int STEPS, int MT, int D, int RT, bool TR, typename OutT, int LAZY = 0>
+template <int KS, int STEPS, int MT, int D, int RT, bool TR, typename OutT, int LAZY = 0, bool XC = false>
 __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __restrict__ x,
                                                              const uint8_t* __restrict__ w,
                                                              OutT* __restrict__ y, uint32_t M,
                                                              uint32_t N, uint32_t K,
                                                              uint32_t token_groups, uint32_t items,
                                                              uint32_t groups_per_xcd) {
-    // LAZY > 0: a workgroup owns at most LAZY items and its waves reduce them
-    // all at the end, behind one barrier, instead of once per item.
-    constexpr int kParts = (LAZY > 0 ? LAZY : 1) * RT * MT;
-    __shared__ float part[KS][kParts][16][17];
     // Transposed loads: wave-private staging of the raw pairs, [row tile][row]
     // [pair of the slice], rows padded by one dword so the 16 rows read by an
     // MFMA operand fall on distinct banks.
     constexpr int kSlicePairs = STEPS * 4;
     constexpr int kStageRow = kSlicePairs * kPairBytes + 4;
-    __shared__ __attribute__((aligned(16))) uint8_t stage[TR ? KS * RT * 16 * kStageRow : 4];
+    constexpr int kStageBytes = TR ? KS * RT * 16 * kStageRow : 4;
+    __shared__ __attribute__((aligned(16))) uint8_t stage[kStageBytes];
+    // LAZY > 0: a workgroup owns at most LAZY items and its waves reduce them
+    // at the end, kChunk items per barrier (as many as fit the 160 KiB of LDS
+    // beside the stage, rounded down to a power of two), instead of once per
+    // item.
+    // XC: the activations are loaded whole cache lines per instruction (lane
+    // l reads bytes 16 l .. 16 l + 15 of a 1 KiB run of the wave's slices of
+    // the 16 tokens) and redistributed to the operand layout through a
+    // wave-private LDS region, kXTok tokens per round.  Loaded directly, each
+    // lane reads its own 128-byte pair, so every instruction touches 64 lines
+    // and 16 tokens' slices outgrow the vector L1, which then refetches them.
+    constexpr int kSliceBytes = STEPS * 512;  // one token's slice of x
+    constexpr int kXRow = kSliceBytes + 16;
+    constexpr int kXTok = 4;
+    constexpr int kXBytes = XC ? KS * kXTok * kXRow : 16;
+    __shared__ __attribute__((aligned(16))) uint8_t xstage[kXBytes];
+    constexpr int kPartItem = KS * RT * MT * 16 * 17 * 4;
+    constexpr int kFit = (160 * 1024 - kStageBytes - kXBytes) / kPartItem;
+    constexpr int kChunk = LAZY == 0 ? 1 : (kFit >= LAZY ? LAZY : kFit >= 4 ? 4 : kFit >= 2 ? 2 : 1);
+    static_assert(LAZY == 0 || LAZY % kChunk == 0, "chunks must tile the items");
+    constexpr int kParts = kChunk * RT * MT;
+    __shared__ float part[KS][kParts][16][17];
 
     const int tid = static_cast<int>(threadIdx.x);
     const int kw = tid >> 6;
@@ -123,26 +141,93 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
         for (int i = 0; i < 9; ++i) c[i] = src[i];
     };
 
-    // The first item's weights, then the activations (reused by every item).
+    // The first item's weights, the activations (reused by every item), and
+    // with D = 2 the second item's weights, issued before the activations are
+    // waited for.
     uint32_t buf0[RT * STEPS][9];
+    uint32_t buf1[RT * STEPS][9];
     load_item(first, buf0);
     // Activations of this wave's K slice for the workgroup's MT token tiles.
+    // Tokens past M read row M - 1: a token only feeds its own output column
+    // of the MFMA, and those columns are never stored.
+    constexpr int kXLoads = XC ? 16 * kSliceBytes / 1024 : 1;
+    u32x4 xg[MT][kXLoads];
+    u32x4 xraw[MT][STEPS][8];
+    if constexpr (XC) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int c = 0; c < kXLoads; ++c) {
+                const uint32_t f = static_cast<uint32_t>(c) * 1024u + static_cast<uint32_t>(lane) * 16u;
+                const uint32_t m = min(tok0 + 16u * mt + f / kSliceBytes, M - 1);
+                const uint16_t* src = x + static_cast<size_t>(m) * K + static_cast<size_t>(kw) * STEPS * 256 +
+                                      (f % kSliceBytes) / 2;
+                xg[mt][c] = *reinterpret_cast<const u32x4*>(src);
+            }
+    } else {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const uint32_t m = min(tok0 + 16u * mt + static_cast<uint32_t>(li), M - 1);
+            const uint16_t* xrow = x + static_cast<size_t>(m) * K;
+#pragma unroll
+            for (int s = 0; s < STEPS; ++s) {
+                const uint32_t p = (static_cast<uint32_t>(kw) * STEPS + s) * 4u + static_cast<uint32_t>(lg);
+                const u32x4* src = reinterpret_cast<const u32x4*>(xrow + static_cast<size_t>(p) * 64);
+#pragma unroll
+                for (int c = 0; c < 8; ++c) xraw[mt][s][c] = src[c];
+            }
+        }
+    }
+    if constexpr (D == 2) load_item(first + groups, buf1);
+    // Permutes the activations into the order of the weight operands (waits
+    // for x; the LAZY path first stages its first item and issues the next
+    // item's loads, so HBM is not idle while x is broadcast to every CU).
     f16x8 xb[MT][STEPS][8];
+    auto convert_x = [&]() {
+    if constexpr (XC) {
+        // Round r: every lane writes the chunks of tokens r kXTok .. r kXTok +
+        // kXTok - 1 it loaded, then the lanes of those tokens read their pairs
+        // back (a wave's LDS operations complete in order).  Tokens past M
+        // are not read back: their operands stay zero.
+        uint8_t* xs = xstage + kw * kXTok * kXRow;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+            for (int s = 0; s < STEPS; ++s)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) xraw[mt][s][c] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int r = 0; r < 16 / kXTok; ++r) {
+                // Rounds of tokens past M only feed unstored columns (their
+                // operands stay zero); uniform over the workgroup.
+                if (tok0 + 16u * mt + static_cast<uint32_t>(r * kXTok) >= M) break;
+#pragma unroll
+                for (int c = 0; c < kXLoads; ++c) {
+                    if ((c * 1024 / kSliceBytes) / kXTok != r) continue;  // folds after unrolling
+                    const uint32_t f = static_cast<uint32_t>(c) * 1024u + static_cast<uint32_t>(lane) * 16u;
+                    const uint32_t tok = f / kSliceBytes - static_cast<uint32_t>(r * kXTok);
+                    *reinterpret_cast<u32x4*>(xs + tok * kXRow + f % kSliceBytes) = xg[mt][c];
+                }
+                if (li / kXTok == r) {
+                    const uint8_t* row = xs + (li - r * kXTok) * kXRow;
+#pragma unroll
+                    for (int s = 0; s < STEPS; ++s)
+#pragma unroll
+                        for (int c = 0; c < 8; ++c)
+                            xraw[mt][s][c] = *reinterpret_cast<const u32x4*>(row + (4 * s + lg) * 128 + 16 * c);
+                }
+            }
+        }
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-        const uint32_t m = tok0 + 16u * mt + static_cast<uint32_t>(li);
-        const bool live = m < M;
-        const uint16_t* xrow = x + static_cast<size_t>(min(m, M - 1)) * K;
 #pragma unroll
         for (int s = 0; s < STEPS; ++s) {
-            const uint32_t p = (static_cast<uint32_t>(kw) * STEPS + s) * 4u + static_cast<uint32_t>(lg);
             uint32_t xr[32];
-            const u32x4* src = reinterpret_cast<const u32x4*>(xrow + static_cast<size_t>(p) * 64);
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                const u32x4 v = src[c];
-                xr[4 * c + 0] = live ? v.x : 0u; xr[4 * c + 1] = live ? v.y : 0u;
-                xr[4 * c + 2] = live ? v.z : 0u; xr[4 * c + 3] = live ? v.w : 0u;
+                const u32x4 v = xraw[mt][s][c];
+                xr[4 * c + 0] = v.x; xr[4 * c + 1] = v.y; xr[4 * c + 2] = v.z; xr[4 * c + 3] = v.w;
             }
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
@@ -155,6 +240,8 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
             }
         }
     }
+    };
+    if constexpr (LAZY == 0) convert_x();
     const DequantConsts dq = dequant_consts();
 
 
@@ -237,7 +324,10 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     if constexpr (LAZY > 0) {
         // Each wave streams its slice of every item of the workgroup with the
         // next item's loads in flight, independently of the other waves; the
-        // partial tiles stay in registers until all items are done.
+        // partial tiles stay in registers until all items are done, then meet
+        // in LDS in chunks of kChunk items.  (A second item in flight measured
+        // slower: a deeper request front lowers the achieved HBM rate.)
+        static_assert(D == 1, "the deferred reduction streams one item ahead");
         f32x4 accs[LAZY][RT][MT];
 #pragma unroll
         for (int i = 0; i < LAZY; ++i)
@@ -250,31 +340,37 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
             const uint32_t it = first + static_cast<uint32_t>(i) * groups;
             if (it < items) {  // uniform over the workgroup
                 stage_item(buf0);
-                load_item(it + groups, buf0);
+                if (i + 1 < LAZY) load_item(it + groups, buf0);
+                __builtin_amdgcn_sched_barrier(0);  // the loads go out before this item's MFMAs
+                if (i == 0) convert_x();
                 mma_item(buf0, accs[i]);
             }
         }
 #pragma unroll
-        for (int i = 0; i < LAZY; ++i)
+        for (int c0 = 0; c0 < LAZY; c0 += kChunk) {
+            if (c0 > 0) __syncthreads();  // the previous chunk has been read
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt)
+            for (int i = 0; i < kChunk; ++i)
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
+                for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        part[kw][(i * RT + rt) * MT + mt][4 * lg + r][li] = accs[i][rt][mt][r];
-        __syncthreads();
-        for (int o = tid; o < 256 * kParts; o += KS * 64) {
-            const int row = o & 15, tok = (o >> 4) & 15, tile = o >> 8;
-            const int i = tile / (RT * MT), rt = (tile / MT) % RT, mt = tile % MT;
-            const uint32_t it = first + static_cast<uint32_t>(i) * groups;
-            if (it >= items) continue;
-            float sum = part[0][tile][row][tok];
+                    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int k = 1; k < KS; ++k) sum += part[k][tile][row][tok];
-            const uint32_t n = rows_of(it) + 16u * rt + static_cast<uint32_t>(row);
-            const uint32_t m = tok0 + 16u * mt + static_cast<uint32_t>(tok);
-            if (n < N && m < M) y[static_cast<size_t>(m) * N + n] = to_out<OutT>(sum);
+                        for (int r = 0; r < 4; ++r)
+                            part[kw][(i * RT + rt) * MT + mt][4 * lg + r][li] = accs[c0 + i][rt][mt][r];
+            __syncthreads();
+            for (int o = tid; o < 256 * kParts; o += KS * 64) {
+                const int row = o & 15, tok = (o >> 4) & 15, tile = o >> 8;
+                const int i = tile / (RT * MT), rt = (tile / MT) % RT, mt = tile % MT;
+                const uint32_t it = first + static_cast<uint32_t>(c0 + i) * groups;
+                if (it >= items) continue;
+                float sum = part[0][tile][row][tok];
+#pragma unroll
+                for (int k = 1; k < KS; ++k) sum += part[k][tile][row][tok];
+                const uint32_t n = rows_of(it) + 16u * rt + static_cast<uint32_t>(row);
+                const uint32_t m = tok0 + 16u * mt + static_cast<uint32_t>(tok);
+                if (n < N && m < M) y[static_cast<size_t>(m) * N + n] = to_out<OutT>(sum);
+            }
         }
     } else if constexpr (TR && D == 1) {
         // The stage frees the registers as soon as an item is written to LDS,
@@ -293,8 +389,6 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
             process(item, cur, item, std::false_type{});
         }
     } else {
-        uint32_t buf1[RT * STEPS][9];
-        load_item(item + groups, buf1);
         for (; item < items; item += 2 * groups) {
             process(item, buf0, item + 2 * groups, std::true_type{});
             if (item + groups < items)  // uniform
@@ -303,7 +397,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     }
 }
 
-template <int KS, int STEPS, int MT, int D, int G, int RT, bool TR = false, int LAZY = 0>
+template <int KS, int STEPS, int MT, int D, int G, int RT, bool TR = false, int LAZY = 0, bool XC = false>
 hipError_t launch_skinny(const Problem& p) {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -329,11 +423,11 @@ hipError_t launch_skinny(const Problem& p) {
     const uint32_t per_xcd = groups / 8u;
     const dim3 grid(groups), block(KS * 64);
     if (p.out == OutType::F32) {
-        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float, LAZY>), grid, block, 0, p.stream,
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float, LAZY, XC>), grid, block, 0, p.stream,
                            static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<float*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
     } else {
-        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, _Float16, LAZY>), grid, block, 0, p.stream,
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, _Float16, LAZY, XC>), grid, block, 0, p.stream,
                            static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<_Float16*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
     }
@@ -346,6 +440,12 @@ hipError_t launch_skinny(const Problem& p) {
 #define MOTE_SKINNY_TRL(KS, STEPS, MT, G, L)                                                      \
     Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d1_g" #G "_r1_tr_l" #L, Kind::SkinnyMfma, KS, \
             STEPS, MT, &launch_skinny<KS, STEPS, MT, 1, G, 1, true, L>}
+#define MOTE_SKINNY_TRLC(KS, STEPS, MT, G, L)                                                    \
+    Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d1_g" #G "_r1_tr_l" #L "_c", Kind::SkinnyMfma, \
+            KS, STEPS, MT, &launch_skinny<KS, STEPS, MT, 1, G, 1, true, L, true>}
+#define MOTE_SKINNY_TRC(KS, STEPS, MT, D, G)                                                      \
+    Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d" #D "_g" #G "_r1_tr_c", Kind::SkinnyMfma, KS, \
+            STEPS, MT, &launch_skinny<KS, STEPS, MT, D, G, 1, true, 0, true>}
 #define MOTE_SKINNY_TR(KS, STEPS, MT, D, G)                                                       \
     Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d" #D "_g" #G "_r1_tr", Kind::SkinnyMfma, KS, \
             STEPS, MT, &launch_skinny<KS, STEPS, MT, D, G, 1, true>}
@@ -362,12 +462,18 @@ const Variant kSkinny[] = {
     MOTE_SKINNY_TR(8, 2, 2, 1, 1), MOTE_SKINNY_TR(8, 2, 2, 2, 1), MOTE_SKINNY_TR(4, 2, 1, 1, 1),
     MOTE_SKINNY_TR(4, 2, 2, 1, 1),
     MOTE_SKINNY_TRL(8, 2, 1, 1, 4), MOTE_SKINNY_TRL(8, 2, 1, 1, 8), MOTE_SKINNY_TRL(8, 2, 2, 1, 4),
-    MOTE_SKINNY_TRL(4, 4, 1, 1, 4), MOTE_SKINNY_TRL(8, 2, 1, 2, 4),
+    MOTE_SKINNY_TRL(4, 4, 1, 1, 4), MOTE_SKINNY_TRL(8, 2, 1, 2, 4), MOTE_SKINNY_TRL(16, 1, 1, 1, 4),
+    MOTE_SKINNY_TRL(16, 1, 1, 1, 8),
+    MOTE_SKINNY_TRLC(16, 1, 1, 1, 4), MOTE_SKINNY_TRLC(16, 1, 1, 1, 8), MOTE_SKINNY_TRLC(8, 2, 1, 1, 4),
+    MOTE_SKINNY_TRLC(8, 2, 1, 1, 8), MOTE_SKINNY_TRLC(4, 4, 1, 1, 4), MOTE_SKINNY_TRC(8, 2, 2, 2, 1),
+    MOTE_SKINNY_TRC(16, 1, 2, 2, 1),
 };
 
 #undef MOTE_SKINNY
 #undef MOTE_SKINNY_TR
 #undef MOTE_SKINNY_TRL
+#undef MOTE_SKINNY_TRLC
+#undef MOTE_SKINNY_TRC
 
 }  // namespace
 

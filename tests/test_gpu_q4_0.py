@@ -281,11 +281,13 @@ def _skinny_k(variant):
 def test_every_skinny_mfma_variant(stream, oracle, variant):
     """Matrix-core skinny GEMM: tokens padded inside a 16-token tile (M = 2, 5),
     exactly one and two tiles (16, 32), one token over (17, 33), the 64-token
-    maximum, N ragged against the 16-row tiles, f32 and f16 outputs."""
+    maximum, N ragged against the 16-row tiles, f32 and f16 outputs; 20 x
+    14336 gives every workgroup several items (the item ring and the deferred
+    reduction over several items)."""
     d = ops.Q4_0Dispatch()
     d.force(variant)
     k = _skinny_k(variant)
-    for m, n in [(2, 100), (5, 33), (16, 16), (17, 130), (32, 61), (33, 7), (64, 80), (3, 4096)]:
+    for m, n in [(2, 100), (5, 33), (16, 16), (17, 130), (32, 61), (33, 7), (64, 80), (20, 14336), (3, 4096)]:
         x = normal_x(wl.seed_for(14, m), m, k)
         w = weights(wl.seed_for(14, 100 + n), n, k)
         y = run_linear(stream, x, w, m, n, k, dispatch=d)
