@@ -156,6 +156,10 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // Output element conversion.
+// SiLU of the fused gate/up epilogue, silu(g) = g / (1 + e^-g) in f32 with the
+// device exponential, shared by every gate/up kernel so they agree bit for bit.
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
 template <typename T>
 __device__ __forceinline__ T to_out(float v);
 template <>

@@ -32,8 +32,6 @@ namespace {
 constexpr int kRowHalves = 72;  // 64 halves + 8 halves padding per LDS row
 constexpr int kRowBytes = kRowHalves * 2;
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
-
 // Dequantises the four k groups of one block.  `g[i]` holds nibble bytes
 // 4i..4i+3 of the block, `scale` the block's f16 scale bits in its low half.
 __device__ __forceinline__ void dequant_block(const uint32_t (&g)[4], uint32_t scale,

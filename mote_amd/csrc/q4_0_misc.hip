@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) void generic_kernel(const uint16_t* __restrict
         float v = g;
         if constexpr (GATE_UP) {
             u = wave_sum(u);
-            v = (g / (1.0f + __expf(-g))) * u;
+            v = silu(g) * u;
         }
         if (lane == 0) y[static_cast<size_t>(m) * N + n] = to_out<OutT>(v);
     }

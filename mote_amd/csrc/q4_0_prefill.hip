@@ -36,8 +36,6 @@ namespace {
 constexpr int kXRow = 144;  // LDS bytes per activation row and step (128 + 16 padding)
 constexpr int kWRow = 36;   // LDS bytes per weight row and step (9 dwords)
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
-
 template <int BM, int BN, bool GATE_UP, typename OutT>
 __global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict__ x,
                                                       const uint8_t* __restrict__ wg,

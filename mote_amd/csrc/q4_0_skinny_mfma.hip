@@ -27,6 +27,11 @@
 //    (deterministic), then written as f32 or f16.
 //
 // The next item's weight loads are issued before the current item's MFMAs.
+//
+// Fused gate/up (GU, RT = 2): row tile 0 of an item is rows n .. n + 15 of the
+// gate matrix and row tile 1 the same rows of the up matrix, and the store
+// writes y[m, n] = silu(gate) * up (the operation the prefill kernels fuse for
+// M >= 64).
 #include "common.hpp"
 #include "q4_0.hpp"
 
@@ -41,9 +46,11 @@ __device__ __forceinline__ uint32_t pick(const uint32_t* x, int a, int b) {
     return __builtin_amdgcn_perm(x[b >> 1], x[a >> 1], hi | lo);
 }
 
-template <int KS, int STEPS, int MT, int D, int RT, bool TR, typename OutT, int LAZY = 0, bool XC = false>
+template <int KS, int STEPS, int MT, int D, int RT, bool TR, typename OutT, int LAZY = 0, bool XC = false,
+          bool GU = false>
 __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __restrict__ x,
                                                              const uint8_t* __restrict__ w,
+                                                             const uint8_t* __restrict__ w_up,
                                                              OutT* __restrict__ y, uint32_t M,
                                                              uint32_t N, uint32_t K,
                                                              uint32_t token_groups, uint32_t items,
@@ -91,7 +98,9 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
 
     // Item -> (row tile, token group of MT 16-token tiles).  The grid size is
     // a multiple of token_groups, so a workgroup keeps one token group.
-    auto rows_of = [&](uint32_t item) { return (item / token_groups) * (16u * RT); };
+    static_assert(!GU || RT == 2, "gate/up items are one gate and one up row tile");
+    constexpr uint32_t kItemRows = GU ? 16u : 16u * RT;
+    auto rows_of = [&](uint32_t item) { return (item / token_groups) * kItemRows; };
     const uint32_t tok0 = (first % token_groups) * (16u * MT);
 
     // Weight loads of one item: RT row tiles x STEPS pairs per lane.  Direct
@@ -115,8 +124,9 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
                     r = static_cast<uint32_t>(li);
                     p = (static_cast<uint32_t>(kw) * STEPS + s) * 4u + static_cast<uint32_t>(lg);
                 }
-                const uint32_t n = min(rows_of(it) + 16u * rt + r, N - 1);
-                load_pair(w + static_cast<size_t>(n) * row_bytes + static_cast<size_t>(p) * kPairBytes,
+                const uint32_t n = min(rows_of(it) + (GU ? 0u : 16u * rt) + r, N - 1);
+                const uint8_t* base = (GU && rt == 1) ? w_up : w;
+                load_pair(base + static_cast<size_t>(n) * row_bytes + static_cast<size_t>(p) * kPairBytes,
                           raw[rt * STEPS + s]);
             }
         }
@@ -283,6 +293,22 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
         }
     };
 
+    // The KS partial tiles of part slot `tile` summed in slice order at
+    // (row, token); with GU, silu(gate) * up from the slot's gate tile and the
+    // up tile MT slots after it.
+    auto reduced = [&](int tile, int row, int tok) {
+        float sum = part[0][tile][row][tok];
+#pragma unroll
+        for (int k = 1; k < KS; ++k) sum += part[k][tile][row][tok];
+        if constexpr (GU) {
+            float up = part[0][tile + MT][row][tok];
+#pragma unroll
+            for (int k = 1; k < KS; ++k) up += part[k][tile + MT][row][tok];
+            sum = silu(sum) * up;
+        }
+        return sum;
+    };
+
     auto process = [&](uint32_t it, uint32_t (&buf)[RT * STEPS][9], uint32_t next, auto refill) {
         if constexpr (TR) {
             // LDS operations of a wave complete in order: the stage is read
@@ -307,15 +333,12 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
 #pragma unroll
                 for (int r = 0; r < 4; ++r) part[kw][rt * MT + mt][4 * lg + r][li] = acc[rt][mt][r];
         __syncthreads();
-        for (int o = tid; o < 256 * RT * MT; o += KS * 64) {
+        for (int o = tid; o < 256 * (GU ? 1 : RT) * MT; o += KS * 64) {
             const int row = o & 15, tok = (o >> 4) & 15, tile = o >> 8;
-            const int rt = tile / MT, mt = tile % MT;
-            float sum = part[0][tile][row][tok];
-#pragma unroll
-            for (int k = 1; k < KS; ++k) sum += part[k][tile][row][tok];
+            const int rt = GU ? 0 : tile / MT, mt = tile % MT;
             const uint32_t n = rows_of(it) + 16u * rt + static_cast<uint32_t>(row);
             const uint32_t m = tok0 + 16u * mt + static_cast<uint32_t>(tok);
-            if (n < N && m < M) y[static_cast<size_t>(m) * N + n] = to_out<OutT>(sum);
+            if (n < N && m < M) y[static_cast<size_t>(m) * N + n] = to_out<OutT>(reduced(tile, row, tok));
         }
         __syncthreads();
     };
@@ -359,17 +382,15 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
                         for (int r = 0; r < 4; ++r)
                             part[kw][(i * RT + rt) * MT + mt][4 * lg + r][li] = accs[c0 + i][rt][mt][r];
             __syncthreads();
-            for (int o = tid; o < 256 * kParts; o += KS * 64) {
-                const int row = o & 15, tok = (o >> 4) & 15, tile = o >> 8;
-                const int i = tile / (RT * MT), rt = (tile / MT) % RT, mt = tile % MT;
+            for (int o = tid; o < 256 * kChunk * (GU ? 1 : RT) * MT; o += KS * 64) {
+                const int row = o & 15, tok = (o >> 4) & 15, t = o >> 8;  // t: (item, [rt,] mt)
+                const int i = t / ((GU ? 1 : RT) * MT), rt = GU ? 0 : (t / MT) % RT, mt = t % MT;
                 const uint32_t it = first + static_cast<uint32_t>(c0 + i) * groups;
                 if (it >= items) continue;
-                float sum = part[0][tile][row][tok];
-#pragma unroll
-                for (int k = 1; k < KS; ++k) sum += part[k][tile][row][tok];
                 const uint32_t n = rows_of(it) + 16u * rt + static_cast<uint32_t>(row);
                 const uint32_t m = tok0 + 16u * mt + static_cast<uint32_t>(tok);
-                if (n < N && m < M) y[static_cast<size_t>(m) * N + n] = to_out<OutT>(sum);
+                if (n < N && m < M)
+                    y[static_cast<size_t>(m) * N + n] = to_out<OutT>(reduced((i * RT + rt) * MT + mt, row, tok));
             }
         }
     } else if constexpr (TR && D == 1) {
@@ -397,7 +418,8 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     }
 }
 
-template <int KS, int STEPS, int MT, int D, int G, int RT, bool TR = false, int LAZY = 0, bool XC = false>
+template <int KS, int STEPS, int MT, int D, int G, int RT, bool TR = false, int LAZY = 0, bool XC = false,
+          bool GU = false>
 hipError_t launch_skinny(const Problem& p) {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -406,7 +428,8 @@ hipError_t launch_skinny(const Problem& p) {
             n = 256;
         return n;
     }();
-    const uint32_t row_tiles = (p.N + 16 * RT - 1) / (16 * RT);
+    constexpr uint32_t kItemRows = GU ? 16u : 16u * RT;
+    const uint32_t row_tiles = (p.N + kItemRows - 1) / kItemRows;
     const uint32_t token_groups = (p.M + 16 * MT - 1) / (16 * MT);
     const uint64_t items64 = static_cast<uint64_t>(row_tiles) * token_groups;
     if (items64 > 0x7fffffffull) return hipErrorInvalidConfiguration;
@@ -423,12 +446,14 @@ hipError_t launch_skinny(const Problem& p) {
     const uint32_t per_xcd = groups / 8u;
     const dim3 grid(groups), block(KS * 64);
     if (p.out == OutType::F32) {
-        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float, LAZY, XC>), grid, block, 0, p.stream,
-                           static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float, LAZY, XC, GU>), grid, block, 0,
+                           p.stream, static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
+                           static_cast<const uint8_t*>(p.w_up),
                            static_cast<float*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
     } else {
-        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, _Float16, LAZY, XC>), grid, block, 0, p.stream,
-                           static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, _Float16, LAZY, XC, GU>), grid, block, 0,
+                           p.stream, static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
+                           static_cast<const uint8_t*>(p.w_up),
                            static_cast<_Float16*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
     }
     return hipGetLastError();
@@ -446,6 +471,9 @@ hipError_t launch_skinny(const Problem& p) {
 #define MOTE_SKINNY_TRC(KS, STEPS, MT, D, G)                                                      \
     Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d" #D "_g" #G "_r1_tr_c", Kind::SkinnyMfma, KS, \
             STEPS, MT, &launch_skinny<KS, STEPS, MT, D, G, 1, true, 0, true>}
+#define MOTE_SKINNY_GU(KS, STEPS, MT, D, L, XC, SUFFIX)                                           \
+    Variant{"gateup_skinny_k" #KS "_s" #STEPS "_t" #MT "_d" #D SUFFIX, Kind::GateUpSkinny, KS, STEPS, MT, \
+            &launch_skinny<KS, STEPS, MT, D, 1, 2, true, L, XC, true>}
 #define MOTE_SKINNY_TR(KS, STEPS, MT, D, G)                                                       \
     Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d" #D "_g" #G "_r1_tr", Kind::SkinnyMfma, KS, \
             STEPS, MT, &launch_skinny<KS, STEPS, MT, D, G, 1, true>}
@@ -467,6 +495,10 @@ const Variant kSkinny[] = {
     MOTE_SKINNY_TRLC(16, 1, 1, 1, 4), MOTE_SKINNY_TRLC(16, 1, 1, 1, 8), MOTE_SKINNY_TRLC(8, 2, 1, 1, 4),
     MOTE_SKINNY_TRLC(8, 2, 1, 1, 8), MOTE_SKINNY_TRLC(4, 4, 1, 1, 4), MOTE_SKINNY_TRC(8, 2, 2, 2, 1),
     MOTE_SKINNY_TRC(16, 1, 2, 2, 1),
+    MOTE_SKINNY_GU(8, 2, 1, 1, 0, false, ""), MOTE_SKINNY_GU(16, 1, 1, 1, 4, false, "_l4"),
+    MOTE_SKINNY_GU(16, 1, 1, 1, 4, true, "_l4_c"), MOTE_SKINNY_GU(8, 2, 1, 1, 4, true, "_l4_c"),
+    MOTE_SKINNY_GU(8, 2, 1, 1, 8, false, "_l8"), MOTE_SKINNY_GU(8, 2, 1, 1, 8, true, "_l8_c"),
+    MOTE_SKINNY_GU(8, 2, 2, 1, 0, true, "_c"),
 };
 
 #undef MOTE_SKINNY
@@ -474,6 +506,7 @@ const Variant kSkinny[] = {
 #undef MOTE_SKINNY_TRL
 #undef MOTE_SKINNY_TRLC
 #undef MOTE_SKINNY_TRC
+#undef MOTE_SKINNY_GU
 
 }  // namespace
 
@@ -483,12 +516,14 @@ const Variant* skinny_mfma_variants(int* count) {
 }
 
 // K exactly KS * STEPS * 256 (each wave one K slice of whole steps), x 16-byte
-// and w dword aligned, at most 64 tokens (MT token tiles per pass, RT row
-// tiles per item).
+// and w (and the up matrix of a gate/up) dword aligned, at most 64 tokens (MT
+// token tiles per pass, RT row tiles per item).
 bool skinny_mfma_supports(const Variant& v, const Problem& p) {
     const uint32_t span = static_cast<uint32_t>(v.p0) * static_cast<uint32_t>(v.p1) * 256u;
+    const bool up_ok = v.kind != Kind::GateUpSkinny ||
+                       (p.w_up != nullptr && reinterpret_cast<uintptr_t>(p.w_up) % 4 == 0);
     return p.M >= 1 && p.M <= 64 && p.K == span && reinterpret_cast<uintptr_t>(p.w) % 4 == 0 &&
-           reinterpret_cast<uintptr_t>(p.x) % 16 == 0;
+           reinterpret_cast<uintptr_t>(p.x) % 16 == 0 && up_ok;
 }
 
 }  // namespace mote::q4_0

@@ -166,38 +166,62 @@ def test_prefill_mfma(stream, oracle, m):
     check_against_oracle(oracle, y, x, w, m, n, k, columns=sample_columns(n, 128))
 
 
-@pytest.mark.parametrize("m", [64, 256, 512])
-def test_fused_gate_up_silu(stream, oracle, m):
-    k, n = 4096, 14336
-    x = normal_x(wl.seed_for(4, 0), m, k)
-    wg = weights(wl.seed_for(4, 1), n, k)
-    wu = weights(wl.seed_for(4, 2), n, k)
-    xb, gb, ub = DeviceBuffer.from_array(x), DeviceBuffer.from_array(wg), DeviceBuffer.from_array(wu)
-    yb = DeviceBuffer(m * n * 4)
-    ops.q4_0_gate_up_silu_f32(xb.ptr, gb.ptr, ub.ptr, yb.ptr, m, n, k, stream)
-    # concatenated [2N, K] form with up == NULL
-    cat = DeviceBuffer.from_array(np.concatenate([wg, wu]))
-    yc = DeviceBuffer(m * n * 4)
-    ops.q4_0_gate_up_silu_f32(xb.ptr, cat.ptr, None, yc.ptr, m, n, k, stream)
+def run_gate_up(stream, x, wg, wu, m, n, k, dispatch=None, f16_out=False, concatenated=False):
+    """The fused gate/up through the C ABI (gate and up buffers, or one
+    concatenated [2N, K] buffer with up = NULL); returns y as f32 [m, n]."""
+    xb = DeviceBuffer.from_array(x)
+    if concatenated:
+        gb, ub = DeviceBuffer.from_array(np.concatenate([wg, wu])), None
+    else:
+        gb, ub = DeviceBuffer.from_array(wg), DeviceBuffer.from_array(wu)
+    out_bytes = m * n * (2 if f16_out else 4)
+    yb = DeviceBuffer(out_bytes)
+    yb.upload(np.full(out_bytes, 0xA5, dtype=np.uint8))  # sentinel: every element must be written
+    up = None if ub is None else ub.ptr
+    if dispatch is not None:
+        dispatch.gate_up_silu(xb.ptr, gb.ptr, up, yb.ptr, m, n, k, stream, f16_out=f16_out)
+    else:
+        assert not f16_out
+        ops.q4_0_gate_up_silu_f32(xb.ptr, gb.ptr, up, yb.ptr, m, n, k, stream)
     stream.synchronize()
-    y = yb.download(np.float32).reshape(m, n)
-    assert np.array_equal(y, yc.download(np.float32).reshape(m, n))
-    cols = sample_columns(n, 96)
+    y = yb.download(np.uint16 if f16_out else np.float32)
+    return (bits_to_f32(y) if f16_out else y).reshape(m, n)
+
+
+def check_gate_up(oracle, y, x, wg, wu, m, n, k, cols=None, f16_out=False, what="gate/up"):
+    """silu(g) u against the f64 oracle: the linear bound of g and of u
+    propagated through the product (|d silu/dg| <= 1.1), so
+    |dy| <= 1.1 |u| tol_g + |silu(g)| tol_u (+2^-11 |y| for f16 outputs)."""
+    from helpers import linear_tolerance
+
     y64 = oracle.gate_up_silu_f64(bits_to_f32(x), wg, wu, m, n, k, cols)
     g64 = oracle.quantized_linear_f64(bits_to_f32(x), wg, m, n, k, cols)
     u64 = oracle.quantized_linear_f64(bits_to_f32(x), wu, m, n, k, cols)
     max_d = float(max(np.abs(q4_0_scales(wg, n, k)).max(), np.abs(q4_0_scales(wu, n, k)).max()))
     max_x = float(np.abs(bits_to_f32(x)).max())
-    # silu(g) u: propagate the linear bound of g and u through the product
-    # (|d silu/dg| <= 1.1): |dy| <= 1.1 |u| tol_g + |silu(g)| tol_u.
-    from helpers import linear_tolerance
-
     silu = g64 / (1.0 + np.exp(-g64))
     tol = 1.1 * np.abs(u64) * linear_tolerance(g64, k, max_d, max_x) + np.abs(silu) * linear_tolerance(
         u64, k, max_d, max_x
     )
-    err = np.abs(y[:, cols] - y64)
-    assert np.all(err <= np.maximum(tol, 1e-3 * np.abs(y64))), float(np.max(err - tol))
+    tol = np.maximum(tol, 1e-3 * np.abs(y64)) + (F16_REL * np.abs(y64) if f16_out else 0.0)
+    got = y if cols is None else y[:, cols]
+    err = np.abs(got - y64)
+    assert np.all(err <= tol), f"{what}: max excess {float(np.max(err - tol))}"
+
+
+@pytest.mark.parametrize("m", [1, 4, 16, 32, 64, 256, 512])
+def test_fused_gate_up_silu(stream, oracle, m):
+    """Default entry point at every token count of the path (the skinny gate/up
+    up to 64 tokens, the prefill tiles above), separate and concatenated
+    weight buffers giving identical outputs."""
+    k, n = 4096, 14336
+    x = normal_x(wl.seed_for(4, 0), m, k)
+    wg = weights(wl.seed_for(4, 1), n, k)
+    wu = weights(wl.seed_for(4, 2), n, k)
+    y = run_gate_up(stream, x, wg, wu, m, n, k)
+    yc = run_gate_up(stream, x, wg, wu, m, n, k, concatenated=True)
+    assert np.array_equal(y, yc)
+    check_gate_up(oracle, y, x, wg, wu, m, n, k, cols=sample_columns(n, 96), what=f"gate/up M={m}")
 
 
 # --- every kernel variant, ragged and misaligned shapes ------------------------------
@@ -273,7 +297,7 @@ def test_every_stream_variant(stream, oracle, variant):
 
 
 def _skinny_k(variant):
-    ks, rest = variant.split("_mfma_k")[1].split("_s")
+    ks, rest = variant.split("_k", 1)[1].split("_s", 1)
     return int(ks) * int(rest.split("_t")[0]) * 256
 
 
@@ -308,7 +332,7 @@ def test_every_mfma_variant(stream, oracle, variant):
         check_against_oracle(oracle, y, x, w, m, n, k, what=f"{variant} {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("variant", _variants("gateup_"))
+@pytest.mark.parametrize("variant", [v for v in _variants("gateup_") if not v.startswith("gateup_skinny_")])
 def test_every_gate_up_variant(stream, oracle, variant):
     d = ops.Q4_0Dispatch()
     d.force(variant)
@@ -322,6 +346,25 @@ def test_every_gate_up_variant(stream, oracle, variant):
     y = yb.download(np.float32).reshape(m, n)
     y64 = oracle.gate_up_silu_f64(bits_to_f32(x), wg, wu, m, n, k)
     assert np.all(np.abs(y - y64) <= np.maximum(2e-2, 2e-3 * np.abs(y64))), float(np.max(np.abs(y - y64)))
+
+
+@pytest.mark.parametrize("variant", _variants("gateup_skinny_"))
+def test_every_skinny_gate_up_variant(stream, oracle, variant):
+    """Skinny gate/up items (one gate and one up row tile): one token, tokens
+    padded inside a tile, one over a tile, the 64-token maximum, N ragged
+    against the 16-row tiles, several items per workgroup (20 x 14336), f32
+    and f16 outputs."""
+    d = ops.Q4_0Dispatch()
+    d.force(variant)
+    k = _skinny_k(variant)
+    for m, n in [(1, 100), (5, 33), (16, 16), (17, 130), (33, 7), (64, 80), (20, 14336)]:
+        x = normal_x(wl.seed_for(15, m), m, k)
+        wg, wu = weights(wl.seed_for(15, 100 + n), n, k), weights(wl.seed_for(15, 200 + n), n, k)
+        y = run_gate_up(stream, x, wg, wu, m, n, k, dispatch=d)
+        cols = None if n < 1000 else sample_columns(n, 96)
+        check_gate_up(oracle, y, x, wg, wu, m, n, k, cols=cols, what=f"{variant} {m}x{n}x{k}")
+    y16 = run_gate_up(stream, x, wg, wu, m, n, k, dispatch=d, f16_out=True)
+    check_gate_up(oracle, y16, x, wg, wu, m, n, k, cols=cols, f16_out=True, what=f"{variant} f16")
 
 
 @pytest.mark.parametrize(
