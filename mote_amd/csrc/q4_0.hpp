@@ -21,7 +21,8 @@ struct Problem {
 };
 
 enum class Kind : int { Gemv = 0, Mfma = 1, Generic = 2, GateUpMfma = 3, GateUpGeneric = 4, GemvRows = 5,
-                        GemvStream = 6, SkinnyMfma = 7, Q8Stream = 8, Q8Generic = 9, GateUpSkinny = 10 };
+                        GemvStream = 6, SkinnyMfma = 7, Q8Stream = 8, Q8Generic = 9, GateUpSkinny = 10,
+                        GateUpStream = 11 };
 
 struct Variant {
     const char* name;

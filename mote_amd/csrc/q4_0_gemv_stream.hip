@@ -18,6 +18,10 @@
 // over more of the matrix and lowers the achieved HBM rate, also for a pure
 // read of the same pattern.
 //
+// Fused gate/up (GU, one token, unsplit rows): a row group reads row n of the
+// gate and of the up matrix in the same step and keeps silu(gate) * up, the
+// decode form of the operation the skinny and prefill kernels fuse.
+//
 // x is staged once per workgroup through LDS (coalesced 16-byte loads, one
 // 144-byte slot per 128-byte pair chunk so the per-lane reads hit distinct
 // banks) and kept in registers, permuted into the order the weight operands
@@ -229,11 +233,14 @@ struct FmtQ8 {
     }
 };
 
-template <class F, int P, int S, int D, int MT, bool LAG, typename OutT>
+template <class F, int P, int S, int D, int MT, bool LAG, typename OutT, bool GU = false>
 __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint16_t* __restrict__ x,
                                                                      const uint8_t* __restrict__ w,
+                                                                     const uint8_t* __restrict__ w_up,
                                                                      OutT* __restrict__ y, uint32_t N,
                                                                      uint32_t K, uint32_t total_groups) {
+    static_assert(!GU || (S == 1 && MT == 1), "the gate/up GEMV keeps whole rows of one token");
+    constexpr int NW = GU ? 2 : 1;             // matrices read per row: gate (and up)
     constexpr int kGroups = kStreamWaves / S;  // row groups per workgroup
     extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
     const int tid = static_cast<int>(threadIdx.x);
@@ -265,10 +272,15 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
     // largest); the others compute clamped rows and store nothing.
     const uint32_t g0 = blockIdx.x * kGroups;
     const uint32_t trips = S == 1 ? nrows : (g0 < N ? (N - 1 - g0) / total_groups + 1 : 0);
-    auto load_row = [&](uint32_t jj, uint32_t (&b)[P][F::kDwords]) {
-        const uint8_t* row = w + static_cast<size_t>(min(g + jj * total_groups, last)) * row_bytes;
+    auto load_row = [&](uint32_t jj, uint32_t (&b)[NW * P][F::kDwords]) {
+        const size_t offset = static_cast<size_t>(min(g + jj * total_groups, last)) * row_bytes;
 #pragma unroll
-        for (int i = 0; i < P; ++i) F::load(row + static_cast<size_t>(pc[i]) * F::kPairBytes, b[i]);
+        for (int mat = 0; mat < NW; ++mat) {
+            const uint8_t* row = (mat == 0 ? w : w_up) + offset;
+#pragma unroll
+            for (int i = 0; i < P; ++i)
+                F::load(row + static_cast<size_t>(pc[i]) * F::kPairBytes, b[mat * P + i]);
+        }
     };
 
     // x chunk loads first (P S MT 16-byte chunks per thread; chunk c of the
@@ -290,7 +302,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
     // wave then waits for row j + 1 before issuing more; without it, D + 1
     // rows are in flight while it waits).
     constexpr int R = D + 1;
-    uint32_t buf[R][P][F::kDwords];
+    uint32_t buf[R][NW * P][F::kDwords];
 #pragma unroll
     for (int d = 0; d < D; ++d) load_row(static_cast<uint32_t>(d), buf[d]);
     __builtin_amdgcn_sched_barrier(0);
@@ -344,7 +356,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
             }
             if (slice == 0 && static_cast<uint32_t>(lane) < count)
                 y[static_cast<size_t>(m) * N + g + (first + static_cast<uint32_t>(lane)) * total_groups] =
-                    to_out<OutT>(F::kFinal * t);
+                    to_out<OutT>(GU ? t : F::kFinal * t);  // gate/up sums are final already
         }
     };
     float mine[MT];
@@ -357,13 +369,16 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
             const uint32_t jj = j + static_cast<uint32_t>(u);
             load_row(jj + D, buf[(u + D) % R]);
             __builtin_amdgcn_sched_barrier(0);
-            float part[MT];
+            float part[MT], part_up = 0.0f;
 #pragma unroll
             for (int m = 0; m < MT; ++m) part[m] = 0.0f;
 #pragma unroll
             for (int i = 0; i < P; ++i) {
                 if constexpr (MT == 1) {  // masks feed the dot chains directly: fewer live registers
                     part[0] += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, F::dot(buf[u][i], xv[0][i])) & keep[i]);
+                    if constexpr (GU)
+                        part_up += __builtin_bit_cast(
+                            float, __builtin_bit_cast(uint32_t, F::dot(buf[u][P + i], xv[0][i])) & keep[i]);
                 } else {
                     Unpacked wu;
                     F::unpack(buf[u][i], wu);
@@ -375,7 +390,8 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
             const bool mine_lane = jj < trips && static_cast<uint32_t>(lane) == (jj & 63u);
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                const float s = wave_sum(part[m]);
+                float s = wave_sum(part[m]);
+                if constexpr (GU) s = silu(F::kFinal * s) * (F::kFinal * wave_sum(part_up));
                 mine[m] = mine_lane ? s : mine[m];
             }
             if ((jj & 63u) == 63u && jj < trips)  // uniform over the workgroup
@@ -383,7 +399,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
             if constexpr (LAG) {
                 // Row j + 1 arrives before row j + 1 + D is issued: D rows in
                 // flight at any time, never D + 1.
-                constexpr int kLater = 9 * P * (D - 1);  // loads of rows j + 2 .. j + D
+                constexpr int kLater = 9 * NW * P * (D - 1);  // loads of rows j + 2 .. j + D
                 __builtin_amdgcn_s_waitcnt((kLater & 0xF) | ((kLater >> 4) << 14) | 0x0F70);
             }
         }
@@ -393,7 +409,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
     if (base < trips) flush(mine, base, nrows > base ? nrows - base : 0u);
 }
 
-template <int P, int S, int D, int G, int MT = 1, bool LAG = true, class F = FmtQ4>
+template <int P, int S, int D, int G, int MT = 1, bool LAG = true, class F = FmtQ4, bool GU = false>
 hipError_t launch_gemv_stream(const Problem& p) {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -410,13 +426,15 @@ hipError_t launch_gemv_stream(const Problem& p) {
     const size_t lds = static_cast<size_t>(p.K / 64) * MT * kSlot + (S > 1 ? kStreamThreads * sizeof(float) : 0);
     const dim3 grid(groups), block(kStreamThreads);
     if (p.out == OutType::F32) {
-        hipLaunchKernelGGL((gemv_stream_kernel<F, P, S, D, MT, LAG, float>), grid, block, lds, p.stream,
+        hipLaunchKernelGGL((gemv_stream_kernel<F, P, S, D, MT, LAG, float, GU>), grid, block, lds, p.stream,
                            static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
-                           static_cast<float*>(p.y), p.N, p.K, total_groups);
+                           static_cast<const uint8_t*>(p.w_up), static_cast<float*>(p.y), p.N, p.K,
+                           total_groups);
     } else {
-        hipLaunchKernelGGL((gemv_stream_kernel<F, P, S, D, MT, LAG, _Float16>), grid, block, lds, p.stream,
+        hipLaunchKernelGGL((gemv_stream_kernel<F, P, S, D, MT, LAG, _Float16, GU>), grid, block, lds, p.stream,
                            static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
-                           static_cast<_Float16*>(p.y), p.N, p.K, total_groups);
+                           static_cast<const uint8_t*>(p.w_up), static_cast<_Float16*>(p.y), p.N, p.K,
+                           total_groups);
     }
     return hipGetLastError();
 }
@@ -442,6 +460,9 @@ hipError_t launch_gemv_stream(const Problem& p) {
 #define MOTE_Q8_M(MT, G)                                                             \
     Variant{"q8_stream_m" #MT "_d1q_g" #G, Kind::Q8Stream, 1, 1, G,                \
             &launch_gemv_stream<1, 1, 1, G, MT, false, FmtQ8>, MT}
+#define MOTE_STREAM_GU(P, G)                                                             \
+    Variant{"gateup_stream_p" #P "_d1_g" #G, Kind::GateUpStream, P, 1, G,               \
+            &launch_gemv_stream<P, 1, 1, G, 1, true, FmtQ4, true>}
 #define MOTE_STREAM_MQ(MT, D, G)                                                         \
     Variant{"stream_m" #MT "_d" #D "q_g" #G, Kind::GemvStream, 1, D, G,                 \
             &launch_gemv_stream<1, 1, D, G, MT, false>, MT}
@@ -459,6 +480,7 @@ const Variant kStream[] = {
     MOTE_STREAM_MQ(2, 1, 1), MOTE_STREAM_MQ(2, 1, 2),
     MOTE_Q8("d1_g1", 1, 1), MOTE_Q8("d1_g2", 1, 2), MOTE_Q8("s2_d1_g1", 2, 1), MOTE_Q8("s2_d1_g2", 2, 2),
     MOTE_Q8("s4_d1_g1", 4, 1), MOTE_Q8("s4_d1_g2", 4, 2), MOTE_Q8_M(2, 1), MOTE_Q8_M(4, 1),
+    MOTE_STREAM_GU(1, 1), MOTE_STREAM_GU(1, 2), MOTE_STREAM_GU(2, 1), MOTE_STREAM_GU(2, 2),
 };
 
 #undef MOTE_STREAM
@@ -470,6 +492,7 @@ const Variant kStream[] = {
 #undef MOTE_STREAM_MQ
 #undef MOTE_Q8
 #undef MOTE_Q8_M
+#undef MOTE_STREAM_GU
 
 }  // namespace
 
@@ -479,11 +502,14 @@ const Variant* gemv_stream_variants(int* count) {
 }
 
 // One token (or exactly the variant's token count), K a multiple of 64 and at
-// most 4096 per 64-pair slot of a row, x 16-byte and w dword aligned.
+// most 4096 per 64-pair slot of a row, x 16-byte and w (and the up matrix of a
+// gate/up) dword aligned.
 bool gemv_stream_supports(const Variant& v, const Problem& p) {
     const uint32_t tokens = v.tokens > 0 ? static_cast<uint32_t>(v.tokens) : 1u;
+    const bool up_ok = v.kind != Kind::GateUpStream ||
+                       (p.w_up != nullptr && reinterpret_cast<uintptr_t>(p.w_up) % 4 == 0);
     return p.M == tokens && p.K % 64 == 0 && p.K > 0 && p.K <= 4096u * static_cast<uint32_t>(v.p0) &&
-           reinterpret_cast<uintptr_t>(p.w) % 4 == 0 && reinterpret_cast<uintptr_t>(p.x) % 16 == 0;
+           reinterpret_cast<uintptr_t>(p.w) % 4 == 0 && reinterpret_cast<uintptr_t>(p.x) % 16 == 0 && up_ok;
 }
 
 }  // namespace mote::q4_0
