@@ -124,14 +124,62 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t q, f16x2 d, uint32_t c1024, u
     return f16x8{l02.x, l02.y, l13.x, l13.y, h02.x, h02.y, h13.x, h13.y};
 }
 
+// GGML Q8_0 (crates/mote-reference/src/quantized.rs:191-195): a block is an
+// f16 scale d and 32 two's-complement bytes v, value v d; a pair of blocks is
+// 68 bytes (17 dwords), dword aligned whenever the row is.
+constexpr uint32_t kQ8PairBytes = 68;
+
+// Loads the seventeen dwords of the Q8_0 pair that starts at `p`.
+__device__ __forceinline__ void load_pair_q8(const uint8_t* p, uint32_t (&d)[17]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const u32x4_a4 v = *reinterpret_cast<const u32x4_a4*>(p + 16 * i);
+        d[4 * i + 0] = v.x; d[4 * i + 1] = v.y; d[4 * i + 2] = v.z; d[4 * i + 3] = v.w;
+    }
+    d[16] = *reinterpret_cast<const uint32_t*>(p + 64);
+}
+
+// Dword i (0..15) of a Q8_0 pair's 64 value bytes (elements 4i .. 4i + 3):
+// block 0's bytes start at pair byte 2 and are re-aligned with one v_perm,
+// block 1's are dwords 9 .. 16.
+__device__ __forceinline__ uint32_t q8_bytes(const uint32_t (&d)[17], int i) {
+    return i < 8 ? __builtin_amdgcn_perm(d[i + 1], d[i], 0x05040302u) : d[i + 1];
+}
+
+// Eight Q8_0 values (bytes b0..b3 of q0, b4..b7 of q1) times d, in the order
+// [b0, b2, b1, b3, b4, b6, b5, b7], as a binary16 pair hi + lo: XOR 0x80 turns
+// v into u = v + 128, a v_perm places u as the low byte of binary16 1024
+// (0x64uu, ulp 1), which reads 1024 + u; adding -1152 gives v exactly; hi is
+// v d rounded once and lo = fma(v, d, -hi) the rounded remainder, so hi + lo
+// carries v d to about 2^-22 (a single binary16 product, enough for the
+// 4-bit values of Q4_0, is not for 8-bit values).  `c64` holds 0x64 in every
+// byte (a register: gfx9-family VOP3 instructions take no literal).
+struct F16x8Pair {
+    f16x8 hi, lo;
+};
+__device__ __forceinline__ F16x8Pair dequant8_q8(uint32_t q0, uint32_t q1, f16x2 d, uint32_t c64) {
+    const f16x2 bias = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+    const uint32_t u0 = q0 ^ 0x80808080u, u1 = q1 ^ 0x80808080u;
+    const f16x2 v02 = as_h2(__builtin_amdgcn_perm(c64, u0, 0x04020400u)) + bias;
+    const f16x2 v13 = as_h2(__builtin_amdgcn_perm(c64, u0, 0x04030401u)) + bias;
+    const f16x2 v46 = as_h2(__builtin_amdgcn_perm(c64, u1, 0x04020400u)) + bias;
+    const f16x2 v57 = as_h2(__builtin_amdgcn_perm(c64, u1, 0x04030401u)) + bias;
+    const f16x2 h02 = v02 * d, h13 = v13 * d, h46 = v46 * d, h57 = v57 * d;
+    const f16x2 l02 = __builtin_elementwise_fma(v02, d, -h02), l13 = __builtin_elementwise_fma(v13, d, -h13);
+    const f16x2 l46 = __builtin_elementwise_fma(v46, d, -h46), l57 = __builtin_elementwise_fma(v57, d, -h57);
+    return {f16x8{h02.x, h02.y, h13.x, h13.y, h46.x, h46.y, h57.x, h57.y},
+            f16x8{l02.x, l02.y, l13.x, l13.y, l46.x, l46.y, l57.x, l57.y}};
+}
+
 // The two VGPR constants of dequant8.
 struct DequantConsts {
-    uint32_t c1024, c64;
+    uint32_t c1024, c64, q8;  // q8: the 0x64 bytes of dequant8_q8
 };
 __device__ __forceinline__ DequantConsts dequant_consts() {
     DequantConsts c;
     asm("v_mov_b32 %0, 0x64006400" : "=v"(c.c1024));
     asm("v_mov_b32 %0, 0x54005400" : "=v"(c.c64));
+    asm("v_mov_b32 %0, 0x64646464" : "=v"(c.q8));
     return c;
 }
 

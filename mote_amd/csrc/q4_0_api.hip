@@ -72,7 +72,8 @@ bool kind_matches(const Variant& v, Op op) {
     if (op == Op::GateUp)
         return v.kind == Kind::GateUpMfma || v.kind == Kind::GateUpSkinny || v.kind == Kind::GateUpStream ||
                v.kind == Kind::GateUpGeneric;
-    if (op == Op::LinearQ8) return v.kind == Kind::Q8Stream || v.kind == Kind::Q8Generic;
+    if (op == Op::LinearQ8)
+        return v.kind == Kind::Q8Stream || v.kind == Kind::Q8Skinny || v.kind == Kind::Q8Generic;
     return v.kind == Kind::Gemv || v.kind == Kind::GemvRows || v.kind == Kind::GemvStream ||
            v.kind == Kind::SkinnyMfma || v.kind == Kind::Mfma || v.kind == Kind::Generic;
 }
@@ -85,7 +86,8 @@ bool supports(const Variant& v, const Problem& p) {
         case Kind::GateUpStream:
         case Kind::Q8Stream: return gemv_stream_supports(v, p);
         case Kind::SkinnyMfma:
-        case Kind::GateUpSkinny: return skinny_mfma_supports(v, p);
+        case Kind::GateUpSkinny:
+        case Kind::Q8Skinny: return skinny_mfma_supports(v, p);
         case Kind::Mfma:
         case Kind::GateUpMfma: return mfma_supports(v, p);
         default: return true;
@@ -110,7 +112,8 @@ std::vector<const Variant*> candidates(const Problem& p, Op op) {
                                 v->kind == Kind::GemvStream || v->kind == Kind::Q8Stream ||
                                 v->kind == Kind::GateUpStream;
         if (vector_alu && p.M >= 64) continue;
-        if ((v->kind == Kind::SkinnyMfma || v->kind == Kind::GateUpSkinny) && p.M > 64) continue;
+        const bool skinny = v->kind == Kind::SkinnyMfma || v->kind == Kind::GateUpSkinny || v->kind == Kind::Q8Skinny;
+        if (skinny && p.M > 64) continue;
         if ((v->kind == Kind::Mfma || v->kind == Kind::GateUpMfma) && p.M < 64) continue;
         out.push_back(v);
     }
@@ -185,6 +188,27 @@ const Variant* skinny_gate_up_heuristic(const Problem& p) {
     return v && skinny_mfma_supports(*v, p) ? v : nullptr;
 }
 
+// Q8_0 skinny GEMM (the Q4_0 kernels' shapes with 68-byte pairs), 3 to 64
+// tokens.  Measured on MI355X at K = 4096, N = 14336: 15.7 us at 8 tokens,
+// 17.4 us at 16, 22.6 us at 32 (two token tiles per item above 16 tokens)
+// and 29.3 us at 64, where the generic kernel took 117-895 us; coalesced
+// activation loads pay above 8 tokens.  (1, 2 and 4 tokens stay on the
+// streaming GEMV: 4 x 4096 x 4096 in 6.9 us against 8.1 us here.)
+const Variant* skinny_q8_heuristic(const Problem& p) {
+    const uint64_t items = static_cast<uint64_t>((p.N + 15) / 16) * ((p.M + 15) / 16);
+    const uint64_t per_group = (items + device_cus() - 1) / static_cast<uint64_t>(device_cus());
+    const bool xc = p.M > 8;
+    const char* name;
+    if (per_group <= 4)
+        name = xc ? "q8_skinny_k16_s1_t1_d1_l4_c" : "q8_skinny_k16_s1_t1_d1_l4";
+    else if (p.M <= 16)
+        name = xc ? "q8_skinny_k8_s2_t1_d1_l8_c" : "q8_skinny_k8_s2_t1_d1_l8";
+    else
+        name = "q8_skinny_k16_s1_t2_d1_c";
+    const Variant* v = by_name(name);
+    return v && skinny_mfma_supports(*v, p) ? v : nullptr;
+}
+
 // Shape heuristic used when autotuning is off.
 const Variant* heuristic(const Problem& p, Op op) {
     const bool fast = fast_eligible(p);
@@ -206,6 +230,8 @@ const Variant* heuristic(const Problem& p, Op op) {
             const Variant* v = by_name(name);
             if (v && gemv_stream_supports(*v, p)) return v;
         }
+        if (fast && p.M <= 64)
+            if (const Variant* v = skinny_q8_heuristic(p)) return v;
         return by_name("q8_generic");
     }
     if (op == Op::GateUp) {

@@ -171,14 +171,7 @@ struct FmtQ8 {
     static constexpr float kFinal = 16777216.0f;            // 2^24
     static constexpr float kStart = -128.0f / 16777216.0f;  // times the block's sum of x
 
-    __device__ static void load(const uint8_t* p, uint32_t (&d)[kDwords]) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const u32x4_a4 v = *reinterpret_cast<const u32x4_a4*>(p + 16 * i);
-            d[4 * i + 0] = v.x; d[4 * i + 1] = v.y; d[4 * i + 2] = v.z; d[4 * i + 3] = v.w;
-        }
-        d[16] = *reinterpret_cast<const uint32_t*>(p + 64);
-    }
+    __device__ static void load(const uint8_t* p, uint32_t (&d)[kDwords]) { load_pair_q8(p, d); }
 
     // Dword i of the pair's 64 bytes (elements 4i .. 4i + 3) takes x as
     // (x[4i], x[4i + 2]) for bytes 0 and 2 and (x[4i + 1], x[4i + 3]) for 1, 3.
@@ -190,10 +183,7 @@ struct FmtQ8 {
         }
     }
 
-    __device__ static uint32_t bytes(const uint32_t (&raw)[kDwords], int i) {
-        // block 0: pair bytes 2 + 4i .. 5 + 4i; block 1: dwords 9 .. 16
-        return i < 8 ? __builtin_amdgcn_perm(raw[i + 1], raw[i], 0x05040302u) : raw[i + 1];
-    }
+    __device__ static uint32_t bytes(const uint32_t (&raw)[kDwords], int i) { return q8_bytes(raw, i); }
 
     __device__ static float dot(const uint32_t (&raw)[kDwords], const XPair& x) {
         float a0 = x.c0, a1 = x.c1;

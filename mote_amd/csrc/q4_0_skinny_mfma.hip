@@ -28,6 +28,11 @@
 //
 // The next item's weight loads are issued before the current item's MFMAs.
 //
+// Q8_0 weights (Q8): a pair is 68 bytes (17 dwords); MFMA t takes elements
+// 8t .. 8t + 7 of each lane's pair, dequantised by dequant8_q8 into a binary16
+// hi + lo pair (two MFMAs, so the 8-bit products keep 22 bits), and the
+// activation operand holds x at those positions in the same order.
+//
 // Fused gate/up (GU, RT = 2): row tile 0 of an item is rows n .. n + 15 of the
 // gate matrix and row tile 1 the same rows of the up matrix, and the store
 // writes y[m, n] = silu(gate) * up (the operation the prefill kernels fuse for
@@ -47,7 +52,7 @@ __device__ __forceinline__ uint32_t pick(const uint32_t* x, int a, int b) {
 }
 
 template <int KS, int STEPS, int MT, int D, int RT, bool TR, typename OutT, int LAZY = 0, bool XC = false,
-          bool GU = false>
+          bool GU = false, bool Q8 = false>
 __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __restrict__ x,
                                                              const uint8_t* __restrict__ w,
                                                              const uint8_t* __restrict__ w_up,
@@ -58,8 +63,10 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     // Transposed loads: wave-private staging of the raw pairs, [row tile][row]
     // [pair of the slice], rows padded by one dword so the 16 rows read by an
     // MFMA operand fall on distinct banks.
+    constexpr uint32_t kPB = Q8 ? kQ8PairBytes : kPairBytes;  // bytes of a block pair
+    constexpr int kDw = Q8 ? 17 : 9;                          // its dwords
     constexpr int kSlicePairs = STEPS * 4;
-    constexpr int kStageRow = kSlicePairs * kPairBytes + 4;
+    constexpr int kStageRow = kSlicePairs * kPB + 4;
     constexpr int kStageBytes = TR ? KS * RT * 16 * kStageRow : 4;
     __shared__ __attribute__((aligned(16))) uint8_t stage[kStageBytes];
     // LAZY > 0: a workgroup owns at most LAZY items and its waves reduce them
@@ -90,7 +97,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     const int li = lane & 15;  // row of the A operand, token of the B operand
     const int lg = lane >> 4;  // lane group: which of the step's 4 pairs
     const uint32_t npairs = K >> 6;
-    const size_t row_bytes = static_cast<size_t>(npairs) * kPairBytes;
+    const size_t row_bytes = static_cast<size_t>(npairs) * kPB;
     const uint32_t groups = gridDim.x;
     // XCD-aware order: workgroups of one XCD take consecutive items, so the
     // token tiles of a row tile read its weights through the same L2.
@@ -110,7 +117,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     // so one instruction spans 16 / STEPS rows of 4 STEPS neighbouring pairs,
     // and the pairs reach their MFMA lanes through the wave's LDS stage.
     constexpr int kRowsPerLoad = 16 / STEPS;
-    auto load_item = [&](uint32_t item, uint32_t (&raw)[RT * STEPS][9]) {
+    auto load_item = [&](uint32_t item, uint32_t (&raw)[RT * STEPS][kDw]) {
         const uint32_t it = min(item, items - 1);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
@@ -126,36 +133,39 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
                 }
                 const uint32_t n = min(rows_of(it) + (GU ? 0u : 16u * rt) + r, N - 1);
                 const uint8_t* base = (GU && rt == 1) ? w_up : w;
-                load_pair(base + static_cast<size_t>(n) * row_bytes + static_cast<size_t>(p) * kPairBytes,
-                          raw[rt * STEPS + s]);
+                const uint8_t* src = base + static_cast<size_t>(n) * row_bytes + static_cast<size_t>(p) * kPB;
+                if constexpr (Q8)
+                    load_pair_q8(src, raw[rt * STEPS + s]);
+                else
+                    load_pair(src, raw[rt * STEPS + s]);
             }
         }
     };
     uint8_t* my_stage = stage + (TR ? kw * RT * 16 * kStageRow : 0);
-    auto stage_item = [&](const uint32_t (&raw)[RT * STEPS][9]) {
+    auto stage_item = [&](const uint32_t (&raw)[RT * STEPS][kDw]) {
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
             for (int s = 0; s < STEPS; ++s) {
                 const int r = s * kRowsPerLoad + lane / kSlicePairs;
                 uint32_t* dst = reinterpret_cast<uint32_t*>(my_stage + (rt * 16 + r) * kStageRow +
-                                                            (lane % kSlicePairs) * kPairBytes);
+                                                            (lane % kSlicePairs) * kPB);
 #pragma unroll
-                for (int i = 0; i < 9; ++i) dst[i] = raw[rt * STEPS + s][i];
+                for (int i = 0; i < kDw; ++i) dst[i] = raw[rt * STEPS + s][i];
             }
     };
-    auto staged_pair = [&](int rt, int s, uint32_t (&c)[9]) {
+    auto staged_pair = [&](int rt, int s, uint32_t (&c)[kDw]) {
         const uint32_t* src = reinterpret_cast<const uint32_t*>(my_stage + (rt * 16 + li) * kStageRow +
-                                                                (4 * s + lg) * kPairBytes);
+                                                                (4 * s + lg) * kPB);
 #pragma unroll
-        for (int i = 0; i < 9; ++i) c[i] = src[i];
+        for (int i = 0; i < kDw; ++i) c[i] = src[i];
     };
 
     // The first item's weights, the activations (reused by every item), and
     // with D = 2 the second item's weights, issued before the activations are
     // waited for.
-    uint32_t buf0[RT * STEPS][9];
-    uint32_t buf1[RT * STEPS][9];
+    uint32_t buf0[RT * STEPS][kDw];
+    uint32_t buf1[RT * STEPS][kDw];
     load_item(first, buf0);
     // Activations of this wave's K slice for the workgroup's MT token tiles.
     // Tokens past M read row M - 1: a token only feeds its own output column
@@ -241,12 +251,19 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
             }
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                const int base = t < 4 ? 0 : 32;
-                const int e0 = base + pair_byte_element(t, 0), e1 = base + pair_byte_element(t, 1);
-                const int e2 = base + pair_byte_element(t, 2), e3 = base + pair_byte_element(t, 3);
-                const f16x2 a = as_h2(pick(xr, e0, e2)), b = as_h2(pick(xr, e1, e3));
-                const f16x2 c = as_h2(pick(xr, e0 + 16, e2 + 16)), d = as_h2(pick(xr, e1 + 16, e3 + 16));
-                xb[mt][s][t] = f16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+                if constexpr (Q8) {  // elements 8t + [0, 2, 1, 3, 4, 6, 5, 7]
+                    const int e = 8 * t;
+                    const f16x2 a = as_h2(pick(xr, e, e + 2)), b = as_h2(pick(xr, e + 1, e + 3));
+                    const f16x2 c = as_h2(pick(xr, e + 4, e + 6)), d = as_h2(pick(xr, e + 5, e + 7));
+                    xb[mt][s][t] = f16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+                } else {
+                    const int base = t < 4 ? 0 : 32;
+                    const int e0 = base + pair_byte_element(t, 0), e1 = base + pair_byte_element(t, 1);
+                    const int e2 = base + pair_byte_element(t, 2), e3 = base + pair_byte_element(t, 3);
+                    const f16x2 a = as_h2(pick(xr, e0, e2)), b = as_h2(pick(xr, e1, e3));
+                    const f16x2 c = as_h2(pick(xr, e0 + 16, e2 + 16)), d = as_h2(pick(xr, e1 + 16, e3 + 16));
+                    xb[mt][s][t] = f16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+                }
             }
         }
     }
@@ -254,40 +271,51 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     if constexpr (LAZY == 0) convert_x();
     const DequantConsts dq = dequant_consts();
 
-
-    // One item: dequantise + MFMA from `buf`, refill `buf` with item `next`
-    // right after its last use (so the refill overlaps the reduction and the
-    // other buffer's item), then reduce the KS partial tiles and store.
     // Dequantise + MFMA one item (staged in LDS with TR, else from `buf`)
     // into `acc`.
-    auto mma_item = [&](const uint32_t (&buf)[RT * STEPS][9], f32x4 (&acc)[RT][MT]) {
+    auto mma_item = [&](const uint32_t (&buf)[RT * STEPS][kDw], f32x4 (&acc)[RT][MT]) {
 #pragma unroll
         for (int s = 0; s < STEPS; ++s) {
-            uint32_t q[RT][8];
+            uint32_t q[RT][Q8 ? 16 : 8];
             f16x2 d0[RT], d1[RT];
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
-                uint32_t c[9];
+                uint32_t c[kDw];
                 if constexpr (TR) {
                     staged_pair(rt, s, c);
                 } else {
 #pragma unroll
-                    for (int i = 0; i < 9; ++i) c[i] = buf[rt * STEPS + s][i];
+                    for (int i = 0; i < kDw; ++i) c[i] = buf[rt * STEPS + s][i];
                 }
-                q[rt][0] = pair_q0(c);
-                q[rt][1] = c[1]; q[rt][2] = c[2]; q[rt][3] = c[3];
-                q[rt][4] = c[5]; q[rt][5] = c[6]; q[rt][6] = c[7]; q[rt][7] = c[8];
+                if constexpr (Q8) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) q[rt][i] = q8_bytes(c, i);
+                    d1[rt] = as_h2(__builtin_amdgcn_perm(c[8], c[8], 0x03020302u));
+                } else {
+                    q[rt][0] = pair_q0(c);
+                    q[rt][1] = c[1]; q[rt][2] = c[2]; q[rt][3] = c[3];
+                    q[rt][4] = c[5]; q[rt][5] = c[6]; q[rt][6] = c[7]; q[rt][7] = c[8];
+                    d1[rt] = as_h2(__builtin_amdgcn_perm(c[4], c[4], 0x03020302u));
+                }
                 d0[rt] = as_h2(__builtin_amdgcn_perm(c[0], c[0], 0x01000100u));
-                d1[rt] = as_h2(__builtin_amdgcn_perm(c[4], c[4], 0x03020302u));
             }
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt) {
-                    const f16x8 a = dequant8(q[rt][t], t < 4 ? d0[rt] : d1[rt], dq.c1024, dq.c64);
+                    if constexpr (Q8) {  // the weight as hi + lo: two MFMAs against the same x
+                        const F16x8Pair a = dequant8_q8(q[rt][2 * t], q[rt][2 * t + 1], t < 4 ? d0[rt] : d1[rt], dq.q8);
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt)
-                        acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xb[mt][s][t], acc[rt][mt], 0, 0, 0);
+                        for (int mt = 0; mt < MT; ++mt) {
+                            acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.hi, xb[mt][s][t], acc[rt][mt], 0, 0, 0);
+                            acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.lo, xb[mt][s][t], acc[rt][mt], 0, 0, 0);
+                        }
+                    } else {
+                        const f16x8 a = dequant8(q[rt][t], t < 4 ? d0[rt] : d1[rt], dq.c1024, dq.c64);
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt)
+                            acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xb[mt][s][t], acc[rt][mt], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -309,7 +337,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
         return sum;
     };
 
-    auto process = [&](uint32_t it, uint32_t (&buf)[RT * STEPS][9], uint32_t next, auto refill) {
+    auto process = [&](uint32_t it, uint32_t (&buf)[RT * STEPS][kDw], uint32_t next, auto refill) {
         if constexpr (TR) {
             // LDS operations of a wave complete in order: the stage is read
             // back below, and rewritten by the next item only after this
@@ -401,11 +429,11 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
         for (; item < items; item += groups) {
             // Copying the buffer waits for this item only; the next item's
             // loads then run under this item's arithmetic.
-            uint32_t cur[RT * STEPS][9];
+            uint32_t cur[RT * STEPS][kDw];
 #pragma unroll
             for (int s = 0; s < RT * STEPS; ++s)
 #pragma unroll
-                for (int i = 0; i < 9; ++i) cur[s][i] = buf0[s][i];
+                for (int i = 0; i < kDw; ++i) cur[s][i] = buf0[s][i];
             load_item(item + groups, buf0);
             process(item, cur, item, std::false_type{});
         }
@@ -419,7 +447,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
 }
 
 template <int KS, int STEPS, int MT, int D, int G, int RT, bool TR = false, int LAZY = 0, bool XC = false,
-          bool GU = false>
+          bool GU = false, bool Q8 = false>
 hipError_t launch_skinny(const Problem& p) {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -446,12 +474,12 @@ hipError_t launch_skinny(const Problem& p) {
     const uint32_t per_xcd = groups / 8u;
     const dim3 grid(groups), block(KS * 64);
     if (p.out == OutType::F32) {
-        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float, LAZY, XC, GU>), grid, block, 0,
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float, LAZY, XC, GU, Q8>), grid, block, 0,
                            p.stream, static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<const uint8_t*>(p.w_up),
                            static_cast<float*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
     } else {
-        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, _Float16, LAZY, XC, GU>), grid, block, 0,
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, _Float16, LAZY, XC, GU, Q8>), grid, block, 0,
                            p.stream, static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<const uint8_t*>(p.w_up),
                            static_cast<_Float16*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
@@ -474,6 +502,9 @@ hipError_t launch_skinny(const Problem& p) {
 #define MOTE_SKINNY_GU(KS, STEPS, MT, D, L, XC, SUFFIX)                                           \
     Variant{"gateup_skinny_k" #KS "_s" #STEPS "_t" #MT "_d" #D SUFFIX, Kind::GateUpSkinny, KS, STEPS, MT, \
             &launch_skinny<KS, STEPS, MT, D, 1, 2, true, L, XC, true>}
+#define MOTE_SKINNY_Q8(KS, STEPS, MT, D, L, XC, SUFFIX)                                          \
+    Variant{"q8_skinny_k" #KS "_s" #STEPS "_t" #MT "_d" #D SUFFIX, Kind::Q8Skinny, KS, STEPS, MT,    \
+            &launch_skinny<KS, STEPS, MT, D, 1, 1, true, L, XC, false, true>}
 #define MOTE_SKINNY_TR(KS, STEPS, MT, D, G)                                                       \
     Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d" #D "_g" #G "_r1_tr", Kind::SkinnyMfma, KS, \
             STEPS, MT, &launch_skinny<KS, STEPS, MT, D, G, 1, true>}
@@ -499,6 +530,9 @@ const Variant kSkinny[] = {
     MOTE_SKINNY_GU(16, 1, 1, 1, 4, true, "_l4_c"), MOTE_SKINNY_GU(8, 2, 1, 1, 4, true, "_l4_c"),
     MOTE_SKINNY_GU(8, 2, 1, 1, 8, false, "_l8"), MOTE_SKINNY_GU(8, 2, 1, 1, 8, true, "_l8_c"),
     MOTE_SKINNY_GU(8, 2, 2, 1, 0, true, "_c"),
+    MOTE_SKINNY_Q8(8, 2, 1, 1, 0, false, ""), MOTE_SKINNY_Q8(16, 1, 1, 1, 4, false, "_l4"),
+    MOTE_SKINNY_Q8(16, 1, 1, 1, 4, true, "_l4_c"), MOTE_SKINNY_Q8(8, 2, 1, 1, 8, false, "_l8"),
+    MOTE_SKINNY_Q8(8, 2, 1, 1, 8, true, "_l8_c"), MOTE_SKINNY_Q8(16, 1, 2, 1, 0, true, "_c"), MOTE_SKINNY_Q8(8, 2, 2, 1, 0, true, "_c"),
 };
 
 #undef MOTE_SKINNY
@@ -507,6 +541,7 @@ const Variant kSkinny[] = {
 #undef MOTE_SKINNY_TRLC
 #undef MOTE_SKINNY_TRC
 #undef MOTE_SKINNY_GU
+#undef MOTE_SKINNY_Q8
 
 }  // namespace
 

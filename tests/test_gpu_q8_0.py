@@ -117,7 +117,10 @@ def test_reference_kat_signed_values_and_scale(stream):
 
 # --- every kernel, bit-exact where the arithmetic is exact ------------------------------
 
-@pytest.mark.parametrize("variant", _variants("q8_"))
+STREAM_AND_GENERIC = [v for v in _variants("q8_") if not v.startswith("q8_skinny_")]
+
+
+@pytest.mark.parametrize("variant", STREAM_AND_GENERIC)
 def test_one_hot_activations_read_back_the_decode_exactly(stream, oracle, variant):
     """x = e_j per token: y = v_j d of each row with no rounding (one product,
     exact in f32, and zeros elsewhere), so the output equals the oracle's
@@ -144,7 +147,7 @@ def test_one_hot_activations_read_back_the_decode_exactly(stream, oracle, varian
             assert np.array_equal(y[t].view(np.uint32), decoded[:, j].view(np.uint32)), (variant, j)
 
 
-@pytest.mark.parametrize("variant", _variants("q8_"))
+@pytest.mark.parametrize("variant", STREAM_AND_GENERIC)
 def test_every_q8_variant(stream, oracle, variant):
     """Ragged N, idle lanes (K below a slot's 4096), K filling every slot and
     one pair past a slot boundary, N = 140001 at K = 64 (register flush past 64
@@ -174,10 +177,31 @@ def test_every_q8_variant(stream, oracle, variant):
     check(oracle, y16, x, w, m, n, k, columns=cols, f16_out=True, what=f"{variant} f16")
 
 
+@pytest.mark.parametrize("variant", _variants("q8_skinny_"))
+def test_every_q8_skinny_variant(stream, oracle, variant):
+    """Matrix-core Q8_0 skinny GEMM (K = 4096): one token, tokens padded inside
+    a 16-token tile, one over a tile, the 64-token maximum, N ragged against
+    the 16-row tiles, several items per workgroup (20 x 14336), f32 and f16
+    outputs.  The products are rounded once to binary16 before the MFMA, so
+    the check is the tolerance, not bit equality."""
+    d = ops.Q4_0Dispatch()
+    d.force(variant)
+    k = 4096
+    for m, n in [(1, 100), (3, 33), (5, 37), (16, 16), (17, 130), (32, 61), (33, 7), (64, 80), (20, 14336)]:
+        x = normal_x(wl.seed_for(24, m), m, k)
+        w = weights(wl.seed_for(24, 100 + n), n, k)
+        y = run(stream, x, w, m, n, k, dispatch=d)
+        cols = None if n < 2000 else sample_columns(n, 256)
+        check(oracle, y, x, w, m, n, k, columns=cols, what=f"{variant} {m}x{n}x{k}")
+    y16 = run(stream, x, w, m, n, k, dispatch=d, f16_out=True)
+    check(oracle, y16, x, w, m, n, k, columns=cols, f16_out=True, what=f"{variant} f16")
+
+
 # --- default entry points at full size ------------------------------------------------
 
 @pytest.mark.parametrize("m,k,n", [(1, 4096, 14336), (1, 14336, 4096), (2, 4096, 4096), (4, 4096, 6144),
-                                   (8, 4096, 4096)])
+                                   (3, 4096, 4096), (8, 4096, 4096), (16, 4096, 14336), (32, 4096, 14336),
+                                   (64, 4096, 14336)])
 def test_llama_shapes_through_the_default_entry_points(stream, oracle, m, k, n):
     x = normal_x(wl.seed_for(22, m), m, k)
     w = weights(wl.seed_for(22, n), n, k)
