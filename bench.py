@@ -367,6 +367,39 @@ class NormRopeCase:
             b.free()
 
 
+class DenseCase:
+    """The dense f16 x f16 -> f32 matmul of the hipBLASLt boundary on the
+    prefill shape M x K x N with the weights as a row-major f16 [K, N]
+    operand, rotated over copies of >= 384 MB so every call reads HBM; the
+    first (warm-up) call tunes and caches the plan.  Algorithmic bytes
+    |A| + |B| + |C| once, flops 2 M N K."""
+
+    def __init__(self, m: int, n: int, k: int) -> None:
+        self.m, self.n, self.k = m, n, k
+        self.ctx = ops.DenseMatmul()
+        self.ws = DeviceBuffer(ops.DenseMatmul.WORKSPACE_BYTES)
+        self.a = DeviceBuffer.from_array(wl.normal_f16(wl.seed_for(6, 0), m * k))
+        b = wl.normal_f16(wl.seed_for(6, 1), k * n, std=0.05)
+        self.copies = max(2, -(-384_000_000 // b.nbytes))
+        self.b = [DeviceBuffer.from_array(b) for _ in range(self.copies)]
+        self.c = DeviceBuffer(m * n * 4)
+
+    def launch(self, i: int, stream: Stream) -> None:
+        self.ctx.matmul_f16_f32(self.m, self.n, self.k, self.a.ptr, self.b[i % self.copies].ptr, self.c.ptr,
+                                self.ws.ptr, ops.DenseMatmul.WORKSPACE_BYTES, stream)
+
+    def algorithmic_bytes(self) -> int:
+        return (self.m * self.k + self.k * self.n) * 2 + self.m * self.n * 4
+
+    def flops(self) -> int:
+        return 2 * self.m * self.n * self.k
+
+    def free(self) -> None:
+        for buf in [self.a, self.c, self.ws, *self.b]:
+            buf.free()
+        self.ctx.close()
+
+
 def run_sweep(stream: Stream, hip: _Hip, steps: int, warmup: int) -> None:
     """One line per configuration; the last column is the kernel variant the
     library's shape heuristic plans for it (the one the default entry points
@@ -394,6 +427,16 @@ def run_sweep(stream: Stream, hip: _Hip, steps: int, warmup: int) -> None:
               file=sys.stderr, flush=True)
         case.free()
     planner.close()
+    for m in (64, 512):
+        case = DenseCase(m, 14336, 4096)
+        t = time_case(case, stream, hip, steps, max(warmup, 1))
+        us = t["kernel_ms_mean"] * 1e3
+        gbs = case.algorithmic_bytes() / (us * 1e-6) / 1e9
+        tf = case.flops() / (us * 1e-6) / 1e12
+        print(f"{'dense f16 mm':<15}{m:>5}{case.k:>7}{case.n:>7}{us:>11.2f}{t['eager_ms_per_step'] * 1e3:>10.2f}"
+              f"{gbs:>9.0f}{100 * gbs / HBM_PEAK_GBS:>6.1f}%{tf:>9.1f}{100 * tf / MFMA_F16_PEAK_TFLOPS:>6.1f}%  "
+              f"mote_hipblaslt_matmul_f16_f32", file=sys.stderr, flush=True)
+        case.free()
     entry = {"rmsnorm": "mote_hip_rms_norm_f16", "fused add+rmsnorm": "mote_hip_fused_add_rms_norm_f16",
              "rope q+k": "mote_hip_rope_qk_f16"}
     for kind in ("rmsnorm", "fused add+rmsnorm", "rope q+k"):

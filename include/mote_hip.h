@@ -116,6 +116,25 @@ int mote_q4_0_dispatch_plan(void* handle, uint64_t rows, uint64_t output_feature
 int mote_q4_0_variant_count(void);
 const char* mote_q4_0_variant_name(int index);
 
+/* ---- Dense F16 x F16 -> F32 matmul (hipBLASLt) ---------------------------- */
+/* [reference] crates/mote-backend-hip/src/hipblaslt_shim.cpp:326-408, bound at
+ * crates/mote-backend-hip/src/ffi.rs:329-417 for matmul_f16_f32
+ * (crates/mote-backend-hip/src/matmul.rs:10-52).  Row-major C[m, n] (f32) =
+ * A[m, k] B[k, n] (f16), f32 accumulation, on `stream`, with a caller-owned
+ * workspace (the reference passes 32 MiB).  A context caches one plan per
+ * (m, n, k); the first call for a shape times hipBLASLt's heuristic
+ * candidates on the stream (synchronising it) and keeps the fastest.
+ * Statuses: 0; -1 for a null argument or an internal error; hipBLAS
+ * statuses from the library; -1000 - hipError for HIP runtime failures;
+ * last_error describes the most recent failure ("" after a success).
+ * m == 0 or n == 0 returns 0 without a launch; k == 0 writes zeros. */
+int mote_hipblaslt_create(void** handle);
+void mote_hipblaslt_destroy(void* handle);
+const char* mote_hipblaslt_last_error(void* handle);
+int mote_hipblaslt_matmul_f16_f32(void* handle, uint64_t m, uint64_t n, uint64_t k, const void* lhs,
+                                  const void* rhs, void* output, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 /* ---- RMSNorm and fused add + RMSNorm -------------------------------------- */
 /* [reference] crates/mote-backend-hip/src/rms_norm.hip:68-98, bound at
  * crates/mote-backend-hip/src/ffi.rs:120-161.  f16 [rows, hidden] in/out,

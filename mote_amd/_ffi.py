@@ -63,6 +63,10 @@ SIGNATURES = {
     "mote_q4_0_dispatch_plan": (_I, [_P, _U64, _U64, _U64, _I, _I, ctypes.c_char_p, _SZ]),
     "mote_q4_0_variant_count": (_I, []),
     "mote_q4_0_variant_name": (ctypes.c_char_p, [_I]),
+    "mote_hipblaslt_create": (_I, [ctypes.POINTER(_P)]),
+    "mote_hipblaslt_destroy": (None, [_P]),
+    "mote_hipblaslt_last_error": (ctypes.c_char_p, [_P]),
+    "mote_hipblaslt_matmul_f16_f32": (_I, [_P, _U64, _U64, _U64, _P, _P, _P, _P, _SZ, _P]),
     "mote_hip_rms_norm_f16": (_I, [_P, _P, _P, _U64, _U64, ctypes.c_float, _P]),
     "mote_hip_fused_add_rms_norm_f16": (_I, [_P, _P, _P, _P, _U64, _U64, ctypes.c_float, _P]),
     "mote_hip_rope_f16": (_I, [_P, _P, _P, _P, _U64, _U64, _U64, _U64, ctypes.c_uint32, _P]),

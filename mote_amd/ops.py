@@ -142,3 +142,38 @@ class Q4_0Dispatch:
             self.close()
         except Exception:
             pass
+
+
+class DenseMatmul:
+    """A hipBLASLt matmul context (the reference's HipBlasLt handle,
+    crates/mote-backend-hip/src/ffi.rs:341-419): row-major f32 C[m, n] =
+    f16 A[m, k] B[k, n], one tuned plan per shape, a caller-owned workspace."""
+
+    WORKSPACE_BYTES = 32 * 1024 * 1024  # the reference context's workspace (src/context.rs:11)
+
+    def __init__(self) -> None:
+        handle = ctypes.c_void_p()
+        check(lib().mote_hipblaslt_create(ctypes.byref(handle)), "create hipBLASLt context")
+        self.handle = handle.value
+
+    def last_error(self) -> str:
+        msg = lib().mote_hipblaslt_last_error(self.handle)
+        return msg.decode() if msg else ""
+
+    def matmul_f16_f32(self, m, n, k, lhs, rhs, out, workspace, workspace_bytes, stream) -> None:
+        status = lib().mote_hipblaslt_matmul_f16_f32(
+            self.handle, m, n, k, lhs, rhs, out, workspace, workspace_bytes, _s(stream)
+        )
+        if status != 0:
+            raise HipError("F16/F32 matmul", status, self.last_error())
+
+    def close(self) -> None:
+        if self.handle:
+            lib().mote_hipblaslt_destroy(self.handle)
+            self.handle = 0
+
+    def __del__(self) -> None:  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass

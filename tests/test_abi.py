@@ -158,6 +158,15 @@ def test_dispatch_context_host_state(lib):
     assert lib.mote_q4_0_dispatch_set_autotune(None, 1) == 1
 
 
+def test_dense_matmul_argument_errors_without_a_device(lib):
+    """The hipBLASLt boundary's host-side checks (no device, no library load):
+    a null out-parameter or context is -1, a null context has no message."""
+    assert lib.mote_hipblaslt_create(None) == -1
+    assert lib.mote_hipblaslt_last_error(None) is None
+    lib.mote_hipblaslt_destroy(None)
+    assert lib.mote_hipblaslt_matmul_f16_f32(None, 1, 1, 1, FAKE, FAKE, FAKE, FAKE, 1 << 20, STREAM) == -1
+
+
 def test_python_wrappers_raise_hip_error(lib):
     from mote_amd import HipError, ops
 
