@@ -1,0 +1,103 @@
+"""The entry points captured in a HIP graph and replayed.
+
+A serving loop captures a decoder step once and replays it; every kernel here
+must then behave exactly as when issued eagerly.  The test issues a step's
+worth of calls eagerly (fused add + RMSNorm, Q4_0 linears at 1, 16 and 512
+tokens, the fused gate/up at 1 and 16 tokens, a Q8_0 linear, q/k RoPE),
+captures the same calls into a graph, and replays it three times.  Before
+every replay the outputs are overwritten with a sentinel and the residual
+(updated in place by the fused norm) is restored, eagerly, on the same stream;
+each replay must reproduce the eager outputs bit for bit.  No entry point
+records a memset or synchronises, so capture needs nothing special once a
+shape's plan is cached (the default entry points choose plans on the host).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import bench
+from mote_amd import ops, workloads as wl
+from mote_amd.device import DeviceBuffer
+
+pytestmark = pytest.mark.gpu
+
+H, FF, HEADS, KV, HD = 4096, 14336, 32, 8, 128
+
+
+def test_decoder_step_graph_replays_match_eager(stream):
+    hip = bench._Hip()
+    bufs = {}
+
+    def buf(name, array):
+        bufs[name] = DeviceBuffer.from_array(array)
+        return bufs[name]
+
+    def out(name, nbytes):
+        bufs[name] = DeviceBuffer(nbytes)
+        return bufs[name]
+
+    x1 = buf("x1", wl.normal_f16(40, H))
+    x16 = buf("x16", wl.normal_f16(41, 16 * H))
+    x512 = buf("x512", wl.normal_f16(42, 512 * H))
+    res = wl.normal_f16(43, 16 * H)
+    r16 = buf("res", res)
+    nw = buf("nw", wl.normal_f16(44, H, mean=1.0, std=0.1))
+    wq4 = buf("wq4", wl.q4_0_weights(45, FF, H))
+    wup = buf("wup", wl.q4_0_weights(46, FF, H))
+    wq8 = buf("wq8", wl.q8_0_weights(47, 1024, H))
+    pos = wl.positions(48, 16)
+    cos, sin = wl.rope_tables(pos, HD, 500000.0)
+    c, s = buf("cos", cos), buf("sin", sin)
+    q = buf("q", wl.normal_f16(49, 16 * HEADS * HD))
+    k = buf("k", wl.normal_f16(50, 16 * KV * HD))
+    outs = {
+        "norm": out("norm", 16 * H * 2),
+        "y1": out("y1", FF * 4),
+        "y16": out("y16", 16 * FF * 4),
+        "y512": out("y512", 512 * FF * 4),
+        "gu1": out("gu1", FF * 4),
+        "gu16": out("gu16", 16 * FF * 4),
+        "q8": out("q8", 1024 * 4),
+        "qo": out("qo", 16 * HEADS * HD * 2),
+        "ko": out("ko", 16 * KV * HD * 2),
+    }
+
+    def step():
+        ops.fused_add_rms_norm_f16(x16.ptr, r16.ptr, nw.ptr, outs["norm"].ptr, 16, H, 1e-5, stream)
+        ops.quantized_linear_q4_0_f32(x1.ptr, wq4.ptr, outs["y1"].ptr, 1, FF, H, stream)
+        ops.quantized_linear_q4_0_f32(x16.ptr, wq4.ptr, outs["y16"].ptr, 16, FF, H, stream)
+        ops.quantized_linear_q4_0_f32(x512.ptr, wq4.ptr, outs["y512"].ptr, 512, FF, H, stream)
+        ops.q4_0_gate_up_silu_f32(x1.ptr, wq4.ptr, wup.ptr, outs["gu1"].ptr, 1, FF, H, stream)
+        ops.q4_0_gate_up_silu_f32(x16.ptr, wq4.ptr, wup.ptr, outs["gu16"].ptr, 16, FF, H, stream)
+        ops.quantized_linear_q8_0_f32(x1.ptr, wq8.ptr, outs["q8"].ptr, 1, 1024, H, stream)
+        ops.rope_qk_f16(q.ptr, k.ptr, c.ptr, s.ptr, outs["qo"].ptr, outs["ko"].ptr, 16, HEADS, KV, HD, HD,
+                        ops.HALF_SPLIT, stream)
+
+    def reset():
+        for b in outs.values():
+            b.upload(np.full(b.nbytes, 0xA5, dtype=np.uint8))
+        r16.upload(res)
+
+    def snapshot():
+        stream.synchronize()
+        return {name: b.download(np.uint8) for name, b in outs.items()} | {"res": r16.download(np.uint8)}
+
+    reset()
+    step()
+    eager = snapshot()
+    assert not np.array_equal(eager["res"], res.view(np.uint8))  # the norm updated the residual
+
+    exe = hip.capture(stream, step)
+    try:
+        for replay in range(3):
+            reset()
+            hip.launch_graph(exe, stream)
+            got = snapshot()
+            for name, want in eager.items():
+                assert np.array_equal(got[name], want), f"replay {replay}: {name} differs from the eager run"
+    finally:
+        hip.destroy_graph(exe)
+        for b in bufs.values():
+            b.free()
