@@ -311,6 +311,7 @@ SWEEP = (
        ("q8_0 down", 1, 14336, 4096, 5, False, "q8"), ("q8_0 2 tok", 2, 4096, 14336, 5, False, "q8"),
        ("q8_0 4 tok", 4, 4096, 14336, 5, False, "q8")]
     + [("q8_0 skinny", m, 4096, 14336, 5, False, "q8") for m in (8, 16, 32, 64)]
+    + [("q8_0 prefill", m, 4096, 14336, 5, False, "q8") for m in (256, 512)]
 )
 
 

@@ -22,7 +22,7 @@ struct Problem {
 
 enum class Kind : int { Gemv = 0, Mfma = 1, Generic = 2, GateUpMfma = 3, GateUpGeneric = 4, GemvRows = 5,
                         GemvStream = 6, SkinnyMfma = 7, Q8Stream = 8, Q8Generic = 9, GateUpSkinny = 10,
-                        GateUpStream = 11, Q8Skinny = 12 };
+                        GateUpStream = 11, Q8Skinny = 12, Q8Prefill = 13 };
 
 struct Variant {
     const char* name;

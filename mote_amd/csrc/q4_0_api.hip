@@ -73,7 +73,8 @@ bool kind_matches(const Variant& v, Op op) {
         return v.kind == Kind::GateUpMfma || v.kind == Kind::GateUpSkinny || v.kind == Kind::GateUpStream ||
                v.kind == Kind::GateUpGeneric;
     if (op == Op::LinearQ8)
-        return v.kind == Kind::Q8Stream || v.kind == Kind::Q8Skinny || v.kind == Kind::Q8Generic;
+        return v.kind == Kind::Q8Stream || v.kind == Kind::Q8Skinny || v.kind == Kind::Q8Prefill ||
+               v.kind == Kind::Q8Generic;
     return v.kind == Kind::Gemv || v.kind == Kind::GemvRows || v.kind == Kind::GemvStream ||
            v.kind == Kind::SkinnyMfma || v.kind == Kind::Mfma || v.kind == Kind::Generic;
 }
@@ -89,7 +90,8 @@ bool supports(const Variant& v, const Problem& p) {
         case Kind::GateUpSkinny:
         case Kind::Q8Skinny: return skinny_mfma_supports(v, p);
         case Kind::Mfma:
-        case Kind::GateUpMfma: return mfma_supports(v, p);
+        case Kind::GateUpMfma:
+        case Kind::Q8Prefill: return mfma_supports(v, p);
         default: return true;
     }
 }
@@ -114,7 +116,8 @@ std::vector<const Variant*> candidates(const Problem& p, Op op) {
         if (vector_alu && p.M >= 64) continue;
         const bool skinny = v->kind == Kind::SkinnyMfma || v->kind == Kind::GateUpSkinny || v->kind == Kind::Q8Skinny;
         if (skinny && p.M > 64) continue;
-        if ((v->kind == Kind::Mfma || v->kind == Kind::GateUpMfma) && p.M < 64) continue;
+        if ((v->kind == Kind::Mfma || v->kind == Kind::GateUpMfma || v->kind == Kind::Q8Prefill) && p.M < 64)
+            continue;
         out.push_back(v);
     }
     return out;
@@ -232,6 +235,12 @@ const Variant* heuristic(const Problem& p, Op op) {
         }
         if (fast && p.M <= 64)
             if (const Variant* v = skinny_q8_heuristic(p)) return v;
+        if (fast && p.M >= 64) {
+            // The prefill tiles with 68-byte pairs: 128 x 128 once that gives
+            // about one tile per CU, 64 x 128 below.
+            const uint64_t tiles = static_cast<uint64_t>((p.M + 127) / 128) * ((p.N + 127) / 128);
+            return by_name(tiles >= 200 ? "q8_mfma_r_m128_n128" : "q8_mfma_r_m64_n128");
+        }
         return by_name("q8_generic");
     }
     if (op == Op::GateUp) {

@@ -27,6 +27,14 @@
 // 4g..4g+3, elements [4g, 4g+2, 4g+1, 4g+3, 16+4g, 16+4g+2, 16+4g+1,
 // 16+4g+3]; MFMA lane group g (lanes 16g..16g+15) takes group g of both
 // operands, so activations and weights agree on k.
+//
+// Q8_0 weights (Q8): a pair is staged as 17 dwords, [d0 | d1 << 16][block 0
+// bytes 0-31][block 1 bytes 0-31] (block 0's bytes re-aligned); k group g is
+// bytes 8g..8g+7 of a block, elements [8g, 8g+2, 8g+1, 8g+3, 8g+4, 8g+6,
+// 8g+5, 8g+7], dequantised by dequant8_q8 into a binary16 hi + lo pair that
+// feeds two MFMAs (a single binary16 product is too coarse for 8-bit values;
+// it is exact for Q4_0's 4-bit ones), and the activations are staged in that
+// order.
 #include "common.hpp"
 #include "q4_0.hpp"
 
@@ -34,9 +42,8 @@ namespace mote::q4_0 {
 namespace {
 
 constexpr int kXRow = 144;  // LDS bytes per activation row and step (128 + 16 padding)
-constexpr int kWRow = 36;   // LDS bytes per weight row and step (9 dwords)
 
-template <int BM, int BN, bool GATE_UP, typename OutT>
+template <int BM, int BN, bool GATE_UP, typename OutT, bool Q8 = false>
 __global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict__ x,
                                                       const uint8_t* __restrict__ wg,
                                                       const uint8_t* __restrict__ wu,
@@ -49,6 +56,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict
     constexpr int XC = BM * 8 / 256;          // 16-byte activation chunks per thread and step
     constexpr int WI = (BN + 255) / 256;      // weight rows per thread and step (per matrix)
     static_assert(BM % 32 == 0 && BN % 32 == 0 && XC >= 1, "tile shape");
+    static_assert(!(Q8 && GATE_UP), "the fused gate/up is a Q4_0 operation");
+    constexpr int kDw = Q8 ? 17 : 9;         // dwords of a staged block pair
+    constexpr int kWRow = kDw * 4;           // LDS bytes per weight row and step
+    constexpr uint32_t kPB = Q8 ? kQ8PairBytes : kPairBytes;
 
     __shared__ __attribute__((aligned(16))) uint8_t xs[2][BM * kXRow];
     __shared__ __attribute__((aligned(16))) uint8_t ws[NW][2][BN * kWRow];
@@ -65,7 +76,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict
     const int wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const uint32_t npairs = K >> 6;
-    const size_t row_bytes = static_cast<size_t>(npairs) * kPairBytes;
+    const size_t row_bytes = static_cast<size_t>(npairs) * kPB;
     const uint8_t* wsrc[NW] = {wg};
     if constexpr (GATE_UP) wsrc[1] = wu;
 
@@ -80,7 +91,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict
         const uint32_t m = min(m0 + row, M - 1);
         xptr[j] = x + static_cast<size_t>(m) * K + chunk * 8;
         const int blk = chunk >> 2, kin = (chunk & 3) * 8;
-        xoff[j] = row * kXRow + blk * 64 + ((kin & 15) >> 2) * 16 + (kin >= 16 ? 8 : 0);
+        if constexpr (Q8)  // k group chunk % 4: both halves together
+            xoff[j] = row * kXRow + blk * 64 + (chunk & 3) * 16;
+        else
+            xoff[j] = row * kXRow + blk * 64 + ((kin & 15) >> 2) * 16 + (kin >= 16 ? 8 : 0);
     }
     // Weight rows: thread t copies the step's block pair of rows t, t + 256, ...
     const uint8_t* wptr[NW][WI];
@@ -95,7 +109,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict
     }
 
     u32x4 xreg[XC];
-    uint32_t wreg[NW][WI][9];
+    uint32_t wreg[NW][WI][kDw];
     auto load_stage = [&](uint32_t kp) {
         kp = min(kp, npairs - 1);  // past the end: a cached re-read, never used
 #pragma unroll
@@ -105,7 +119,13 @@ __global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict
         for (int s = 0; s < NW; ++s)
 #pragma unroll
             for (int j = 0; j < WI; ++j)
-                if (wlive[j]) load_pair(wptr[s][j] + static_cast<size_t>(kp) * kPairBytes, wreg[s][j]);
+                if (wlive[j]) {
+                    const uint8_t* src = wptr[s][j] + static_cast<size_t>(kp) * kPB;
+                    if constexpr (Q8)
+                        load_pair_q8(src, wreg[s][j]);
+                    else
+                        load_pair(src, wreg[s][j]);
+                }
     };
     auto store_stage = [&](int buf) {
 #pragma unroll
@@ -117,21 +137,27 @@ __global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict
             b.x = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);  // (x4, x6)
             b.y = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);  // (x5, x7)
             *reinterpret_cast<u32x2*>(&xs[buf][xoff[j]]) = a;
-            *reinterpret_cast<u32x2*>(&xs[buf][xoff[j] + 16]) = b;
+            *reinterpret_cast<u32x2*>(&xs[buf][xoff[j] + (Q8 ? 8 : 16)]) = b;
         }
 #pragma unroll
         for (int s = 0; s < NW; ++s)
 #pragma unroll
             for (int j = 0; j < WI; ++j) {
                 if (!wlive[j]) continue;
-                const uint32_t (&d)[9] = wreg[s][j];
+                const uint32_t (&d)[kDw] = wreg[s][j];
                 uint32_t* dst = reinterpret_cast<uint32_t*>(&ws[s][buf][(tid + 256 * j) * kWRow]);
-                dst[0] = __builtin_amdgcn_perm(d[4], d[0], 0x07060100u);  // d0 (bytes 0-1) | d1 (bytes 18-19)
-                dst[1] = __builtin_amdgcn_perm(d[1], d[0], 0x05040302u);  // block 0 nibble bytes 0-3
-                dst[2] = __builtin_amdgcn_perm(d[2], d[1], 0x05040302u);
-                dst[3] = __builtin_amdgcn_perm(d[3], d[2], 0x05040302u);
-                dst[4] = __builtin_amdgcn_perm(d[4], d[3], 0x05040302u);
-                dst[5] = d[5]; dst[6] = d[6]; dst[7] = d[7]; dst[8] = d[8];
+                if constexpr (Q8) {
+                    dst[0] = __builtin_amdgcn_perm(d[8], d[0], 0x07060100u);  // d0 (bytes 0-1) | d1 (bytes 34-35)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) dst[1 + i] = q8_bytes(d, i);
+                } else {
+                    dst[0] = __builtin_amdgcn_perm(d[4], d[0], 0x07060100u);  // d0 (bytes 0-1) | d1 (bytes 18-19)
+                    dst[1] = __builtin_amdgcn_perm(d[1], d[0], 0x05040302u);  // block 0 nibble bytes 0-3
+                    dst[2] = __builtin_amdgcn_perm(d[2], d[1], 0x05040302u);
+                    dst[3] = __builtin_amdgcn_perm(d[3], d[2], 0x05040302u);
+                    dst[4] = __builtin_amdgcn_perm(d[4], d[3], 0x05040302u);
+                    dst[5] = d[5]; dst[6] = d[6]; dst[7] = d[7]; dst[8] = d[8];
+                }
             }
     };
 
@@ -166,14 +192,26 @@ __global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict
             for (int s = 0; s < NW; ++s) {
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
-                    const uint32_t q = *reinterpret_cast<const uint32_t*>(
-                        &ws[s][buf][b_base + j * 16 * kWRow + 4 + blk * 16 + lgrp * 4]);
                     const f16x2 d = as_h2(__builtin_amdgcn_perm(scales[s][j], scales[s][j],
                                                                 blk ? 0x03020302u : 0x01000100u));
-                    const f16x8 b = dequant8(q, d, dq.c1024, dq.c64);
+                    if constexpr (Q8) {
+                        // two dword reads: the 68-byte rows keep the pair only dword aligned
+                        const uint32_t* q = reinterpret_cast<const uint32_t*>(
+                            &ws[s][buf][b_base + j * 16 * kWRow + 4 + blk * 32 + lgrp * 8]);
+                        const F16x8Pair b = dequant8_q8(q[0], q[1], d, dq.q8);
 #pragma unroll
-                    for (int i = 0; i < TM; ++i)
-                        acc[s][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b, acc[s][i][j], 0, 0, 0);
+                        for (int i = 0; i < TM; ++i) {
+                            acc[s][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b.hi, acc[s][i][j], 0, 0, 0);
+                            acc[s][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b.lo, acc[s][i][j], 0, 0, 0);
+                        }
+                    } else {
+                        const uint32_t q = *reinterpret_cast<const uint32_t*>(
+                            &ws[s][buf][b_base + j * 16 * kWRow + 4 + blk * 16 + lgrp * 4]);
+                        const f16x8 b = dequant8(q, d, dq.c1024, dq.c64);
+#pragma unroll
+                        for (int i = 0; i < TM; ++i)
+                            acc[s][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b, acc[s][i][j], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -212,7 +250,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict
     }
 }
 
-template <int BM, int BN, bool GATE_UP>
+template <int BM, int BN, bool GATE_UP, bool Q8 = false>
 hipError_t launch_prefill(const Problem& p) {
     const uint32_t m_tiles = (p.M + BM - 1) / BM;
     const uint32_t n_tiles = (p.N + BN - 1) / BN;
@@ -225,10 +263,10 @@ hipError_t launch_prefill(const Problem& p) {
     const auto* wg = static_cast<const uint8_t*>(p.w);
     const auto* wu = static_cast<const uint8_t*>(p.w_up);
     if (p.out == OutType::F32) {
-        hipLaunchKernelGGL((prefill_kernel<BM, BN, GATE_UP, float>), grid, block, 0, p.stream, x, wg, wu,
+        hipLaunchKernelGGL((prefill_kernel<BM, BN, GATE_UP, float, Q8>), grid, block, 0, p.stream, x, wg, wu,
                            static_cast<float*>(p.y), p.M, p.N, p.K, m_tiles, total, per_xcd);
     } else {
-        hipLaunchKernelGGL((prefill_kernel<BM, BN, GATE_UP, _Float16>), grid, block, 0, p.stream, x, wg,
+        hipLaunchKernelGGL((prefill_kernel<BM, BN, GATE_UP, _Float16, Q8>), grid, block, 0, p.stream, x, wg,
                            wu, static_cast<_Float16*>(p.y), p.M, p.N, p.K, m_tiles, total, per_xcd);
     }
     return hipGetLastError();
@@ -238,6 +276,8 @@ hipError_t launch_prefill(const Problem& p) {
     Variant{"mfma_r_m" #BM "_n" #BN, Kind::Mfma, BM, BN, 1, &launch_prefill<BM, BN, false>}
 #define MOTE_PREFILL_GU(BM, BN)                                                                   \
     Variant{"gateup_mfma_r_m" #BM "_n" #BN, Kind::GateUpMfma, BM, BN, 1, &launch_prefill<BM, BN, true>}
+#define MOTE_PREFILL_Q8(BM, BN)                                                                   \
+    Variant{"q8_mfma_r_m" #BM "_n" #BN, Kind::Q8Prefill, BM, BN, 1, &launch_prefill<BM, BN, false, true>}
 
 // 128 x 224 tiles: N = 14336 splits into 64 of them, so M = 512 makes exactly
 // one tile per CU of a 256-CU MI355X.
@@ -245,10 +285,12 @@ const Variant kPrefill[] = {
     MOTE_PREFILL(128, 256), MOTE_PREFILL(128, 128), MOTE_PREFILL(64, 256), MOTE_PREFILL(256, 128),
     MOTE_PREFILL(64, 128), MOTE_PREFILL(128, 224), MOTE_PREFILL(64, 224),
     MOTE_PREFILL_GU(128, 128), MOTE_PREFILL_GU(64, 128), MOTE_PREFILL_GU(128, 64), MOTE_PREFILL_GU(64, 64),
+    MOTE_PREFILL_Q8(128, 128), MOTE_PREFILL_Q8(64, 128), MOTE_PREFILL_Q8(128, 64), MOTE_PREFILL_Q8(64, 64),
 };
 
 #undef MOTE_PREFILL
 #undef MOTE_PREFILL_GU
+#undef MOTE_PREFILL_Q8
 
 }  // namespace
 

@@ -117,7 +117,7 @@ def test_reference_kat_signed_values_and_scale(stream):
 
 # --- every kernel, bit-exact where the arithmetic is exact ------------------------------
 
-STREAM_AND_GENERIC = [v for v in _variants("q8_") if not v.startswith("q8_skinny_")]
+STREAM_AND_GENERIC = [v for v in _variants("q8_") if not v.startswith(("q8_skinny_", "q8_mfma_"))]
 
 
 @pytest.mark.parametrize("variant", STREAM_AND_GENERIC)
@@ -197,11 +197,26 @@ def test_every_q8_skinny_variant(stream, oracle, variant):
     check(oracle, y16, x, w, m, n, k, columns=cols, f16_out=True, what=f"{variant} f16")
 
 
+@pytest.mark.parametrize("variant", _variants("q8_mfma_"))
+def test_every_q8_prefill_variant(stream, oracle, variant):
+    """Prefill tiles over Q8_0 pairs (64 or more tokens): M and N ragged
+    against the tiles, K of one pair and K = 4160 (65 pairs), f32 and f16."""
+    d = ops.Q4_0Dispatch()
+    d.force(variant)
+    for m, n, k in [(70, 200, 512), (130, 67, 1024), (64, 128, 64), (65, 33, 4160)]:
+        x = normal_x(wl.seed_for(25, m), m, k)
+        w = weights(wl.seed_for(25, 100 + n), n, k)
+        y = run(stream, x, w, m, n, k, dispatch=d)
+        check(oracle, y, x, w, m, n, k, what=f"{variant} {m}x{n}x{k}")
+    y16 = run(stream, x, w, m, n, k, dispatch=d, f16_out=True)
+    check(oracle, y16, x, w, m, n, k, f16_out=True, what=f"{variant} f16")
+
+
 # --- default entry points at full size ------------------------------------------------
 
 @pytest.mark.parametrize("m,k,n", [(1, 4096, 14336), (1, 14336, 4096), (2, 4096, 4096), (4, 4096, 6144),
                                    (3, 4096, 4096), (8, 4096, 4096), (16, 4096, 14336), (32, 4096, 14336),
-                                   (64, 4096, 14336)])
+                                   (64, 4096, 14336), (128, 4096, 14336), (512, 4096, 14336)])
 def test_llama_shapes_through_the_default_entry_points(stream, oracle, m, k, n):
     x = normal_x(wl.seed_for(22, m), m, k)
     w = weights(wl.seed_for(22, n), n, k)
