@@ -451,6 +451,51 @@ def run_sweep(stream: Stream, hip: _Hip, steps: int, warmup: int) -> None:
         case.free()
 
 
+class ReadCase:
+    """One pure-read pattern of mote_hip_read_probe_u128 over the headline
+    matrix's 33 095 680 bytes, rotated over 13 copies (429 MB > MALL)."""
+
+    BYTES = 33_095_680
+
+    def __init__(self, bufs, sink, grid, threads, in_flight, nt) -> None:
+        self.bufs, self.sink = bufs, sink
+        self.args = (grid, threads, in_flight, nt)
+
+    def launch(self, i: int, stream: Stream) -> None:
+        grid, threads, in_flight, nt = self.args
+        _ffi.check(_ffi.lib().mote_hip_read_probe_u128(self.bufs[i % len(self.bufs)].ptr, self.BYTES, grid,
+                                                        threads, in_flight, nt, self.sink.ptr, stream.handle),
+                   "read probe")
+
+
+def run_read_floor() -> int:
+    """Times grid-stride pure reads (threads x loads in flight x non-temporal
+    x grid) with graph replays, fastest first, as a markdown table."""
+    stream, hip = Stream(), _Hip()
+    bufs = [DeviceBuffer(ReadCase.BYTES) for _ in range(13)]
+    for i, b in enumerate(bufs):
+        b.upload(np.full(ReadCase.BYTES, i * 7 + 1, dtype=np.uint8))
+    sink = DeviceBuffer(16)
+    rows = []
+    for threads, in_flight in ((256, 2), (256, 4), (256, 8), (512, 2), (512, 4), (1024, 2)):
+        for nt in (1, 0):
+            for grid in (256, 512, 768, 1024, 2048):
+                case = ReadCase(bufs, sink, grid, threads, in_flight, nt)
+                us = time_case(case, stream, hip, 100, 26)["kernel_ms_mean"] * 1e3
+                rows.append((us, f"t{threads} u{in_flight} {'nt' if nt else '--'} grid {grid}"))
+                print(f"read floor: {rows[-1][1]}: {us:.2f} us", file=sys.stderr, flush=True)
+    rows.sort()
+    print("| pattern (threads, loads in flight, non-temporal, grid) | µs / launch | GB/s | % of 8 TB/s |")
+    print("|---|---|---|---|")
+    for us, name in rows:
+        gbs = ReadCase.BYTES / (us * 1e-6) / 1e9
+        print(f"| {name} | {us:.2f} | {gbs:.0f} | {100 * gbs / HBM_PEAK_GBS:.1f} % |")
+    for b in bufs + [sink]:
+        b.free()
+    stream.close()
+    return 0
+
+
 def run_comparator(steps: int = 40) -> int:
     """Comparators from the vendor libraries, through torch.  Prefill: the
     dense f16 GEMM (torch.matmul, i.e. hipBLASLt on ROCm) at M in {64, 256,
@@ -545,9 +590,14 @@ def main() -> int:
     ap.add_argument("--comparator", action="store_true",
                     help="time the vendor library's dense f16 GEMM at the prefill shapes (needs torch; "
                          "stderr table, no result line)")
+    ap.add_argument("--read-floor", action="store_true",
+                    help="time pure 16-byte reads of the headline's 33 MB matrix in many grid shapes "
+                         "(the HBM floor of the decode GEMV; stdout table, no result line)")
     args = ap.parse_args()
     if args.comparator:
         return run_comparator()
+    if args.read_floor:
+        return run_read_floor()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the Q4_0 linear shards by output rows with no exchange; see the design notes)",

@@ -1,0 +1,81 @@
+// HBM read probe: a pure-read kernel that measures the read floor the
+// quantized GEMVs are held against (bench.py --read-floor).
+//
+// Grid-stride 16-byte loads: thread t of a grid of T threads reads chunks
+// t, t + T, t + 2T, ... of the buffer, `in_flight` loads per thread issued
+// before any is used, optionally non-temporal.  The values are folded into
+// one word that is stored only if it equals a constant no buffer here
+// produces, so the loads stay live and nothing is written in practice.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "common.hpp"
+#include "export.hpp"
+
+namespace mote {
+namespace {
+
+template <int THREADS, int UNROLL, bool NT>
+__global__ __launch_bounds__(THREADS) void read_probe_kernel(const u32x4* __restrict__ p, uint64_t n16,
+                                                             uint32_t* __restrict__ sink) {
+    uint32_t acc = 0;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * THREADS;
+    uint64_t i = static_cast<uint64_t>(blockIdx.x) * THREADS + threadIdx.x;
+    for (; i + (UNROLL - 1) * stride < n16; i += UNROLL * stride) {
+        u32x4 v[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) v[u] = NT ? __builtin_nontemporal_load(p + i + u * stride) : p[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) acc = acc * 3u + (v[u].x ^ v[u].y ^ v[u].z ^ v[u].w);
+    }
+    for (; i < n16; i += stride) {
+        const u32x4 v = p[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+
+template <int THREADS, int UNROLL, bool NT>
+hipError_t launch(const void* data, uint64_t n16, uint32_t grid, void* sink, hipStream_t stream) {
+    hipLaunchKernelGGL((read_probe_kernel<THREADS, UNROLL, NT>), dim3(grid), dim3(THREADS), 0, stream,
+                       static_cast<const u32x4*>(data), n16, static_cast<uint32_t*>(sink));
+    return hipGetLastError();
+}
+
+template <int THREADS, bool NT>
+hipError_t by_unroll(uint32_t in_flight, const void* data, uint64_t n16, uint32_t grid, void* sink,
+                     hipStream_t stream) {
+    switch (in_flight) {
+        case 2: return launch<THREADS, 2, NT>(data, n16, grid, sink, stream);
+        case 4: return launch<THREADS, 4, NT>(data, n16, grid, sink, stream);
+        case 8: return launch<THREADS, 8, NT>(data, n16, grid, sink, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <bool NT>
+hipError_t by_threads(uint32_t threads, uint32_t in_flight, const void* data, uint64_t n16, uint32_t grid,
+                      void* sink, hipStream_t stream) {
+    switch (threads) {
+        case 256: return by_unroll<256, NT>(in_flight, data, n16, grid, sink, stream);
+        case 512: return by_unroll<512, NT>(in_flight, data, n16, grid, sink, stream);
+        case 1024: return by_unroll<1024, NT>(in_flight, data, n16, grid, sink, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+}  // namespace mote
+
+MOTE_EXPORT int mote_hip_read_probe_u128(const void* data, size_t bytes, uint32_t grid, uint32_t threads,
+                                         uint32_t in_flight, int non_temporal, void* sink, void* stream) noexcept {
+    if (data == nullptr || sink == nullptr || stream == nullptr || bytes % 16 != 0 || grid == 0 ||
+        reinterpret_cast<uintptr_t>(data) % 16 != 0)
+        return hipErrorInvalidValue;
+    if (bytes == 0) return hipSuccess;
+    const auto s = static_cast<hipStream_t>(stream);
+    const uint64_t n16 = bytes / 16;
+    return static_cast<int>(non_temporal ? mote::by_threads<true>(threads, in_flight, data, n16, grid, sink, s)
+                                         : mote::by_threads<false>(threads, in_flight, data, n16, grid, sink, s));
+}
