@@ -167,6 +167,16 @@ def test_dense_matmul_argument_errors_without_a_device(lib):
     assert lib.mote_hipblaslt_matmul_f16_f32(None, 1, 1, 1, FAKE, FAKE, FAKE, FAKE, 1 << 20, STREAM) == -1
 
 
+def test_read_probe_argument_errors_without_a_device(lib):
+    """Bad arguments return 1 before any launch: null pointers, a size that
+    is not a multiple of 16, unsupported thread or in-flight counts."""
+    assert lib.mote_hip_read_probe_u128(None, 16, 1, 256, 2, 0, FAKE, STREAM) == 1
+    assert lib.mote_hip_read_probe_u128(FAKE, 17, 1, 256, 2, 0, FAKE, STREAM) == 1
+    assert lib.mote_hip_read_probe_u128(FAKE, 16, 1, 300, 2, 0, FAKE, STREAM) == 1
+    assert lib.mote_hip_read_probe_u128(FAKE, 16, 1, 256, 3, 1, FAKE, STREAM) == 1
+    assert lib.mote_hip_read_probe_u128(FAKE, 0, 1, 256, 2, 0, FAKE, STREAM) == 0  # nothing to read
+
+
 def test_python_wrappers_raise_hip_error(lib):
     from mote_amd import HipError, ops
 
