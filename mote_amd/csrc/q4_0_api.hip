@@ -293,11 +293,12 @@ const Variant* heuristic(const Problem& p, Op op) {
         // the persistent pipelined GEMV, with rows split over S waves for
         // K > 4096 (4096 x 14336: 7.3 us; 14336 x 4096: 8.0 us, against
         // 9.9 us for the row-streaming GEMV).  Two workgroups per CU pay off
-        // once every row group then still owns at least two rows.
+        // once every row group then owns about 1.5 rows or more (4096 x 6144:
+        // 5.14 us against 5.35 us; 4096 x 4096: 5.06 us against 4.29 us).
         uint32_t split = 1;
         while (split < 4 && p.K > 4096u * split) split *= 2;
         const uint64_t row_groups_g2 = static_cast<uint64_t>(device_cus()) * 2u * (8u / split);
-        const unsigned g = p.N >= 2u * row_groups_g2 ? 2u : 1u;
+        const unsigned g = 2u * p.N >= 3u * row_groups_g2 ? 2u : 1u;
         char name[32];
         if (split == 1)
             std::snprintf(name, sizeof name, "stream_d1_g%u", g);
