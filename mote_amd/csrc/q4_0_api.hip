@@ -151,6 +151,11 @@ const Variant* by_name(const char* name) {
 // 8.0 us); up to 4 tokens the direct loads are level or faster, and with at
 // most one item per workgroup 8 waves of two steps without the deferred
 // reduction are fastest (4 x 4096 x 4096: 5.7 us against 6.1 us).
+// Output tiles of a BM x BN prefill tiling of the problem.
+uint64_t prefill_tiles(const Problem& p, uint32_t bm, uint32_t bn) {
+    return static_cast<uint64_t>((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
+}
+
 const Variant* skinny_heuristic(const Problem& p) {
     const uint64_t items = static_cast<uint64_t>((p.N + 15) / 16) * ((p.M + 15) / 16);
     const uint64_t per_group = (items + device_cus() - 1) / static_cast<uint64_t>(device_cus());
@@ -236,10 +241,14 @@ const Variant* heuristic(const Problem& p, Op op) {
         if (fast && p.M <= 64)
             if (const Variant* v = skinny_q8_heuristic(p)) return v;
         if (fast && p.M >= 64) {
-            // The prefill tiles with 68-byte pairs: 128 x 128 once that gives
-            // about one tile per CU, 64 x 128 below.
-            const uint64_t tiles = static_cast<uint64_t>((p.M + 127) / 128) * ((p.N + 127) / 128);
-            return by_name(tiles >= 200 ? "q8_mfma_r_m128_n128" : "q8_mfma_r_m64_n128");
+            // The prefill tiles with 68-byte pairs: the largest 32 x 32 MFMA
+            // tile with staging waves that still gives about one tile per CU
+            // (measured on MI355X at K = 4096, N = 14336: 256 tokens 67-69 us,
+            // 512 tokens 112 us, against 79 and 126 us for 16 x 16 MFMA
+            // tiles), the 64 x 64 tiles below (128 tokens: 56.7 us).
+            if (prefill_tiles(p, 128, 256) >= 200) return by_name("q8_mfma_x32s_m128_n256_w1");
+            if (prefill_tiles(p, 128, 128) >= 200) return by_name("q8_mfma_x32s_m128_n128_w1");
+            return by_name("q8_mfma_r_m64_n64");
         }
         return by_name("q8_generic");
     }
@@ -260,7 +269,13 @@ const Variant* heuristic(const Problem& p, Op op) {
         }
         if (fast && p.M <= 64)
             if (const Variant* v = skinny_gate_up_heuristic(p)) return v;
-        if (fast && p.M >= 64) return by_name(p.M >= 128 ? "gateup_mfma_r_m128_n64" : "gateup_mfma_r_m64_n64");
+        if (fast && p.M >= 64) {
+            // 32 x 32 MFMA tiles with staging waves once 128 x 128 tiles give
+            // about one per CU (256 tokens: 72.7-75.4 us, 512: 139.5-144.6 us,
+            // against 84.5 and 164 us for 16 x 16 tiles).
+            if (prefill_tiles(p, 128, 128) >= 200) return by_name("gateup_mfma_x32s_m128_n128_w1");
+            return by_name(p.M >= 128 ? "gateup_mfma_r_m128_n64" : "gateup_mfma_r_m64_n64");
+        }
         return by_name("gateup_generic");
     }
     if (!fast) return by_name("generic");
@@ -270,10 +285,13 @@ const Variant* heuristic(const Problem& p, Op op) {
         if (v) return v;
     }
     if (p.M >= 64) {
-        // Prefer the largest tile that still gives about one tile per CU
-        // (raw-weight tiles: 128 x 128 at M = 256 and 512, 64 x 128 below).
-        static const char* const order[] = {"mfma_r_m128_n128", "mfma_r_m64_n128", "mfma_m128_n64_p1",
-                                            "mfma_m64_n64_p1"};
+        // Prefer the largest tile that still gives about one tile per CU: 32
+        // x 32 MFMA tiles with staging waves (measured on MI355X at K = 4096,
+        // N = 14336: 128 x 256 at 512 tokens, 68-72 us; 128 x 128 at 256
+        // tokens, 46.5-47.1 us; 64 x 128 at 128 tokens, 39.8 us; the 16 x 16
+        // tiles took 83, 59.4 and 46.1 us).
+        static const char* const order[] = {"mfma_x32s_m128_n256_w1", "mfma_x32s_m128_n128_w1",
+                                            "mfma_x32s_m64_n128_w1", "mfma_r_m64_n128", "mfma_m64_n64_p1"};
         const Variant* best = nullptr;
         uint64_t best_tiles = 0;
         for (const char* name : order) {

@@ -8,8 +8,11 @@
 // quantized_linear.hip:13-52 (oracle crates/mote-reference/src/quantized.rs:
 // 89-144); the fused gate/up has no counterpart in the reference.
 //
-// One 256-thread workgroup computes a BM x BN output tile with 2 x 2 waves,
-// each wave a (BM/2) x (BN/2) grid of 16x16 v_mfma_f32_16x16x32_f16 tiles.
+// One 256-thread workgroup computes a BM x BN output tile with WM x (4 / WM)
+// waves, each wave a (BM / WM) x (BN / (4 / WM)) grid of MFMA tiles: 16 x 16
+// tiles of v_mfma_f32_16x16x32_f16, or (T32) 32 x 32 tiles of
+// v_mfma_f32_32x32x16_f16, which measured 2.2-2.4 PFLOP/s on MI355X against
+// 0.86-1.3 PFLOP/s for the 16 x 16 form (one to four waves per SIMD).
 // K advances one Q4_0 block pair (64 elements) per step through a
 // double-buffered LDS stage, one barrier per step:
 //  * activations: BM rows x 64 f16 copied from HBM, stored in the k order of
@@ -25,8 +28,10 @@
 //    product).
 // A 32-element block is split into four k groups g = 0..3: nibble bytes
 // 4g..4g+3, elements [4g, 4g+2, 4g+1, 4g+3, 16+4g, 16+4g+2, 16+4g+1,
-// 16+4g+3]; MFMA lane group g (lanes 16g..16g+15) takes group g of both
-// operands, so activations and weights agree on k.
+// 16+4g+3]; a 16 x 16 x 32 MFMA spans one block, lane group g (lanes
+// 16g..16g+15) taking group g of both operands; a 32 x 32 x 16 MFMA spans two
+// groups, 2h and 2h + 1 in its h-th half block, lane half c (lanes 32c..32c+31)
+// taking group 2h + c.  Activations and weights agree on k either way.
 //
 // Q8_0 weights (Q8): a pair is staged as 17 dwords, [d0 | d1 << 16][block 0
 // bytes 0-31][block 1 bytes 0-31] (block 0's bytes re-aligned); k group g is
@@ -38,24 +43,32 @@
 #include "common.hpp"
 #include "q4_0.hpp"
 
+#include <type_traits>
+
 namespace mote::q4_0 {
 namespace {
 
 constexpr int kXRow = 144;  // LDS bytes per activation row and step (128 + 16 padding)
 
-template <int BM, int BN, bool GATE_UP, typename OutT, bool Q8 = false>
-__global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict__ x,
+template <int BM, int BN, bool GATE_UP, typename OutT, bool Q8 = false, int WM = 2, bool T32 = false,
+          bool SPEC = false>
+__global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_t* __restrict__ x,
                                                       const uint8_t* __restrict__ wg,
                                                       const uint8_t* __restrict__ wu,
                                                       OutT* __restrict__ y, uint32_t M, uint32_t N,
                                                       uint32_t K, uint32_t m_tiles, uint32_t total,
                                                       uint32_t per_xcd) {
     constexpr int NW = GATE_UP ? 2 : 1;
-    constexpr int TM = BM / 32;               // 16-row MFMA tiles per wave along M
-    constexpr int TN = BN / 32;               // along N
+    constexpr int WN = 4 / WM;                // waves along N
+    constexpr int T = T32 ? 32 : 16;          // MFMA tile edge
+    constexpr int TM = BM / (WM * T);         // MFMA tiles per wave along M
+    constexpr int TN = BN / (WN * T);         // along N
     constexpr int XC = BM * 8 / 256;          // 16-byte activation chunks per thread and step
     constexpr int WI = (BN + 255) / 256;      // weight rows per thread and step (per matrix)
-    static_assert(BM % 32 == 0 && BN % 32 == 0 && XC >= 1, "tile shape");
+    static_assert((WM == 1 || WM == 2 || WM == 4) && TM >= 1 && TN >= 1 && BM % (WM * T) == 0 &&
+                      BN % (WN * T) == 0 && XC >= 1, "tile shape");
+    using Acc = std::conditional_t<T32, f32x16, f32x4>;
+    constexpr int kAccRows = T32 ? 16 : 4;    // accumulator registers per lane and tile
     static_assert(!(Q8 && GATE_UP), "the fused gate/up is a Q4_0 operation");
     constexpr int kDw = Q8 ? 17 : 9;         // dwords of a staged block pair
     constexpr int kWRow = kDw * 4;           // LDS bytes per weight row and step
@@ -71,10 +84,14 @@ __global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict
     const uint32_t m0 = tile_m * BM;
     const uint32_t n0 = tile_n * BN;
 
-    const int tid = static_cast<int>(threadIdx.x);
+    // SPEC: waves 4-7 only stage (loads, LDS stores) and waves 0-3 only
+    // multiply, so each SIMD interleaves a staging wave's memory work with a
+    // compute wave's MFMAs; both meet at the one barrier per step.
+    const int tid = static_cast<int>(threadIdx.x) & 255;  // staging thread / compute thread index
+    const bool stager = SPEC && threadIdx.x >= 256;       // uniform over a wave
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     const uint32_t npairs = K >> 6;
     const size_t row_bytes = static_cast<size_t>(npairs) * kPB;
     const uint8_t* wsrc[NW] = {wg};
@@ -161,19 +178,27 @@ __global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict
             }
     };
 
-    f32x4 acc[NW][TM][TN];
+    Acc acc[NW][TM][TN];
 #pragma unroll
     for (int s = 0; s < NW; ++s)
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < TN; ++j) acc[s][i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < kAccRows; ++r) acc[s][i][j][r] = 0.0f;
 
     const DequantConsts dq = dequant_consts();
-    const int lrow = lane & 15;
-    const int lgrp = lane >> 4;
-    const int a_base = (wm * (BM / 2) + lrow) * kXRow + lgrp * 16;
-    const int b_base = (wn * (BN / 2) + lrow) * kWRow;
+    const int lrow = lane % T;  // row of the activation operand, column of the weight operand
+    const int lgrp = lane / T;  // k group (16 x 16) or lane half (32 x 32)
+    const int a_base = (wm * (BM / WM) + lrow) * kXRow;
+    const int b_base = (wn * (BN / WN) + lrow) * kWRow;
+    auto mfma = [](const f16x8& a, const f16x8& b, const Acc& c) {
+        if constexpr (T32)
+            return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    };
 
     auto mma_step = [&](int buf) {
         uint32_t scales[NW][TN];
@@ -181,36 +206,39 @@ __global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict
         for (int s = 0; s < NW; ++s)
 #pragma unroll
             for (int j = 0; j < TN; ++j)
-                scales[s][j] = *reinterpret_cast<const uint32_t*>(&ws[s][buf][b_base + j * 16 * kWRow]);
+                scales[s][j] = *reinterpret_cast<const uint32_t*>(&ws[s][buf][b_base + j * T * kWRow]);
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
-            f16x8 a[TM];
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
-                a[i] = *reinterpret_cast<const f16x8*>(&xs[buf][a_base + i * 16 * kXRow + blk * 64]);
+            for (int h = 0; h < (T32 ? 2 : 1); ++h) {
+                const int g = T32 ? 2 * h + lgrp : lgrp;  // k group of this lane's operands
+                f16x8 a[TM];
 #pragma unroll
-            for (int s = 0; s < NW; ++s) {
+                for (int i = 0; i < TM; ++i)
+                    a[i] = *reinterpret_cast<const f16x8*>(&xs[buf][a_base + i * T * kXRow + blk * 64 + g * 16]);
 #pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    const f16x2 d = as_h2(__builtin_amdgcn_perm(scales[s][j], scales[s][j],
-                                                                blk ? 0x03020302u : 0x01000100u));
-                    if constexpr (Q8) {
-                        // two dword reads: the 68-byte rows keep the pair only dword aligned
-                        const uint32_t* q = reinterpret_cast<const uint32_t*>(
-                            &ws[s][buf][b_base + j * 16 * kWRow + 4 + blk * 32 + lgrp * 8]);
-                        const F16x8Pair b = dequant8_q8(q[0], q[1], d, dq.q8);
+                for (int s = 0; s < NW; ++s) {
 #pragma unroll
-                        for (int i = 0; i < TM; ++i) {
-                            acc[s][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b.hi, acc[s][i][j], 0, 0, 0);
-                            acc[s][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b.lo, acc[s][i][j], 0, 0, 0);
+                    for (int j = 0; j < TN; ++j) {
+                        const f16x2 d = as_h2(__builtin_amdgcn_perm(scales[s][j], scales[s][j],
+                                                                    blk ? 0x03020302u : 0x01000100u));
+                        if constexpr (Q8) {
+                            // two dword reads: the 68-byte rows keep the pair only dword aligned
+                            const uint32_t* q = reinterpret_cast<const uint32_t*>(
+                                &ws[s][buf][b_base + j * T * kWRow + 4 + blk * 32 + g * 8]);
+                            const F16x8Pair b = dequant8_q8(q[0], q[1], d, dq.q8);
+#pragma unroll
+                            for (int i = 0; i < TM; ++i) {
+                                acc[s][i][j] = mfma(a[i], b.hi, acc[s][i][j]);
+                                acc[s][i][j] = mfma(a[i], b.lo, acc[s][i][j]);
+                            }
+                        } else {
+                            const uint32_t q = *reinterpret_cast<const uint32_t*>(
+                                &ws[s][buf][b_base + j * T * kWRow + 4 + blk * 16 + g * 4]);
+                            const f16x8 b = dequant8(q, d, dq.c1024, dq.c64);
+#pragma unroll
+                            for (int i = 0; i < TM; ++i) acc[s][i][j] = mfma(a[i], b, acc[s][i][j]);
                         }
-                    } else {
-                        const uint32_t q = *reinterpret_cast<const uint32_t*>(
-                            &ws[s][buf][b_base + j * 16 * kWRow + 4 + blk * 16 + lgrp * 4]);
-                        const f16x8 b = dequant8(q, d, dq.c1024, dq.c64);
-#pragma unroll
-                        for (int i = 0; i < TM; ++i)
-                            acc[s][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b, acc[s][i][j], 0, 0, 0);
                     }
                 }
             }
@@ -219,29 +247,50 @@ __global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict
 
     // Step k: write step k + 1 (loaded during step k - 1) to the other LDS
     // buffer, issue the loads of step k + 2, multiply step k, barrier.
-    load_stage(0);
-    store_stage(0);
-    load_stage(1);
+    if (!SPEC || stager) {
+        load_stage(0);
+        store_stage(0);
+        load_stage(1);
+    }
     __syncthreads();
-    for (uint32_t kp = 0; kp < npairs; ++kp) {
-        const int buf = static_cast<int>(kp & 1u);
-        if (kp + 1 < npairs) {  // uniform
-            store_stage(buf ^ 1);
-            load_stage(kp + 2);
+    if constexpr (SPEC) {
+        if (stager) {
+            for (uint32_t kp = 0; kp < npairs; ++kp) {
+                if (kp + 1 < npairs) {  // uniform
+                    store_stage(static_cast<int>(kp & 1u) ^ 1);
+                    load_stage(kp + 2);
+                }
+                __syncthreads();
+            }
+            return;  // the compute waves hold the results
         }
-        mma_step(buf);
-        __syncthreads();
+        for (uint32_t kp = 0; kp < npairs; ++kp) {
+            mma_step(static_cast<int>(kp & 1u));
+            __syncthreads();
+        }
+    } else {
+        for (uint32_t kp = 0; kp < npairs; ++kp) {
+            const int buf = static_cast<int>(kp & 1u);
+            if (kp + 1 < npairs) {  // uniform
+                store_stage(buf ^ 1);
+                load_stage(kp + 2);
+            }
+            mma_step(buf);
+            __syncthreads();
+        }
     }
 
-    // Epilogue: lane holds rows 4*lgrp .. 4*lgrp+3, column lrow of each tile.
+    // Epilogue: lane holds column lrow of each tile, rows 4 lgrp + r (16 x 16)
+    // or 8 (r / 4) + 4 lgrp + r % 4 (32 x 32).
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const uint32_t n = n0 + wn * (BN / 2) + j * 16 + lrow;
+            const uint32_t n = n0 + wn * (BN / WN) + j * T + lrow;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t m = m0 + wm * (BM / 2) + i * 16 + lgrp * 4 + r;
+            for (int r = 0; r < kAccRows; ++r) {
+                const int row = T32 ? 8 * (r / 4) + 4 * lgrp + r % 4 : 4 * lgrp + r;
+                const uint32_t m = m0 + wm * (BM / WM) + i * T + row;
                 float v = acc[0][i][j][r];
                 if constexpr (GATE_UP) v = silu(v) * acc[NW - 1][i][j][r];
                 if (m < M && n < N) y[static_cast<size_t>(m) * N + n] = to_out<OutT>(v);
@@ -250,7 +299,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const uint16_t* __restrict
     }
 }
 
-template <int BM, int BN, bool GATE_UP, bool Q8 = false>
+template <int BM, int BN, bool GATE_UP, bool Q8 = false, int WM = 2, bool T32 = false, bool SPEC = false>
 hipError_t launch_prefill(const Problem& p) {
     const uint32_t m_tiles = (p.M + BM - 1) / BM;
     const uint32_t n_tiles = (p.N + BN - 1) / BN;
@@ -258,15 +307,15 @@ hipError_t launch_prefill(const Problem& p) {
     if (total64 > 0x7fffffffull) return hipErrorInvalidConfiguration;
     const uint32_t total = static_cast<uint32_t>(total64);
     const uint32_t per_xcd = (total + 7u) / 8u;
-    const dim3 grid(per_xcd * 8u), block(256);
+    const dim3 grid(per_xcd * 8u), block(SPEC ? 512 : 256);
     const auto* x = static_cast<const uint16_t*>(p.x);
     const auto* wg = static_cast<const uint8_t*>(p.w);
     const auto* wu = static_cast<const uint8_t*>(p.w_up);
     if (p.out == OutType::F32) {
-        hipLaunchKernelGGL((prefill_kernel<BM, BN, GATE_UP, float, Q8>), grid, block, 0, p.stream, x, wg, wu,
+        hipLaunchKernelGGL((prefill_kernel<BM, BN, GATE_UP, float, Q8, WM, T32, SPEC>), grid, block, 0, p.stream, x, wg, wu,
                            static_cast<float*>(p.y), p.M, p.N, p.K, m_tiles, total, per_xcd);
     } else {
-        hipLaunchKernelGGL((prefill_kernel<BM, BN, GATE_UP, _Float16, Q8>), grid, block, 0, p.stream, x, wg,
+        hipLaunchKernelGGL((prefill_kernel<BM, BN, GATE_UP, _Float16, Q8, WM, T32, SPEC>), grid, block, 0, p.stream, x, wg,
                            wu, static_cast<_Float16*>(p.y), p.M, p.N, p.K, m_tiles, total, per_xcd);
     }
     return hipGetLastError();
@@ -278,6 +327,25 @@ hipError_t launch_prefill(const Problem& p) {
     Variant{"gateup_mfma_r_m" #BM "_n" #BN, Kind::GateUpMfma, BM, BN, 1, &launch_prefill<BM, BN, true>}
 #define MOTE_PREFILL_Q8(BM, BN)                                                                   \
     Variant{"q8_mfma_r_m" #BM "_n" #BN, Kind::Q8Prefill, BM, BN, 1, &launch_prefill<BM, BN, false, true>}
+// 32 x 32 x 16 MFMA tiles, WM waves along M.
+#define MOTE_PREFILL_X32(BM, BN, WM)                                                                 \
+    Variant{"mfma_x32_m" #BM "_n" #BN "_w" #WM, Kind::Mfma, BM, BN, 1,                               \
+            &launch_prefill<BM, BN, false, false, WM, true>}
+#define MOTE_PREFILL_X32S(BM, BN, WM)                                                                \
+    Variant{"mfma_x32s_m" #BM "_n" #BN "_w" #WM, Kind::Mfma, BM, BN, 1,                              \
+            &launch_prefill<BM, BN, false, false, WM, true, true>}
+#define MOTE_PREFILL_GU_X32S(BM, BN, WM)                                                             \
+    Variant{"gateup_mfma_x32s_m" #BM "_n" #BN "_w" #WM, Kind::GateUpMfma, BM, BN, 1,                 \
+            &launch_prefill<BM, BN, true, false, WM, true, true>}
+#define MOTE_PREFILL_Q8_X32S(BM, BN, WM)                                                             \
+    Variant{"q8_mfma_x32s_m" #BM "_n" #BN "_w" #WM, Kind::Q8Prefill, BM, BN, 1,                      \
+            &launch_prefill<BM, BN, false, true, WM, true, true>}
+#define MOTE_PREFILL_GU_X32(BM, BN, WM)                                                              \
+    Variant{"gateup_mfma_x32_m" #BM "_n" #BN "_w" #WM, Kind::GateUpMfma, BM, BN, 1,                  \
+            &launch_prefill<BM, BN, true, false, WM, true>}
+#define MOTE_PREFILL_Q8_X32(BM, BN, WM)                                                              \
+    Variant{"q8_mfma_x32_m" #BM "_n" #BN "_w" #WM, Kind::Q8Prefill, BM, BN, 1,                       \
+            &launch_prefill<BM, BN, false, true, WM, true>}
 
 // 128 x 224 tiles: N = 14336 splits into 64 of them, so M = 512 makes exactly
 // one tile per CU of a 256-CU MI355X.
@@ -286,11 +354,27 @@ const Variant kPrefill[] = {
     MOTE_PREFILL(64, 128), MOTE_PREFILL(128, 224), MOTE_PREFILL(64, 224),
     MOTE_PREFILL_GU(128, 128), MOTE_PREFILL_GU(64, 128), MOTE_PREFILL_GU(128, 64), MOTE_PREFILL_GU(64, 64),
     MOTE_PREFILL_Q8(128, 128), MOTE_PREFILL_Q8(64, 128), MOTE_PREFILL_Q8(128, 64), MOTE_PREFILL_Q8(64, 64),
+    MOTE_PREFILL_X32(128, 128, 1), MOTE_PREFILL_X32(128, 256, 1), MOTE_PREFILL_X32(64, 128, 1),
+    MOTE_PREFILL_X32(128, 128, 2), MOTE_PREFILL_X32(256, 128, 2), MOTE_PREFILL_X32(128, 256, 2),
+    MOTE_PREFILL_GU_X32(128, 128, 1), MOTE_PREFILL_GU_X32(64, 128, 1), MOTE_PREFILL_GU_X32(128, 128, 2),
+    MOTE_PREFILL_Q8_X32(128, 128, 1), MOTE_PREFILL_Q8_X32(64, 128, 1), MOTE_PREFILL_Q8_X32(128, 128, 2),
+    MOTE_PREFILL_X32S(128, 128, 1), MOTE_PREFILL_X32S(128, 128, 2), MOTE_PREFILL_X32S(64, 128, 1),
+    MOTE_PREFILL_X32S(128, 256, 1), MOTE_PREFILL_X32S(128, 256, 2), MOTE_PREFILL_X32S(64, 256, 1),
+    MOTE_PREFILL_GU_X32S(128, 128, 1), MOTE_PREFILL_GU_X32S(128, 128, 2), MOTE_PREFILL_GU_X32S(64, 128, 1),
+    MOTE_PREFILL_GU_X32S(64, 256, 1),
+    MOTE_PREFILL_Q8_X32S(128, 128, 1), MOTE_PREFILL_Q8_X32S(128, 128, 2), MOTE_PREFILL_Q8_X32S(64, 256, 1),
+    MOTE_PREFILL_Q8_X32S(128, 256, 1), MOTE_PREFILL_Q8_X32S(64, 128, 1),
 };
 
 #undef MOTE_PREFILL
 #undef MOTE_PREFILL_GU
 #undef MOTE_PREFILL_Q8
+#undef MOTE_PREFILL_X32
+#undef MOTE_PREFILL_GU_X32
+#undef MOTE_PREFILL_X32S
+#undef MOTE_PREFILL_GU_X32S
+#undef MOTE_PREFILL_Q8_X32S
+#undef MOTE_PREFILL_Q8_X32
 
 }  // namespace
 
