@@ -139,57 +139,64 @@ const Variant* by_name(const char* name) {
     return v;
 }
 
-// Skinny GEMM (3 <= M <= 64, K = 4096) on the matrix cores, transposed weight
-// loads; null when the K slicing does not fit.  Measured on MI355X (graph
-// replays, weights rotated past the MALL): one (16-row, 16-token) item per
-// step of a workgroup, with the reduction deferred over up to 4 items (16
-// waves, one K step each) or 8 items (8 waves, two steps); past 8 items per
-// workgroup with more than 16 tokens, both token tiles in one item.  Above 4
-// tokens the activations are loaded whole lines per instruction and
-// redistributed through LDS (16 x 4096 x 14336: 11.8 us against 12.3 us;
-// 32 x 4096 x 14336: 15.7 against 16.9 us; 16 x 4096 x 4096: 6.8 against
-// 8.0 us); up to 4 tokens the direct loads are level or faster, and with at
-// most one item per workgroup 8 waves of two steps without the deferred
-// reduction are fastest (4 x 4096 x 4096: 5.7 us against 6.1 us).
 // Output tiles of a BM x BN prefill tiling of the problem.
 uint64_t prefill_tiles(const Problem& p, uint32_t bm, uint32_t bn) {
     return static_cast<uint64_t>((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
 }
 
+// Skinny GEMM (3 <= M <= 64, K = 4096) on the matrix cores, transposed weight
+// loads; null when the K slicing does not fit.  One (16-row, token-group) item
+// per step of a workgroup, with the reduction deferred over up to 4 items (16
+// waves, one K step each) or 8 items (8 waves, two steps); above 4 tokens the
+// activations are loaded whole lines per instruction and redistributed through
+// LDS (16 x 4096 x 14336: 11.8 us against 12.3 us); with at most one item per
+// workgroup 8 waves of two steps without the deferred reduction are fastest
+// (4 x 4096 x 4096: 5.7 us against 6.1 us).
+//
+// Tiles, 3 to 64 tokens: items of one 16-token tile up to 16 tokens or
+// while a workgroup owns at most 4 of them, else of two (a 32-token group
+// sharing each dequantised weight operand; its 256 KB of activations per CU
+// cost more than they save when a workgroup owns one or two items: 32 x 4096
+// x 4096 took 9.4 us against 8.4 us).  The activations are loaded and converted before the first weight
+// load (_w).  Measured on MI355X at K = 4096, N = 14336 (graph replays,
+// weights rotated past the MALL): 4 tokens 9.5 us, 8: 9.5 us, 16: 11.0 us,
+// 32: 14.6 us, 64: 20.4 us (the same tiles with the weight loads issued
+// first: 9.9, 10.7, 11.9, 15.7 (16-token items) and 21.5 us).
 const Variant* skinny_heuristic(const Problem& p) {
-    const uint64_t items = static_cast<uint64_t>((p.N + 15) / 16) * ((p.M + 15) / 16);
-    const uint64_t per_group = (items + device_cus() - 1) / static_cast<uint64_t>(device_cus());
-    const bool xc = p.M > 4;
+    const uint64_t cus = static_cast<uint64_t>(device_cus());
+    const uint64_t row_tiles = (p.N + 15) / 16;
+    const uint64_t per16 = (row_tiles * ((p.M + 15) / 16) + cus - 1) / cus;  // items per workgroup
+    const uint64_t per32 = (row_tiles * ((p.M + 31) / 32) + cus - 1) / cus;
     const char* name;
-    if (per_group <= 1 && !xc)
+    if (p.M <= 4 && per16 <= 1)
         name = "skinny_mfma_k8_s2_t1_d1_g1_r1_tr";
-    else if (per_group <= 4)
-        name = xc ? "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c" : "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4";
-    else if (per_group <= 8 || p.M <= 16)
-        name = xc ? "skinny_mfma_k8_s2_t1_d1_g1_r1_tr_l8_c" : "skinny_mfma_k8_s2_t1_d1_g1_r1_tr_l8";
+    else if (per16 <= 4)
+        name = "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w";
+    else if (p.M <= 16)
+        name = "skinny_mfma_k8_s2_t1_d1_g1_r1_tr_l8_c_w";
     else
-        name = "skinny_mfma_k16_s1_t2_d2_g1_r1_tr_c";
+        name = per32 <= 4 ? "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l4_c_w" : "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l8_c_w";
     const Variant* v = by_name(name);
     return v && skinny_mfma_supports(*v, p) ? v : nullptr;
 }
 
 // The fused gate/up up to 64 tokens as a skinny GEMM whose items are one gate
-// and one up row tile (the 32-token items use 8 waves, whose LDS holds the two
-// tiles' stages).  Measured on MI355X at K = 4096, N = 14336: 17.8 us for one
-// token, 20.6 us for 16, 27.3 us for 32 and 36.1 us for 64 (the prefill tiles:
-// 53.0 us); with at most one item per workgroup the per-item kernel (8 x 4096
-// x 4096: 8.5 against 9.6 us).
+// and one up row tile.  Measured on MI355X at K = 4096, N = 14336: 18.2 us for
+// 4 tokens, 19.9 us for 16, 24.4 us for 32 (32-token items, activations
+// first) and 35.6 us for 64 (the prefill tiles: 53.0 us); with at most one
+// item per workgroup the per-item kernel (8 x 4096 x 4096: 8.5 against 9.6 us).
 const Variant* skinny_gate_up_heuristic(const Problem& p) {
-    const uint64_t items = static_cast<uint64_t>((p.N + 15) / 16) * ((p.M + 15) / 16);
-    const uint64_t per_group = (items + device_cus() - 1) / static_cast<uint64_t>(device_cus());
-    const bool xc = p.M > 4;
+    const uint64_t cus = static_cast<uint64_t>(device_cus());
+    const uint64_t per16 = ((p.N + 15) / 16 * ((p.M + 15) / 16) + cus - 1) / cus;
     const char* name;
-    if (per_group <= 1)
+    if (p.M <= 16 && per16 <= 1)
         name = "gateup_skinny_k8_s2_t1_d1";
-    else if (per_group <= 4)
-        name = xc ? "gateup_skinny_k16_s1_t1_d1_l4_c" : "gateup_skinny_k16_s1_t1_d1_l4";
-    else if (per_group <= 8 || p.M <= 16)
-        name = xc ? "gateup_skinny_k8_s2_t1_d1_l8_c" : "gateup_skinny_k8_s2_t1_d1_l8";
+    else if (p.M <= 32 && per16 <= 4)
+        name = p.M <= 8 ? "gateup_skinny_k16_s1_t1_d1_l4_w" : "gateup_skinny_k16_s1_t1_d1_l4_c_w";
+    else if (p.M <= 16)
+        name = "gateup_skinny_k8_s2_t1_d1_l8_c_w";
+    else if (p.M <= 32)
+        name = "gateup_skinny_k8_s2_t2_d1_l4_c_w";
     else
         name = "gateup_skinny_k8_s2_t2_d1_c";
     const Variant* v = by_name(name);
@@ -197,20 +204,21 @@ const Variant* skinny_gate_up_heuristic(const Problem& p) {
 }
 
 // Q8_0 skinny GEMM (the Q4_0 kernels' shapes with 68-byte pairs), 3 to 64
-// tokens.  Measured on MI355X at K = 4096, N = 14336: 15.7 us at 8 tokens,
-// 17.4 us at 16, 22.6 us at 32 (two token tiles per item above 16 tokens)
-// and 29.3 us at 64, where the generic kernel took 117-895 us; coalesced
-// activation loads pay above 8 tokens.  (1, 2 and 4 tokens stay on the
-// streaming GEMV: 4 x 4096 x 4096 in 6.9 us against 8.1 us here.)
+// tokens.  Measured on MI355X at K = 4096, N = 14336: 15.5 us at 8 tokens,
+// 17.1 us at 16, 21.3 us at 32 (32-token items, activations first) and
+// 29.1 us at 64, where the generic kernel took 117-895 us.  (1, 2 and 4
+// tokens stay on the streaming GEMV: 4 x 4096 x 4096 in 6.9 us against 8.1
+// us here.)
 const Variant* skinny_q8_heuristic(const Problem& p) {
-    const uint64_t items = static_cast<uint64_t>((p.N + 15) / 16) * ((p.M + 15) / 16);
-    const uint64_t per_group = (items + device_cus() - 1) / static_cast<uint64_t>(device_cus());
-    const bool xc = p.M > 8;
+    const uint64_t cus = static_cast<uint64_t>(device_cus());
+    const uint64_t per16 = ((p.N + 15) / 16 * ((p.M + 15) / 16) + cus - 1) / cus;
     const char* name;
-    if (per_group <= 4)
-        name = xc ? "q8_skinny_k16_s1_t1_d1_l4_c" : "q8_skinny_k16_s1_t1_d1_l4";
+    if (p.M <= 32 && per16 <= 4)
+        name = p.M <= 8 ? "q8_skinny_k16_s1_t1_d1_l4_w" : "q8_skinny_k16_s1_t1_d1_l4_c_w";
     else if (p.M <= 16)
-        name = xc ? "q8_skinny_k8_s2_t1_d1_l8_c" : "q8_skinny_k8_s2_t1_d1_l8";
+        name = "q8_skinny_k8_s2_t1_d1_l8_c_w";
+    else if (p.M <= 32)
+        name = "q8_skinny_k8_s2_t2_d1_l4_c_w";
     else
         name = "q8_skinny_k16_s1_t2_d1_c";
     const Variant* v = by_name(name);

@@ -52,7 +52,7 @@ __device__ __forceinline__ uint32_t pick(const uint32_t* x, int a, int b) {
 }
 
 template <int KS, int STEPS, int MT, int D, int RT, bool TR, typename OutT, int LAZY = 0, bool XC = false,
-          bool GU = false, bool Q8 = false>
+          bool GU = false, bool Q8 = false, bool XW = false>
 __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __restrict__ x,
                                                              const uint8_t* __restrict__ w,
                                                              const uint8_t* __restrict__ w_up,
@@ -166,7 +166,11 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     // waited for.
     uint32_t buf0[RT * STEPS][kDw];
     uint32_t buf1[RT * STEPS][kDw];
-    load_item(first, buf0);
+    // XW: the activations first, converted before any weight load is issued
+    // (every CU needs all of x; with weight loads queued ahead of it, its
+    // broadcast took twice as long).
+    static_assert(!XW || LAZY > 0, "x first is a variant of the deferred reduction");
+    if constexpr (!XW) load_item(first, buf0);
     // Activations of this wave's K slice for the workgroup's MT token tiles.
     // Tokens past M read row M - 1: a token only feeds its own output column
     // of the MFMA, and those columns are never stored.
@@ -269,6 +273,10 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     }
     };
     if constexpr (LAZY == 0) convert_x();
+    if constexpr (XW) {
+        convert_x();
+        load_item(first, buf0);
+    }
     const DequantConsts dq = dequant_consts();
 
     // Dequantise + MFMA one item (staged in LDS with TR, else from `buf`)
@@ -393,7 +401,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
                 stage_item(buf0);
                 if (i + 1 < LAZY) load_item(it + groups, buf0);
                 __builtin_amdgcn_sched_barrier(0);  // the loads go out before this item's MFMAs
-                if (i == 0) convert_x();
+                if (i == 0 && !XW) convert_x();
                 mma_item(buf0, accs[i]);
             }
         }
@@ -447,7 +455,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
 }
 
 template <int KS, int STEPS, int MT, int D, int G, int RT, bool TR = false, int LAZY = 0, bool XC = false,
-          bool GU = false, bool Q8 = false>
+          bool GU = false, bool Q8 = false, bool XW = false>
 hipError_t launch_skinny(const Problem& p) {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -474,12 +482,12 @@ hipError_t launch_skinny(const Problem& p) {
     const uint32_t per_xcd = groups / 8u;
     const dim3 grid(groups), block(KS * 64);
     if (p.out == OutType::F32) {
-        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float, LAZY, XC, GU, Q8>), grid, block, 0,
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float, LAZY, XC, GU, Q8, XW>), grid, block, 0,
                            p.stream, static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<const uint8_t*>(p.w_up),
                            static_cast<float*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
     } else {
-        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, _Float16, LAZY, XC, GU, Q8>), grid, block, 0,
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, _Float16, LAZY, XC, GU, Q8, XW>), grid, block, 0,
                            p.stream, static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<const uint8_t*>(p.w_up),
                            static_cast<_Float16*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
@@ -505,6 +513,17 @@ hipError_t launch_skinny(const Problem& p) {
 #define MOTE_SKINNY_Q8(KS, STEPS, MT, D, L, XC, SUFFIX)                                          \
     Variant{"q8_skinny_k" #KS "_s" #STEPS "_t" #MT "_d" #D SUFFIX, Kind::Q8Skinny, KS, STEPS, MT,    \
             &launch_skinny<KS, STEPS, MT, D, 1, 1, true, L, XC, false, true>}
+// x first (_w): the activations are loaded and converted before the first
+// weight load.
+#define MOTE_SKINNY_W(KS, STEPS, MT, L, XC, SUFFIX)                                                 \
+    Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d1_g1_r1_tr_l" #L SUFFIX "_w", Kind::SkinnyMfma, KS, \
+            STEPS, MT, &launch_skinny<KS, STEPS, MT, 1, 1, 1, true, L, XC, false, false, true>}
+#define MOTE_SKINNY_GU_W(KS, STEPS, MT, L, XC, SUFFIX)                                              \
+    Variant{"gateup_skinny_k" #KS "_s" #STEPS "_t" #MT "_d1_l" #L SUFFIX "_w", Kind::GateUpSkinny, KS, STEPS, \
+            MT, &launch_skinny<KS, STEPS, MT, 1, 1, 2, true, L, XC, true, false, true>}
+#define MOTE_SKINNY_Q8_W(KS, STEPS, MT, L, XC, SUFFIX)                                              \
+    Variant{"q8_skinny_k" #KS "_s" #STEPS "_t" #MT "_d1_l" #L SUFFIX "_w", Kind::Q8Skinny, KS, STEPS, MT, \
+            &launch_skinny<KS, STEPS, MT, 1, 1, 1, true, L, XC, false, true, true>}
 #define MOTE_SKINNY_TR(KS, STEPS, MT, D, G)                                                       \
     Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d" #D "_g" #G "_r1_tr", Kind::SkinnyMfma, KS, \
             STEPS, MT, &launch_skinny<KS, STEPS, MT, D, G, 1, true>}
@@ -533,6 +552,13 @@ const Variant kSkinny[] = {
     MOTE_SKINNY_Q8(8, 2, 1, 1, 0, false, ""), MOTE_SKINNY_Q8(16, 1, 1, 1, 4, false, "_l4"),
     MOTE_SKINNY_Q8(16, 1, 1, 1, 4, true, "_l4_c"), MOTE_SKINNY_Q8(8, 2, 1, 1, 8, false, "_l8"),
     MOTE_SKINNY_Q8(8, 2, 1, 1, 8, true, "_l8_c"), MOTE_SKINNY_Q8(16, 1, 2, 1, 0, true, "_c"), MOTE_SKINNY_Q8(8, 2, 2, 1, 0, true, "_c"),
+    MOTE_SKINNY_W(16, 1, 1, 4, false, ""), MOTE_SKINNY_W(16, 1, 1, 4, true, "_c"), MOTE_SKINNY_W(8, 2, 1, 8, true, "_c"),
+    MOTE_SKINNY_W(8, 2, 2, 4, true, "_c"), MOTE_SKINNY_W(8, 2, 2, 8, true, "_c"), MOTE_SKINNY_W(8, 2, 1, 4, true, "_c"),
+    MOTE_SKINNY_W(16, 1, 1, 8, true, "_c"),
+    MOTE_SKINNY_GU_W(16, 1, 1, 4, false, ""), MOTE_SKINNY_GU_W(16, 1, 1, 4, true, "_c"),
+    MOTE_SKINNY_GU_W(8, 2, 1, 8, true, "_c"), MOTE_SKINNY_GU_W(8, 2, 2, 4, true, "_c"),
+    MOTE_SKINNY_Q8_W(16, 1, 1, 4, false, ""), MOTE_SKINNY_Q8_W(16, 1, 1, 4, true, "_c"),
+    MOTE_SKINNY_Q8_W(8, 2, 2, 4, true, "_c"), MOTE_SKINNY_Q8_W(8, 2, 1, 8, true, "_c"),
 };
 
 #undef MOTE_SKINNY
@@ -542,6 +568,9 @@ const Variant kSkinny[] = {
 #undef MOTE_SKINNY_TRC
 #undef MOTE_SKINNY_GU
 #undef MOTE_SKINNY_Q8
+#undef MOTE_SKINNY_W
+#undef MOTE_SKINNY_GU_W
+#undef MOTE_SKINNY_Q8_W
 
 }  // namespace
 
