@@ -225,6 +225,55 @@ const Variant* skinny_q8_heuristic(const Problem& p) {
     return v && skinny_mfma_supports(*v, p) ? v : nullptr;
 }
 
+// Split-K skinny GEMM (1 to 64 tokens, K a multiple of 2048 from 8192 up, or
+// any K no plain slicing fits): K cut into parts of 2048 or 4096, partial
+// tiles added by a second kernel.  Measured on MI355X (the choices below):
+//   K = 14336, N = 4096: 2-16 tokens 13.0-14.2 us, 24: 18.9 us, 32: 19.9 us,
+//     64: 27.4 us (the vector-ALU GEMV it replaces: 14.9 us at 2 tokens,
+//     42.3 at 8, 76.2 at 16, 129.8 at 32);
+//   K = 28672, N = 8192: 16 tokens 35.0 us, 32: 45.4 us, 64: 85.6 us;
+//   K = 8192, N = 8192: 3 tokens 12.2 us, 16: 13.4 us, 32: 17.5 us, 64:
+//     24.5 us (one 8192 slice at 16 tokens: 19.5 us);
+//   gate/up K = 8192, N = 28672: 4 tokens 66.0 us, 16: 72.1 us, 32: 92.8 us
+//     (the 64 x 128 prefill tiles: 116.6 us at 32 tokens, 117.8 at 48).
+// 16-wave workgroups (one per CU) take 4 items while that fits one round of
+// CUs; past that, and for 32-token items, 8 items per workgroup of 8 waves
+// with the larger K part once the smaller one gives more than 256 workgroups.
+const Variant* split_k_heuristic(const Problem& p, Op op) {
+    if (p.M > 64 || p.K % 2048 != 0 || p.K < 4096) return nullptr;
+    const uint64_t cus = static_cast<uint64_t>(device_cus());
+    const uint64_t row_tiles = (p.N + 15) / 16;
+    const uint64_t items2k = row_tiles * ((p.M + 15) / 16) * (p.K / 2048);  // 16-token items, parts of 2048
+    const uint64_t items4k = row_tiles * ((p.M + 15) / 16) * (p.K / 4096);
+    const uint64_t items2k_t2 = row_tiles * ((p.M + 31) / 32) * (p.K / 2048);  // 32-token items
+    const bool k4 = p.K % 4096 == 0;
+    const char* name;
+    if (op == Op::LinearQ8) {
+        name = p.M <= 32 ? "q8_skinny_k8_s1_t1_d1_l4_c_w_sk" : "q8_skinny_k8_s1_t2_d1_l8_c_w_sk";
+    } else if (op == Op::GateUp) {
+        if (p.M > 32) return nullptr;  // the prefill tiles
+        if (p.M > 16)
+            name = "gateup_skinny_k8_s1_t2_d1_l8_c_w_sk";
+        else
+            name = items2k > 4 * 512 ? "gateup_skinny_k8_s1_t1_d1_l8_c_w_sk" : "gateup_skinny_k8_s1_t1_d1_l4_c_w_sk";
+    } else if (p.M > 16) {
+        if (!k4)
+            name = p.M > 32 ? "skinny_mfma_k8_s1_t2_d1_g1_r1_tr_l8_c_w_sk" : "skinny_mfma_k8_s1_t2_d1_g1_r1_tr_l4_c_w_sk";
+        else if (p.M <= 32 && items2k_t2 <= 8 * 256)
+            name = "skinny_mfma_k8_s1_t2_d1_g1_r1_tr_l8_c_w_sk";
+        else
+            name = "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l8_c_w_sk";
+    } else if (k4) {
+        name = items4k > 4 * cus ? "skinny_mfma_k8_s2_t1_d1_g1_r1_tr_l8_c_w_sk"
+                                 : "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w_sk";
+    } else {
+        name = items2k > 4 * 512 ? "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l8_c_w_sk"
+                                 : "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l4_c_w_sk";
+    }
+    const Variant* v = by_name(name);
+    return v && skinny_mfma_supports(*v, p) ? v : nullptr;
+}
+
 // Shape heuristic used when autotuning is off.
 const Variant* heuristic(const Problem& p, Op op) {
     const bool fast = fast_eligible(p);
@@ -246,8 +295,10 @@ const Variant* heuristic(const Problem& p, Op op) {
             const Variant* v = by_name(name);
             if (v && gemv_stream_supports(*v, p)) return v;
         }
-        if (fast && p.M <= 64)
+        if (fast && p.M <= 64) {
             if (const Variant* v = skinny_q8_heuristic(p)) return v;
+            if (const Variant* v = split_k_heuristic(p, op)) return v;
+        }
         if (fast && p.M >= 64) {
             // The prefill tiles with 68-byte pairs: the largest 32 x 32 MFMA
             // tile with staging waves that still gives about one tile per CU
@@ -275,12 +326,17 @@ const Variant* heuristic(const Problem& p, Op op) {
             const Variant* v = by_name(name);
             if (v && gemv_stream_supports(*v, p)) return v;
         }
-        if (fast && p.M <= 64)
+        if (fast && p.M <= 64) {
             if (const Variant* v = skinny_gate_up_heuristic(p)) return v;
-        if (fast && p.M >= 64) {
+            if (const Variant* v = split_k_heuristic(p, op)) return v;
+        }
+        if (fast && p.M > 32) {
             // 32 x 32 MFMA tiles with staging waves once 128 x 128 tiles give
             // about one per CU (256 tokens: 72.7-75.4 us, 512: 139.5-144.6 us,
-            // against 84.5 and 164 us for 16 x 16 tiles).
+            // against 84.5 and 164 us for 16 x 16 tiles); up to 64 tokens
+            // the 64 x 128 tiles (64 x 8192 x 28672: 119.4 us, against 150.3
+            // us for 128 x 128 tiles).
+            if (p.M <= 64 && prefill_tiles(p, 64, 128) >= 200) return by_name("gateup_mfma_x32s_m64_n128_w1");
             if (prefill_tiles(p, 128, 128) >= 200) return by_name("gateup_mfma_x32s_m128_n128_w1");
             return by_name(p.M >= 128 ? "gateup_mfma_r_m128_n64" : "gateup_mfma_r_m64_n64");
         }
@@ -290,6 +346,7 @@ const Variant* heuristic(const Problem& p, Op op) {
     if (p.M == 64) {
         // 64 tokens still run as a skinny GEMM (faster than the prefill tiles).
         const Variant* v = skinny_heuristic(p);
+        if (!v) v = split_k_heuristic(p, op);
         if (v) return v;
     }
     if (p.M >= 64) {
@@ -354,6 +411,7 @@ const Variant* heuristic(const Problem& p, Op op) {
         if (v && gemv_stream_supports(*v, p)) return v;
     }
     if (const Variant* v = skinny_heuristic(p)) return v;
+    if (const Variant* v = split_k_heuristic(p, op)) return v;
     const char* suffix = p.M <= 16 ? "_t1_d1_g1_r1" : p.M <= 32 ? "_t1_d2_g1_r1" : "_t2_d2_g1_r1";
     for (const char* name : {"skinny_mfma_k16_s1", "skinny_mfma_k8_s2", "skinny_mfma_k16_s2",
                              "skinny_mfma_k8_s1", "skinny_mfma_k4_s2", "skinny_mfma_k4_s1"}) {
@@ -473,6 +531,36 @@ int gate_up(Dispatcher* d, const void* input, const void* gate, const void* up, 
 }
 
 }  // namespace
+
+hipError_t stream_scratch(hipStream_t stream, size_t bytes, void** ptr) {
+    static std::mutex mu;
+    static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> buffers;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    auto& b = buffers[{dev, stream}];
+    if (b.second < bytes) {
+        if (b.first != nullptr) {
+            // Earlier calls on this stream may still read the old buffer.
+            e = hipStreamSynchronize(stream);
+            if (e != hipSuccess) return e;
+            e = hipFree(b.first);
+            b = {nullptr, 0};
+            if (e != hipSuccess) return e;
+        }
+        const size_t want = std::max<size_t>(bytes, size_t{1} << 20);
+        e = hipMalloc(&b.first, want);
+        if (e != hipSuccess) {
+            b = {nullptr, 0};
+            return e;
+        }
+        b.second = want;
+    }
+    *ptr = b.first;
+    return hipSuccess;
+}
+
 }  // namespace mote::q4_0
 
 using namespace mote::q4_0;

@@ -40,6 +40,7 @@
 #include "common.hpp"
 #include "q4_0.hpp"
 
+#include <cstring>
 #include <type_traits>
 
 namespace mote::q4_0 {
@@ -52,14 +53,15 @@ __device__ __forceinline__ uint32_t pick(const uint32_t* x, int a, int b) {
 }
 
 template <int KS, int STEPS, int MT, int D, int RT, bool TR, typename OutT, int LAZY = 0, bool XC = false,
-          bool GU = false, bool Q8 = false, bool XW = false>
+          bool GU = false, bool Q8 = false, bool XW = false, bool SK = false>
 __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __restrict__ x,
                                                              const uint8_t* __restrict__ w,
                                                              const uint8_t* __restrict__ w_up,
                                                              OutT* __restrict__ y, uint32_t M,
                                                              uint32_t N, uint32_t K,
                                                              uint32_t token_groups, uint32_t items,
-                                                             uint32_t groups_per_xcd) {
+                                                             uint32_t groups_per_xcd, float* __restrict__ kpartial,
+                                                             uint32_t kparts) {
     // Transposed loads: wave-private staging of the raw pairs, [row tile][row]
     // [pair of the slice], rows padded by one dword so the 16 rows read by an
     // MFMA operand fall on distinct banks.
@@ -103,12 +105,20 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     // token tiles of a row tile read its weights through the same L2.
     const uint32_t first = (blockIdx.x % 8u) * groups_per_xcd + blockIdx.x / 8u;
 
-    // Item -> (row tile, token group of MT 16-token tiles).  The grid size is
-    // a multiple of token_groups, so a workgroup keeps one token group.
+    // Item -> (row tile, token group of MT 16-token tiles, K part).  The grid
+    // size is a multiple of token_groups x kparts, so a workgroup keeps one
+    // token group and one K part.  Split K (SK): K is cut into kparts parts of
+    // KS x STEPS x 256; each item writes its part's partial sums to
+    // `kpartial` ([kparts][M][N] f32; gate/up: the gate planes, then the up
+    // planes), which a second kernel adds in part order.
     static_assert(!GU || RT == 2, "gate/up items are one gate and one up row tile");
     constexpr uint32_t kItemRows = GU ? 16u : 16u * RT;
-    auto rows_of = [&](uint32_t item) { return (item / token_groups) * kItemRows; };
-    const uint32_t tok0 = (first % token_groups) * (16u * MT);
+    const uint32_t combos = token_groups * kparts;
+    auto rows_of = [&](uint32_t item) { return (item / combos) * kItemRows; };
+    const uint32_t combo = first % combos;
+    const uint32_t tok0 = (combo % token_groups) * (16u * MT);
+    const uint32_t kpart = combo / token_groups;
+    const uint32_t pair0 = kpart * (npairs / kparts);  // first block pair of this K part
 
     // Weight loads of one item: RT row tiles x STEPS pairs per lane.  Direct
     // mapping: lane (li, lg) loads the pair it feeds to the MFMAs, so one
@@ -126,10 +136,10 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
                 uint32_t r, p;
                 if constexpr (TR) {
                     r = static_cast<uint32_t>(s * kRowsPerLoad + lane / kSlicePairs);
-                    p = static_cast<uint32_t>(kw * kSlicePairs + lane % kSlicePairs);
+                    p = pair0 + static_cast<uint32_t>(kw * kSlicePairs + lane % kSlicePairs);
                 } else {
                     r = static_cast<uint32_t>(li);
-                    p = (static_cast<uint32_t>(kw) * STEPS + s) * 4u + static_cast<uint32_t>(lg);
+                    p = pair0 + (static_cast<uint32_t>(kw) * STEPS + s) * 4u + static_cast<uint32_t>(lg);
                 }
                 const uint32_t n = min(rows_of(it) + (GU ? 0u : 16u * rt) + r, N - 1);
                 const uint8_t* base = (GU && rt == 1) ? w_up : w;
@@ -184,8 +194,8 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
             for (int c = 0; c < kXLoads; ++c) {
                 const uint32_t f = static_cast<uint32_t>(c) * 1024u + static_cast<uint32_t>(lane) * 16u;
                 const uint32_t m = min(tok0 + 16u * mt + f / kSliceBytes, M - 1);
-                const uint16_t* src = x + static_cast<size_t>(m) * K + static_cast<size_t>(kw) * STEPS * 256 +
-                                      (f % kSliceBytes) / 2;
+                const uint16_t* src = x + static_cast<size_t>(m) * K + static_cast<size_t>(pair0) * 64 +
+                                      static_cast<size_t>(kw) * STEPS * 256 + (f % kSliceBytes) / 2;
                 xg[mt][c] = *reinterpret_cast<const u32x4*>(src);
             }
     } else {
@@ -195,7 +205,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
             const uint16_t* xrow = x + static_cast<size_t>(m) * K;
 #pragma unroll
             for (int s = 0; s < STEPS; ++s) {
-                const uint32_t p = (static_cast<uint32_t>(kw) * STEPS + s) * 4u + static_cast<uint32_t>(lg);
+                const uint32_t p = pair0 + (static_cast<uint32_t>(kw) * STEPS + s) * 4u + static_cast<uint32_t>(lg);
                 const u32x4* src = reinterpret_cast<const u32x4*>(xrow + static_cast<size_t>(p) * 64);
 #pragma unroll
                 for (int c = 0; c < 8; ++c) xraw[mt][s][c] = src[c];
@@ -330,19 +340,26 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     };
 
     // The KS partial tiles of part slot `tile` summed in slice order at
-    // (row, token); with GU, silu(gate) * up from the slot's gate tile and the
-    // up tile MT slots after it.
-    auto reduced = [&](int tile, int row, int tok) {
+    // (row, token).
+    auto tile_sum = [&](int tile, int row, int tok) {
         float sum = part[0][tile][row][tok];
 #pragma unroll
         for (int k = 1; k < KS; ++k) sum += part[k][tile][row][tok];
-        if constexpr (GU) {
-            float up = part[0][tile + MT][row][tok];
-#pragma unroll
-            for (int k = 1; k < KS; ++k) up += part[k][tile + MT][row][tok];
-            sum = silu(sum) * up;
-        }
         return sum;
+    };
+    // Output (m, n) from part slot `tile`; with GU, silu(gate) * up from the
+    // slot's gate tile and the up tile MT slots after it (split K: both sums
+    // to their planes, the second kernel applies silu(gate) * up).
+    auto store = [&](uint32_t m, uint32_t n, int tile, int row, int tok) {
+        if constexpr (SK) {
+            float* dst = kpartial + (static_cast<size_t>(kpart) * M + m) * N + n;
+            dst[0] = tile_sum(tile, row, tok);
+            if constexpr (GU) dst[static_cast<size_t>(kparts) * M * N] = tile_sum(tile + MT, row, tok);
+        } else {
+            float v = tile_sum(tile, row, tok);
+            if constexpr (GU) v = silu(v) * tile_sum(tile + MT, row, tok);
+            y[static_cast<size_t>(m) * N + n] = to_out<OutT>(v);
+        }
     };
 
     auto process = [&](uint32_t it, uint32_t (&buf)[RT * STEPS][kDw], uint32_t next, auto refill) {
@@ -374,7 +391,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
             const int rt = GU ? 0 : tile / MT, mt = tile % MT;
             const uint32_t n = rows_of(it) + 16u * rt + static_cast<uint32_t>(row);
             const uint32_t m = tok0 + 16u * mt + static_cast<uint32_t>(tok);
-            if (n < N && m < M) y[static_cast<size_t>(m) * N + n] = to_out<OutT>(reduced(tile, row, tok));
+            if (n < N && m < M) store(m, n, tile, row, tok);
         }
         __syncthreads();
     };
@@ -425,8 +442,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
                 if (it >= items) continue;
                 const uint32_t n = rows_of(it) + 16u * rt + static_cast<uint32_t>(row);
                 const uint32_t m = tok0 + 16u * mt + static_cast<uint32_t>(tok);
-                if (n < N && m < M)
-                    y[static_cast<size_t>(m) * N + n] = to_out<OutT>(reduced((i * RT + rt) * MT + mt, row, tok));
+                if (n < N && m < M) store(m, n, (i * RT + rt) * MT + mt, row, tok);
             }
         }
     } else if constexpr (TR && D == 1) {
@@ -454,8 +470,28 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     }
 }
 
+// Split-K epilogue: y[i] = sum over the K parts of part[k][i], in part order
+// (deterministic), converted to the output type; gate/up (GU): silu of the
+// gate sum times the up sum, the up planes following the kparts gate planes.
+template <typename OutT, bool GU>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, uint32_t kparts,
+                                                            uint64_t count, OutT* __restrict__ y) {
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < count;
+         i += static_cast<uint64_t>(gridDim.x) * 256) {
+        float s = part[i];
+        for (uint32_t k = 1; k < kparts; ++k) s += part[static_cast<uint64_t>(k) * count + i];
+        if constexpr (GU) {
+            const float* up = part + static_cast<uint64_t>(kparts) * count;
+            float u = up[i];
+            for (uint32_t k = 1; k < kparts; ++k) u += up[static_cast<uint64_t>(k) * count + i];
+            s = silu(s) * u;
+        }
+        y[i] = to_out<OutT>(s);
+    }
+}
+
 template <int KS, int STEPS, int MT, int D, int G, int RT, bool TR = false, int LAZY = 0, bool XC = false,
-          bool GU = false, bool Q8 = false, bool XW = false>
+          bool GU = false, bool Q8 = false, bool XW = false, bool SK = false>
 hipError_t launch_skinny(const Problem& p) {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -467,30 +503,53 @@ hipError_t launch_skinny(const Problem& p) {
     constexpr uint32_t kItemRows = GU ? 16u : 16u * RT;
     const uint32_t row_tiles = (p.N + kItemRows - 1) / kItemRows;
     const uint32_t token_groups = (p.M + 16 * MT - 1) / (16 * MT);
-    const uint64_t items64 = static_cast<uint64_t>(row_tiles) * token_groups;
+    const uint32_t kparts = SK ? p.K / (KS * STEPS * 256) : 1u;
+    const uint64_t items64 = static_cast<uint64_t>(row_tiles) * token_groups * kparts;
     if (items64 > 0x7fffffffull) return hipErrorInvalidConfiguration;
     const uint32_t items = static_cast<uint32_t>(items64);
-    // Whole XCD rounds (8 groups) that are also a multiple of token_groups, so
-    // every workgroup keeps one token group; extra groups find no item.
-    uint32_t a = 8u, b = token_groups;
+    // Whole XCD rounds (8 groups) that are also a multiple of token_groups x
+    // kparts, so every workgroup keeps one token group and K part; extra
+    // groups find no item.
+    const uint32_t combos = token_groups * kparts;
+    uint32_t a = 8u, b = combos;
     while (b != 0) { const uint32_t t = a % b; a = b; b = t; }
-    const uint32_t unit = 8u / a * token_groups;  // lcm(8, token_groups)
+    const uint32_t unit = 8u / a * combos;  // lcm(8, combos)
     uint32_t groups = static_cast<uint32_t>(cus) * G;
     if (groups > items) groups = items;
     if (LAZY > 0 && groups < (items + LAZY - 1) / LAZY) groups = (items + LAZY - 1) / LAZY;  // <= LAZY items each
     groups = (groups + unit - 1) / unit * unit;
     const uint32_t per_xcd = groups / 8u;
     const dim3 grid(groups), block(KS * 64);
+    float* part = nullptr;
+    const uint64_t count = static_cast<uint64_t>(p.M) * p.N;
+    if constexpr (SK) {
+        void* buf = nullptr;
+        const hipError_t e = stream_scratch(p.stream, count * kparts * (GU ? 2 : 1) * sizeof(float), &buf);
+        if (e != hipSuccess) return e;
+        part = static_cast<float*>(buf);
+    }
     if (p.out == OutType::F32) {
-        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float, LAZY, XC, GU, Q8, XW>), grid, block, 0,
-                           p.stream, static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
-                           static_cast<const uint8_t*>(p.w_up),
-                           static_cast<float*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float, LAZY, XC, GU, Q8, XW, SK>), grid,
+                           block, 0, p.stream, static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
+                           static_cast<const uint8_t*>(p.w_up), static_cast<float*>(p.y), p.M, p.N, p.K,
+                           token_groups, items, per_xcd, part, kparts);
     } else {
-        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, _Float16, LAZY, XC, GU, Q8, XW>), grid, block, 0,
-                           p.stream, static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
-                           static_cast<const uint8_t*>(p.w_up),
-                           static_cast<_Float16*>(p.y), p.M, p.N, p.K, token_groups, items, per_xcd);
+        hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, _Float16, LAZY, XC, GU, Q8, XW, SK>), grid,
+                           block, 0, p.stream, static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
+                           static_cast<const uint8_t*>(p.w_up), static_cast<_Float16*>(p.y), p.M, p.N, p.K,
+                           token_groups, items, per_xcd, part, kparts);
+    }
+    if constexpr (SK) {
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const uint64_t blocks64 = (count + 255) / 256;
+        const dim3 rgrid(static_cast<uint32_t>(blocks64 < 2048 ? blocks64 : 2048)), rblock(256);
+        if (p.out == OutType::F32)
+            hipLaunchKernelGGL((splitk_reduce_kernel<float, GU>), rgrid, rblock, 0, p.stream, part, kparts, count,
+                               static_cast<float*>(p.y));
+        else
+            hipLaunchKernelGGL((splitk_reduce_kernel<_Float16, GU>), rgrid, rblock, 0, p.stream, part, kparts, count,
+                               static_cast<_Float16*>(p.y));
     }
     return hipGetLastError();
 }
@@ -524,6 +583,18 @@ hipError_t launch_skinny(const Problem& p) {
 #define MOTE_SKINNY_Q8_W(KS, STEPS, MT, L, XC, SUFFIX)                                              \
     Variant{"q8_skinny_k" #KS "_s" #STEPS "_t" #MT "_d1_l" #L SUFFIX "_w", Kind::Q8Skinny, KS, STEPS, MT, \
             &launch_skinny<KS, STEPS, MT, 1, 1, 1, true, L, XC, false, true, true>}
+// Split K (_sk): K any multiple of KS x STEPS x 256, cut into that many
+// parts; partial tiles in a per-stream scratch buffer, added by a second
+// kernel.
+#define MOTE_SKINNY_SK(KS, STEPS, MT, L, SUFFIX)                                                   \
+    Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d1_g1_r1_tr_l" #L SUFFIX "_w_sk", Kind::SkinnyMfma, KS, \
+            STEPS, MT, &launch_skinny<KS, STEPS, MT, 1, 1, 1, true, L, true, false, false, true, true>}
+#define MOTE_SKINNY_Q8_SK(KS, STEPS, MT, L, SUFFIX)                                                \
+    Variant{"q8_skinny_k" #KS "_s" #STEPS "_t" #MT "_d1_l" #L SUFFIX "_w_sk", Kind::Q8Skinny, KS, STEPS, MT, \
+            &launch_skinny<KS, STEPS, MT, 1, 1, 1, true, L, true, false, true, true, true>}
+#define MOTE_SKINNY_GU_SK(KS, STEPS, MT, L, SUFFIX)                                                \
+    Variant{"gateup_skinny_k" #KS "_s" #STEPS "_t" #MT "_d1_l" #L SUFFIX "_w_sk", Kind::GateUpSkinny, KS, STEPS, \
+            MT, &launch_skinny<KS, STEPS, MT, 1, 1, 2, true, L, true, true, false, true, true>}
 #define MOTE_SKINNY_TR(KS, STEPS, MT, D, G)                                                       \
     Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d" #D "_g" #G "_r1_tr", Kind::SkinnyMfma, KS, \
             STEPS, MT, &launch_skinny<KS, STEPS, MT, D, G, 1, true>}
@@ -559,6 +630,13 @@ const Variant kSkinny[] = {
     MOTE_SKINNY_GU_W(8, 2, 1, 8, true, "_c"), MOTE_SKINNY_GU_W(8, 2, 2, 4, true, "_c"),
     MOTE_SKINNY_Q8_W(16, 1, 1, 4, false, ""), MOTE_SKINNY_Q8_W(16, 1, 1, 4, true, "_c"),
     MOTE_SKINNY_Q8_W(8, 2, 2, 4, true, "_c"), MOTE_SKINNY_Q8_W(8, 2, 1, 8, true, "_c"),
+    MOTE_SKINNY_SK(8, 1, 1, 8, "_c"), MOTE_SKINNY_SK(8, 1, 2, 8, "_c"), MOTE_SKINNY_SK(16, 1, 1, 4, "_c"),
+    MOTE_SKINNY_SK(16, 1, 1, 8, "_c"), MOTE_SKINNY_SK(8, 1, 1, 4, "_c"), MOTE_SKINNY_SK(16, 1, 2, 4, "_c"),
+    MOTE_SKINNY_SK(8, 2, 1, 8, "_c"), MOTE_SKINNY_SK(8, 2, 2, 8, "_c"),
+    MOTE_SKINNY_Q8_SK(8, 1, 1, 8, "_c"), MOTE_SKINNY_Q8_SK(8, 1, 2, 8, "_c"), MOTE_SKINNY_Q8_SK(16, 1, 1, 4, "_c"),
+    MOTE_SKINNY_SK(8, 1, 2, 4, "_c"), MOTE_SKINNY_Q8_SK(8, 1, 1, 4, "_c"), MOTE_SKINNY_Q8_SK(8, 1, 2, 4, "_c"),
+    MOTE_SKINNY_GU_SK(8, 1, 1, 4, "_c"), MOTE_SKINNY_GU_SK(8, 1, 1, 8, "_c"), MOTE_SKINNY_GU_SK(16, 1, 1, 4, "_c"),
+    MOTE_SKINNY_GU_SK(8, 1, 2, 4, "_c"), MOTE_SKINNY_GU_SK(8, 1, 2, 8, "_c"),
 };
 
 #undef MOTE_SKINNY
@@ -569,6 +647,9 @@ const Variant kSkinny[] = {
 #undef MOTE_SKINNY_GU
 #undef MOTE_SKINNY_Q8
 #undef MOTE_SKINNY_W
+#undef MOTE_SKINNY_SK
+#undef MOTE_SKINNY_Q8_SK
+#undef MOTE_SKINNY_GU_SK
 #undef MOTE_SKINNY_GU_W
 #undef MOTE_SKINNY_Q8_W
 
@@ -584,6 +665,14 @@ const Variant* skinny_mfma_variants(int* count) {
 // token tiles per pass, RT row tiles per item).
 bool skinny_mfma_supports(const Variant& v, const Problem& p) {
     const uint32_t span = static_cast<uint32_t>(v.p0) * static_cast<uint32_t>(v.p1) * 256u;
+    const size_t len = std::strlen(v.name);
+    if (len > 3 && std::strcmp(v.name + len - 3, "_sk") == 0) {  // split K: any multiple of the slice, two parts or more
+        const bool up_ok = v.kind == Kind::GateUpSkinny
+                               ? p.w_up != nullptr && reinterpret_cast<uintptr_t>(p.w_up) % 4 == 0
+                               : p.w_up == nullptr;
+        return p.M >= 1 && p.M <= 64 && p.K >= 2 * span && p.K % span == 0 && reinterpret_cast<uintptr_t>(p.w) % 4 == 0 &&
+               reinterpret_cast<uintptr_t>(p.x) % 16 == 0 && up_ok;
+    }
     const bool up_ok = v.kind != Kind::GateUpSkinny ||
                        (p.w_up != nullptr && reinterpret_cast<uintptr_t>(p.w_up) % 4 == 0);
     return p.M >= 1 && p.M <= 64 && p.K == span && reinterpret_cast<uintptr_t>(p.w) % 4 == 0 &&

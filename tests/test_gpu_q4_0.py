@@ -301,7 +301,7 @@ def _skinny_k(variant):
     return int(ks) * int(rest.split("_t")[0]) * 256
 
 
-@pytest.mark.parametrize("variant", _variants("skinny_mfma_"))
+@pytest.mark.parametrize("variant", [v for v in _variants("skinny_mfma_") if not v.endswith("_sk")])
 def test_every_skinny_mfma_variant(stream, oracle, variant):
     """Matrix-core skinny GEMM: tokens padded inside a 16-token tile (M = 2, 5),
     exactly one and two tiles (16, 32), one token over (17, 33), the 64-token
@@ -372,7 +372,7 @@ def test_every_stream_gate_up_variant(stream, oracle, variant):
         check_gate_up(oracle, y16, x, wg, wu, 1, n, k, cols=cols, f16_out=True, what=f"{variant} f16 1x{n}x{k}")
 
 
-@pytest.mark.parametrize("variant", _variants("gateup_skinny_"))
+@pytest.mark.parametrize("variant", [v for v in _variants("gateup_skinny_") if not v.endswith("_sk")])
 def test_every_skinny_gate_up_variant(stream, oracle, variant):
     """Skinny gate/up items (one gate and one up row tile): one token, tokens
     padded inside a tile, one over a tile, the 64-token maximum, N ragged

@@ -1,0 +1,120 @@
+"""GPU parity of the split-K skinny GEMM (1-64 tokens, K a multiple of the
+K slice: the MLP down projection, K = 14336, among others; the fused gate/up at
+K = 8192) against the oracle.
+
+The split-K tiles cut K into parts, write each part's partial tile to a
+per-stream scratch buffer and add the parts in a second kernel, in part order;
+the products are rounded once to binary16 before the MFMA, so the check is the
+path's tolerance (|y - y64| <= 1e-3 |y64| or <= 2e-3 sqrt(K) max|d| max|x|,
+y64 the f64-accumulated oracle), and two runs must agree bit for bit.
+"""
+
+from __future__ import annotations
+
+import functools
+
+import numpy as np
+import pytest
+
+from mote_amd import ops, workloads as wl
+from test_gpu_q4_0 import check_against_oracle, check_gate_up, run_gate_up, run_linear, sample_columns
+import test_gpu_q8_0 as q8
+
+pytestmark = pytest.mark.gpu
+
+
+@functools.lru_cache(maxsize=None)
+def q4_weights(seed: int, n: int, k: int) -> np.ndarray:
+    return wl.q4_0_weights(seed, n, k)
+
+
+@functools.lru_cache(maxsize=None)
+def normal_x(seed: int, m: int, k: int) -> np.ndarray:
+    return wl.normal_f16(seed, m * k)
+
+
+def _slice(variant: str) -> int:
+    ks, rest = variant.split("_k", 1)[1].split("_s", 1)
+    return int(ks) * int(rest.split("_t")[0]) * 256
+
+
+SPLIT_K = [v for v in ops.variant_names() if v.startswith("skinny_mfma_") and v.endswith("_sk")]
+GATE_UP_SPLIT_K = [v for v in ops.variant_names() if v.startswith("gateup_skinny_") and v.endswith("_sk")]
+Q8_SPLIT_K = [v for v in ops.variant_names() if v.startswith("q8_skinny_") and v.endswith("_sk")]
+
+
+@pytest.mark.parametrize("variant", SPLIT_K)
+def test_every_split_k_variant(stream, oracle, variant):
+    """Two, three and seven K parts; tokens padded inside a tile, exactly one
+    and two tiles, one over, the 64-token maximum; N ragged against the
+    16-row tiles; f32 and f16 outputs; a repeat is bitwise equal."""
+    d = ops.Q4_0Dispatch()
+    d.force(variant)
+    span = _slice(variant)
+    for m, n, parts in [(3, 100, 2), (16, 48, 3), (17, 130, 2), (33, 7, 7), (64, 80, 2), (20, 1000, 3)]:
+        k = span * parts
+        x = normal_x(wl.seed_for(40, m), m, k)
+        w = q4_weights(wl.seed_for(40, 100 + n), n, k)
+        y = run_linear(stream, x, w, m, n, k, dispatch=d)
+        check_against_oracle(oracle, y, x, w, m, n, k, what=f"{variant} {m}x{n}x{k}")
+    assert np.array_equal(y, run_linear(stream, x, w, m, n, k, dispatch=d)), "split-K result differs between runs"
+    y16 = run_linear(stream, x, w, m, n, k, dispatch=d, f16_out=True)
+    check_against_oracle(oracle, y16, x, w, m, n, k, f16_out=True, what=f"{variant} f16")
+
+
+@pytest.mark.parametrize("m", [3, 8, 16, 32, 64])
+def test_llama_down_projection_through_the_default_entry_point(stream, oracle, m):
+    """The Llama-3-8B MLP down projection (K = 14336, N = 4096) at several
+    token counts, through mote_hip_quantized_linear_q4_0_f32 (the library's
+    own choice of kernel), checked on sampled columns."""
+    k, n = 14336, 4096
+    x = normal_x(wl.seed_for(41, m), m, k)
+    w = q4_weights(wl.seed_for(41, 1), n, k)
+    y = run_linear(stream, x, w, m, n, k)
+    check_against_oracle(oracle, y, x, w, m, n, k, columns=sample_columns(n, 128), what=f"down {m}")
+
+
+@pytest.mark.parametrize("variant", Q8_SPLIT_K)
+def test_every_q8_split_k_variant(stream, oracle, variant):
+    d = ops.Q4_0Dispatch()
+    d.force(variant)
+    span = _slice(variant)
+    for m, n, parts in [(3, 100, 2), (16, 48, 3), (33, 7, 7), (64, 80, 2)]:
+        k = span * parts
+        x = q8.normal_x(wl.seed_for(42, m), m, k)
+        w = q8.weights(wl.seed_for(42, 100 + n), n, k)
+        y = q8.run(stream, x, w, m, n, k, dispatch=d)
+        q8.check(oracle, y, x, w, m, n, k, what=f"{variant} {m}x{n}x{k}")
+    y16 = q8.run(stream, x, w, m, n, k, dispatch=d, f16_out=True)
+    q8.check(oracle, y16, x, w, m, n, k, f16_out=True, what=f"{variant} f16")
+
+
+@pytest.mark.parametrize("variant", GATE_UP_SPLIT_K)
+def test_every_gate_up_split_k_variant(stream, oracle, variant):
+    """silu(gate) * up applied after the K parts are added: ragged tokens and
+    rows, two, three and seven parts, f32 and f16 outputs, a repeat bitwise
+    equal, separate and concatenated weight buffers identical."""
+    d = ops.Q4_0Dispatch()
+    d.force(variant)
+    span = _slice(variant)
+    for m, n, parts in [(1, 40, 2), (5, 33, 3), (17, 130, 2), (33, 7, 7), (64, 80, 2)]:
+        k = span * parts
+        x = normal_x(wl.seed_for(43, m), m, k)
+        wg, wu = q4_weights(wl.seed_for(43, 100 + n), n, k), q4_weights(wl.seed_for(43, 200 + n), n, k)
+        y = run_gate_up(stream, x, wg, wu, m, n, k, dispatch=d)
+        check_gate_up(oracle, y, x, wg, wu, m, n, k, what=f"{variant} {m}x{n}x{k}")
+    assert np.array_equal(y, run_gate_up(stream, x, wg, wu, m, n, k, dispatch=d)), "split-K result differs between runs"
+    assert np.array_equal(y, run_gate_up(stream, x, wg, wu, m, n, k, dispatch=d, concatenated=True))
+    y16 = run_gate_up(stream, x, wg, wu, m, n, k, dispatch=d, f16_out=True)
+    check_gate_up(oracle, y16, x, wg, wu, m, n, k, f16_out=True, what=f"{variant} f16")
+
+
+@pytest.mark.parametrize("m", [4, 32])
+def test_llama_70b_gate_up_through_the_default_entry_point(stream, oracle, m):
+    """The Llama-3-70B fused gate/up (K = 8192, N = 28672) through
+    mote_hip_quantized_gate_up_silu_q4_0_f32, checked on sampled columns."""
+    k, n = 8192, 28672
+    x = normal_x(wl.seed_for(44, m), m, k)
+    wg, wu = q4_weights(wl.seed_for(44, 1), n, k), q4_weights(wl.seed_for(44, 2), n, k)
+    y = run_gate_up(stream, x, wg, wu, m, n, k)
+    check_gate_up(oracle, y, x, wg, wu, m, n, k, cols=sample_columns(n, 96), what=f"70b gate/up {m}")
