@@ -284,7 +284,7 @@ const Variant* heuristic(const Problem& p, Op op) {
         // otherwise.
         if (fast && (p.M == 1 || p.M == 2 || p.M == 4)) {
             uint32_t split = 1;
-            while (split < 4 && p.K > 4096u * split) split *= 2;
+            while (split < 8 && p.K > 4096u * split) split *= 2;
             char name[32];
             if (p.M > 1)
                 std::snprintf(name, sizeof name, "q8_stream_m%u_d1q_g1", p.M);
@@ -379,7 +379,7 @@ const Variant* heuristic(const Problem& p, Op op) {
         // once every row group then owns about 1.5 rows or more (4096 x 6144:
         // 5.14 us against 5.35 us; 4096 x 4096: 5.06 us against 4.29 us).
         uint32_t split = 1;
-        while (split < 4 && p.K > 4096u * split) split *= 2;
+        while (split < 8 && p.K > 4096u * split) split *= 2;
         const uint64_t row_groups_g2 = static_cast<uint64_t>(device_cus()) * 2u * (8u / split);
         const unsigned g = 2u * p.N >= 3u * row_groups_g2 ? 2u : 1u;
         char name[32];
