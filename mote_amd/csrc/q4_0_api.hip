@@ -378,15 +378,20 @@ const Variant* heuristic(const Problem& p, Op op) {
         // 9.9 us for the row-streaming GEMV).  Two workgroups per CU pay off
         // once every row group then owns about 1.5 rows or more (4096 x 6144:
         // 5.14 us against 5.35 us; 4096 x 4096: 5.06 us against 4.29 us).
+        // The queued form (the next row issued while waiting for the one
+        // after the current) wins with one workgroup per CU and with rows
+        // split 4 ways (4096 x 4096: 4.18-4.21 us against 4.29-4.30;
+        // 14336 x 4096: 7.99-8.06 us against 8.20-8.31), and loses at
+        // 8192 x 28672 (23.4 us against 22.5).
         uint32_t split = 1;
         while (split < 8 && p.K > 4096u * split) split *= 2;
         const uint64_t row_groups_g2 = static_cast<uint64_t>(device_cus()) * 2u * (8u / split);
         const unsigned g = 2u * p.N >= 3u * row_groups_g2 ? 2u : 1u;
         char name[32];
         if (split == 1)
-            std::snprintf(name, sizeof name, "stream_d1_g%u", g);
+            std::snprintf(name, sizeof name, "stream_d1%s_g%u", g == 1 ? "q" : "", g);
         else
-            std::snprintf(name, sizeof name, "stream_s%u_d1_g%u", split, g);
+            std::snprintf(name, sizeof name, "stream_s%u_d1%s_g%u", split, split == 4 ? "q" : "", g);
         const Variant* st = by_name(name);
         if (st && gemv_stream_supports(*st, p)) return st;
         uint32_t ks = 1;

@@ -466,7 +466,7 @@ const Variant kStream[] = {
     MOTE_STREAM_P(3, 1, 1), MOTE_STREAM_P(4, 1, 1),
     MOTE_STREAM_S(2, 1, 1), MOTE_STREAM_S(2, 1, 2), MOTE_STREAM_S(4, 1, 1), MOTE_STREAM_S(4, 1, 2),
     MOTE_STREAM_S(4, 2, 2), MOTE_STREAM_SQ(4, 1, 2), MOTE_STREAM_SQ(2, 1, 2), MOTE_STREAM_SQ(4, 1, 1),
-    MOTE_STREAM_S(8, 1, 1), MOTE_STREAM_S(8, 1, 2),
+    MOTE_STREAM_S(8, 1, 1), MOTE_STREAM_S(8, 1, 2), MOTE_STREAM_SQ(8, 1, 1), MOTE_STREAM_SQ(8, 1, 2),
     MOTE_STREAM_M(2, 1, 1), MOTE_STREAM_M(3, 1, 1), MOTE_STREAM_M(4, 1, 1),
     MOTE_STREAM_MQ(2, 1, 1), MOTE_STREAM_MQ(2, 1, 2),
     MOTE_Q8("d1_g1", 1, 1), MOTE_Q8("d1_g2", 1, 2), MOTE_Q8("s2_d1_g1", 2, 1), MOTE_Q8("s2_d1_g2", 2, 2),
