@@ -473,19 +473,33 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
 // Split-K epilogue: y[i] = sum over the K parts of part[k][i], in part order
 // (deterministic), converted to the output type; gate/up (GU): silu of the
 // gate sum times the up sum, the up planes following the kparts gate planes.
+// Up to kMaxParts parts every load of an element is issued before the first
+// add (one memory latency instead of one per part); more parts loop.
+constexpr uint32_t kMaxParts = 16;
+
+__device__ __forceinline__ float sum_parts(const float* __restrict__ p, uint32_t kparts, uint64_t count, uint64_t i) {
+    if (kparts > kMaxParts) {
+        float s = p[i];
+        for (uint32_t k = 1; k < kparts; ++k) s += p[static_cast<uint64_t>(k) * count + i];
+        return s;
+    }
+    float v[kMaxParts];
+#pragma unroll
+    for (uint32_t k = 0; k < kMaxParts; ++k) v[k] = k < kparts ? p[static_cast<uint64_t>(k) * count + i] : 0.0f;
+    float s = v[0];
+#pragma unroll
+    for (uint32_t k = 1; k < kMaxParts; ++k)
+        if (k < kparts) s += v[k];
+    return s;
+}
+
 template <typename OutT, bool GU>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, uint32_t kparts,
                                                             uint64_t count, OutT* __restrict__ y) {
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < count;
          i += static_cast<uint64_t>(gridDim.x) * 256) {
-        float s = part[i];
-        for (uint32_t k = 1; k < kparts; ++k) s += part[static_cast<uint64_t>(k) * count + i];
-        if constexpr (GU) {
-            const float* up = part + static_cast<uint64_t>(kparts) * count;
-            float u = up[i];
-            for (uint32_t k = 1; k < kparts; ++k) u += up[static_cast<uint64_t>(k) * count + i];
-            s = silu(s) * u;
-        }
+        float s = sum_parts(part, kparts, count, i);
+        if constexpr (GU) s = silu(s) * sum_parts(part + static_cast<uint64_t>(kparts) * count, kparts, count, i);
         y[i] = to_out<OutT>(s);
     }
 }
