@@ -53,7 +53,8 @@ hipError_t launch_zero_fill(void* y, uint64_t count, OutType out, hipStream_t st
 // Device scratch owned by the library, one buffer per (device, stream), grown
 // on demand and kept until the process ends: calls on one stream run in
 // order and share it; calls on different streams never do.  Growing it
-// allocates (and first waits for the stream), so the first call that needs
+// allocates (a grown-out buffer is kept, never freed, as a launch another
+// thread just made on the stream may use it), so the first call that needs
 // more scratch on a stream must not be under graph capture.
 hipError_t stream_scratch(hipStream_t stream, size_t bytes, void** ptr);
 hipError_t launch_decode_f32(const void* w, float* out, uint64_t rows, uint64_t cols,

@@ -538,29 +538,27 @@ int gate_up(Dispatcher* d, const void* input, const void* gate, const void* up, 
 }  // namespace
 
 hipError_t stream_scratch(hipStream_t stream, size_t bytes, void** ptr) {
+    // One buffer per (device, stream), grown to the next power of two (at
+    // least 1 MB) when a call needs more.  A grown-out buffer is retired, not
+    // freed: another host thread may have taken it for a launch on the same
+    // stream a moment ago, and earlier launches may still read it.  The few
+    // retired buffers live until the process ends.
     static std::mutex mu;
     static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> buffers;
+    static std::vector<void*> retired;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     std::lock_guard<std::mutex> lock(mu);
     auto& b = buffers[{dev, stream}];
     if (b.second < bytes) {
-        if (b.first != nullptr) {
-            // Earlier calls on this stream may still read the old buffer.
-            e = hipStreamSynchronize(stream);
-            if (e != hipSuccess) return e;
-            e = hipFree(b.first);
-            b = {nullptr, 0};
-            if (e != hipSuccess) return e;
-        }
-        const size_t want = std::max<size_t>(bytes, size_t{1} << 20);
-        e = hipMalloc(&b.first, want);
-        if (e != hipSuccess) {
-            b = {nullptr, 0};
-            return e;
-        }
-        b.second = want;
+        size_t want = size_t{1} << 20;
+        while (want < bytes) want <<= 1;
+        void* fresh = nullptr;
+        e = hipMalloc(&fresh, want);
+        if (e != hipSuccess) return e;
+        if (b.first != nullptr) retired.push_back(b.first);
+        b = {fresh, want};
     }
     *ptr = b.first;
     return hipSuccess;

@@ -118,3 +118,32 @@ def test_llama_70b_gate_up_through_the_default_entry_point(stream, oracle, m):
     wg, wu = q4_weights(wl.seed_for(44, 1), n, k), q4_weights(wl.seed_for(44, 2), n, k)
     y = run_gate_up(stream, x, wg, wu, m, n, k)
     check_gate_up(oracle, y, x, wg, wu, m, n, k, cols=sample_columns(n, 96), what=f"70b gate/up {m}")
+
+
+def test_scratch_growth_with_launches_in_flight(oracle):
+    """Split-K calls on a new stream at growing sizes (then a small one),
+    issued back to back with no synchronisation between them: the partial-tile
+    buffer grows from 128 KB to 32 MB while earlier launches may still read
+    the buffer they were given, and every output must match the oracle."""
+    from mote_amd.device import DeviceBuffer, Stream
+
+    s = Stream()
+    d = ops.Q4_0Dispatch()
+    d.force("skinny_mfma_k8_s1_t2_d1_g1_r1_tr_l8_c_w_sk")  # 14 parts of 2048 at K = 28672
+    k, n_max = 28672, 8192
+    w = q4_weights(wl.seed_for(45, 1), n_max, k)
+    wb = DeviceBuffer.from_array(w)
+    cases = []
+    for m, n in [(2, 1024), (16, 4096), (64, 8192), (3, 2048)]:
+        x = normal_x(wl.seed_for(45, m), m, k)
+        cases.append((m, n, x, DeviceBuffer.from_array(x), DeviceBuffer(m * n * 4)))
+    for m, n, _, xb, yb in cases:  # uploads done: the launches queue up behind each other
+        d.linear(xb.ptr, wb.ptr, yb.ptr, m, n, k, s)
+    s.synchronize()
+    row_bytes = wl.q4_0_row_bytes(k)
+    for m, n, x, _, yb in cases:
+        y = yb.download(np.float32).reshape(m, n)
+        check_against_oracle(oracle, y, x, w[: n * row_bytes], m, n, k, columns=sample_columns(n, 64),
+                             what=f"growth {m}x{n}x{k}")
+    d.close()
+    s.close()
