@@ -286,7 +286,9 @@ const Variant* heuristic(const Problem& p, Op op) {
             uint32_t split = 1;
             while (split < 8 && p.K > 4096u * split) split *= 2;
             char name[32];
-            if (p.M > 1)
+            if (p.M == 2 && split > 1)
+                std::snprintf(name, sizeof name, "q8_stream_s%u_m2_d1q_g1", split);
+            else if (p.M > 1)
                 std::snprintf(name, sizeof name, "q8_stream_m%u_d1q_g1", p.M);
             else if (split == 1)
                 std::snprintf(name, sizeof name, "q8_stream_d1_g1");
@@ -412,7 +414,18 @@ const Variant* heuristic(const Problem& p, Op op) {
     // tokens: the skinny GEMM of skinny_heuristic, then any skinny variant
     // whose K slicing fits, then the vector-ALU GEMV.
     if (p.M == 2) {
-        const Variant* v = by_name("stream_m2_d1q_g1");
+        // Rows split over S waves past K = 4096, one workgroup per CU
+        // (measured on MI355X: 8192 x 8192 in 9.35 us, 14336 x 4096 in 9.35
+        // us, 28672 x 8192 in 26.0 us, against 11.8, 11.8 and 31.4 us for the
+        // split-K tiles).
+        uint32_t split = 1;
+        while (split < 8 && p.K > 4096u * split) split *= 2;
+        char name[32];
+        if (split == 1)
+            std::snprintf(name, sizeof name, "stream_m2_d1q_g1");
+        else
+            std::snprintf(name, sizeof name, "stream_s%u_m2_d1q_g1", split);
+        const Variant* v = by_name(name);
         if (v && gemv_stream_supports(*v, p)) return v;
     }
     if (const Variant* v = skinny_heuristic(p)) return v;

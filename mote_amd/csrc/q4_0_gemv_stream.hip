@@ -450,9 +450,15 @@ hipError_t launch_gemv_stream(const Problem& p) {
 #define MOTE_Q8_M(MT, G)                                                             \
     Variant{"q8_stream_m" #MT "_d1q_g" #G, Kind::Q8Stream, 1, 1, G,                \
             &launch_gemv_stream<1, 1, 1, G, MT, false, FmtQ8>, MT}
+#define MOTE_Q8_SM(S, MT)                                                               \
+    Variant{"q8_stream_s" #S "_m" #MT "_d1q_g1", Kind::Q8Stream, S, 1, 1,                \
+            &launch_gemv_stream<1, S, 1, 1, MT, false, FmtQ8>, MT}
 #define MOTE_STREAM_GU(P, G)                                                             \
     Variant{"gateup_stream_p" #P "_d1_g" #G, Kind::GateUpStream, P, 1, G,               \
             &launch_gemv_stream<P, 1, 1, G, 1, true, FmtQ4, true>}
+#define MOTE_STREAM_SMQ(S, MT, G)                                                        \
+    Variant{"stream_s" #S "_m" #MT "_d1q_g" #G, Kind::GemvStream, S, 1, G,              \
+            &launch_gemv_stream<1, S, 1, G, MT, false>, MT}
 #define MOTE_STREAM_MQ(MT, D, G)                                                         \
     Variant{"stream_m" #MT "_d" #D "q_g" #G, Kind::GemvStream, 1, D, G,                 \
             &launch_gemv_stream<1, 1, D, G, MT, false>, MT}
@@ -469,8 +475,11 @@ const Variant kStream[] = {
     MOTE_STREAM_S(8, 1, 1), MOTE_STREAM_S(8, 1, 2), MOTE_STREAM_SQ(8, 1, 1), MOTE_STREAM_SQ(8, 1, 2),
     MOTE_STREAM_M(2, 1, 1), MOTE_STREAM_M(3, 1, 1), MOTE_STREAM_M(4, 1, 1),
     MOTE_STREAM_MQ(2, 1, 1), MOTE_STREAM_MQ(2, 1, 2),
+    MOTE_STREAM_SMQ(2, 2, 1), MOTE_STREAM_SMQ(4, 2, 1), MOTE_STREAM_SMQ(8, 2, 1), MOTE_STREAM_SMQ(2, 2, 2),
+    MOTE_STREAM_SMQ(4, 2, 2), MOTE_STREAM_SMQ(8, 2, 2),
     MOTE_Q8("d1_g1", 1, 1), MOTE_Q8("d1_g2", 1, 2), MOTE_Q8("s2_d1_g1", 2, 1), MOTE_Q8("s2_d1_g2", 2, 2),
-    MOTE_Q8("s4_d1_g1", 4, 1), MOTE_Q8("s4_d1_g2", 4, 2), MOTE_Q8("s8_d1_g1", 8, 1), MOTE_Q8("s8_d1_g2", 8, 2), MOTE_Q8_M(2, 1), MOTE_Q8_M(4, 1),
+    MOTE_Q8("s4_d1_g1", 4, 1), MOTE_Q8("s4_d1_g2", 4, 2), MOTE_Q8("s8_d1_g1", 8, 1), MOTE_Q8("s8_d1_g2", 8, 2),
+    MOTE_Q8_SM(2, 2), MOTE_Q8_SM(4, 2), MOTE_Q8_SM(8, 2), MOTE_Q8_M(2, 1), MOTE_Q8_M(4, 1),
     MOTE_STREAM_GU(1, 1), MOTE_STREAM_GU(1, 2), MOTE_STREAM_GU(2, 1), MOTE_STREAM_GU(2, 2),
 };
 
@@ -481,6 +490,8 @@ const Variant kStream[] = {
 #undef MOTE_STREAM_Q
 #undef MOTE_STREAM_SQ
 #undef MOTE_STREAM_MQ
+#undef MOTE_STREAM_SMQ
+#undef MOTE_Q8_SM
 #undef MOTE_Q8
 #undef MOTE_Q8_M
 #undef MOTE_STREAM_GU

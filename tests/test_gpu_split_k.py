@@ -62,11 +62,12 @@ def test_every_split_k_variant(stream, oracle, variant):
     check_against_oracle(oracle, y16, x, w, m, n, k, f16_out=True, what=f"{variant} f16")
 
 
-@pytest.mark.parametrize("m", [3, 8, 16, 32, 64])
+@pytest.mark.parametrize("m", [2, 3, 8, 16, 32, 64])
 def test_llama_down_projection_through_the_default_entry_point(stream, oracle, m):
     """The Llama-3-8B MLP down projection (K = 14336, N = 4096) at several
     token counts, through mote_hip_quantized_linear_q4_0_f32 (the library's
-    own choice of kernel), checked on sampled columns."""
+    own choice of kernel: the two-token streaming GEMV with rows split over
+    4 waves, then the split-K tiles), checked on sampled columns."""
     k, n = 14336, 4096
     x = normal_x(wl.seed_for(41, m), m, k)
     w = q4_weights(wl.seed_for(41, 1), n, k)
