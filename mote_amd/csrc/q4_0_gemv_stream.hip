@@ -510,8 +510,12 @@ bool gemv_stream_supports(const Variant& v, const Problem& p) {
     const uint32_t tokens = v.tokens > 0 ? static_cast<uint32_t>(v.tokens) : 1u;
     const bool up_ok = v.kind != Kind::GateUpStream ||
                        (p.w_up != nullptr && reinterpret_cast<uintptr_t>(p.w_up) % 4 == 0);
+    // the activations of every token (and the split-row sums) fit one
+    // workgroup's 160 KB of LDS
+    const uint64_t lds = static_cast<uint64_t>(p.K / 64) * tokens * kSlot + kStreamThreads * sizeof(float);
     return p.M == tokens && p.K % 64 == 0 && p.K > 0 && p.K <= 4096u * static_cast<uint32_t>(v.p0) &&
-           reinterpret_cast<uintptr_t>(p.w) % 4 == 0 && reinterpret_cast<uintptr_t>(p.x) % 16 == 0 && up_ok;
+           lds <= 160u * 1024u && reinterpret_cast<uintptr_t>(p.w) % 4 == 0 &&
+           reinterpret_cast<uintptr_t>(p.x) % 16 == 0 && up_ok;
 }
 
 }  // namespace mote::q4_0
