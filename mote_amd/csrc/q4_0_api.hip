@@ -240,7 +240,24 @@ const Variant* skinny_q8_heuristic(const Problem& p) {
 // CUs; past that, and for 32-token items, 8 items per workgroup of 8 waves
 // with the larger K part once the smaller one gives more than 256 workgroups.
 const Variant* split_k_heuristic(const Problem& p, Op op) {
-    if (p.M > 64 || p.K % 2048 != 0 || p.K < 4096) return nullptr;
+    if (p.M > 64 || p.K % 1024 != 0 || p.K < 2048) return nullptr;
+    if (p.K % 2048 != 0 || p.K < 4096) {
+        // Parts of 1024 (4 waves of 256): K = 3072, 5120, 7168, ... and the
+        // gate/up at K = 2048, which no plain slicing fits (a linear at K =
+        // 2048 takes the one-slice tiles).
+        if (op == Op::Linear && p.K == 2048) return nullptr;
+        if (op == Op::GateUp && p.M > 32) return nullptr;  // the prefill tiles
+        // 16-token items up to 32 tokens (measured on MI355X: 32 x 3072 x
+        // 8192 in 14.6 us against 21.3 us with 32-token items; 4 x 5120 x
+        // 5120 in 10.9 us against 15.5 us on the vector-ALU GEMV)
+        const bool t2 = p.M > 32;
+        const char* name = op == Op::LinearQ8 ? (t2 ? "q8_skinny_k4_s1_t2_d1_l8_c_w_sk" : "q8_skinny_k4_s1_t1_d1_l8_c_w_sk")
+                           : op == Op::GateUp ? (t2 ? "gateup_skinny_k4_s1_t2_d1_l8_c_w_sk" : "gateup_skinny_k4_s1_t1_d1_l8_c_w_sk")
+                                              : (t2 ? "skinny_mfma_k4_s1_t2_d1_g1_r1_tr_l8_c_w_sk"
+                                                    : "skinny_mfma_k4_s1_t1_d1_g1_r1_tr_l8_c_w_sk");
+        const Variant* v = by_name(name);
+        return v && skinny_mfma_supports(*v, p) ? v : nullptr;
+    }
     const uint64_t cus = static_cast<uint64_t>(device_cus());
     const uint64_t row_tiles = (p.N + 15) / 16;
     const uint64_t items2k = row_tiles * ((p.M + 15) / 16) * (p.K / 2048);  // 16-token items, parts of 2048
@@ -326,6 +343,13 @@ const Variant* heuristic(const Problem& p, Op op) {
             char name[32];
             std::snprintf(name, sizeof name, "gateup_stream_p%u_d1_g1", slots);
             const Variant* v = by_name(name);
+            if (v && gemv_stream_supports(*v, p)) return v;
+        }
+        if (fast && p.M == 2) {
+            // Two tokens per row read (measured on MI355X: 4096 x 14336 in
+            // 15.7 us, 4096 x 11008 in 12.8 us, against 17.8 and 15.4 us for
+            // the skinny gate/up).
+            const Variant* v = by_name("gateup_stream_p1_m2_d1q_g1");
             if (v && gemv_stream_supports(*v, p)) return v;
         }
         if (fast && p.M <= 64) {

@@ -229,7 +229,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
                                                                      const uint8_t* __restrict__ w_up,
                                                                      OutT* __restrict__ y, uint32_t N,
                                                                      uint32_t K, uint32_t total_groups) {
-    static_assert(!GU || (S == 1 && MT == 1), "the gate/up GEMV keeps whole rows of one token");
+    static_assert(!GU || S == 1, "the gate/up GEMV keeps whole rows");
     constexpr int NW = GU ? 2 : 1;             // matrices read per row: gate (and up)
     constexpr int kGroups = kStreamWaves / S;  // row groups per workgroup
     extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
@@ -359,15 +359,15 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
             const uint32_t jj = j + static_cast<uint32_t>(u);
             load_row(jj + D, buf[(u + D) % R]);
             __builtin_amdgcn_sched_barrier(0);
-            float part[MT], part_up = 0.0f;
+            float part[MT], part_up[MT];
 #pragma unroll
-            for (int m = 0; m < MT; ++m) part[m] = 0.0f;
+            for (int m = 0; m < MT; ++m) part[m] = part_up[m] = 0.0f;
 #pragma unroll
             for (int i = 0; i < P; ++i) {
                 if constexpr (MT == 1) {  // masks feed the dot chains directly: fewer live registers
                     part[0] += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, F::dot(buf[u][i], xv[0][i])) & keep[i]);
                     if constexpr (GU)
-                        part_up += __builtin_bit_cast(
+                        part_up[0] += __builtin_bit_cast(
                             float, __builtin_bit_cast(uint32_t, F::dot(buf[u][P + i], xv[0][i])) & keep[i]);
                 } else {
                     Unpacked wu;
@@ -375,13 +375,21 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
 #pragma unroll
                     for (int m = 0; m < MT; ++m)
                         part[m] += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, F::dot(wu, xv[m][i])) & keep[i]);
+                    if constexpr (GU) {
+                        Unpacked uu;
+                        F::unpack(buf[u][P + i], uu);
+#pragma unroll
+                        for (int m = 0; m < MT; ++m)
+                            part_up[m] += __builtin_bit_cast(
+                                float, __builtin_bit_cast(uint32_t, F::dot(uu, xv[m][i])) & keep[i]);
+                    }
                 }
             }
             const bool mine_lane = jj < trips && static_cast<uint32_t>(lane) == (jj & 63u);
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
                 float s = wave_sum(part[m]);
-                if constexpr (GU) s = silu(F::kFinal * s) * (F::kFinal * wave_sum(part_up));
+                if constexpr (GU) s = silu(F::kFinal * s) * (F::kFinal * wave_sum(part_up[m]));
                 mine[m] = mine_lane ? s : mine[m];
             }
             if ((jj & 63u) == 63u && jj < trips)  // uniform over the workgroup
@@ -459,6 +467,9 @@ hipError_t launch_gemv_stream(const Problem& p) {
 #define MOTE_STREAM_SMQ(S, MT, G)                                                        \
     Variant{"stream_s" #S "_m" #MT "_d1q_g" #G, Kind::GemvStream, S, 1, G,              \
             &launch_gemv_stream<1, S, 1, G, MT, false>, MT}
+#define MOTE_STREAM_GU_MQ(P, MT)                                                         \
+    Variant{"gateup_stream_p" #P "_m" #MT "_d1q_g1", Kind::GateUpStream, P, 1, 1,       \
+            &launch_gemv_stream<P, 1, 1, 1, MT, false, FmtQ4, true>, MT}
 #define MOTE_STREAM_MQ(MT, D, G)                                                         \
     Variant{"stream_m" #MT "_d" #D "q_g" #G, Kind::GemvStream, 1, D, G,                 \
             &launch_gemv_stream<1, 1, D, G, MT, false>, MT}
@@ -481,6 +492,7 @@ const Variant kStream[] = {
     MOTE_Q8("s4_d1_g1", 4, 1), MOTE_Q8("s4_d1_g2", 4, 2), MOTE_Q8("s8_d1_g1", 8, 1), MOTE_Q8("s8_d1_g2", 8, 2),
     MOTE_Q8_SM(2, 2), MOTE_Q8_SM(4, 2), MOTE_Q8_SM(8, 2), MOTE_Q8_M(2, 1), MOTE_Q8_M(4, 1),
     MOTE_STREAM_GU(1, 1), MOTE_STREAM_GU(1, 2), MOTE_STREAM_GU(2, 1), MOTE_STREAM_GU(2, 2),
+    MOTE_STREAM_GU_MQ(1, 2),
 };
 
 #undef MOTE_STREAM
@@ -490,6 +502,7 @@ const Variant kStream[] = {
 #undef MOTE_STREAM_Q
 #undef MOTE_STREAM_SQ
 #undef MOTE_STREAM_MQ
+#undef MOTE_STREAM_GU_MQ
 #undef MOTE_STREAM_SMQ
 #undef MOTE_Q8_SM
 #undef MOTE_Q8

@@ -651,6 +651,9 @@ const Variant kSkinny[] = {
     MOTE_SKINNY_SK(8, 1, 2, 4, "_c"), MOTE_SKINNY_Q8_SK(8, 1, 1, 4, "_c"), MOTE_SKINNY_Q8_SK(8, 1, 2, 4, "_c"),
     MOTE_SKINNY_GU_SK(8, 1, 1, 4, "_c"), MOTE_SKINNY_GU_SK(8, 1, 1, 8, "_c"), MOTE_SKINNY_GU_SK(16, 1, 1, 4, "_c"),
     MOTE_SKINNY_GU_SK(8, 1, 2, 4, "_c"), MOTE_SKINNY_GU_SK(8, 1, 2, 8, "_c"),
+    // parts of 1024 for K a multiple of 1024 only (2048 for the gate/up)
+    MOTE_SKINNY_SK(4, 1, 1, 8, "_c"), MOTE_SKINNY_SK(4, 1, 2, 8, "_c"), MOTE_SKINNY_GU_SK(4, 1, 1, 8, "_c"),
+    MOTE_SKINNY_GU_SK(4, 1, 2, 8, "_c"), MOTE_SKINNY_Q8_SK(4, 1, 1, 8, "_c"), MOTE_SKINNY_Q8_SK(4, 1, 2, 8, "_c"),
 };
 
 #undef MOTE_SKINNY

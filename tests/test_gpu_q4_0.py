@@ -210,7 +210,7 @@ def check_gate_up(oracle, y, x, wg, wu, m, n, k, cols=None, f16_out=False, what=
     assert np.all(err <= tol), f"{what}: max excess {float(np.max(err - tol))}"
 
 
-@pytest.mark.parametrize("m", [1, 4, 16, 32, 64, 256, 512])
+@pytest.mark.parametrize("m", [1, 2, 4, 16, 32, 64, 256, 512])
 def test_fused_gate_up_silu(stream, oracle, m):
     """Default entry point at every token count of the path (the skinny gate/up
     up to 64 tokens, the prefill tiles above), separate and concatenated
@@ -353,24 +353,26 @@ def test_every_gate_up_variant(stream, oracle, variant):
 
 @pytest.mark.parametrize("variant", _variants("gateup_stream_"))
 def test_every_stream_gate_up_variant(stream, oracle, variant):
-    """One-token gate/up on the streaming GEMV (both rows per step): N below one
-    workgroup, ragged N, idle lanes (K < 4096), N = 140001 at K = 64 (waves
-    flush register-held results mid-loop), K filling all P 64-pair slots and
-    one pair past P - 1 slots, the 4096 x 14336 MLP shape; f32 and f16."""
+    """Gate/up on the streaming GEMV (both rows per step, one or two tokens per
+    row read): N below one workgroup, ragged N, idle lanes (K < 4096), N =
+    140001 at K = 64 (waves flush register-held results mid-loop), K filling
+    all P 64-pair slots and one pair past P - 1 slots, the 4096 x 14336 MLP
+    shape; f32 and f16."""
     d = ops.Q4_0Dispatch()
     d.force(variant)
     slots = int(variant.split("_p")[1].split("_")[0])
+    m = int(variant.split("_m")[1].split("_")[0]) if "_m" in variant else 1
     shapes = [(100, 4096), (4099, 1024), (140001, 64), (7, 4096 * slots), (14336, 4096)]
     if slots > 1:
         shapes.append((513, 4096 * (slots - 1) + 64))
     for n, k in shapes:
-        x = normal_x(wl.seed_for(16, k), 1, k)
+        x = normal_x(wl.seed_for(16, k), m, k)
         wg, wu = weights(wl.seed_for(16, 100 + n), n, k), weights(wl.seed_for(16, 300 + n), n, k)
         cols = None if n < 5000 else sample_columns(n, 128)
-        y = run_gate_up(stream, x, wg, wu, 1, n, k, dispatch=d)
-        check_gate_up(oracle, y, x, wg, wu, 1, n, k, cols=cols, what=f"{variant} 1x{n}x{k}")
-        y16 = run_gate_up(stream, x, wg, wu, 1, n, k, dispatch=d, f16_out=True)
-        check_gate_up(oracle, y16, x, wg, wu, 1, n, k, cols=cols, f16_out=True, what=f"{variant} f16 1x{n}x{k}")
+        y = run_gate_up(stream, x, wg, wu, m, n, k, dispatch=d)
+        check_gate_up(oracle, y, x, wg, wu, m, n, k, cols=cols, what=f"{variant} {m}x{n}x{k}")
+        y16 = run_gate_up(stream, x, wg, wu, m, n, k, dispatch=d, f16_out=True)
+        check_gate_up(oracle, y16, x, wg, wu, m, n, k, cols=cols, f16_out=True, what=f"{variant} f16 {m}x{n}x{k}")
 
 
 @pytest.mark.parametrize("variant", [v for v in _variants("gateup_skinny_") if not v.endswith("_sk")])

@@ -148,3 +148,28 @@ def test_scratch_growth_with_launches_in_flight(oracle):
                              what=f"growth {m}x{n}x{k}")
     d.close()
     s.close()
+
+
+@pytest.mark.parametrize("m,k,n,kind", [(4, 5120, 5120, "linear"), (32, 3072, 8192, "linear"), (64, 5120, 1024, "linear"),
+                                        (8, 3072, 8192, "gate_up"), (24, 2048, 5632, "gate_up"),
+                                        (4, 5120, 5120, "q8"), (40, 3072, 3072, "q8")])
+def test_k_multiple_of_1024_through_the_default_entry_points(stream, oracle, m, k, n, kind):
+    """Hidden sizes that no 2048-wide K slice divides (3072, 5120) and the
+    gate/up at K = 2048: the default entry points use split-K parts of 1024;
+    checked on sampled columns."""
+    cols = sample_columns(n, 96)
+    if kind == "q8":
+        x = q8.normal_x(wl.seed_for(46, m), m, k)
+        w = q8.weights(wl.seed_for(46, n), n, k)
+        y = q8.run(stream, x, w, m, n, k)
+        q8.check(oracle, y, x, w, m, n, k, columns=cols, what=f"q8 {m}x{n}x{k}")
+        return
+    x = normal_x(wl.seed_for(46, m), m, k)
+    w = q4_weights(wl.seed_for(46, n), n, k)
+    if kind == "linear":
+        y = run_linear(stream, x, w, m, n, k)
+        check_against_oracle(oracle, y, x, w, m, n, k, columns=cols, what=f"linear {m}x{n}x{k}")
+    else:
+        wu = q4_weights(wl.seed_for(47, n), n, k)
+        y = run_gate_up(stream, x, w, wu, m, n, k)
+        check_gate_up(oracle, y, x, w, wu, m, n, k, cols=cols, what=f"gate/up {m}x{n}x{k}")
