@@ -319,8 +319,9 @@ SWEEP = (
     + [("prefill", m, 4096, 14336, 4, False, False) for m in (64, 256, 512)]
     + [("down split-K", m, 14336, 4096, 2, False, False) for m in (2, 4, 16, 32, 64)]
     + [("70b o split-K", m, 8192, 8192, 2, False, False) for m in (16, 64)]
-    + [("70b down", m, 28672, 8192, 2, False, False) for m in (1, 16, 64)]
-    + [("fused gate/up", m, 4096, 14336, 4, False, True) for m in (1, 4, 16, 32, 64, 256, 512)]
+    + [("70b down", m, 28672, 8192, 2, False, False) for m in (1, 2, 16, 64)]
+    + [("13b linear", m, 5120, 5120, 2, False, False) for m in (4, 32)]
+    + [("fused gate/up", m, 4096, 14336, 4, False, True) for m in (1, 2, 4, 16, 32, 64, 256, 512)]
     + [("70b gate/up", m, 8192, 28672, 4, False, True) for m in (1, 4, 16, 32, 64)]
     + [("q8_0 decode", 1, 4096, 4096, 5, False, "q8"), ("q8_0 up/gate", 1, 4096, 14336, 5, False, "q8"),
        ("q8_0 down", 1, 14336, 4096, 5, False, "q8"), ("q8_0 2 tok", 2, 4096, 14336, 5, False, "q8"),
