@@ -3,7 +3,9 @@
 A serving loop captures a decoder step once and replays it; every kernel here
 must then behave exactly as when issued eagerly.  The test issues a step's
 worth of calls eagerly (fused add + RMSNorm, Q4_0 linears at 1, 16 and 512
-tokens, the fused gate/up at 1 and 16 tokens, a Q8_0 linear, q/k RoPE),
+tokens, the 16-token down projection on the split-K tiles, whose scratch the
+eager call sizes, the fused gate/up at 1 and 16 tokens, a Q8_0 linear, q/k
+RoPE),
 captures the same calls into a graph, and replays it three times.  Before
 every replay the outputs are overwritten with a sentinel and the residual
 (updated in place by the fused norm) is restored, eagerly, on the same stream;
@@ -41,6 +43,7 @@ def test_decoder_step_graph_replays_match_eager(stream):
     x1 = buf("x1", wl.normal_f16(40, H))
     x16 = buf("x16", wl.normal_f16(41, 16 * H))
     x512 = buf("x512", wl.normal_f16(42, 512 * H))
+    x16ff = buf("x16ff", wl.normal_f16(51, 16 * FF))
     res = wl.normal_f16(43, 16 * H)
     r16 = buf("res", res)
     nw = buf("nw", wl.normal_f16(44, H, mean=1.0, std=0.1))
@@ -57,6 +60,7 @@ def test_decoder_step_graph_replays_match_eager(stream):
         "y1": out("y1", FF * 4),
         "y16": out("y16", 16 * FF * 4),
         "y512": out("y512", 512 * FF * 4),
+        "down16": out("down16", 16 * H * 4),
         "gu1": out("gu1", FF * 4),
         "gu16": out("gu16", 16 * FF * 4),
         "q8": out("q8", 1024 * 4),
@@ -69,6 +73,8 @@ def test_decoder_step_graph_replays_match_eager(stream):
         ops.quantized_linear_q4_0_f32(x1.ptr, wq4.ptr, outs["y1"].ptr, 1, FF, H, stream)
         ops.quantized_linear_q4_0_f32(x16.ptr, wq4.ptr, outs["y16"].ptr, 16, FF, H, stream)
         ops.quantized_linear_q4_0_f32(x512.ptr, wq4.ptr, outs["y512"].ptr, 512, FF, H, stream)
+        # the gate bytes read as [H, FF]: the same 18-byte blocks, regrouped into rows
+        ops.quantized_linear_q4_0_f32(x16ff.ptr, wq4.ptr, outs["down16"].ptr, 16, H, FF, stream)
         ops.q4_0_gate_up_silu_f32(x1.ptr, wq4.ptr, wup.ptr, outs["gu1"].ptr, 1, FF, H, stream)
         ops.q4_0_gate_up_silu_f32(x16.ptr, wq4.ptr, wup.ptr, outs["gu16"].ptr, 16, FF, H, stream)
         ops.quantized_linear_q8_0_f32(x1.ptr, wq8.ptr, outs["q8"].ptr, 1, 1024, H, stream)
