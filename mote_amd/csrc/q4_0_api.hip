@@ -334,22 +334,22 @@ const Variant* heuristic(const Problem& p, Op op) {
         // Up to 64 tokens the skinny gate/up; above, the prefill tiles with
         // raw Q4_0 weights staged in LDS (measured on MI355X at N = 14336,
         // K = 4096: 1.4x-1.8x faster than dequantised f16 weight tiles).
-        if (fast && p.M == 1) {
-            // One token: the streaming GEMV reading both rows per step, one
-            // workgroup per CU (measured on MI355X: 4096 x 14336 in 13.6 us,
-            // 4.85 TB/s, against 2 x 7.8 us for two linears; 8192 x 28672 in
-            // 45.0 us, 5.9 TB/s).
-            const uint32_t slots = (p.K + 4095u) / 4096u;
-            char name[32];
-            std::snprintf(name, sizeof name, "gateup_stream_p%u_d1_g1", slots);
+        if (fast && (p.M == 1 || p.M == 2)) {
+            // One or two tokens: the streaming GEMV reading both rows per
+            // step (and, for two tokens, each row once for both), rows split
+            // over S waves past K = 4096 (measured on MI355X: one token,
+            // 4096 x 14336 in 13.6 us, 4.85 TB/s; 8192 x 28672 in 43.9 us,
+            // 6.0 TB/s; two tokens, 4096 x 14336 in 15.5 us, 8192 x 28672 in
+            // 46.9 us and 14336 x 4096 in 15.0 us, against 17.8, 65.5 and
+            // 21.7 us on the skinny tiles).
+            uint32_t split = 1;
+            while (split < 8 && p.K > 4096u * split) split *= 2;
+            char name[40];
+            if (split == 1)
+                std::snprintf(name, sizeof name, p.M == 1 ? "gateup_stream_p1_d1_g1" : "gateup_stream_p1_m2_d1q_g1");
+            else
+                std::snprintf(name, sizeof name, "gateup_stream_s%u_m%u_d1q_g1", split, p.M);
             const Variant* v = by_name(name);
-            if (v && gemv_stream_supports(*v, p)) return v;
-        }
-        if (fast && p.M == 2) {
-            // Two tokens per row read (measured on MI355X: 4096 x 14336 in
-            // 15.7 us, 4096 x 11008 in 12.8 us, against 17.8 and 15.4 us for
-            // the skinny gate/up).
-            const Variant* v = by_name("gateup_stream_p1_m2_d1q_g1");
             if (v && gemv_stream_supports(*v, p)) return v;
         }
         if (fast && p.M <= 64) {

@@ -229,7 +229,10 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
                                                                      const uint8_t* __restrict__ w_up,
                                                                      OutT* __restrict__ y, uint32_t N,
                                                                      uint32_t K, uint32_t total_groups) {
-    static_assert(!GU || S == 1, "the gate/up GEMV keeps whole rows");
+    // Gate/up with rows split over S waves (SPLIT_GU) carries the gate and up
+    // sums separately through the cross-wave reduction and applies the SiLU
+    // once they are whole.
+    constexpr bool SPLIT_GU = GU && S > 1;
     constexpr int NW = GU ? 2 : 1;             // matrices read per row: gate (and up)
     constexpr int kGroups = kStreamWaves / S;  // row groups per workgroup
     extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
@@ -331,27 +334,32 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
     // ring size, so slots are compile-time registers; steps past the last row
     // compute clamped rows and store nothing.
     float* red = reinterpret_cast<float*>(xs + static_cast<size_t>(npairs) * MT * kSlot);
-    auto flush = [&](const float (&v)[MT], uint32_t first, uint32_t count) {
+    auto flush = [&](const float (&v)[MT], const float (&vu)[MT], uint32_t first, uint32_t count) {
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            float t = v[m];
+            float t = v[m], tu = vu[m];
             if constexpr (S > 1) {
                 red[wave * 64 + lane] = t;
+                if constexpr (SPLIT_GU) red[kStreamThreads + wave * 64 + lane] = tu;
                 __syncthreads();
                 if (slice == 0) {
 #pragma unroll
-                    for (int r = 1; r < S; ++r) t += red[(wave + r) * 64 + lane];
+                    for (int r = 1; r < S; ++r) {
+                        t += red[(wave + r) * 64 + lane];
+                        if constexpr (SPLIT_GU) tu += red[kStreamThreads + (wave + r) * 64 + lane];
+                    }
                 }
                 __syncthreads();
             }
+            if constexpr (SPLIT_GU) t = silu(F::kFinal * t) * (F::kFinal * tu);
             if (slice == 0 && static_cast<uint32_t>(lane) < count)
                 y[static_cast<size_t>(m) * N + g + (first + static_cast<uint32_t>(lane)) * total_groups] =
-                    to_out<OutT>(GU ? t : F::kFinal * t);  // gate/up sums are final already
+                    to_out<OutT>(GU ? t : F::kFinal * t);  // gate/up values are final here
         }
     };
-    float mine[MT];
+    float mine[MT], mine_up[MT];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) mine[m] = 0.0f;
+    for (int m = 0; m < MT; ++m) mine[m] = mine_up[m] = 0.0f;
     uint32_t j = 0;
     do {
 #pragma unroll
@@ -389,11 +397,16 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
                 float s = wave_sum(part[m]);
-                if constexpr (GU) s = silu(F::kFinal * s) * (F::kFinal * wave_sum(part_up[m]));
+                if constexpr (SPLIT_GU) {
+                    const float su = wave_sum(part_up[m]);
+                    mine_up[m] = mine_lane ? su : mine_up[m];
+                } else if constexpr (GU) {
+                    s = silu(F::kFinal * s) * (F::kFinal * wave_sum(part_up[m]));
+                }
                 mine[m] = mine_lane ? s : mine[m];
             }
             if ((jj & 63u) == 63u && jj < trips)  // uniform over the workgroup
-                flush(mine, jj - 63u, nrows > jj - 63u ? min(nrows - (jj - 63u), 64u) : 0u);
+                flush(mine, mine_up, jj - 63u, nrows > jj - 63u ? min(nrows - (jj - 63u), 64u) : 0u);
             if constexpr (LAG) {
                 // Row j + 1 arrives before row j + 1 + D is issued: D rows in
                 // flight at any time, never D + 1.
@@ -404,7 +417,7 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
         j += R;
     } while (j < trips);
     const uint32_t base = trips & ~63u;
-    if (base < trips) flush(mine, base, nrows > base ? nrows - base : 0u);
+    if (base < trips) flush(mine, mine_up, base, nrows > base ? nrows - base : 0u);
 }
 
 template <int P, int S, int D, int G, int MT = 1, bool LAG = true, class F = FmtQ4, bool GU = false>
@@ -421,7 +434,7 @@ hipError_t launch_gemv_stream(const Problem& p) {
     const uint32_t need = (p.N + kGroups - 1) / kGroups;  // no idle workgroups
     if (groups > need) groups = need;
     const uint32_t total_groups = groups * kGroups;
-    const size_t lds = static_cast<size_t>(p.K / 64) * MT * kSlot + (S > 1 ? kStreamThreads * sizeof(float) : 0);
+    const size_t lds = static_cast<size_t>(p.K / 64) * MT * kSlot + (S > 1 ? (GU ? 2 : 1) * kStreamThreads * sizeof(float) : 0);
     const dim3 grid(groups), block(kStreamThreads);
     if (p.out == OutType::F32) {
         hipLaunchKernelGGL((gemv_stream_kernel<F, P, S, D, MT, LAG, float, GU>), grid, block, lds, p.stream,
@@ -467,6 +480,9 @@ hipError_t launch_gemv_stream(const Problem& p) {
 #define MOTE_STREAM_SMQ(S, MT, G)                                                        \
     Variant{"stream_s" #S "_m" #MT "_d1q_g" #G, Kind::GemvStream, S, 1, G,              \
             &launch_gemv_stream<1, S, 1, G, MT, false>, MT}
+#define MOTE_STREAM_GU_SMQ(S, MT)                                                        \
+    Variant{"gateup_stream_s" #S "_m" #MT "_d1q_g1", Kind::GateUpStream, S, 1, 1,        \
+            &launch_gemv_stream<1, S, 1, 1, MT, false, FmtQ4, true>, MT}
 #define MOTE_STREAM_GU_MQ(P, MT)                                                         \
     Variant{"gateup_stream_p" #P "_m" #MT "_d1q_g1", Kind::GateUpStream, P, 1, 1,       \
             &launch_gemv_stream<P, 1, 1, 1, MT, false, FmtQ4, true>, MT}
@@ -492,7 +508,8 @@ const Variant kStream[] = {
     MOTE_Q8("s4_d1_g1", 4, 1), MOTE_Q8("s4_d1_g2", 4, 2), MOTE_Q8("s8_d1_g1", 8, 1), MOTE_Q8("s8_d1_g2", 8, 2),
     MOTE_Q8_SM(2, 2), MOTE_Q8_SM(4, 2), MOTE_Q8_SM(8, 2), MOTE_Q8_M(2, 1), MOTE_Q8_M(4, 1),
     MOTE_STREAM_GU(1, 1), MOTE_STREAM_GU(1, 2), MOTE_STREAM_GU(2, 1), MOTE_STREAM_GU(2, 2),
-    MOTE_STREAM_GU_MQ(1, 2),
+    MOTE_STREAM_GU_MQ(1, 2), MOTE_STREAM_GU_SMQ(2, 2), MOTE_STREAM_GU_SMQ(4, 2), MOTE_STREAM_GU_SMQ(8, 2),
+    MOTE_STREAM_GU_SMQ(2, 1), MOTE_STREAM_GU_SMQ(4, 1), MOTE_STREAM_GU_SMQ(8, 1),
 };
 
 #undef MOTE_STREAM
@@ -503,6 +520,7 @@ const Variant kStream[] = {
 #undef MOTE_STREAM_SQ
 #undef MOTE_STREAM_MQ
 #undef MOTE_STREAM_GU_MQ
+#undef MOTE_STREAM_GU_SMQ
 #undef MOTE_STREAM_SMQ
 #undef MOTE_Q8_SM
 #undef MOTE_Q8
@@ -525,7 +543,7 @@ bool gemv_stream_supports(const Variant& v, const Problem& p) {
                        (p.w_up != nullptr && reinterpret_cast<uintptr_t>(p.w_up) % 4 == 0);
     // the activations of every token (and the split-row sums) fit one
     // workgroup's 160 KB of LDS
-    const uint64_t lds = static_cast<uint64_t>(p.K / 64) * tokens * kSlot + kStreamThreads * sizeof(float);
+    const uint64_t lds = static_cast<uint64_t>(p.K / 64) * tokens * kSlot + 2 * kStreamThreads * sizeof(float);
     return p.M == tokens && p.K % 64 == 0 && p.K > 0 && p.K <= 4096u * static_cast<uint32_t>(v.p0) &&
            lds <= 160u * 1024u && reinterpret_cast<uintptr_t>(p.w) % 4 == 0 &&
            reinterpret_cast<uintptr_t>(p.x) % 16 == 0 && up_ok;

@@ -354,13 +354,14 @@ def test_every_gate_up_variant(stream, oracle, variant):
 @pytest.mark.parametrize("variant", _variants("gateup_stream_"))
 def test_every_stream_gate_up_variant(stream, oracle, variant):
     """Gate/up on the streaming GEMV (both rows per step, one or two tokens per
-    row read): N below one workgroup, ragged N, idle lanes (K < 4096), N =
+    row read, rows whole or split over S waves): N below one workgroup, ragged N, idle lanes (K < 4096), N =
     140001 at K = 64 (waves flush register-held results mid-loop), K filling
     all P 64-pair slots and one pair past P - 1 slots, the 4096 x 14336 MLP
     shape; f32 and f16."""
     d = ops.Q4_0Dispatch()
     d.force(variant)
-    slots = int(variant.split("_p")[1].split("_")[0])
+    slots = int(variant.split("_p")[1].split("_")[0]) if "_p" in variant else 1
+    slots *= int(variant.split("_s")[2].split("_")[0]) if variant.count("_s") > 1 else 1  # rows split over S waves
     m = int(variant.split("_m")[1].split("_")[0]) if "_m" in variant else 1
     shapes = [(100, 4096), (4099, 1024), (140001, 64), (7, 4096 * slots), (14336, 4096)]
     if slots > 1:
