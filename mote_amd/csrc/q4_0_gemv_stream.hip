@@ -18,9 +18,11 @@
 // over more of the matrix and lowers the achieved HBM rate, also for a pure
 // read of the same pattern.
 //
-// Fused gate/up (GU, one token, unsplit rows): a row group reads row n of the
-// gate and of the up matrix in the same step and keeps silu(gate) * up, the
-// decode form of the operation the skinny and prefill kernels fuse.
+// Fused gate/up (GU, one or two tokens): a row group reads row n of the gate
+// and of the up matrix in the same step and keeps silu(gate) * up, the decode
+// form of the operation the skinny and prefill kernels fuse.  With rows split
+// over S waves the gate and up slice sums meet in LDS separately and the SiLU
+// is applied once they are whole.
 //
 // x is staged once per workgroup through LDS (coalesced 16-byte loads, one
 // 144-byte slot per 128-byte pair chunk so the per-lane reads hit distinct
