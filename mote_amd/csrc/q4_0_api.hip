@@ -346,7 +346,7 @@ const Variant* heuristic(const Problem& p, Op op) {
             while (split < 8 && p.K > 4096u * split) split *= 2;
             char name[40];
             if (split == 1)
-                std::snprintf(name, sizeof name, p.M == 1 ? "gateup_stream_p1_d1_g1" : "gateup_stream_p1_m2_d1q_g1");
+                std::snprintf(name, sizeof name, "%s", p.M == 1 ? "gateup_stream_p1_d1_g1" : "gateup_stream_p1_m2_d1q_g1");
             else
                 std::snprintf(name, sizeof name, "gateup_stream_s%u_m%u_d1q_g1", split, p.M);
             const Variant* v = by_name(name);
@@ -446,7 +446,7 @@ const Variant* heuristic(const Problem& p, Op op) {
         while (split < 8 && p.K > 4096u * split) split *= 2;
         char name[32];
         if (split == 1)
-            std::snprintf(name, sizeof name, "stream_m2_d1q_g1");
+            std::snprintf(name, sizeof name, "%s", "stream_m2_d1q_g1");
         else
             std::snprintf(name, sizeof name, "stream_s%u_m2_d1q_g1", split);
         const Variant* v = by_name(name);
