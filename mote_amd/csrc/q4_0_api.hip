@@ -334,14 +334,15 @@ const Variant* heuristic(const Problem& p, Op op) {
         // Up to 64 tokens the skinny gate/up; above, the prefill tiles with
         // raw Q4_0 weights staged in LDS (measured on MI355X at N = 14336,
         // K = 4096: 1.4x-1.8x faster than dequantised f16 weight tiles).
-        if (fast && (p.M == 1 || p.M == 2)) {
+        if (fast && (p.M == 1 || p.M == 2 || (p.M == 3 && p.K > 4096))) {
             // One or two tokens: the streaming GEMV reading both rows per
             // step (and, for two tokens, each row once for both), rows split
             // over S waves past K = 4096 (measured on MI355X: one token,
             // 4096 x 14336 in 13.6 us, 4.85 TB/s; 8192 x 28672 in 43.9 us,
             // 6.0 TB/s; two tokens, 4096 x 14336 in 15.5 us, 8192 x 28672 in
             // 46.9 us and 14336 x 4096 in 15.0 us, against 17.8, 65.5 and
-            // 21.7 us on the skinny tiles).
+            // 21.7 us on the skinny tiles; three tokens past K = 4096,
+            // 8192 x 28672 in 54.4 us against 65.4 us).
             uint32_t split = 1;
             while (split < 8 && p.K > 4096u * split) split *= 2;
             char name[40];

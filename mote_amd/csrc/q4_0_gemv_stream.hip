@@ -512,6 +512,7 @@ const Variant kStream[] = {
     MOTE_STREAM_GU(1, 1), MOTE_STREAM_GU(1, 2), MOTE_STREAM_GU(2, 1), MOTE_STREAM_GU(2, 2),
     MOTE_STREAM_GU_MQ(1, 2), MOTE_STREAM_GU_SMQ(2, 2), MOTE_STREAM_GU_SMQ(4, 2), MOTE_STREAM_GU_SMQ(8, 2),
     MOTE_STREAM_GU_SMQ(2, 1), MOTE_STREAM_GU_SMQ(4, 1), MOTE_STREAM_GU_SMQ(8, 1),
+    MOTE_STREAM_GU_SMQ(2, 3), MOTE_STREAM_GU_SMQ(4, 3),
 };
 
 #undef MOTE_STREAM

@@ -110,10 +110,12 @@ def test_every_gate_up_split_k_variant(stream, oracle, variant):
     check_gate_up(oracle, y16, x, wg, wu, m, n, k, f16_out=True, what=f"{variant} f16")
 
 
-@pytest.mark.parametrize("m", [4, 32])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 32])
 def test_llama_70b_gate_up_through_the_default_entry_point(stream, oracle, m):
     """The Llama-3-70B fused gate/up (K = 8192, N = 28672) through
-    mote_hip_quantized_gate_up_silu_q4_0_f32, checked on sampled columns."""
+    mote_hip_quantized_gate_up_silu_q4_0_f32 (1-3 tokens on the streaming
+    GEMV with rows split over 2 waves, then the split-K tiles), checked on
+    sampled columns."""
     k, n = 8192, 28672
     x = normal_x(wl.seed_for(44, m), m, k)
     wg, wu = q4_weights(wl.seed_for(44, 1), n, k), q4_weights(wl.seed_for(44, 2), n, k)
