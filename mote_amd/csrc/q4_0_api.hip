@@ -439,18 +439,19 @@ const Variant* heuristic(const Problem& p, Op op) {
     // (4096 x 14336: 9.2 us against 11.9 us on the matrix cores).  From 3
     // tokens: the skinny GEMM of skinny_heuristic, then any skinny variant
     // whose K slicing fits, then the vector-ALU GEMV.
-    if (p.M == 2) {
+    if (p.M == 2 || (p.M == 3 && p.K > 4096 && p.K <= 16384)) {
         // Rows split over S waves past K = 4096, one workgroup per CU
         // (measured on MI355X: 8192 x 8192 in 9.35 us, 14336 x 4096 in 9.35
         // us, 28672 x 8192 in 26.0 us, against 11.8, 11.8 and 31.4 us for the
-        // split-K tiles).
+        // split-K tiles; three tokens, 8192 x 8192 in 11.1 us and 14336 x
+        // 4096 in 11.6 us, against 11.9 and 11.8 us).
         uint32_t split = 1;
         while (split < 8 && p.K > 4096u * split) split *= 2;
         char name[32];
         if (split == 1)
             std::snprintf(name, sizeof name, "%s", "stream_m2_d1q_g1");
         else
-            std::snprintf(name, sizeof name, "stream_s%u_m2_d1q_g1", split);
+            std::snprintf(name, sizeof name, "stream_s%u_m%u_d1q_g1", split, p.M);
         const Variant* v = by_name(name);
         if (v && gemv_stream_supports(*v, p)) return v;
     }
