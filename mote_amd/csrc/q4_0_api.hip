@@ -267,7 +267,13 @@ const Variant* split_k_heuristic(const Problem& p, Op op) {
     const bool k4 = p.K % 4096 == 0;
     const char* name;
     if (op == Op::LinearQ8) {
-        name = p.M <= 32 ? "q8_skinny_k8_s1_t1_d1_l4_c_w_sk" : "q8_skinny_k8_s1_t2_d1_l8_c_w_sk";
+        // 8 items per workgroup where K is a multiple of 4096 (3 x 8192 x 8192:
+        // 17.6 us against 19.4 us with 4), else 4 (3 x 14336 x 4096: 18.3 us
+        // against 24.0 us with 8)
+        if (p.M > 32)
+            name = "q8_skinny_k8_s1_t2_d1_l8_c_w_sk";
+        else
+            name = k4 ? "q8_skinny_k8_s1_t1_d1_l8_c_w_sk" : "q8_skinny_k8_s1_t1_d1_l4_c_w_sk";
     } else if (op == Op::GateUp) {
         if (p.M > 32) return nullptr;  // the prefill tiles
         if (p.M > 16)
@@ -300,12 +306,12 @@ const Variant* heuristic(const Problem& p, Op op) {
         // over S waves above K = 4096; one workgroup per CU measured fastest
         // for Q8_0's 68-byte pairs at every Llama shape), the generic kernel
         // otherwise.
-        if (fast && (p.M == 1 || p.M == 2 || p.M == 4)) {
+        if (fast && (p.M == 1 || p.M == 2 || p.M == 4 || (p.M == 3 && p.K > 4096 && p.K <= 16384))) {
             uint32_t split = 1;
             while (split < 8 && p.K > 4096u * split) split *= 2;
             char name[32];
-            if (p.M == 2 && split > 1)
-                std::snprintf(name, sizeof name, "q8_stream_s%u_m2_d1q_g1", split);
+            if ((p.M == 2 || p.M == 3) && split > 1)  // 3 x 8192 x 8192: 15.2 us (split-K tiles 17.6)
+                std::snprintf(name, sizeof name, "q8_stream_s%u_m%u_d1q_g1", split, p.M);
             else if (p.M > 1)
                 std::snprintf(name, sizeof name, "q8_stream_m%u_d1q_g1", p.M);
             else if (split == 1)
