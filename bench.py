@@ -52,77 +52,13 @@ sys.path.insert(0, ROOT)
 
 from mote_amd import _ffi, ops, workloads as wl  # noqa: E402
 from mote_amd.device import DeviceBuffer, Stream, device_count  # noqa: E402
+from mote_amd.hip_runtime import HipRuntime  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 << 20
 ROTATION_BYTES = 384 << 20
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "q4_0_gemv_m1_k4096_n14336_traffic.md")
-
-
-# --- HIP events and graphs from the runtime libmote_hip.so is linked against ---
-
-class _Hip:
-    """hipEvent / hipGraph entry points of the libamdhip64.so.7 instance that
-    libmote_hip.so loaded (the same runtime, so its streams are valid here)."""
-
-    CAPTURE_THREAD_LOCAL = 1
-
-    def __init__(self) -> None:
-        _ffi.lib()  # loads libamdhip64.so.7 as a dependency first
-        h = ctypes.CDLL("libamdhip64.so.7")
-        P = ctypes.c_void_p
-        h.hipEventCreate.argtypes = [ctypes.POINTER(P)]
-        h.hipEventRecord.argtypes = [P, P]
-        h.hipEventSynchronize.argtypes = [P]
-        h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), P, P]
-        h.hipEventDestroy.argtypes = [P]
-        h.hipStreamBeginCapture.argtypes = [P, ctypes.c_int]
-        h.hipStreamEndCapture.argtypes = [P, ctypes.POINTER(P)]
-        h.hipGraphInstantiate.argtypes = [ctypes.POINTER(P), P, P, P, ctypes.c_size_t]
-        h.hipGraphLaunch.argtypes = [P, P]
-        h.hipGraphExecDestroy.argtypes = [P]
-        h.hipGraphDestroy.argtypes = [P]
-        self.h = h
-
-    def create(self) -> int:
-        e = ctypes.c_void_p()
-        _ffi.check(self.h.hipEventCreate(ctypes.byref(e)), "create event")
-        return e.value
-
-    def record(self, event: int, stream: Stream) -> None:
-        _ffi.check(self.h.hipEventRecord(event, stream.handle), "record event")
-
-    def elapsed_ms(self, start: int, stop: int) -> float:
-        _ffi.check(self.h.hipEventSynchronize(stop), "synchronize event")
-        ms = ctypes.c_float()
-        _ffi.check(self.h.hipEventElapsedTime(ctypes.byref(ms), start, stop), "event elapsed time")
-        return float(ms.value)
-
-    def destroy(self, event: int) -> None:
-        self.h.hipEventDestroy(event)
-
-    def capture(self, stream: Stream, body) -> int:
-        """Records the launches `body()` enqueues on `stream` into an
-        executable graph (nothing runs during capture)."""
-        _ffi.check(self.h.hipStreamBeginCapture(stream.handle, self.CAPTURE_THREAD_LOCAL), "begin capture")
-        try:
-            body()
-        finally:
-            graph = ctypes.c_void_p()
-            status = self.h.hipStreamEndCapture(stream.handle, ctypes.byref(graph))
-        _ffi.check(status, "end capture")
-        exe = ctypes.c_void_p()
-        status = self.h.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0)
-        self.h.hipGraphDestroy(graph)
-        _ffi.check(status, "instantiate graph")
-        return exe.value
-
-    def launch_graph(self, exe: int, stream: Stream) -> None:
-        _ffi.check(self.h.hipGraphLaunch(exe, stream.handle), "launch graph")
-
-    def destroy_graph(self, exe: int) -> None:
-        self.h.hipGraphExecDestroy(exe)
 
 
 def linear_bytes(m: int, n: int, k: int, out_bytes: int = 4) -> int:
@@ -195,7 +131,7 @@ class LinearCase:
 SETTLE_S = 0.02  # untimed graph replays before the timed ones
 
 
-def time_case(case: LinearCase, stream: Stream, hip: _Hip, steps: int, warmup: int,
+def time_case(case: LinearCase, stream: Stream, hip: HipRuntime, steps: int, warmup: int,
               replays: int = 3) -> dict:
     """`steps` calls back to back, issued two ways.
 
@@ -293,14 +229,12 @@ def check_output(case: LinearCase, y_cpu: np.ndarray) -> None:
         raise SystemExit(f"bench: GPU output differs from the oracle in {int(bad.sum())} elements")
 
 
-def profile_run(case: LinearCase, stream: Stream, hip: _Hip) -> int:
+def profile_run(case: LinearCase, stream: Stream, hip: HipRuntime) -> int:
     """Copy one weight matrix device to device (reads and writes |W| bytes:
     the runtime's copy kernel calibrates the HBM byte counters), then run the
     headline linear 20 times on rotating weight copies."""
     dst = DeviceBuffer(case.w.nbytes)
-    h = hip.h
-    h.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
-    _ffi.check(h.hipMemcpy(dst.ptr, case.wb[0][0].ptr, case.w.nbytes, 3), "device-to-device copy")
+    hip.copy_device_to_device(dst.ptr, case.wb[0][0].ptr, case.w.nbytes)
     for i in range(20):
         case.launch(i + 1, stream)
     stream.synchronize()
@@ -417,7 +351,7 @@ class DenseCase:
         self.ctx.close()
 
 
-def run_sweep(stream: Stream, hip: _Hip, steps: int, warmup: int) -> None:
+def run_sweep(stream: Stream, hip: HipRuntime, steps: int, warmup: int) -> None:
     """One line per configuration; the last column is the kernel variant the
     library's shape heuristic plans for it (the one the default entry points
     launch)."""
@@ -467,47 +401,68 @@ def run_sweep(stream: Stream, hip: _Hip, steps: int, warmup: int) -> None:
         case.free()
 
 
+READ_FLOOR_BYTES = (9_461_760, 14_188_544, 33_095_680)  # 1 x 4096 x {4096, 6144, 14336} linears
+
+
 class ReadCase:
-    """One pure-read pattern of mote_hip_read_probe_u128 over the headline
-    matrix's 33 095 680 bytes, rotated over 13 copies (429 MB > MALL)."""
+    """One pure-read pattern of the probe library's mote_probe_read_u128 over
+    `nbytes`, rotated over copies of >= 384 MB in all (past the MALL)."""
 
-    BYTES = 33_095_680
-
-    def __init__(self, bufs, sink, grid, threads, in_flight, nt) -> None:
-        self.bufs, self.sink = bufs, sink
+    def __init__(self, probe, bufs, nbytes, sink, grid, threads, in_flight, nt) -> None:
+        self.probe, self.bufs, self.nbytes, self.sink = probe, bufs, nbytes, sink
         self.args = (grid, threads, in_flight, nt)
 
     def launch(self, i: int, stream: Stream) -> None:
         grid, threads, in_flight, nt = self.args
-        _ffi.check(_ffi.lib().mote_hip_read_probe_u128(self.bufs[i % len(self.bufs)].ptr, self.BYTES, grid,
-                                                        threads, in_flight, nt, self.sink.ptr, stream.handle),
+        _ffi.check(self.probe.mote_probe_read_u128(self.bufs[i % len(self.bufs)].ptr, self.nbytes, grid,
+                                                   threads, in_flight, nt, self.sink.ptr, stream.handle),
                    "read probe")
 
 
-def run_read_floor() -> int:
+def load_probe():
+    """libmote_probe.so, the measuring kernels built beside the library."""
+    path = os.path.join(ROOT, "mote_amd", "libmote_probe.so")
+    if not os.path.exists(path):
+        raise SystemExit(f"bench.py: {path} is missing: build with `python -m mote_amd.build`")
+    _ffi.lib()  # the HIP runtime first
+    probe = ctypes.CDLL(path)
+    P, U32 = ctypes.c_void_p, ctypes.c_uint32
+    probe.mote_probe_read_u128.restype = ctypes.c_int
+    probe.mote_probe_read_u128.argtypes = [P, ctypes.c_size_t, U32, U32, U32, ctypes.c_int, P, P]
+    return probe
+
+
+def run_read_floor(sizes=READ_FLOOR_BYTES) -> int:
     """Times grid-stride pure reads (threads x loads in flight x non-temporal
-    x grid) with graph replays, fastest first, as a markdown table."""
-    stream, hip = Stream(), _Hip()
-    bufs = [DeviceBuffer(ReadCase.BYTES) for _ in range(13)]
-    for i, b in enumerate(bufs):
-        b.upload(np.full(ReadCase.BYTES, i * 7 + 1, dtype=np.uint8))
+    x grid) of each byte count with graph replays, as one markdown table per
+    size, fastest first: the HBM floor of the linears that stream as many
+    bytes."""
+    probe = load_probe()
+    stream, hip = Stream(), HipRuntime()
     sink = DeviceBuffer(16)
-    rows = []
-    for threads, in_flight in ((256, 2), (256, 4), (256, 8), (512, 2), (512, 4), (1024, 2)):
-        for nt in (1, 0):
-            for grid in (256, 512, 768, 1024, 2048):
-                case = ReadCase(bufs, sink, grid, threads, in_flight, nt)
-                us = time_case(case, stream, hip, 100, 26)["kernel_ms_mean"] * 1e3
-                rows.append((us, f"t{threads} u{in_flight} {'nt' if nt else '--'} grid {grid}"))
-                print(f"read floor: {rows[-1][1]}: {us:.2f} us", file=sys.stderr, flush=True)
-    rows.sort()
-    print("| pattern (threads, loads in flight, non-temporal, grid) | µs / launch | GB/s | % of 8 TB/s |")
-    print("|---|---|---|---|")
-    for us, name in rows:
-        gbs = ReadCase.BYTES / (us * 1e-6) / 1e9
-        print(f"| {name} | {us:.2f} | {gbs:.0f} | {100 * gbs / HBM_PEAK_GBS:.1f} % |")
-    for b in bufs + [sink]:
-        b.free()
+    for nbytes in sizes:
+        copies = max(2, math.ceil(ROTATION_BYTES / nbytes))
+        bufs = [DeviceBuffer(nbytes) for _ in range(copies)]
+        for i, b in enumerate(bufs):
+            b.upload(np.full(nbytes, i * 7 + 1, dtype=np.uint8))
+        rows = []
+        for threads, in_flight in ((256, 2), (256, 4), (256, 8), (512, 2), (512, 4), (1024, 2)):
+            for nt in (1, 0):
+                for grid in (256, 512, 768, 1024, 2048):
+                    case = ReadCase(probe, bufs, nbytes, sink, grid, threads, in_flight, nt)
+                    us = time_case(case, stream, hip, 100, 26)["kernel_ms_mean"] * 1e3
+                    rows.append((us, f"t{threads} u{in_flight} {'nt' if nt else '--'} grid {grid}"))
+                    print(f"read floor {nbytes} B: {rows[-1][1]}: {us:.2f} us", file=sys.stderr, flush=True)
+        rows.sort()
+        print(f"\n{nbytes} bytes, {copies} copies\n")
+        print("| pattern (threads, loads in flight, non-temporal, grid) | µs / launch | GB/s | % of 8 TB/s |")
+        print("|---|---|---|---|")
+        for us, name in rows:
+            gbs = nbytes / (us * 1e-6) / 1e9
+            print(f"| {name} | {us:.2f} | {gbs:.0f} | {100 * gbs / HBM_PEAK_GBS:.1f} % |")
+        for b in bufs:
+            b.free()
+    sink.free()
     stream.close()
     return 0
 
@@ -610,14 +565,18 @@ def main() -> int:
                     help="time the vendor library's dense f16 GEMM at the prefill shapes (needs torch; "
                          "stderr table, no result line)")
     ap.add_argument("--read-floor", action="store_true",
-                    help="time pure 16-byte reads of the headline's 33 MB matrix in many grid shapes "
-                         "(the HBM floor of the decode GEMV; stdout table, no result line)")
+                    help="time pure 16-byte reads of 9.46, 14.2 and 33.1 MB (the bytes of the 1 x 4096 x "
+                         "{4096, 6144, 14336} linears) in many grid shapes: the HBM floor of the GEMVs "
+                         "(probe library; stdout tables, no result line)")
+    ap.add_argument("--read-bytes", default=None, metavar="B1,B2,...",
+                    help="with --read-floor: these byte counts (multiples of 16) instead")
     args = ap.parse_args()
     SETTLE_S = max(args.settle_ms, 0.0) / 1e3
     if args.comparator:
         return run_comparator()
     if args.read_floor:
-        return run_read_floor()
+        sizes = tuple(int(v) for v in args.read_bytes.split(",")) if args.read_bytes else READ_FLOOR_BYTES
+        return run_read_floor(sizes)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the Q4_0 linear shards by output rows with no exchange; see the design notes)",
@@ -631,7 +590,7 @@ def main() -> int:
         return 1
 
     stream = Stream()
-    hip = _Hip()
+    hip = HipRuntime()
     m, k, n = 1, 4096, 14336
     if args.profile_run:
         if args.profile_shape:

@@ -135,17 +135,6 @@ int mote_hipblaslt_matmul_f16_f32(void* handle, uint64_t m, uint64_t n, uint64_t
                                   const void* rhs, void* output, void* workspace, size_t workspace_bytes,
                                   void* stream);
 
-/* ---- HBM read probe ---------------------------------------------------------- */
-/* [new] No counterpart in the reference: a diagnostic that measures the HBM
- * read floor the GEMVs are held against (bench.py --read-floor).  Reads
- * `bytes` (a multiple of 16, data 16-byte aligned) with grid-stride 16-byte
- * loads: `grid` workgroups of `threads` (256, 512 or 1024) threads,
- * `in_flight` (2, 4 or 8) loads per thread before use, non-temporal when
- * non_temporal != 0.  `sink` (4 bytes) is written only for one impossible
- * fold value.  Status: hipError_t (1 for a bad argument). */
-int mote_hip_read_probe_u128(const void* data, size_t bytes, uint32_t grid, uint32_t threads,
-                             uint32_t in_flight, int non_temporal, void* sink, void* stream);
-
 /* ---- RMSNorm and fused add + RMSNorm -------------------------------------- */
 /* [reference] crates/mote-backend-hip/src/rms_norm.hip:68-98, bound at
  * crates/mote-backend-hip/src/ffi.rs:120-161.  f16 [rows, hidden] in/out,

@@ -67,7 +67,6 @@ SIGNATURES = {
     "mote_hipblaslt_destroy": (None, [_P]),
     "mote_hipblaslt_last_error": (ctypes.c_char_p, [_P]),
     "mote_hipblaslt_matmul_f16_f32": (_I, [_P, _U64, _U64, _U64, _P, _P, _P, _P, _SZ, _P]),
-    "mote_hip_read_probe_u128": (_I, [_P, _SZ, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, _I, _P, _P]),
     "mote_hip_rms_norm_f16": (_I, [_P, _P, _P, _U64, _U64, ctypes.c_float, _P]),
     "mote_hip_fused_add_rms_norm_f16": (_I, [_P, _P, _P, _P, _U64, _U64, ctypes.c_float, _P]),
     "mote_hip_rope_f16": (_I, [_P, _P, _P, _P, _U64, _U64, _U64, _U64, ctypes.c_uint32, _P]),

@@ -2,7 +2,9 @@
 
 Every ``csrc/*.hip`` file is compiled to an object in ``mote_amd/_build`` and
 the objects are linked into one shared library whose exported symbols are the
-C ABI declared in ``include/mote_hip.h``.  Packed-FP32 instructions are
+C ABI declared in ``include/mote_hip.h``.  The measuring probes under
+``probes/`` (the HBM read-floor kernel of ``bench.py --read-floor``) go into a
+second library, ``mote_amd/libmote_probe.so``, which only the benchmark loads.  Packed-FP32 instructions are
 disabled for the device pass; hipcc's host pass warns that it does not know
 that target feature, which is harmless and filtered from the log.
 
@@ -19,8 +21,10 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
+PROBES = os.path.join(HERE, "probes")
 BUILD = os.path.join(HERE, "_build")
 LIBRARY = os.path.join(HERE, "libmote_hip.so")
+PROBE_LIBRARY = os.path.join(HERE, "libmote_probe.so")
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -43,7 +47,7 @@ def _filter_log(text: str) -> str:
 
 def _compile(source: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(source) + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", source, "-o", obj]
+    cmd = [HIPCC, *COMMON_FLAGS, f"-I{CSRC}", "-c", source, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     log = _filter_log(proc.stdout + proc.stderr)
     if proc.returncode != 0:
@@ -53,27 +57,34 @@ def _compile(source: str) -> str:
     return obj
 
 
-def sources() -> list[str]:
+def sources(directory: str = CSRC) -> list[str]:
     return sorted(
-        os.path.join(CSRC, name) for name in os.listdir(CSRC) if name.endswith(".hip")
+        os.path.join(directory, name) for name in os.listdir(directory) if name.endswith(".hip")
     )
 
 
-def build(jobs: int | None = None) -> str:
-    """Compiles every source and links the library; returns its path."""
-    if shutil.which(HIPCC) is None and not os.path.exists(HIPCC):
-        raise RuntimeError(f"hipcc not found at {HIPCC}")
-    os.makedirs(BUILD, exist_ok=True)
-    srcs = sources()
-    workers = jobs or min(8, os.cpu_count() or 4, len(srcs))
-    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
-        objects = list(pool.map(_compile, srcs))
-    tmp = LIBRARY + ".tmp"
+def _link(objects: list[str], library: str) -> None:
+    tmp = library + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objects]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError("link failed:\n" + _filter_log(proc.stdout + proc.stderr))
-    os.replace(tmp, LIBRARY)
+    os.replace(tmp, library)
+
+
+def build(jobs: int | None = None) -> str:
+    """Compiles every source, links the library and the probe library;
+    returns the library's path."""
+    if shutil.which(HIPCC) is None and not os.path.exists(HIPCC):
+        raise RuntimeError(f"hipcc not found at {HIPCC}")
+    os.makedirs(BUILD, exist_ok=True)
+    srcs = sources()
+    probes = sources(PROBES)
+    workers = jobs or min(8, os.cpu_count() or 4, len(srcs) + len(probes))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
+        objects = list(pool.map(_compile, srcs + probes))
+    _link(objects[: len(srcs)], LIBRARY)
+    _link(objects[len(srcs):], PROBE_LIBRARY)
     return LIBRARY
 
 

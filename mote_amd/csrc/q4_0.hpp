@@ -6,6 +6,8 @@
 
 #include <cstdint>
 
+#include "scratch_pool.hpp"
+
 namespace mote::q4_0 {
 
 enum class OutType : int { F32 = 0, F16 = 1 };
@@ -50,13 +52,14 @@ bool mfma_supports(const Variant& v, const Problem& p);
 
 hipError_t launch_zero_fill(void* y, uint64_t count, OutType out, hipStream_t stream);
 
-// Device scratch owned by the library, one buffer per (device, stream), grown
-// on demand and kept until the process ends: calls on one stream run in
-// order and share it; calls on different streams never do.  Growing it
-// allocates (a grown-out buffer is kept, never freed, as a launch another
-// thread just made on the stream may use it), so the first call that needs
-// more scratch on a stream must not be under graph capture.
-hipError_t stream_scratch(hipStream_t stream, size_t bytes, void** ptr);
+// Split-K scratch owned by the library, one buffer per (device, stream)
+// (scratch_pool.hpp): the lease holds the stream's scratch lock, so a caller
+// queues every kernel that uses the buffer before the lease goes out of
+// scope.  Growing a buffer allocates, so the first call that needs more
+// scratch on a stream must not be under graph capture.
+hipError_t acquire_scratch(hipStream_t stream, size_t bytes, ScratchPool::Lease* lease);
+// Frees the scratch of a stream whose queued work has completed.
+hipError_t release_stream_scratch(hipStream_t stream);
 hipError_t launch_decode_f32(const void* w, float* out, uint64_t rows, uint64_t cols,
                              hipStream_t stream);
 

@@ -583,31 +583,30 @@ int gate_up(Dispatcher* d, const void* input, const void* gate, const void* up, 
 
 }  // namespace
 
-hipError_t stream_scratch(hipStream_t stream, size_t bytes, void** ptr) {
-    // One buffer per (device, stream), grown to the next power of two (at
-    // least 1 MB) when a call needs more.  A grown-out buffer is retired, not
-    // freed: another host thread may have taken it for a launch on the same
-    // stream a moment ago, and earlier launches may still read it.  The few
-    // retired buffers live until the process ends.
-    static std::mutex mu;
-    static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> buffers;
-    static std::vector<void*> retired;
+namespace {
+
+int device_alloc(void** ptr, size_t bytes) { return static_cast<int>(hipMalloc(ptr, bytes)); }
+int device_free(void* ptr) { return static_cast<int>(hipFree(ptr)); }
+
+ScratchPool& scratch_pool() {
+    static ScratchPool* pool = new ScratchPool(device_alloc, device_free);  // lives until exit
+    return *pool;
+}
+
+}  // namespace
+
+hipError_t acquire_scratch(hipStream_t stream, size_t bytes, ScratchPool::Lease* lease) {
     int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
+    const hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    std::lock_guard<std::mutex> lock(mu);
-    auto& b = buffers[{dev, stream}];
-    if (b.second < bytes) {
-        size_t want = size_t{1} << 20;
-        while (want < bytes) want <<= 1;
-        void* fresh = nullptr;
-        e = hipMalloc(&fresh, want);
-        if (e != hipSuccess) return e;
-        if (b.first != nullptr) retired.push_back(b.first);
-        b = {fresh, want};
-    }
-    *ptr = b.first;
-    return hipSuccess;
+    return static_cast<hipError_t>(scratch_pool().acquire(dev, stream, bytes, lease));
+}
+
+hipError_t release_stream_scratch(hipStream_t stream) {
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    return static_cast<hipError_t>(scratch_pool().release(dev, stream));
 }
 
 }  // namespace mote::q4_0

@@ -536,11 +536,13 @@ hipError_t launch_skinny(const Problem& p) {
     const dim3 grid(groups), block(KS * 64);
     float* part = nullptr;
     const uint64_t count = static_cast<uint64_t>(p.M) * p.N;
+    // Split K: the stream's scratch lock is held until both kernels are queued
+    // (the lease goes out of scope at return).
+    ScratchPool::Lease lease;
     if constexpr (SK) {
-        void* buf = nullptr;
-        const hipError_t e = stream_scratch(p.stream, count * kparts * (GU ? 2 : 1) * sizeof(float), &buf);
+        const hipError_t e = acquire_scratch(p.stream, count * kparts * (GU ? 2 : 1) * sizeof(float), &lease);
         if (e != hipSuccess) return e;
-        part = static_cast<float*>(buf);
+        part = static_cast<float*>(lease.ptr());
     }
     if (p.out == OutType::F32) {
         hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float, LAZY, XC, GU, Q8, XW, SK>), grid,

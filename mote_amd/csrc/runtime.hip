@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include "export.hpp"
+#include "q4_0.hpp"
 
 #include <cstddef>
 
@@ -50,8 +51,20 @@ MOTE_EXPORT int mote_hip_stream_create(void** stream) noexcept {
     return static_cast<int>(status);
 }
 
+// Before the stream goes, its queued work is waited for and the split-K
+// scratch the library keeps for it is freed, so a stream created later at the
+// same address starts without it.
 MOTE_EXPORT int mote_hip_stream_destroy(void* stream) noexcept {
-    return static_cast<int>(hipStreamDestroy(static_cast<hipStream_t>(stream)));
+    const auto s = static_cast<hipStream_t>(stream);
+    hipError_t status = hipStreamSynchronize(s);
+    if (status != hipSuccess) return static_cast<int>(status);
+    try {
+        status = mote::q4_0::release_stream_scratch(s);
+    } catch (...) {
+        status = hipErrorUnknown;
+    }
+    const hipError_t destroyed = hipStreamDestroy(s);
+    return static_cast<int>(status != hipSuccess ? status : destroyed);
 }
 
 MOTE_EXPORT int mote_hip_stream_synchronize(void* stream) noexcept {

@@ -3,11 +3,15 @@
 ownership model of ``crates/mote-backend-hip/src/storage.rs:8-96``: a buffer
 owns one ``hipMalloc`` allocation (at least one byte, so even an empty tensor
 has a non-null pointer), uploads and reads back synchronously, and frees on
-``free()`` / garbage collection."""
+``free()`` / garbage collection.  Every runtime status is checked: ``free()``
+and ``close()`` raise :class:`mote_amd._ffi.HipError` when the runtime
+refuses, and forget the handle only once the runtime has released it (garbage
+collection, which cannot raise, reports a failure on stderr)."""
 
 from __future__ import annotations
 
 import ctypes
+import sys
 
 import numpy as np
 
@@ -27,15 +31,15 @@ class Stream:
 
     def close(self) -> None:
         if self.handle:
-            lib().mote_hip_stream_synchronize(self.handle)
-            lib().mote_hip_stream_destroy(self.handle)
+            check(lib().mote_hip_stream_synchronize(self.handle), "synchronize stream")
+            check(lib().mote_hip_stream_destroy(self.handle), "destroy stream")
             self.handle = 0
 
     def __del__(self) -> None:  # pragma: no cover - best effort
         try:
             self.close()
-        except Exception:
-            pass
+        except Exception as e:
+            print(f"mote_amd: stream not released: {e}", file=sys.stderr)
 
 
 class DeviceBuffer:
@@ -77,14 +81,14 @@ class DeviceBuffer:
 
     def free(self) -> None:
         if self.ptr:
-            lib().mote_hip_free(self.ptr)
+            check(lib().mote_hip_free(self.ptr), "free device storage")
             self.ptr = 0
 
     def __del__(self) -> None:  # pragma: no cover - best effort
         try:
             self.free()
-        except Exception:
-            pass
+        except Exception as e:
+            print(f"mote_amd: device buffer not released: {e}", file=sys.stderr)
 
 
 def device_count() -> int:

@@ -1,5 +1,7 @@
 // HBM read probe: a pure-read kernel that measures the read floor the
-// quantized GEMVs are held against (bench.py --read-floor).
+// quantized GEMVs are held against (bench.py --read-floor).  It is built into
+// its own library, libmote_probe.so, which only the benchmark loads: it is a
+// measuring instrument, not part of the drop-in C ABI of libmote_hip.so.
 //
 // Grid-stride 16-byte loads: thread t of a grid of T threads reads chunks
 // t, t + T, t + 2T, ... of the buffer, `in_flight` loads per thread issued
@@ -68,8 +70,13 @@ hipError_t by_threads(uint32_t threads, uint32_t in_flight, const void* data, ui
 }  // namespace
 }  // namespace mote
 
-MOTE_EXPORT int mote_hip_read_probe_u128(const void* data, size_t bytes, uint32_t grid, uint32_t threads,
-                                         uint32_t in_flight, int non_temporal, void* sink, void* stream) noexcept {
+// Reads `bytes` (a multiple of 16, data 16-byte aligned) with grid-stride
+// 16-byte loads: `grid` workgroups of `threads` (256, 512 or 1024) threads,
+// `in_flight` (2, 4 or 8) loads per thread before use, non-temporal when
+// non_temporal != 0.  `sink` (4 bytes) is written only for one impossible
+// fold value.  Status: hipError_t (1 for a bad argument).
+MOTE_EXPORT int mote_probe_read_u128(const void* data, size_t bytes, uint32_t grid, uint32_t threads,
+                                     uint32_t in_flight, int non_temporal, void* sink, void* stream) noexcept {
     if (data == nullptr || sink == nullptr || stream == nullptr || bytes % 16 != 0 || grid == 0 ||
         reinterpret_cast<uintptr_t>(data) % 16 != 0)
         return hipErrorInvalidValue;

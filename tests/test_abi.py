@@ -167,14 +167,23 @@ def test_dense_matmul_argument_errors_without_a_device(lib):
     assert lib.mote_hipblaslt_matmul_f16_f32(None, 1, 1, 1, FAKE, FAKE, FAKE, FAKE, 1 << 20, STREAM) == -1
 
 
-def test_read_probe_argument_errors_without_a_device(lib):
-    """Bad arguments return 1 before any launch: null pointers, a size that
-    is not a multiple of 16, unsupported thread or in-flight counts."""
-    assert lib.mote_hip_read_probe_u128(None, 16, 1, 256, 2, 0, FAKE, STREAM) == 1
-    assert lib.mote_hip_read_probe_u128(FAKE, 17, 1, 256, 2, 0, FAKE, STREAM) == 1
-    assert lib.mote_hip_read_probe_u128(FAKE, 16, 1, 300, 2, 0, FAKE, STREAM) == 1
-    assert lib.mote_hip_read_probe_u128(FAKE, 16, 1, 256, 3, 1, FAKE, STREAM) == 1
-    assert lib.mote_hip_read_probe_u128(FAKE, 0, 1, 256, 2, 0, FAKE, STREAM) == 0  # nothing to read
+def test_read_probe_is_a_separate_library(lib):
+    """The HBM read probe of bench.py --read-floor lives in libmote_probe.so,
+    not in the drop-in library; bad arguments return 1 before any launch:
+    null pointers, a size that is not a multiple of 16, unsupported thread or
+    in-flight counts."""
+    assert not hasattr(lib, "mote_hip_read_probe_u128")
+    path = os.path.join(ROOT, "mote_amd", "libmote_probe.so")
+    probe = ctypes.CDLL(path)
+    fn = probe.mote_probe_read_u128
+    P, U32 = ctypes.c_void_p, ctypes.c_uint32
+    fn.restype = ctypes.c_int
+    fn.argtypes = [P, ctypes.c_size_t, U32, U32, U32, ctypes.c_int, P, P]
+    assert fn(None, 16, 1, 256, 2, 0, FAKE, STREAM) == 1
+    assert fn(FAKE, 17, 1, 256, 2, 0, FAKE, STREAM) == 1
+    assert fn(FAKE, 16, 1, 300, 2, 0, FAKE, STREAM) == 1
+    assert fn(FAKE, 16, 1, 256, 3, 1, FAKE, STREAM) == 1
+    assert fn(FAKE, 0, 1, 256, 2, 0, FAKE, STREAM) == 0  # nothing to read
 
 
 def test_python_wrappers_raise_hip_error(lib):

@@ -19,9 +19,9 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-import bench
 from mote_amd import ops, workloads as wl
 from mote_amd.device import DeviceBuffer
+from mote_amd.hip_runtime import HipRuntime
 
 pytestmark = pytest.mark.gpu
 
@@ -29,7 +29,7 @@ H, FF, HEADS, KV, HD = 4096, 14336, 32, 8, 128
 
 
 def test_decoder_step_graph_replays_match_eager(stream):
-    hip = bench._Hip()
+    hip = HipRuntime()
     bufs = {}
 
     def buf(name, array):
