@@ -38,6 +38,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import faulthandler
 import json
 import math
 import os
@@ -82,10 +83,18 @@ class LinearCase:
     """Device buffers for one Q4_0 (or Q8_0) linear problem with rotating weight copies."""
 
     def __init__(self, m: int, n: int, k: int, workload: int, x_uniform: bool = False,
-                 gate_up: bool = False, q8_0: bool = False) -> None:
+                 gate_up: bool = False, q8_0: bool = False, reference_inputs: bool = False) -> None:
+        """`reference_inputs`: the reference benchmark's closed-form inputs
+        and weights, through the F16-output entry point it times
+        (crates/mote-backend-hip/benches/quantized_linear.rs:8-13,128-152)."""
         self.m, self.n, self.k, self.gate_up, self.q8_0 = m, n, k, gate_up, q8_0
-        self.x = (wl.uniform_f16 if x_uniform else wl.normal_f16)(wl.seed_for(workload, 0), m * k)
-        self.w = (wl.q8_0_weights if q8_0 else wl.q4_0_weights)(wl.seed_for(workload, 1), n, k)
+        self.f16_out = reference_inputs
+        if reference_inputs:
+            self.x = wl.reference_bench_inputs(m, k)
+            self.w = wl.reference_bench_q4_0_weights(n, k)
+        else:
+            self.x = (wl.uniform_f16 if x_uniform else wl.normal_f16)(wl.seed_for(workload, 0), m * k)
+            self.w = (wl.q8_0_weights if q8_0 else wl.q4_0_weights)(wl.seed_for(workload, 1), n, k)
         self.w_up = wl.q4_0_weights(wl.seed_for(workload, 2), n, k) if gate_up else None
         per_copy = self.w.nbytes * (2 if gate_up else 1)
         self.copies = max(2, math.ceil(ROTATION_BYTES / per_copy))
@@ -104,6 +113,9 @@ class LinearCase:
         elif self.q8_0:
             ops.quantized_linear_q8_0_f32(self.xb.ptr, bufs[0].ptr, self.yb.ptr,
                                           self.m, self.n, self.k, stream)
+        elif self.f16_out:
+            ops.quantized_linear_q4_0_f16(self.xb.ptr, bufs[0].ptr, self.yb.ptr,
+                                          self.m, self.n, self.k, stream)
         else:
             ops.quantized_linear_q4_0_f32(self.xb.ptr, bufs[0].ptr, self.yb.ptr,
                                           self.m, self.n, self.k, stream)
@@ -111,7 +123,7 @@ class LinearCase:
     def algorithmic_bytes(self) -> int:
         if self.q8_0:
             return self.w.nbytes + 2 * self.m * self.k + 4 * self.m * self.n
-        b = linear_bytes(self.m, self.n, self.k)
+        b = linear_bytes(self.m, self.n, self.k, 2 if self.f16_out else 4)
         return b + (self.w_up.nbytes if self.gate_up else 0)
 
     def flops(self) -> int:
@@ -262,6 +274,11 @@ SWEEP = (
        ("q8_0 4 tok", 4, 4096, 14336, 5, False, "q8")]
     + [("q8_0 skinny", m, 4096, 14336, 5, False, "q8") for m in (8, 16, 32, 64)]
     + [("q8_0 prefill", m, 4096, 14336, 5, False, "q8") for m in (256, 512)]
+    + [("3 tok o proj", 3, 8192, 8192, 2, False, False), ("3 tok down", 3, 14336, 4096, 2, False, False),
+       ("q8_0 3 tok", 3, 8192, 8192, 5, False, "q8"), ("3 tok gate/up", 3, 8192, 28672, 4, False, True)]
+    # the reference benchmark's cases (rows, N, K), its inputs, the F16-output entry point
+    + [("ref bench f16", m, k, n, 0, False, "ref") for m, n, k in
+       ((1, 4096, 4096), (1, 11008, 4096), (1, 4096, 11008), (16, 4096, 4096))]
 )
 
 
@@ -359,7 +376,8 @@ def run_sweep(stream: Stream, hip: HipRuntime, steps: int, warmup: int) -> None:
           f"{'%HBM':>7}{'TFLOP/s':>9}{'%MFMA':>7}  kernel", file=sys.stderr)
     planner = ops.Q4_0Dispatch()  # no autotuning: the default entry points' heuristic
     for name, m, k, n, workload, uni, kind in SWEEP:
-        case = LinearCase(m, n, k, workload, x_uniform=uni, gate_up=kind is True, q8_0=kind == "q8")
+        case = LinearCase(m, n, k, workload, x_uniform=uni, gate_up=kind is True, q8_0=kind == "q8",
+                          reference_inputs=kind == "ref")
         t = time_case(case, stream, hip, steps, warmup)
         us = t["kernel_ms_mean"] * 1e3
         w = case.wb[0]
@@ -368,9 +386,9 @@ def run_sweep(stream: Stream, hip: HipRuntime, steps: int, warmup: int) -> None:
         elif kind == "q8":
             planner.linear_q8_0(case.xb.ptr, w[0].ptr, case.yb.ptr, m, n, k, stream)
         else:
-            planner.linear(case.xb.ptr, w[0].ptr, case.yb.ptr, m, n, k, stream)
+            planner.linear(case.xb.ptr, w[0].ptr, case.yb.ptr, m, n, k, stream, f16_out=kind == "ref")
         stream.synchronize()
-        variant = planner.plan(m, n, k, gate_up=kind is True, q8_0=kind == "q8")
+        variant = planner.plan(m, n, k, gate_up=kind is True, q8_0=kind == "q8", f16_out=kind == "ref")
         gbs = case.algorithmic_bytes() / (us * 1e-6) / 1e9
         tf = case.flops() / (us * 1e-6) / 1e12
         print(f"{name:<15}{m:>5}{k:>7}{n:>7}{us:>11.2f}{t['eager_ms_per_step'] * 1e3:>10.2f}{gbs:>9.0f}"
@@ -571,6 +589,9 @@ def main() -> int:
     ap.add_argument("--read-bytes", default=None, metavar="B1,B2,...",
                     help="with --read-floor: these byte counts (multiples of 16) instead")
     args = ap.parse_args()
+    # A crash inside a runtime or profiler call then names the Python line
+    # (and so the C-ABI call) it happened in.
+    faulthandler.enable()
     SETTLE_S = max(args.settle_ms, 0.0) / 1e3
     if args.comparator:
         return run_comparator()

@@ -113,6 +113,13 @@ int mote_q4_0_dispatch_linear_q8_0(void* handle, const void* input, const void* 
 int mote_q4_0_dispatch_plan(void* handle, uint64_t rows, uint64_t output_features,
                             uint64_t input_features, int gate_up_op, int output_f16,
                             char* name, size_t capacity);
+/* The variant the context would plan for a problem with 256-byte aligned
+ * operands (op: 0 linear, 1 gate/up, 2 Q8_0 linear): the forced variant, else
+ * the shape heuristic's choice.  Host only: nothing is launched or cached,
+ * and no device is needed.  hipErrorInvalidValue (1) for an empty or
+ * unsupported shape, hipErrorNotFound (500) when no variant fits. */
+int mote_q4_0_dispatch_select(void* handle, uint64_t rows, uint64_t output_features,
+                              uint64_t input_features, int op, char* name, size_t capacity);
 int mote_q4_0_variant_count(void);
 const char* mote_q4_0_variant_name(int index);
 

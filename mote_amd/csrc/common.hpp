@@ -172,6 +172,43 @@ __device__ __forceinline__ F16x8Pair dequant8_q8(uint32_t q0, uint32_t q1, f16x2
             f16x8{l02.x, l02.y, l13.x, l13.y, l46.x, l46.y, l57.x, l57.y}};
 }
 
+// ---------------------------------------------------------------------------
+// Scales whose binary16 products overflow.
+//
+// The matrix-core kernels round each dequantised weight, (q - 8) d for Q4_0
+// or v d for Q8_0, to binary16 before the MFMA.  With |q - 8| <= 8 the
+// product stays finite for |d| <= 8188 (the largest binary16 below 8192); with
+// |v| <= 128, for |d| <= 511.75.  The reference decodes in f32
+// (crates/mote-reference/src/quantized.rs:187-195), where any finite d gives a
+// finite value.  So when a wave's MFMA step holds a larger scale (no model's
+// weights do), the step runs with every scale of the wave times 2^-S (S = 4
+// for Q4_0, 8 for Q8_0, so 8 * 65504 / 16 and 128 * 65504 / 256 stay finite)
+// and its f32 accumulators scaled by 2^-S before the step and by 2^S after.
+// Scaling by a power of two is exact in f32, and in binary16 for every
+// product that stays normal, so for Q4_0 the step computes exactly what an
+// unbounded binary16 would wherever |d| >= 2^-10; scales below that in the
+// same step as one of at least 8192, and the small low halves of Q8_0's
+// hi + lo products, lose up to S bits to binary16 subnormals, which the
+// tolerance, scaled by the largest |d|, absorbs by orders of magnitude.  Inf and NaN scales take the same path and propagate as the
+// direct products would.  The test is one wave-uniform branch per step that
+// ordinary weights never take; the step's code exists once, so the register
+// use stays that of the ordinary step.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kQ4BigScale = 0x7000u;  // binary16 8192: (q - 8) d may overflow from here
+constexpr uint32_t kQ8BigScale = 0x6000u;  // binary16 512: v d may overflow from here
+constexpr float kQ4BigDown = 0.0625f;      // 2^-4
+constexpr float kQ8BigDown = 0.00390625f;  // 2^-8
+
+// Whether either binary16 scale in the two halves of `scales` has a
+// magnitude field of at least kLimit (inf and NaN included).
+template <uint32_t kLimit>
+__device__ __forceinline__ bool big_scales(uint32_t scales) {
+    constexpr uint32_t kAdd = (0x8000u - kLimit) * 0x10001u;  // carries into bit 15 of a half from kLimit up
+    return (((scales & 0x7FFF7FFFu) + kAdd) & 0x80008000u) != 0u;
+}
+
+__device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
+
 // The two VGPR constants of dequant8.
 struct DequantConsts {
     uint32_t c1024, c64, q8;  // q8: the 0x64 bytes of dequant8_q8

@@ -39,7 +39,6 @@ const Variant* gemv_variants(int* count);
 const Variant* gemv_rows_variants(int* count);
 const Variant* gemv_stream_variants(int* count);
 const Variant* skinny_mfma_variants(int* count);
-const Variant* mfma_variants(int* count);
 const Variant* prefill_variants(int* count);
 const Variant* generic_variants(int* count);
 
@@ -48,7 +47,7 @@ bool gemv_supports(const Variant& v, const Problem& p);
 bool gemv_rows_supports(const Variant& v, const Problem& p);
 bool gemv_stream_supports(const Variant& v, const Problem& p);
 bool skinny_mfma_supports(const Variant& v, const Problem& p);
-bool mfma_supports(const Variant& v, const Problem& p);
+bool prefill_supports(const Variant& v, const Problem& p);
 
 hipError_t launch_zero_fill(void* y, uint64_t count, OutType out, hipStream_t stream);
 

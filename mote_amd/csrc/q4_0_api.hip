@@ -55,7 +55,7 @@ std::vector<const Variant*> all_variants() {
     std::vector<const Variant*> out;
     int count = 0;
     for (auto table : {gemv_stream_variants, gemv_rows_variants, gemv_variants, skinny_mfma_variants,
-                       mfma_variants, prefill_variants, generic_variants}) {
+                       prefill_variants, generic_variants}) {
         const Variant* v = table(&count);
         for (int i = 0; i < count; ++i) out.push_back(&v[i]);
     }
@@ -91,7 +91,7 @@ bool supports(const Variant& v, const Problem& p) {
         case Kind::Q8Skinny: return skinny_mfma_supports(v, p);
         case Kind::Mfma:
         case Kind::GateUpMfma:
-        case Kind::Q8Prefill: return mfma_supports(v, p);
+        case Kind::Q8Prefill: return prefill_supports(v, p);
         default: return true;
     }
 }
@@ -341,15 +341,16 @@ const Variant* heuristic(const Problem& p, Op op) {
         // Up to 64 tokens the skinny gate/up; above, the prefill tiles with
         // raw Q4_0 weights staged in LDS (measured on MI355X at N = 14336,
         // K = 4096: 1.4x-1.8x faster than dequantised f16 weight tiles).
-        if (fast && (p.M == 1 || p.M == 2 || (p.M == 3 && p.K > 4096))) {
+        if (fast && (p.M == 1 || p.M == 2 || (p.M == 3 && p.K > 4096 && p.K <= 16384))) {
             // One or two tokens: the streaming GEMV reading both rows per
             // step (and, for two tokens, each row once for both), rows split
             // over S waves past K = 4096 (measured on MI355X: one token,
             // 4096 x 14336 in 13.6 us, 4.85 TB/s; 8192 x 28672 in 43.9 us,
             // 6.0 TB/s; two tokens, 4096 x 14336 in 15.5 us, 8192 x 28672 in
             // 46.9 us and 14336 x 4096 in 15.0 us, against 17.8, 65.5 and
-            // 21.7 us on the skinny tiles; three tokens past K = 4096,
-            // 8192 x 28672 in 54.4 us against 65.4 us).
+            // 21.7 us on the skinny tiles; three tokens for 4096 < K <=
+            // 16384, rows split up to 4 ways, 8192 x 28672 in 54.4 us against
+            // 65.4 us).
             uint32_t split = 1;
             while (split < 8 && p.K > 4096u * split) split *= 2;
             char name[40];
@@ -390,7 +391,7 @@ const Variant* heuristic(const Problem& p, Op op) {
         // tokens, 46.5-47.1 us; 64 x 128 at 128 tokens, 39.8 us; the 16 x 16
         // tiles took 83, 59.4 and 46.1 us).
         static const char* const order[] = {"mfma_x32s_m128_n256_w1", "mfma_x32s_m128_n128_w1",
-                                            "mfma_x32s_m64_n128_w1", "mfma_r_m64_n128", "mfma_m64_n64_p1"};
+                                            "mfma_x32s_m64_n128_w1", "mfma_r_m64_n128", "mfma_r_m64_n64"};
         const Variant* best = nullptr;
         uint64_t best_tiles = 0;
         for (const char* name : order) {
@@ -463,11 +464,9 @@ const Variant* heuristic(const Problem& p, Op op) {
     }
     if (const Variant* v = skinny_heuristic(p)) return v;
     if (const Variant* v = split_k_heuristic(p, op)) return v;
-    const char* suffix = p.M <= 16 ? "_t1_d1_g1_r1" : p.M <= 32 ? "_t1_d2_g1_r1" : "_t2_d2_g1_r1";
-    for (const char* name : {"skinny_mfma_k16_s1", "skinny_mfma_k8_s2", "skinny_mfma_k16_s2",
-                             "skinny_mfma_k8_s1", "skinny_mfma_k4_s2", "skinny_mfma_k4_s1"}) {
-        const Variant* v = by_name((std::string(name) + suffix).c_str());
-        if (!v) v = by_name((std::string(name) + "_t1_d1_g1_r1").c_str());
+    // one K slice of 2048 or 1024 (K that no split fits)
+    for (const char* name : {"skinny_mfma_k8_s1_t1_d1_g1_r1", "skinny_mfma_k4_s1_t1_d1_g1_r1"}) {
+        const Variant* v = by_name(name);
         if (v && skinny_mfma_supports(*v, p)) return v;
     }
     if (p.M == 2) return by_name("gemv_r4_t2_k1");
@@ -787,6 +786,32 @@ MOTE_EXPORT int mote_q4_0_dispatch_plan(void* handle, uint64_t rows, uint64_t ou
     }
     name[0] = '\0';
     return hipErrorNotFound;
+}
+
+MOTE_EXPORT int mote_q4_0_dispatch_select(void* handle, uint64_t rows, uint64_t output_features,
+                                         uint64_t input_features, int op, char* name, size_t capacity) noexcept {
+    auto* d = static_cast<mote::q4_0::Dispatcher*>(handle);
+    if (!d || !name || capacity == 0 || op < 0 || op > 2) return hipErrorInvalidValue;
+    name[0] = '\0';
+    if (rows == 0 || output_features == 0 || input_features == 0 || input_features % 32 != 0 ||
+        rows > UINT_MAX || output_features > UINT_MAX || input_features > 0x7fffffffull)
+        return hipErrorInvalidValue;
+    try {
+        // Stand-in operands at the library's 256-byte allocation alignment;
+        // nothing is dereferenced or launched.
+        const auto* base = reinterpret_cast<const uint8_t*>(uintptr_t{1} << 20);
+        const Problem p{base, base, op == static_cast<int>(Op::GateUp) ? base : nullptr, const_cast<uint8_t*>(base),
+                        static_cast<uint32_t>(rows), static_cast<uint32_t>(output_features),
+                        static_cast<uint32_t>(input_features), OutType::F32, nullptr};
+        std::lock_guard<std::mutex> lock(d->mutex);
+        const Variant* v = d->forced.empty() ? heuristic(p, static_cast<Op>(op)) : find_variant(d->forced);
+        if (!v) return hipErrorNotFound;
+        std::strncpy(name, v->name, capacity - 1);
+        name[capacity - 1] = '\0';
+        return 0;
+    } catch (...) {
+        return hipErrorUnknown;
+    }
 }
 
 MOTE_EXPORT int mote_q4_0_variant_count(void) noexcept {

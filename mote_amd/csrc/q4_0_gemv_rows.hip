@@ -198,10 +198,7 @@ hipError_t launch_gemv_rows(const Problem& p) {
     Variant{"rows_r" #R "_k" #KS, Kind::GemvRows, R, 1, KS, &launch_gemv_rows<R, KS>}
 
 const Variant kRows[] = {
-    MOTE_ROWS(1, 1), MOTE_ROWS(2, 1), MOTE_ROWS(4, 1), MOTE_ROWS(7, 1), MOTE_ROWS(8, 1),
-    MOTE_ROWS(2, 2), MOTE_ROWS(4, 2), MOTE_ROWS(8, 2),
-    MOTE_ROWS(2, 4), MOTE_ROWS(4, 4), MOTE_ROWS(8, 4),
-    MOTE_ROWS(4, 8), MOTE_ROWS(8, 8),
+    MOTE_ROWS(4, 1), MOTE_ROWS(4, 2), MOTE_ROWS(4, 4), MOTE_ROWS(4, 8),
 };
 
 #undef MOTE_ROWS

@@ -458,8 +458,6 @@ hipError_t launch_gemv_stream(const Problem& p) {
     Variant{"stream_d" #D "_g" #G, Kind::GemvStream, 1, D, G, &launch_gemv_stream<1, 1, D, G>}
 #define MOTE_STREAM_Q(D, G) \
     Variant{"stream_d" #D "q_g" #G, Kind::GemvStream, 1, D, G, &launch_gemv_stream<1, 1, D, G, 1, false>}
-#define MOTE_STREAM_P(P, D, G) \
-    Variant{"stream_p" #P "_d" #D "_g" #G, Kind::GemvStream, P, D, G, &launch_gemv_stream<P, 1, D, G>}
 #define MOTE_STREAM_S(S, D, G) \
     Variant{"stream_s" #S "_d" #D "_g" #G, Kind::GemvStream, S, D, G, &launch_gemv_stream<1, S, D, G>}
 #define MOTE_STREAM_SQ(S, D, G)                                              \
@@ -492,31 +490,28 @@ hipError_t launch_gemv_stream(const Problem& p) {
     Variant{"stream_m" #MT "_d" #D "q_g" #G, Kind::GemvStream, 1, D, G,                 \
             &launch_gemv_stream<1, 1, D, G, MT, false>, MT}
 
-// "q" variants queue row j + 1 + D while waiting for row j + 1.
+// "q" variants queue row j + 1 + D while waiting for row j + 1.  The table
+// holds the forms the dispatch heuristic picks plus the measured alternatives
+// it is compared with (two rows in flight, the other queueing form, one or
+// two workgroups per CU, three and four tokens per row read).
 const Variant kStream[] = {
-    MOTE_STREAM(1, 1), MOTE_STREAM(2, 1), MOTE_STREAM(3, 1),
-    MOTE_STREAM(1, 2), MOTE_STREAM(2, 2),
-    MOTE_STREAM_Q(1, 1), MOTE_STREAM_Q(1, 2), MOTE_STREAM_Q(2, 1),
-    MOTE_STREAM_P(2, 1, 1), MOTE_STREAM_P(2, 1, 2),
-    MOTE_STREAM_P(3, 1, 1), MOTE_STREAM_P(4, 1, 1),
-    MOTE_STREAM_S(2, 1, 1), MOTE_STREAM_S(2, 1, 2), MOTE_STREAM_S(4, 1, 1), MOTE_STREAM_S(4, 1, 2),
-    MOTE_STREAM_S(4, 2, 2), MOTE_STREAM_SQ(4, 1, 2), MOTE_STREAM_SQ(2, 1, 2), MOTE_STREAM_SQ(4, 1, 1),
-    MOTE_STREAM_S(8, 1, 1), MOTE_STREAM_S(8, 1, 2), MOTE_STREAM_SQ(8, 1, 1), MOTE_STREAM_SQ(8, 1, 2),
-    MOTE_STREAM_M(2, 1, 1), MOTE_STREAM_M(3, 1, 1), MOTE_STREAM_M(4, 1, 1),
-    MOTE_STREAM_MQ(2, 1, 1), MOTE_STREAM_MQ(2, 1, 2),
-    MOTE_STREAM_SMQ(2, 2, 1), MOTE_STREAM_SMQ(4, 2, 1), MOTE_STREAM_SMQ(8, 2, 1), MOTE_STREAM_SMQ(2, 2, 2),
-    MOTE_STREAM_SMQ(4, 2, 2), MOTE_STREAM_SMQ(8, 2, 2), MOTE_STREAM_SMQ(2, 3, 1), MOTE_STREAM_SMQ(4, 3, 1),
-    MOTE_Q8("d1_g1", 1, 1), MOTE_Q8("d1_g2", 1, 2), MOTE_Q8("s2_d1_g1", 2, 1), MOTE_Q8("s2_d1_g2", 2, 2),
-    MOTE_Q8("s4_d1_g1", 4, 1), MOTE_Q8("s4_d1_g2", 4, 2), MOTE_Q8("s8_d1_g1", 8, 1), MOTE_Q8("s8_d1_g2", 8, 2),
+    MOTE_STREAM(1, 1), MOTE_STREAM(2, 1), MOTE_STREAM(1, 2),
+    MOTE_STREAM_Q(1, 1), MOTE_STREAM_Q(1, 2),
+    MOTE_STREAM_S(2, 1, 1), MOTE_STREAM_S(2, 1, 2), MOTE_STREAM_SQ(4, 1, 1), MOTE_STREAM_SQ(4, 1, 2),
+    MOTE_STREAM_S(8, 1, 1), MOTE_STREAM_S(8, 1, 2),
+    MOTE_STREAM_M(3, 1, 1), MOTE_STREAM_M(4, 1, 1), MOTE_STREAM_MQ(2, 1, 1),
+    MOTE_STREAM_SMQ(2, 2, 1), MOTE_STREAM_SMQ(4, 2, 1), MOTE_STREAM_SMQ(8, 2, 1),
+    MOTE_STREAM_SMQ(2, 3, 1), MOTE_STREAM_SMQ(4, 3, 1),
+    MOTE_Q8("d1_g1", 1, 1), MOTE_Q8("d1_g2", 1, 2), MOTE_Q8("s2_d1_g1", 2, 1), MOTE_Q8("s4_d1_g1", 4, 1),
+    MOTE_Q8("s8_d1_g1", 8, 1),
     MOTE_Q8_SM(2, 2), MOTE_Q8_SM(4, 2), MOTE_Q8_SM(8, 2), MOTE_Q8_SM(2, 3), MOTE_Q8_SM(4, 3), MOTE_Q8_M(2, 1), MOTE_Q8_M(4, 1),
-    MOTE_STREAM_GU(1, 1), MOTE_STREAM_GU(1, 2), MOTE_STREAM_GU(2, 1), MOTE_STREAM_GU(2, 2),
+    MOTE_STREAM_GU(1, 1), MOTE_STREAM_GU(1, 2),
     MOTE_STREAM_GU_MQ(1, 2), MOTE_STREAM_GU_SMQ(2, 2), MOTE_STREAM_GU_SMQ(4, 2), MOTE_STREAM_GU_SMQ(8, 2),
     MOTE_STREAM_GU_SMQ(2, 1), MOTE_STREAM_GU_SMQ(4, 1), MOTE_STREAM_GU_SMQ(8, 1),
     MOTE_STREAM_GU_SMQ(2, 3), MOTE_STREAM_GU_SMQ(4, 3),
 };
 
 #undef MOTE_STREAM
-#undef MOTE_STREAM_P
 #undef MOTE_STREAM_S
 #undef MOTE_STREAM_M
 #undef MOTE_STREAM_Q

@@ -200,13 +200,22 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
             return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     };
 
+    // Scales past binary16 range go through the scaled MFMA (common.hpp).
+    constexpr uint32_t kBig = Q8 ? kQ8BigScale : kQ4BigScale;
+    constexpr float kDown = Q8 ? kQ8BigDown : kQ4BigDown;
     auto mma_step = [&](int buf) {
         uint32_t scales[NW][TN];
+        bool big = false;
 #pragma unroll
         for (int s = 0; s < NW; ++s)
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
+            for (int j = 0; j < TN; ++j) {
                 scales[s][j] = *reinterpret_cast<const uint32_t*>(&ws[s][buf][b_base + j * T * kWRow]);
+                big = big || big_scales<kBig>(scales[s][j]);
+            }
+        // The step's MFMAs with the scale words sc (block 0's scale in the low
+        // half, block 1's in the high half of each weight row's word).
+        auto body = [&](const uint32_t (&sc)[NW][TN]) {
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
@@ -220,7 +229,7 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
                 for (int s = 0; s < NW; ++s) {
 #pragma unroll
                     for (int j = 0; j < TN; ++j) {
-                        const f16x2 d = as_h2(__builtin_amdgcn_perm(scales[s][j], scales[s][j],
+                        const f16x2 d = as_h2(__builtin_amdgcn_perm(sc[s][j], sc[s][j],
                                                                     blk ? 0x03020302u : 0x01000100u));
                         if constexpr (Q8) {
                             // two dword reads: the 68-byte rows keep the pair only dword aligned
@@ -242,6 +251,31 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
                     }
                 }
             }
+        }
+        };
+        // A step with a scale past binary16 range runs with every scale times
+        // 2^-S and the accumulators scaled by 2^-S before and by 2^S after
+        // (common.hpp).
+        const bool big_step = wave_any(big);
+        if (__builtin_expect(big_step, 0)) {
+            const f16x2 dd = {static_cast<_Float16>(kDown), static_cast<_Float16>(kDown)};
+#pragma unroll
+            for (int s = 0; s < NW; ++s)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    scales[s][j] = __builtin_bit_cast(uint32_t, as_h2(scales[s][j]) * dd);
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) acc[s][i][j] *= kDown;
+                }
+        }
+        body(scales);
+        if (__builtin_expect(big_step, 0)) {
+#pragma unroll
+            for (int s = 0; s < NW; ++s)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) acc[s][i][j] *= 1.0f / kDown;
         }
     };
 
@@ -340,47 +374,43 @@ hipError_t launch_prefill(const Problem& p) {
 #define MOTE_PREFILL_Q8_X32S(BM, BN, WM)                                                             \
     Variant{"q8_mfma_x32s_m" #BM "_n" #BN "_w" #WM, Kind::Q8Prefill, BM, BN, 1,                      \
             &launch_prefill<BM, BN, false, true, WM, true, true>}
-#define MOTE_PREFILL_GU_X32(BM, BN, WM)                                                              \
-    Variant{"gateup_mfma_x32_m" #BM "_n" #BN "_w" #WM, Kind::GateUpMfma, BM, BN, 1,                  \
-            &launch_prefill<BM, BN, true, false, WM, true>}
-#define MOTE_PREFILL_Q8_X32(BM, BN, WM)                                                              \
-    Variant{"q8_mfma_x32_m" #BM "_n" #BN "_w" #WM, Kind::Q8Prefill, BM, BN, 1,                       \
-            &launch_prefill<BM, BN, false, true, WM, true>}
 
-// 128 x 224 tiles: N = 14336 splits into 64 of them, so M = 512 makes exactly
-// one tile per CU of a 256-CU MI355X.
+// The tiles the dispatch heuristic picks (32 x 32 MFMA tiles with staging
+// waves where about one tile per CU fits, 16 x 16 tiles below that) and the
+// measured alternatives of the same tile without staging waves and with
+// 16 x 16 MFMAs.
 const Variant kPrefill[] = {
-    MOTE_PREFILL(128, 256), MOTE_PREFILL(128, 128), MOTE_PREFILL(64, 256), MOTE_PREFILL(256, 128),
-    MOTE_PREFILL(64, 128), MOTE_PREFILL(128, 224), MOTE_PREFILL(64, 224),
-    MOTE_PREFILL_GU(128, 128), MOTE_PREFILL_GU(64, 128), MOTE_PREFILL_GU(128, 64), MOTE_PREFILL_GU(64, 64),
-    MOTE_PREFILL_Q8(128, 128), MOTE_PREFILL_Q8(64, 128), MOTE_PREFILL_Q8(128, 64), MOTE_PREFILL_Q8(64, 64),
-    MOTE_PREFILL_X32(128, 128, 1), MOTE_PREFILL_X32(128, 256, 1), MOTE_PREFILL_X32(64, 128, 1),
-    MOTE_PREFILL_X32(128, 128, 2), MOTE_PREFILL_X32(256, 128, 2), MOTE_PREFILL_X32(128, 256, 2),
-    MOTE_PREFILL_GU_X32(128, 128, 1), MOTE_PREFILL_GU_X32(64, 128, 1), MOTE_PREFILL_GU_X32(128, 128, 2),
-    MOTE_PREFILL_Q8_X32(128, 128, 1), MOTE_PREFILL_Q8_X32(64, 128, 1), MOTE_PREFILL_Q8_X32(128, 128, 2),
-    MOTE_PREFILL_X32S(128, 128, 1), MOTE_PREFILL_X32S(128, 128, 2), MOTE_PREFILL_X32S(64, 128, 1),
-    MOTE_PREFILL_X32S(128, 256, 1), MOTE_PREFILL_X32S(128, 256, 2), MOTE_PREFILL_X32S(64, 256, 1),
-    MOTE_PREFILL_GU_X32S(128, 128, 1), MOTE_PREFILL_GU_X32S(128, 128, 2), MOTE_PREFILL_GU_X32S(64, 128, 1),
-    MOTE_PREFILL_GU_X32S(64, 256, 1),
-    MOTE_PREFILL_Q8_X32S(128, 128, 1), MOTE_PREFILL_Q8_X32S(128, 128, 2), MOTE_PREFILL_Q8_X32S(64, 256, 1),
-    MOTE_PREFILL_Q8_X32S(128, 256, 1), MOTE_PREFILL_Q8_X32S(64, 128, 1),
+    MOTE_PREFILL(128, 128), MOTE_PREFILL(64, 128), MOTE_PREFILL(64, 64),
+    MOTE_PREFILL_GU(128, 64), MOTE_PREFILL_GU(64, 64),
+    MOTE_PREFILL_Q8(64, 64),
+    MOTE_PREFILL_X32(128, 128, 1),
+    MOTE_PREFILL_X32S(128, 128, 1), MOTE_PREFILL_X32S(64, 128, 1), MOTE_PREFILL_X32S(128, 256, 1),
+    MOTE_PREFILL_GU_X32S(128, 128, 1), MOTE_PREFILL_GU_X32S(64, 128, 1),
+    MOTE_PREFILL_Q8_X32S(128, 128, 1), MOTE_PREFILL_Q8_X32S(128, 256, 1),
 };
 
 #undef MOTE_PREFILL
 #undef MOTE_PREFILL_GU
 #undef MOTE_PREFILL_Q8
 #undef MOTE_PREFILL_X32
-#undef MOTE_PREFILL_GU_X32
 #undef MOTE_PREFILL_X32S
 #undef MOTE_PREFILL_GU_X32S
 #undef MOTE_PREFILL_Q8_X32S
-#undef MOTE_PREFILL_Q8_X32
 
 }  // namespace
 
 const Variant* prefill_variants(int* count) {
     *count = static_cast<int>(sizeof(kPrefill) / sizeof(kPrefill[0]));
     return kPrefill;
+}
+
+// K a multiple of 64, x 16-byte and the weights (and the up matrix of a
+// gate/up) dword aligned; any M and N (partial tiles are masked).
+bool prefill_supports(const Variant& v, const Problem& p) {
+    (void)v;
+    const bool up_ok = p.w_up == nullptr || reinterpret_cast<uintptr_t>(p.w_up) % 4 == 0;
+    return p.K % 64 == 0 && p.K > 0 && up_ok && reinterpret_cast<uintptr_t>(p.w) % 4 == 0 &&
+           reinterpret_cast<uintptr_t>(p.x) % 16 == 0;
 }
 
 }  // namespace mote::q4_0

@@ -291,11 +291,15 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
 
     // Dequantise + MFMA one item (staged in LDS with TR, else from `buf`)
     // into `acc`.
+    // Scales past binary16 range go through the scaled MFMA (common.hpp).
+    constexpr uint32_t kBig = Q8 ? kQ8BigScale : kQ4BigScale;
+    constexpr float kDown = Q8 ? kQ8BigDown : kQ4BigDown;
     auto mma_item = [&](const uint32_t (&buf)[RT * STEPS][kDw], f32x4 (&acc)[RT][MT]) {
 #pragma unroll
         for (int s = 0; s < STEPS; ++s) {
             uint32_t q[RT][Q8 ? 16 : 8];
             f16x2 d0[RT], d1[RT];
+            bool big = false;
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
                 uint32_t c[kDw];
@@ -309,32 +313,58 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
 #pragma unroll
                     for (int i = 0; i < 16; ++i) q[rt][i] = q8_bytes(c, i);
                     d1[rt] = as_h2(__builtin_amdgcn_perm(c[8], c[8], 0x03020302u));
+                    big = big || big_scales<kBig>((c[0] & 0xFFFFu) | (c[8] & 0xFFFF0000u));
                 } else {
                     q[rt][0] = pair_q0(c);
                     q[rt][1] = c[1]; q[rt][2] = c[2]; q[rt][3] = c[3];
                     q[rt][4] = c[5]; q[rt][5] = c[6]; q[rt][6] = c[7]; q[rt][7] = c[8];
                     d1[rt] = as_h2(__builtin_amdgcn_perm(c[4], c[4], 0x03020302u));
+                    big = big || big_scales<kBig>((c[0] & 0xFFFFu) | (c[4] & 0xFFFF0000u));
                 }
                 d0[rt] = as_h2(__builtin_amdgcn_perm(c[0], c[0], 0x01000100u));
             }
+            // The step's MFMAs with block scales e0 (dwords 0-3) and e1 (4-7).
+            auto t_loop = [&](const f16x2 (&e0)[RT], const f16x2 (&e1)[RT]) {
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt) {
                     if constexpr (Q8) {  // the weight as hi + lo: two MFMAs against the same x
-                        const F16x8Pair a = dequant8_q8(q[rt][2 * t], q[rt][2 * t + 1], t < 4 ? d0[rt] : d1[rt], dq.q8);
+                        const F16x8Pair a = dequant8_q8(q[rt][2 * t], q[rt][2 * t + 1], t < 4 ? e0[rt] : e1[rt], dq.q8);
 #pragma unroll
                         for (int mt = 0; mt < MT; ++mt) {
                             acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.hi, xb[mt][s][t], acc[rt][mt], 0, 0, 0);
                             acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.lo, xb[mt][s][t], acc[rt][mt], 0, 0, 0);
                         }
                     } else {
-                        const f16x8 a = dequant8(q[rt][t], t < 4 ? d0[rt] : d1[rt], dq.c1024, dq.c64);
+                        const f16x8 a = dequant8(q[rt][t], t < 4 ? e0[rt] : e1[rt], dq.c1024, dq.c64);
 #pragma unroll
                         for (int mt = 0; mt < MT; ++mt)
                             acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xb[mt][s][t], acc[rt][mt], 0, 0, 0);
                     }
                 }
+            }
+            };
+            // A step with a scale past binary16 range runs with every scale
+            // times 2^-S and the accumulators scaled by 2^-S before and by 2^S
+            // after (common.hpp).
+            const bool big_step = wave_any(big);
+            if (__builtin_expect(big_step, 0)) {
+                const f16x2 dd = {static_cast<_Float16>(kDown), static_cast<_Float16>(kDown)};
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    d0[rt] = d0[rt] * dd;
+                    d1[rt] = d1[rt] * dd;
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc[rt][mt] *= kDown;
+                }
+            }
+            t_loop(d0, d1);
+            if (__builtin_expect(big_step, 0)) {
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc[rt][mt] *= 1.0f / kDown;
             }
         }
     };
@@ -573,15 +603,9 @@ hipError_t launch_skinny(const Problem& p) {
 #define MOTE_SKINNY(KS, STEPS, MT, D, G, RT)                                                     \
     Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d" #D "_g" #G "_r" #RT, Kind::SkinnyMfma, KS, \
             STEPS, MT, &launch_skinny<KS, STEPS, MT, D, G, RT>}
-#define MOTE_SKINNY_TRL(KS, STEPS, MT, G, L)                                                      \
-    Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d1_g" #G "_r1_tr_l" #L, Kind::SkinnyMfma, KS, \
-            STEPS, MT, &launch_skinny<KS, STEPS, MT, 1, G, 1, true, L>}
 #define MOTE_SKINNY_TRLC(KS, STEPS, MT, G, L)                                                    \
     Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d1_g" #G "_r1_tr_l" #L "_c", Kind::SkinnyMfma, \
             KS, STEPS, MT, &launch_skinny<KS, STEPS, MT, 1, G, 1, true, L, true>}
-#define MOTE_SKINNY_TRC(KS, STEPS, MT, D, G)                                                      \
-    Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d" #D "_g" #G "_r1_tr_c", Kind::SkinnyMfma, KS, \
-            STEPS, MT, &launch_skinny<KS, STEPS, MT, D, G, 1, true, 0, true>}
 #define MOTE_SKINNY_GU(KS, STEPS, MT, D, L, XC, SUFFIX)                                           \
     Variant{"gateup_skinny_k" #KS "_s" #STEPS "_t" #MT "_d" #D SUFFIX, Kind::GateUpSkinny, KS, STEPS, MT, \
             &launch_skinny<KS, STEPS, MT, D, 1, 2, true, L, XC, true>}
@@ -615,44 +639,27 @@ hipError_t launch_skinny(const Problem& p) {
     Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d" #D "_g" #G "_r1_tr", Kind::SkinnyMfma, KS, \
             STEPS, MT, &launch_skinny<KS, STEPS, MT, D, G, 1, true>}
 
+// The tiles the dispatch heuristic picks, the one-slice fallbacks for K =
+// 1024 and 2048, and three measured alternatives (one item per barrier, and
+// the deferred reduction with the weight loads issued before the
+// activations).
 const Variant kSkinny[] = {
-    MOTE_SKINNY(16, 1, 1, 1, 1, 1), MOTE_SKINNY(16, 1, 1, 2, 1, 1), MOTE_SKINNY(16, 1, 2, 1, 1, 1),
-    MOTE_SKINNY(16, 1, 2, 2, 1, 1), MOTE_SKINNY(16, 1, 1, 2, 2, 1), MOTE_SKINNY(16, 1, 1, 2, 1, 2),
-    MOTE_SKINNY(8, 2, 1, 1, 1, 1), MOTE_SKINNY(8, 2, 1, 2, 1, 1), MOTE_SKINNY(8, 2, 1, 2, 2, 1),
-    MOTE_SKINNY(8, 1, 1, 1, 1, 1), MOTE_SKINNY(8, 1, 2, 1, 1, 1), MOTE_SKINNY(8, 1, 1, 2, 1, 1),
-    MOTE_SKINNY(4, 2, 1, 1, 1, 1), MOTE_SKINNY(4, 1, 1, 1, 1, 1), MOTE_SKINNY(4, 1, 1, 2, 1, 1),
-    MOTE_SKINNY(16, 2, 1, 1, 1, 1),
-    MOTE_SKINNY_TR(4, 4, 1, 1, 1), MOTE_SKINNY_TR(4, 4, 1, 1, 2), MOTE_SKINNY_TR(4, 4, 1, 2, 1),
-    MOTE_SKINNY_TR(4, 4, 1, 2, 2), MOTE_SKINNY_TR(8, 2, 1, 1, 1), MOTE_SKINNY_TR(8, 2, 1, 1, 2),
-    MOTE_SKINNY_TR(8, 2, 2, 1, 1), MOTE_SKINNY_TR(8, 2, 2, 2, 1), MOTE_SKINNY_TR(4, 2, 1, 1, 1),
-    MOTE_SKINNY_TR(4, 2, 2, 1, 1),
-    MOTE_SKINNY_TRL(8, 2, 1, 1, 4), MOTE_SKINNY_TRL(8, 2, 1, 1, 8), MOTE_SKINNY_TRL(8, 2, 2, 1, 4),
-    MOTE_SKINNY_TRL(4, 4, 1, 1, 4), MOTE_SKINNY_TRL(8, 2, 1, 2, 4), MOTE_SKINNY_TRL(16, 1, 1, 1, 4),
-    MOTE_SKINNY_TRL(16, 1, 1, 1, 8),
-    MOTE_SKINNY_TRLC(16, 1, 1, 1, 4), MOTE_SKINNY_TRLC(16, 1, 1, 1, 8), MOTE_SKINNY_TRLC(8, 2, 1, 1, 4),
-    MOTE_SKINNY_TRLC(8, 2, 1, 1, 8), MOTE_SKINNY_TRLC(4, 4, 1, 1, 4), MOTE_SKINNY_TRC(8, 2, 2, 2, 1),
-    MOTE_SKINNY_TRC(16, 1, 2, 2, 1),
-    MOTE_SKINNY_GU(8, 2, 1, 1, 0, false, ""), MOTE_SKINNY_GU(16, 1, 1, 1, 4, false, "_l4"),
-    MOTE_SKINNY_GU(16, 1, 1, 1, 4, true, "_l4_c"), MOTE_SKINNY_GU(8, 2, 1, 1, 4, true, "_l4_c"),
-    MOTE_SKINNY_GU(8, 2, 1, 1, 8, false, "_l8"), MOTE_SKINNY_GU(8, 2, 1, 1, 8, true, "_l8_c"),
-    MOTE_SKINNY_GU(8, 2, 2, 1, 0, true, "_c"),
-    MOTE_SKINNY_Q8(8, 2, 1, 1, 0, false, ""), MOTE_SKINNY_Q8(16, 1, 1, 1, 4, false, "_l4"),
-    MOTE_SKINNY_Q8(16, 1, 1, 1, 4, true, "_l4_c"), MOTE_SKINNY_Q8(8, 2, 1, 1, 8, false, "_l8"),
-    MOTE_SKINNY_Q8(8, 2, 1, 1, 8, true, "_l8_c"), MOTE_SKINNY_Q8(16, 1, 2, 1, 0, true, "_c"), MOTE_SKINNY_Q8(8, 2, 2, 1, 0, true, "_c"),
-    MOTE_SKINNY_W(16, 1, 1, 4, false, ""), MOTE_SKINNY_W(16, 1, 1, 4, true, "_c"), MOTE_SKINNY_W(8, 2, 1, 8, true, "_c"),
-    MOTE_SKINNY_W(8, 2, 2, 4, true, "_c"), MOTE_SKINNY_W(8, 2, 2, 8, true, "_c"), MOTE_SKINNY_W(8, 2, 1, 4, true, "_c"),
-    MOTE_SKINNY_W(16, 1, 1, 8, true, "_c"),
+    MOTE_SKINNY(8, 1, 1, 1, 1, 1), MOTE_SKINNY(4, 1, 1, 1, 1, 1),
+    MOTE_SKINNY_TR(8, 2, 1, 1, 1), MOTE_SKINNY_TRLC(16, 1, 1, 1, 4), MOTE_SKINNY_TRLC(8, 2, 1, 1, 8),
+    MOTE_SKINNY_W(16, 1, 1, 4, true, "_c"), MOTE_SKINNY_W(8, 2, 1, 8, true, "_c"),
+    MOTE_SKINNY_W(8, 2, 2, 4, true, "_c"), MOTE_SKINNY_W(8, 2, 2, 8, true, "_c"),
+    MOTE_SKINNY_GU(8, 2, 1, 1, 0, false, ""), MOTE_SKINNY_GU(8, 2, 2, 1, 0, true, "_c"),
     MOTE_SKINNY_GU_W(16, 1, 1, 4, false, ""), MOTE_SKINNY_GU_W(16, 1, 1, 4, true, "_c"),
     MOTE_SKINNY_GU_W(8, 2, 1, 8, true, "_c"), MOTE_SKINNY_GU_W(8, 2, 2, 4, true, "_c"),
+    MOTE_SKINNY_Q8(16, 1, 2, 1, 0, true, "_c"),
     MOTE_SKINNY_Q8_W(16, 1, 1, 4, false, ""), MOTE_SKINNY_Q8_W(16, 1, 1, 4, true, "_c"),
-    MOTE_SKINNY_Q8_W(8, 2, 2, 4, true, "_c"), MOTE_SKINNY_Q8_W(8, 2, 1, 8, true, "_c"),
-    MOTE_SKINNY_SK(8, 1, 1, 8, "_c"), MOTE_SKINNY_SK(8, 1, 2, 8, "_c"), MOTE_SKINNY_SK(16, 1, 1, 4, "_c"),
-    MOTE_SKINNY_SK(16, 1, 1, 8, "_c"), MOTE_SKINNY_SK(8, 1, 1, 4, "_c"), MOTE_SKINNY_SK(16, 1, 2, 4, "_c"),
-    MOTE_SKINNY_SK(8, 2, 1, 8, "_c"), MOTE_SKINNY_SK(8, 2, 2, 8, "_c"),
-    MOTE_SKINNY_Q8_SK(8, 1, 1, 8, "_c"), MOTE_SKINNY_Q8_SK(8, 1, 2, 8, "_c"), MOTE_SKINNY_Q8_SK(16, 1, 1, 4, "_c"),
-    MOTE_SKINNY_SK(8, 1, 2, 4, "_c"), MOTE_SKINNY_Q8_SK(8, 1, 1, 4, "_c"), MOTE_SKINNY_Q8_SK(8, 1, 2, 4, "_c"),
-    MOTE_SKINNY_GU_SK(8, 1, 1, 4, "_c"), MOTE_SKINNY_GU_SK(8, 1, 1, 8, "_c"), MOTE_SKINNY_GU_SK(16, 1, 1, 4, "_c"),
-    MOTE_SKINNY_GU_SK(8, 1, 2, 4, "_c"), MOTE_SKINNY_GU_SK(8, 1, 2, 8, "_c"),
+    MOTE_SKINNY_Q8_W(8, 2, 1, 8, true, "_c"), MOTE_SKINNY_Q8_W(8, 2, 2, 4, true, "_c"),
+    // split K, parts of 2048 or 4096
+    MOTE_SKINNY_SK(8, 1, 1, 4, "_c"), MOTE_SKINNY_SK(8, 1, 1, 8, "_c"), MOTE_SKINNY_SK(8, 1, 2, 4, "_c"),
+    MOTE_SKINNY_SK(8, 1, 2, 8, "_c"), MOTE_SKINNY_SK(16, 1, 1, 4, "_c"), MOTE_SKINNY_SK(8, 2, 1, 8, "_c"),
+    MOTE_SKINNY_SK(8, 2, 2, 8, "_c"),
+    MOTE_SKINNY_Q8_SK(8, 1, 1, 4, "_c"), MOTE_SKINNY_Q8_SK(8, 1, 1, 8, "_c"), MOTE_SKINNY_Q8_SK(8, 1, 2, 8, "_c"),
+    MOTE_SKINNY_GU_SK(8, 1, 1, 4, "_c"), MOTE_SKINNY_GU_SK(8, 1, 1, 8, "_c"), MOTE_SKINNY_GU_SK(8, 1, 2, 8, "_c"),
     // parts of 1024 for K a multiple of 1024 only (2048 for the gate/up)
     MOTE_SKINNY_SK(4, 1, 1, 8, "_c"), MOTE_SKINNY_SK(4, 1, 2, 8, "_c"), MOTE_SKINNY_GU_SK(4, 1, 1, 8, "_c"),
     MOTE_SKINNY_GU_SK(4, 1, 2, 8, "_c"), MOTE_SKINNY_Q8_SK(4, 1, 1, 8, "_c"), MOTE_SKINNY_Q8_SK(4, 1, 2, 8, "_c"),
@@ -660,9 +667,7 @@ const Variant kSkinny[] = {
 
 #undef MOTE_SKINNY
 #undef MOTE_SKINNY_TR
-#undef MOTE_SKINNY_TRL
 #undef MOTE_SKINNY_TRLC
-#undef MOTE_SKINNY_TRC
 #undef MOTE_SKINNY_GU
 #undef MOTE_SKINNY_Q8
 #undef MOTE_SKINNY_W

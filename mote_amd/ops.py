@@ -132,6 +132,14 @@ class Q4_0Dispatch:
         status = lib().mote_q4_0_dispatch_plan(self.handle, rows, n, k, op, int(f16_out), buf, 64)
         return buf.value.decode() if status == 0 else None
 
+    def select(self, rows, n, k, gate_up: bool = False, q8_0: bool = False) -> str:
+        """The variant a call of this shape would plan (aligned operands),
+        chosen on the host without launching anything."""
+        buf = ctypes.create_string_buffer(64)
+        op = 2 if q8_0 else int(gate_up)
+        self._check(lib().mote_q4_0_dispatch_select(self.handle, rows, n, k, op, buf, 64), "select Q4_0 variant")
+        return buf.value.decode()
+
     def close(self) -> None:
         if self.handle:
             lib().mote_q4_0_dispatch_destroy(self.handle)

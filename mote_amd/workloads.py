@@ -97,6 +97,31 @@ def q8_0_weights(seed: int, rows: int, cols: int, std: float = 0.02) -> np.ndarr
     return out.reshape(-1)
 
 
+def reference_bench_q4_0_weights(rows: int, cols: int) -> np.ndarray:
+    """The closed-form Q4_0 matrix of the reference's own benchmark
+    (crates/mote-backend-hip/benches/quantized_linear.rs:134-152): block b of
+    row o has scale f16(2^-6 ((3 o + b) % 4 + 1)), and byte j of it the low
+    nibble (5 o + 3 b + j) % 16 and the high nibble (7 o + b + 3 j + 1) % 16."""
+    blocks = cols // Q4_0_BLOCK_ELEMENTS
+    o = np.arange(rows)[:, None]
+    b = np.arange(blocks)[None, :]
+    scale = (0.015625 * (((o * 3 + b) % 4) + 1)).astype(np.float16).view(np.uint16)
+    out = np.empty((rows, blocks, Q4_0_BLOCK_BYTES), dtype=np.uint8)
+    out[:, :, 0:2] = scale.astype("<u2").view(np.uint8).reshape(rows, blocks, 2)
+    j = np.arange(16)[None, None, :]
+    low = (o[:, :, None] * 5 + b[:, :, None] * 3 + j) % 16
+    high = (o[:, :, None] * 7 + b[:, :, None] + j * 3 + 1) % 16
+    out[:, :, 2:] = (low | (high << 4)).astype(np.uint8)
+    return out.reshape(-1)
+
+
+def reference_bench_inputs(rows: int, cols: int) -> np.ndarray:
+    """The reference benchmark's f16 activations, element i = f16((i % 29) /
+    14 - 1) (crates/mote-backend-hip/benches/quantized_linear.rs:128-132)."""
+    i = np.arange(rows * cols)
+    return ((i % 29).astype(np.float32) / 14.0 - 1.0).astype(np.float16).view(np.uint16)
+
+
 def positions(seed: int, count: int, high: int = 8191) -> np.ndarray:
     """Uniform integers in ``[0, high]`` by rejection sampling on 13-bit draws."""
     bits = int(high).bit_length()

@@ -47,24 +47,18 @@ def ref_test_q4_0_inputs(rows: int, k: int) -> np.ndarray:
 
 
 def ref_bench_q4_0_weights(n: int, k: int) -> np.ndarray:
-    """crates/mote-backend-hip/benches/quantized_linear.rs:134-152 (vectorised)."""
-    blocks = k // 32
-    o = np.arange(n)[:, None]
-    b = np.arange(blocks)[None, :]
-    scale = f16_bits(0.015625 * (((o * 3 + b) % 4) + 1).astype(np.float32))
-    out = np.empty((n, blocks, BLOCK_BYTES), dtype=np.uint8)
-    out[:, :, 0:2] = scale.astype("<u2").view(np.uint8).reshape(n, blocks, 2)
-    j = np.arange(16)[None, None, :]
-    low = (o[:, :, None] * 5 + b[:, :, None] * 3 + j) % 16
-    high = (o[:, :, None] * 7 + b[:, :, None] + j * 3 + 1) % 16
-    out[:, :, 2:] = (low | (high << 4)).astype(np.uint8)
-    return out.reshape(-1)
+    """crates/mote-backend-hip/benches/quantized_linear.rs:134-152 (the
+    generator the benchmark shares, mote_amd.workloads)."""
+    from mote_amd.workloads import reference_bench_q4_0_weights
+
+    return reference_bench_q4_0_weights(n, k)
 
 
 def ref_bench_q4_0_inputs(rows: int, k: int) -> np.ndarray:
     """crates/mote-backend-hip/benches/quantized_linear.rs:128-132."""
-    i = np.arange(rows * k)
-    return f16_bits((i % 29).astype(np.float32) / 14.0 - 1.0)
+    from mote_amd.workloads import reference_bench_inputs
+
+    return reference_bench_inputs(rows, k)
 
 
 def ref_norm_input(count: int) -> np.ndarray:
@@ -121,3 +115,88 @@ def assert_linear_close(y, y64, k, max_d, max_x, extra_rel: float = 0.0, what: s
         idx = np.argwhere(bad)[:5]
         details = ", ".join(f"{tuple(i)}: got {y[tuple(i)]!r} want {y64[tuple(i)]!r}" for i in idx)
         raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} elements out of tolerance; {details}")
+
+
+# --- weights whose scales span the binary16 range ------------------------------
+
+def wide_scale_bits(rng: np.random.Generator, count: int, mode: str, big_limit: int) -> np.ndarray:
+    """`count` binary16 scale patterns, both signs:
+    * "full": magnitude field uniform over every finite pattern (subnormals
+      from 2^-24 up to 65504);
+    * "big": every magnitude from `big_limit` (the first binary16 whose
+      products can overflow) up to 65504;
+    * "subnormal": nonzero subnormals only;
+    * "special": "full" with one pattern in 64 replaced by +inf, -inf or NaN."""
+    sign = (rng.integers(0, 2, count) << 15).astype(np.uint32)
+    if mode in ("full", "special"):
+        mag = rng.integers(1, 0x7C00, count)
+    elif mode == "big":
+        mag = rng.integers(big_limit, 0x7C00, count)
+    elif mode == "subnormal":
+        mag = rng.integers(1, 0x0400, count)
+    else:
+        raise ValueError(mode)
+    bits = (sign | mag.astype(np.uint32)).astype(np.uint16)
+    if mode == "special":
+        idx = rng.choice(count, size=max(1, count // 64), replace=False)
+        bits[idx] = rng.choice(np.array([0x7C00, 0xFC00, 0x7E00], dtype=np.uint16), size=idx.size)
+    return bits
+
+
+def wide_q4_0_weights(seed: int, n: int, k: int, mode: str) -> np.ndarray:
+    """Q4_0 [n, k] with uniform nibbles and scales from wide_scale_bits
+    (products overflow binary16 from |d| = 8192, pattern 0x7000)."""
+    rng = np.random.default_rng(seed)
+    blocks = n * (k // 32)
+    out = np.empty((blocks, 18), dtype=np.uint8)
+    out[:, 0:2] = wide_scale_bits(rng, blocks, mode, 0x7000).astype("<u2").view(np.uint8).reshape(blocks, 2)
+    out[:, 2:] = rng.integers(0, 256, (blocks, 16), dtype=np.uint8)
+    return out.reshape(-1)
+
+
+def wide_q8_0_weights(seed: int, n: int, k: int, mode: str) -> np.ndarray:
+    """Q8_0 [n, k] with uniform bytes and scales from wide_scale_bits
+    (products overflow binary16 from |d| = 512, pattern 0x6000)."""
+    rng = np.random.default_rng(seed)
+    blocks = n * (k // 32)
+    out = np.empty((blocks, 34), dtype=np.uint8)
+    out[:, 0:2] = wide_scale_bits(rng, blocks, mode, 0x6000).astype("<u2").view(np.uint8).reshape(blocks, 2)
+    out[:, 2:] = rng.integers(0, 256, (blocks, 32), dtype=np.uint8)
+    return out.reshape(-1)
+
+
+def block_scales(w: np.ndarray, n: int, k: int, block_bytes: int = BLOCK_BYTES) -> np.ndarray:
+    """The f32 value of every block's scale, [n, k / 32]."""
+    blocks = w.reshape(n, k // 32, block_bytes)
+    return bits_to_f32(blocks[:, :, 0:2].copy().view("<u2")[..., 0])
+
+
+# --- full-output f64 judge ---------------------------------------------------------
+
+_DECODED: dict = {}
+
+
+def decoded_f64(oracle, w: np.ndarray, n: int, k: int, fmt: int) -> np.ndarray:
+    """The weights decoded by the oracle's block decoder (bit-exact, pinned by
+    its own tests) as float64 [n, k].  The matrix is one run of whole blocks,
+    so it decodes as one long row.  A few matrices are kept for reuse."""
+    key = (w.ctypes.data, w.nbytes, n, k, fmt)
+    hit = _DECODED.get(key)
+    if hit is not None and hit[0] is w:  # the entry holds `w`, so its address cannot be reused
+        return hit[1]
+    if len(_DECODED) >= 4:
+        _DECODED.pop(next(iter(_DECODED)))
+    decoded = oracle.dequantize_row(w, fmt, n * k).astype(np.float64).reshape(n, k)
+    _DECODED[key] = (w, decoded)
+    return decoded
+
+
+def linear_f64_full(oracle, x_bits: np.ndarray, w: np.ndarray, m: int, n: int, k: int, fmt: int) -> np.ndarray:
+    """Every output of the linear in float64: the f16 activations times the
+    oracle-decoded weights (each product exact in binary64), summed by the
+    host BLAS, whose rounding (about K 2^-53 of the absolute sum) is many
+    orders below the parity tolerance.  A CPU test holds it to the oracle's
+    own f64 linear."""
+    x64 = bits_to_f32(x_bits).astype(np.float64).reshape(m, k)
+    with np.errstate(invalid="ignore", over="ignore"):  # inf and NaN scales give NaN, as in the oracle
+        return x64 @ decoded_f64(oracle, w, n, k, fmt).T

@@ -1,0 +1,92 @@
+"""CPU tests of the dispatch heuristic (host logic, no device): the variant
+each configuration of the path plans, through mote_q4_0_dispatch_select,
+which runs the same heuristic as a call without launching.
+
+Every selected name must be a compiled variant; the decode, skinny, split-K,
+prefill, Q8_0 and fused gate/up shapes land on the kernels the measurements
+chose, including three tokens past K = 4096 (rows split over 2 or 4 waves up
+to K = 16384, the split-K tiles beyond)."""
+
+from __future__ import annotations
+
+import pytest
+
+from mote_amd import HipError, ops
+
+
+@pytest.fixture(scope="module")
+def d():
+    ctx = ops.Q4_0Dispatch()
+    yield ctx
+    ctx.close()
+
+
+LINEAR = [
+    # (M, K, N) -> variant
+    ((1, 4096, 14336), "stream_d1_g2"),
+    ((1, 4096, 4096), "stream_d1q_g1"),
+    ((1, 14336, 4096), "stream_s4_d1q_g2"),
+    ((1, 11008, 4096), "stream_s4_d1q_g2"),
+    ((1, 4096, 11008), "stream_d1_g2"),
+    ((1, 28672, 8192), "stream_s8_d1_g2"),
+    ((2, 4096, 14336), "stream_m2_d1q_g1"),
+    ((2, 14336, 4096), "stream_s4_m2_d1q_g1"),
+    ((3, 8192, 8192), "stream_s2_m3_d1q_g1"),
+    ((3, 14336, 4096), "stream_s4_m3_d1q_g1"),
+    ((4, 4096, 4096), "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w"),
+    ((16, 4096, 14336), "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w"),
+    ((24, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l4_c_w"),
+    ((32, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l4_c_w"),
+    ((64, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l8_c_w"),
+    ((256, 4096, 14336), "mfma_x32s_m128_n128_w1"),
+    ((512, 4096, 14336), "mfma_x32s_m128_n256_w1"),
+]
+
+
+@pytest.mark.parametrize("shape,want", LINEAR, ids=[f"{m}x{k}x{n}" for (m, k, n), _ in LINEAR])
+def test_linear_plans(d, shape, want):
+    m, k, n = shape
+    assert d.select(m, n, k) == want
+
+
+def test_every_selection_is_a_compiled_variant(d):
+    names = set(ops.variant_names())
+    for m in (1, 2, 3, 4, 5, 8, 16, 17, 24, 32, 33, 48, 64, 65, 128, 256, 512):
+        for k in (64, 1024, 2048, 3072, 4096, 5120, 8192, 11008, 14336, 28672):
+            for n in (7, 4096, 14336):
+                assert d.select(m, n, k) in names, (m, k, n)
+                assert d.select(m, n, k, q8_0=True) in names, (m, k, n)
+                assert d.select(m, n, k, gate_up=True) in names, (m, k, n)
+
+
+def test_three_tokens_past_4096(d):
+    """Linear, Q8_0 and gate/up: rows split over 2 / 4 waves for 4096 < K <=
+    16384; beyond that the split-K tiles (no 8-way three-token form)."""
+    assert d.select(3, 8192, 8192, q8_0=True) == "q8_stream_s2_m3_d1q_g1"
+    assert d.select(3, 4096, 14336, q8_0=True) == "q8_stream_s4_m3_d1q_g1"
+    assert d.select(3, 28672, 8192, gate_up=True) == "gateup_stream_s2_m3_d1q_g1"
+    assert d.select(3, 4096, 14336, gate_up=True) == "gateup_stream_s4_m3_d1q_g1"
+    assert d.select(3, 8192, 28672).endswith("_sk")
+    assert d.select(3, 8192, 28672, q8_0=True).endswith("_sk")
+    assert d.select(3, 8192, 28672, gate_up=True).endswith("_sk")
+
+
+def test_gate_up_and_q8_plans(d):
+    assert d.select(1, 14336, 4096, gate_up=True) == "gateup_stream_p1_d1_g1"
+    assert d.select(2, 14336, 4096, gate_up=True) == "gateup_stream_p1_m2_d1q_g1"
+    assert d.select(16, 14336, 4096, gate_up=True).startswith("gateup_skinny_")
+    assert d.select(256, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m128_n128_w1"
+    assert d.select(1, 14336, 4096, q8_0=True) == "q8_stream_d1_g1"
+    assert d.select(16, 14336, 4096, q8_0=True).startswith("q8_skinny_")
+    assert d.select(512, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m128_n256_w1"
+
+
+def test_forced_variant_and_bad_shapes(d):
+    d.force("stream_d1q_g1")
+    try:
+        assert d.select(7, 100, 64) == "stream_d1q_g1"
+    finally:
+        d.force(None)
+    for shape in [(0, 1, 32), (1, 0, 32), (1, 1, 0), (1, 1, 33)]:
+        with pytest.raises(HipError):
+            d.select(*shape)

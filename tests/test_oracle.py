@@ -361,3 +361,24 @@ def test_regression_vectors(oracle):
         assert hashlib.sha256(w.tobytes()).hexdigest() == case["w_sha256"]
         y = oracle.quantized_linear_f32(bits_to_f32(x), w, oracle.Q4_0, m, n, k)
         assert y.view(np.uint32).tolist() == case["y_f32_bits"]
+
+
+@pytest.mark.parametrize("mode", ["full", "big", "subnormal", "special"])
+def test_full_output_judge_matches_the_f64_linear(oracle, mode):
+    """The BLAS float64 judge of the full-size GPU checks (oracle-decoded
+    weights times the f16 activations) equals the oracle's sequential f64
+    linear to 1e-13 of the absolute sum, on weights whose scales span the
+    whole binary16 range; NaN where the oracle has NaN."""
+    from helpers import linear_f64_full, wide_q4_0_weights, wide_q8_0_weights
+
+    m, n, k = 3, 19, 512
+    x = f16_bits(np.random.default_rng(3).standard_normal(m * k))
+    for fmt, gen in ((oracle.Q4_0, wide_q4_0_weights), (oracle.Q8_0, wide_q8_0_weights)):
+        w = gen(11, n, k, mode)
+        got = linear_f64_full(oracle, x, w, m, n, k, fmt)
+        want = oracle.quantized_linear_f64(bits_to_f32(x), w, m, n, k, fmt=fmt).reshape(m, n)
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        fin = ~np.isnan(want)
+        absum = np.abs(bits_to_f32(x).astype(np.float64).reshape(m, k)) @ np.abs(
+            oracle.dequantize_row(w, fmt, n * k).astype(np.float64).reshape(n, k)).T
+        assert np.all(np.abs(got[fin] - want[fin]) <= 1e-13 * absum[fin])

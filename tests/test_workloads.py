@@ -44,3 +44,22 @@ def test_positions_and_tables():
     c, s = wl.rope_tables(np.array([0, 3]), 8, 500000.0)
     assert c.shape == (2, 4) and np.all(c[0] == 1) and np.all(s[0] == 0)
     assert c[1, 0] == np.float32(np.cos(3.0))
+
+
+def test_reference_bench_generators_follow_the_reference_loops():
+    """The vectorised generators equal a direct transcription of the reference
+    benchmark's loops (crates/mote-backend-hip/benches/quantized_linear.rs:
+    128-152) on a small matrix, including the first block's known bytes."""
+    n, k = 7, 96
+    want = bytearray()
+    for o in range(n):
+        for b in range(k // 32):
+            scale = np.float16(0.015625 * ((o * 3 + b) % 4 + 1)).view(np.uint16)
+            want += int(scale).to_bytes(2, "little")
+            for j in range(16):
+                want.append(((o * 5 + b * 3 + j) % 16) | (((o * 7 + b + j * 3 + 1) % 16) << 4))
+    got = wl.reference_bench_q4_0_weights(n, k)
+    assert bytes(got) == bytes(want)
+    assert bytes(got[:3]) == b"\x00\x24\x10"  # f16(1/64) = 0x2400, byte 0: low 0, high 1
+    x = wl.reference_bench_inputs(2, 40)
+    assert np.array_equal(x, np.array([np.float16(i % 29 / 14.0 - 1.0) for i in range(80)]).view(np.uint16))
