@@ -56,6 +56,21 @@ int mote_hip_quantized_linear_q4_0_f32(const void* input, const void* weights, v
                                        uint64_t rows, uint64_t output_features,
                                        uint64_t input_features, void* stream);
 
+/* [new] No counterpart in the reference.  mote_hip_quantized_linear_q4_0_f32
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops or harnesses that forbid hipMalloc): the same
+ * arguments, checks, statuses, plans and kernels, but the split-K partial
+ * tiles (1-64 tokens where K exceeds one K slice) go to the library's static
+ * 16 MiB device array instead of a per-stream buffer the library allocates;
+ * nothing is allocated on any call.  Every call on one GPU shares that
+ * array, and it keeps the last call's contents: calls that overlap in time on
+ * one GPU (several streams or threads) race.  A problem whose partial tiles
+ * need more than 16 MiB (M x N x K-parts x 4 bytes) returns 2
+ * (hipErrorOutOfMemory) before any launch. */
+int mote_hip_quantized_linear_q4_0_f32_no_alloc(const void* input, const void* weights, void* output,
+                                                uint64_t rows, uint64_t output_features,
+                                                uint64_t input_features, void* stream);
+
 /* [new] Fused gate/up projection: output[rows, N] (f32) =
  * silu(input . gate^T) * (input . up^T), silu(z) = z / (1 + e^-z); gate and up
  * are Q4_0 [N, K].  up_weights == NULL means gate_weights is the concatenated

@@ -48,6 +48,7 @@ SIGNATURES = {
     "mote_hip_mem_get_info": (_I, [ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
     "mote_hip_quantized_linear_q4_0_f16": (_I, [_P, _P, _P, _U64, _U64, _U64, _P]),
     "mote_hip_quantized_linear_q4_0_f32": (_I, [_P, _P, _P, _U64, _U64, _U64, _P]),
+    "mote_hip_quantized_linear_q4_0_f32_no_alloc": (_I, [_P, _P, _P, _U64, _U64, _U64, _P]),
     "mote_hip_quantized_linear_q8_0_f16": (_I, [_P, _P, _P, _U64, _U64, _U64, _P]),
     "mote_hip_quantized_linear_q8_0_f32": (_I, [_P, _P, _P, _U64, _U64, _U64, _P]),
     "mote_hip_q4_0_gate_up_silu_f32": (_I, [_P, _P, _P, _P, _U64, _U64, _U64, _P]),

@@ -20,6 +20,10 @@ struct Problem {
     uint32_t M, N, K;
     OutType out;
     hipStream_t stream;
+    // Caller-provided split-K scratch (device memory of scratch_bytes); null:
+    // the stream's buffer from the library's scratch pool.
+    float* scratch = nullptr;
+    size_t scratch_bytes = 0;
 };
 
 enum class Kind : int { Gemv = 0, Mfma = 1, Generic = 2, GateUpMfma = 3, GateUpGeneric = 4, GemvRows = 5,

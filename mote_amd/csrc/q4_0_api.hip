@@ -532,6 +532,28 @@ int run(Dispatcher& d, const Problem& p, Op op) {
     return 0;
 }
 
+// The launch of the entry point that allocates nothing: the cached plan, or
+// on the first call of a shape the shape heuristic (never the autotuner,
+// which would create events and synchronise), then the launch.
+int run_no_alloc(Dispatcher& d, const Problem& p) {
+    std::lock_guard<std::mutex> lock(d.mutex);
+    const Variant* v = nullptr;
+    if (!d.forced.empty()) {
+        v = find_variant(d.forced);
+        if (!v || !kind_matches(*v, Op::Linear) || !supports(*v, p)) return hipErrorInvalidValue;
+    } else {
+        const Key key{p.M, p.N, p.K, static_cast<int>(Op::Linear), static_cast<int>(p.out), fast_eligible(p) ? 1 : 0};
+        auto found = d.plans.find(key);
+        if (found == d.plans.end()) {
+            const Variant* chosen = heuristic(p, Op::Linear);
+            if (!chosen) return hipErrorInvalidValue;
+            found = d.plans.emplace(key, chosen).first;
+        }
+        v = found->second;
+    }
+    return static_cast<int>(v->launch(p));
+}
+
 Dispatcher& default_dispatcher() {
     static Dispatcher* d = [] {
         auto* x = new Dispatcher();
@@ -612,6 +634,39 @@ hipError_t release_stream_scratch(hipStream_t stream) {
 
 using namespace mote::q4_0;
 
+namespace {
+
+// Split-K scratch of mote_hip_quantized_linear_q4_0_f32_no_alloc: a
+// file-scope device array, so the entry point never allocates.  Every GPU
+// that loads the library holds its own copy until the process ends.  In host
+// code the name `scratch` is only a stand-in for the symbol, not a device
+// address: the address each device's copy has is fetched once per device
+// with hipGetSymbolAddress and only that address is passed to kernels.
+constexpr size_t kNoAllocScratchBytes = size_t{16} << 20;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+// The current device's address of `scratch`, fetched on the first call on
+// that device (with the device current) and kept.
+hipError_t no_alloc_scratch(void** ptr) {
+    static std::mutex mu;
+    static void* addresses[64] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (addresses[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        addresses[dev] = p;
+    }
+    *ptr = addresses[dev];
+    return hipSuccess;
+}
+
+}  // namespace
+
 MOTE_EXPORT int mote_hip_quantized_linear_q4_0_f16(const void* input, const void* weights,
                                                   void* output, uint64_t rows,
                                                   uint64_t output_features,
@@ -631,6 +686,35 @@ MOTE_EXPORT int mote_hip_quantized_linear_q4_0_f32(const void* input, const void
     try {
         return linear(nullptr, input, weights, output, rows, output_features, input_features,
                       OutType::F32, stream);
+    } catch (...) {
+        return hipErrorUnknown;
+    }
+}
+
+// mote_hip_quantized_linear_q4_0_f32 for callers that cannot allocate (code
+// under graph capture, serving loops that forbid hipMalloc): the same
+// checks, plans and kernels, with the split-K partial tiles in the library's
+// static 16 MiB device array instead of the per-stream pool.  Calls on one
+// GPU share that array, so calls that overlap in time on one GPU (other
+// streams, other threads) race; a problem whose partial tiles exceed it
+// returns hipErrorOutOfMemory (2) before any launch.
+MOTE_EXPORT int mote_hip_quantized_linear_q4_0_f32_no_alloc(const void* input, const void* weights,
+                                                           void* output, uint64_t rows,
+                                                           uint64_t output_features,
+                                                           uint64_t input_features, void* stream) noexcept {
+    try {
+        const int pre = check_linear(input, weights, output, rows, output_features, input_features, stream);
+        if (pre >= 0) return pre;
+        const auto s = static_cast<hipStream_t>(stream);
+        if (input_features == 0) return static_cast<int>(launch_zero_fill(output, rows * output_features, OutType::F32, s));
+        void* buf = nullptr;
+        const hipError_t e = no_alloc_scratch(&buf);
+        if (e != hipSuccess) return static_cast<int>(e);
+        Problem p{input, weights, nullptr, output, static_cast<uint32_t>(rows), static_cast<uint32_t>(output_features),
+                  static_cast<uint32_t>(input_features), OutType::F32, s};
+        p.scratch = static_cast<float*>(buf);
+        p.scratch_bytes = kNoAllocScratchBytes;
+        return run_no_alloc(default_dispatcher(), p);
     } catch (...) {
         return hipErrorUnknown;
     }

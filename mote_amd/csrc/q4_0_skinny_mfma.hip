@@ -570,9 +570,15 @@ hipError_t launch_skinny(const Problem& p) {
     // (the lease goes out of scope at return).
     ScratchPool::Lease lease;
     if constexpr (SK) {
-        const hipError_t e = acquire_scratch(p.stream, count * kparts * (GU ? 2 : 1) * sizeof(float), &lease);
-        if (e != hipSuccess) return e;
-        part = static_cast<float*>(lease.ptr());
+        const size_t need = count * kparts * (GU ? 2 : 1) * sizeof(float);
+        if (p.scratch != nullptr) {  // the caller's buffer: too small is an error, before any launch
+            if (need > p.scratch_bytes) return hipErrorOutOfMemory;
+            part = p.scratch;
+        } else {
+            const hipError_t e = acquire_scratch(p.stream, need, &lease);
+            if (e != hipSuccess) return e;
+            part = static_cast<float*>(lease.ptr());
+        }
     }
     if (p.out == OutType::F32) {
         hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float, LAZY, XC, GU, Q8, XW, SK>), grid,

@@ -24,6 +24,13 @@ def quantized_linear_q4_0_f32(x, w, y, rows, n, k, stream) -> None:
     check(lib().mote_hip_quantized_linear_q4_0_f32(x, w, y, rows, n, k, _s(stream)), "launch Q4_0 linear kernel")
 
 
+def quantized_linear_q4_0_f32_no_alloc(x, w, y, rows, n, k, stream) -> None:
+    """The f32 linear without any device allocation (split-K scratch in the
+    library's static device array; overlapping calls on one GPU race)."""
+    check(lib().mote_hip_quantized_linear_q4_0_f32_no_alloc(x, w, y, rows, n, k, _s(stream)),
+          "launch Q4_0 linear kernel (no allocation)")
+
+
 def quantized_linear_q8_0_f16(x, w, y, rows, n, k, stream) -> None:
     check(lib().mote_hip_quantized_linear_q8_0_f16(x, w, y, rows, n, k, _s(stream)), "launch Q8_0 linear kernel")
 
