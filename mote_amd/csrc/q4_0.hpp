@@ -28,7 +28,7 @@ struct Problem {
 
 enum class Kind : int { Gemv = 0, Mfma = 1, Generic = 2, GateUpMfma = 3, GateUpGeneric = 4, GemvRows = 5,
                         GemvStream = 6, SkinnyMfma = 7, Q8Stream = 8, Q8Generic = 9, GateUpSkinny = 10,
-                        GateUpStream = 11, Q8Skinny = 12, Q8Prefill = 13 };
+                        GateUpStream = 11, Q8Skinny = 12, Q8Prefill = 13, GemvLds = 14 };
 
 struct Variant {
     const char* name;
@@ -42,6 +42,7 @@ struct Variant {
 const Variant* gemv_variants(int* count);
 const Variant* gemv_rows_variants(int* count);
 const Variant* gemv_stream_variants(int* count);
+const Variant* gemv_lds_variants(int* count);
 const Variant* skinny_mfma_variants(int* count);
 const Variant* prefill_variants(int* count);
 const Variant* generic_variants(int* count);
@@ -50,6 +51,7 @@ const Variant* generic_variants(int* count);
 bool gemv_supports(const Variant& v, const Problem& p);
 bool gemv_rows_supports(const Variant& v, const Problem& p);
 bool gemv_stream_supports(const Variant& v, const Problem& p);
+bool gemv_lds_supports(const Variant& v, const Problem& p);
 bool skinny_mfma_supports(const Variant& v, const Problem& p);
 bool prefill_supports(const Variant& v, const Problem& p);
 

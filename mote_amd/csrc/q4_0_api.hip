@@ -54,8 +54,8 @@ struct Dispatcher {
 std::vector<const Variant*> all_variants() {
     std::vector<const Variant*> out;
     int count = 0;
-    for (auto table : {gemv_stream_variants, gemv_rows_variants, gemv_variants, skinny_mfma_variants,
-                       prefill_variants, generic_variants}) {
+    for (auto table : {gemv_lds_variants, gemv_stream_variants, gemv_rows_variants, gemv_variants,
+                       skinny_mfma_variants, prefill_variants, generic_variants}) {
         const Variant* v = table(&count);
         for (int i = 0; i < count; ++i) out.push_back(&v[i]);
     }
@@ -76,13 +76,14 @@ bool kind_matches(const Variant& v, Op op) {
         return v.kind == Kind::Q8Stream || v.kind == Kind::Q8Skinny || v.kind == Kind::Q8Prefill ||
                v.kind == Kind::Q8Generic;
     return v.kind == Kind::Gemv || v.kind == Kind::GemvRows || v.kind == Kind::GemvStream ||
-           v.kind == Kind::SkinnyMfma || v.kind == Kind::Mfma || v.kind == Kind::Generic;
+           v.kind == Kind::GemvLds || v.kind == Kind::SkinnyMfma || v.kind == Kind::Mfma || v.kind == Kind::Generic;
 }
 
 bool supports(const Variant& v, const Problem& p) {
     switch (v.kind) {
         case Kind::Gemv: return gemv_supports(v, p);
         case Kind::GemvRows: return gemv_rows_supports(v, p);
+        case Kind::GemvLds: return gemv_lds_supports(v, p);
         case Kind::GemvStream:
         case Kind::GateUpStream:
         case Kind::Q8Stream: return gemv_stream_supports(v, p);
@@ -110,7 +111,7 @@ std::vector<const Variant*> candidates(const Problem& p, Op op) {
         if (!kind_matches(*v, op) || !supports(*v, p)) continue;
         const bool generic = v->kind == Kind::Generic || v->kind == Kind::GateUpGeneric;
         if (generic && fast_eligible(p)) continue;
-        const bool vector_alu = v->kind == Kind::Gemv || v->kind == Kind::GemvRows ||
+        const bool vector_alu = v->kind == Kind::Gemv || v->kind == Kind::GemvRows || v->kind == Kind::GemvLds ||
                                 v->kind == Kind::GemvStream || v->kind == Kind::Q8Stream ||
                                 v->kind == Kind::GateUpStream;
         if (vector_alu && p.M >= 64) continue;
@@ -407,6 +408,16 @@ const Variant* heuristic(const Problem& p, Op op) {
         return best;
     }
     if (p.M == 1) {
+        // K a multiple of 256 up to 4096: rows through the per-wave LDS ring
+        // with coalesced non-temporal loads (q4_0_gemv_lds.hip), two rows in
+        // flight from three rows per wave, one below (measured on MI355X at K
+        // = 4096: N = 14336 7.27 us, 6144 4.62 us, 4096 3.90 us, 1024 3.12 us,
+        // against 7.62, 5.14, 4.22 and 3.51 us for the pair-load GEMV).
+        {
+            const uint64_t rows_per_wave = p.N / (static_cast<uint64_t>(device_cus()) * 8u);
+            const Variant* v = by_name(rows_per_wave >= 3 ? "rowlds_r3d2" : "rowlds_r2d1");
+            if (v && gemv_lds_supports(*v, p)) return v;
+        }
         // Measured on MI355X (graph replays, weights rotated past the MALL):
         // the persistent pipelined GEMV, with rows split over S waves for
         // K > 4096 (4096 x 14336: 7.3 us; 14336 x 4096: 8.0 us, against

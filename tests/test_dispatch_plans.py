@@ -23,11 +23,14 @@ def d():
 
 LINEAR = [
     # (M, K, N) -> variant
-    ((1, 4096, 14336), "stream_d1_g2"),
-    ((1, 4096, 4096), "stream_d1q_g1"),
+    ((1, 4096, 14336), "rowlds_r3d2"),
+    ((1, 4096, 4096), "rowlds_r2d1"),
+    ((1, 4096, 6144), "rowlds_r3d2"),
+    ((1, 1024, 4096), "rowlds_r2d1"),
+    ((1, 4160, 4096), "stream_s2_d1_g2"),
     ((1, 14336, 4096), "stream_s4_d1q_g2"),
     ((1, 11008, 4096), "stream_s4_d1q_g2"),
-    ((1, 4096, 11008), "stream_d1_g2"),
+    ((1, 4096, 11008), "rowlds_r3d2"),
     ((1, 28672, 8192), "stream_s8_d1_g2"),
     ((2, 4096, 14336), "stream_m2_d1q_g1"),
     ((2, 14336, 4096), "stream_s4_m2_d1q_g1"),
