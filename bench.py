@@ -462,7 +462,7 @@ def run_read_floor(sizes=READ_FLOOR_BYTES) -> int:
         copies = max(2, math.ceil(ROTATION_BYTES / nbytes))
         bufs = [DeviceBuffer(nbytes) for _ in range(copies)]
         for i, b in enumerate(bufs):
-            b.upload(np.full(nbytes, i * 7 + 1, dtype=np.uint8))
+            b.upload(np.full(nbytes, (i * 7 + 1) % 256, dtype=np.uint8))
         rows = []
         for threads, in_flight in ((256, 2), (256, 4), (256, 8), (512, 2), (512, 4), (1024, 2)):
             for nt in (1, 0):
