@@ -90,22 +90,28 @@ void test_streams_do_not_wait_for_each_other() {
     ScratchPool pool(fake_alloc, fake_free);
     const void* s1 = reinterpret_cast<const void*>(0x1000);
     const void* s2 = reinterpret_cast<const void*>(0x2000);
-    ScratchPool::Lease held;
-    CHECK(pool.acquire(0, s1, 64, &held) == 0);
-    std::atomic<bool> done{false};
-    std::thread other([&] {
-        ScratchPool::Lease lease;
-        CHECK(pool.acquire(0, s2, 64, &lease) == 0);  // a different stream: no wait
-        CHECK(lease.ptr() != held.ptr());
-        done = true;
-    });
-    for (int i = 0; i < 2000 && !done; ++i) std::this_thread::sleep_for(std::chrono::milliseconds(1));
-    CHECK(done.load());
-    other.join();
-    // same stream on another device: its own buffer
-    ScratchPool::Lease dev1;
-    CHECK(pool.acquire(1, s1, 64, &dev1) == 0);
-    CHECK(dev1.ptr() != held.ptr());
+    {
+        ScratchPool::Lease held;
+        CHECK(pool.acquire(0, s1, 64, &held) == 0);
+        std::atomic<bool> done{false};
+        std::thread other([&] {
+            ScratchPool::Lease lease;
+            CHECK(pool.acquire(0, s2, 64, &lease) == 0);  // a different stream: no wait
+            CHECK(lease.ptr() != held.ptr());
+            done = true;
+        });
+        for (int i = 0; i < 2000 && !done; ++i) std::this_thread::sleep_for(std::chrono::milliseconds(1));
+        CHECK(done.load());
+        other.join();
+        // same stream on another device: its own buffer
+        ScratchPool::Lease dev1;
+        CHECK(pool.acquire(1, s1, 64, &dev1) == 0);
+        CHECK(dev1.ptr() != held.ptr());
+    }
+    CHECK(pool.release(0, s1) == 0);
+    CHECK(pool.release(0, s2) == 0);
+    CHECK(pool.release(1, s1) == 0);
+    CHECK(pool.streams() == 0);
 }
 
 void test_growth_retires_and_release_frees_everything() {
@@ -135,9 +141,13 @@ void test_growth_retires_and_release_frees_everything() {
         CHECK(g_frees - frees0 == 2);
         CHECK(pool.release(0, s) == 0);  // nothing left: no second free
         CHECK(g_frees - frees0 == 2);
-        ScratchPool::Lease l;  // a stream used again after release starts afresh
-        CHECK(pool.acquire(0, s, 16, &l) == 0);
-        CHECK(g_allocs - allocs0 == 3);
+        {
+            ScratchPool::Lease l;  // a stream used again after release starts afresh
+            CHECK(pool.acquire(0, s, 16, &l) == 0);
+            CHECK(g_allocs - allocs0 == 3);
+        }
+        CHECK(pool.release(0, s) == 0);
+        CHECK(g_frees - frees0 == 3);
     }
 }
 
@@ -156,6 +166,7 @@ void test_release_waits_for_a_held_lease() {
     delete lease;
     t.join();
     CHECK(released.load());
+    CHECK(pool.streams() == 0);
 }
 
 }  // namespace
@@ -165,6 +176,8 @@ int main() {
     test_streams_do_not_wait_for_each_other();
     test_growth_retires_and_release_frees_everything();
     test_release_waits_for_a_held_lease();
+    CHECK(g_live.empty());  // every buffer the pools allocated was freed once
+    CHECK(g_allocs == g_frees);
     if (failures == 0) std::printf("scratch pool: all checks passed\n");
     return failures == 0 ? 0 : 1;
 }
