@@ -24,6 +24,14 @@ Functions and the reference code they restate:
   ``lib.rs:333-384``.
 * ``rope_tables``: theta/position cos-sin tables in binary64.  The reference has
   no table builder; this is pinned by the closed form.
+* ``dequantize_kquant_row`` / ``kquant_linear_f64``: Q4_K and Q6_K super-blocks
+  as GGML defines them (ggml-common.h ``block_q4_K`` / ``block_q6_K``,
+  ggml-quants.c ``dequantize_row_q4_K`` / ``dequantize_row_q6_K``).  The
+  reference has their geometry only (``crates/mote-types/src/lib.rs:39-74``)
+  and its oracle rejects them (``quantized.rs:154-156``): parity against the
+  reference is unpinned; the tests pin the layout with hand-derived
+  known-answer blocks and an encoder-side packer, and the rounding with the
+  exact-rational value of every element.
 
 Errors raise :class:`OracleError` carrying the variant name and fields of the
 Rust error enum.
@@ -123,6 +131,8 @@ def _declare(h: ctypes.CDLL) -> None:
     h.mote_oracle_fused_add_rms_norm_f32.argtypes = [_P, _S, _P, _S, _P, _S, _S, ctypes.c_float, _P, _P, _P]
     h.mote_oracle_time_quantized_linear_f32.restype = ctypes.c_double
     h.mote_oracle_time_quantized_linear_f32.argtypes = [_P, _P, _S, _S, _S, _P, ctypes.c_int]
+    h.mote_oracle_dequantize_kquant_row.argtypes = [_P, _S, ctypes.c_int, _S, _P]
+    h.mote_oracle_kquant_linear_f64.argtypes = [_P, _P, ctypes.c_int, _S, _S, _S, _P]
 
 
 def _ptr(a: np.ndarray | None):
@@ -217,6 +227,27 @@ def gate_up_silu_f64(x, gate, up, rows: int, n: int, k: int, columns=None) -> np
     count = n if cols is None else cols.size
     out = np.zeros((rows, count), dtype=np.float64)
     code = lib().mote_oracle_gate_up_silu_f64(_ptr(xv), _ptr(g), _ptr(u), rows, n, k, _ptr(cols), count, _ptr(out))
+    if code != 0:
+        raise OracleError(code, np.zeros(3))
+    return out
+
+
+def dequantize_kquant_row(data, fmt: int, row_elements: int) -> np.ndarray:
+    """Q4_K / Q6_K bytes of ``row_elements`` (a multiple of 256) elements to f32."""
+    w = _u8(data)
+    out = np.zeros(max(row_elements, 1), dtype=np.float32)
+    code = lib().mote_oracle_dequantize_kquant_row(_ptr(w), w.size, fmt, row_elements, _ptr(out))
+    if code != 0:
+        raise OracleError(code, np.zeros(3))
+    return out[:row_elements]
+
+
+def kquant_linear_f64(x, weights, fmt: int, rows: int, n: int, k: int) -> np.ndarray:
+    """f64-accumulated ``x @ W^T`` for Q4_K / Q6_K weights ``[n, k]``; ``[rows, n]``."""
+    xv = _f32(x).reshape(-1)
+    w = _u8(weights)
+    out = np.zeros((rows, n), dtype=np.float64)
+    code = lib().mote_oracle_kquant_linear_f64(_ptr(xv), _ptr(w), fmt, rows, n, k, _ptr(out))
     if code != 0:
         raise OracleError(code, np.zeros(3))
     return out

@@ -192,6 +192,101 @@ int mote_oracle_dequantize_row(const uint8_t* bytes, size_t bytes_len, int forma
     return MOTE_ORACLE_OK;
 }
 
+/* ------------------------------------------------------------------------ */
+/* K-quant super-blocks: GGML's block_q4_K / block_q6_K (ggml-common.h) and  */
+/* dequantize_row_q4_K / dequantize_row_q6_K (ggml-quants.c); the reference  */
+/* has their geometry only (TYP/src/lib.rs:39-74).  Element order and f32   */
+/* rounding points as GGML's C: d1 = d * sc and m1 = dmin * m rounded to f32, */
+/* then d1 * q - m1 (Q4_K); d * sc then times (q - 32) (Q6_K).              */
+/* ------------------------------------------------------------------------ */
+
+/* get_scale_min_k4 of ggml-quants.c: 6-bit scale and min of sub-block j. */
+static void q4k_scale_min(const uint8_t* s, int j, uint8_t* sc, uint8_t* m) {
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *m = s[j + 4] & 63;
+    } else {
+        *sc = (uint8_t)((s[j + 4] & 0x0f) | ((s[j - 4] >> 6) << 4));
+        *m = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+    }
+}
+
+static void decode_q4_k_block(const uint8_t* b, float* y) {
+    const float d = mote_oracle_f16_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+    const float dmin = mote_oracle_f16_to_f32((uint16_t)(b[2] | (b[3] << 8)));
+    const uint8_t* s = b + 4;
+    const uint8_t* q = b + 16;
+    for (int p = 0; p < 4; ++p) {
+        for (int h = 0; h < 2; ++h) {
+            uint8_t sc, m;
+            q4k_scale_min(s, 2 * p + h, &sc, &m);
+            const float d1 = d * (float)sc;
+            const float m1 = dmin * (float)m;
+            for (int l = 0; l < 32; ++l) {
+                const int nib = h ? (q[32 * p + l] >> 4) : (q[32 * p + l] & 0x0f);
+                const float prod = d1 * (float)nib;
+                y[64 * p + 32 * h + l] = prod - m1;
+            }
+        }
+    }
+}
+
+static void decode_q6_k_block(const uint8_t* b, float* y) {
+    const uint8_t* ql = b;
+    const uint8_t* qh = b + 128;
+    const int8_t* sc = (const int8_t*)(b + 192);
+    const float d = mote_oracle_f16_to_f32((uint16_t)(b[208] | (b[209] << 8)));
+    for (int g = 0; g < 2; ++g) {
+        for (int c = 0; c < 4; ++c) {
+            for (int l = 0; l < 32; ++l) {
+                const int e = 128 * g + 32 * c + l;
+                const uint8_t lowbyte = ql[64 * g + 32 * (c & 1) + l];
+                const int low = (c >> 1) ? (lowbyte >> 4) : (lowbyte & 0x0f);
+                const int high = (qh[32 * g + l] >> (2 * c)) & 3;
+                const int q = (low | (high << 4)) - 32;
+                const float ds = d * (float)sc[e / 16];
+                y[e] = ds * (float)q;
+            }
+        }
+    }
+}
+
+int mote_oracle_dequantize_kquant_row(const uint8_t* bytes, size_t bytes_len, int format,
+                                      size_t row_elements, float* out) {
+    if (format != MOTE_ORACLE_Q4_K && format != MOTE_ORACLE_Q6_K) return MOTE_ORACLE_UNSUPPORTED_FORMAT;
+    if (row_elements % 256 != 0) return MOTE_ORACLE_ROW_MISALIGNED;
+    const size_t block_bytes = mote_oracle_block_bytes(format);
+    if (bytes_len != row_elements / 256 * block_bytes) return MOTE_ORACLE_ROW_BYTE_LENGTH_MISMATCH;
+    for (size_t b = 0; b < row_elements / 256; ++b) {
+        if (format == MOTE_ORACLE_Q4_K)
+            decode_q4_k_block(bytes + b * block_bytes, out + 256 * b);
+        else
+            decode_q6_k_block(bytes + b * block_bytes, out + 256 * b);
+    }
+    return MOTE_ORACLE_OK;
+}
+
+int mote_oracle_kquant_linear_f64(const float* input, const uint8_t* weights, int format,
+                                  size_t rows, size_t output_features, size_t input_features,
+                                  double* out) {
+    if (format != MOTE_ORACLE_Q4_K && format != MOTE_ORACLE_Q6_K) return MOTE_ORACLE_UNSUPPORTED_FORMAT;
+    if (input_features % 256 != 0) return MOTE_ORACLE_ROW_MISALIGNED;
+    const size_t row_bytes = input_features / 256 * mote_oracle_block_bytes(format);
+    float* w = (float*)malloc((input_features ? input_features : 1) * sizeof(float));
+    if (!w) return -1;
+    for (size_t n = 0; n < output_features; ++n) {
+        mote_oracle_dequantize_kquant_row(weights + n * row_bytes, row_bytes, format, input_features, w);
+        for (size_t r = 0; r < rows; ++r) {
+            const float* x = input + r * input_features;
+            double acc = 0.0;
+            for (size_t k = 0; k < input_features; ++k) acc += (double)x[k] * (double)w[k];
+            out[r * output_features + n] = acc;
+        }
+    }
+    free(w);
+    return MOTE_ORACLE_OK;
+}
+
 /* quantized_linear_f32: REF/src/quantized.rs:89-144.  Same loop order: decode
  * one weight row, then a sequential f32 multiply-then-add over K per row. */
 int mote_oracle_quantized_linear_f32(const float* input, size_t input_len,

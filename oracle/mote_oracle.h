@@ -100,6 +100,39 @@ int mote_oracle_gate_up_silu_f64(const float* input, const uint8_t* gate,
                                  size_t input_features, const uint64_t* columns,
                                  size_t n_cols, double* out);
 
+/* --- K-quant super-blocks (Q4_K, Q6_K) ------------------------------------
+ * The reference defines only their geometry (TYP/src/lib.rs:39-74: 256
+ * elements in 144 / 210 bytes, "ggml-common.h ABI") and its oracle rejects
+ * them (REF/src/quantized.rs:154-156, mirrored by the functions above), so
+ * these follow the GGML definition the reference names: ggml-common.h
+ * block_q4_K / block_q6_K, decoded as ggml-quants.c dequantize_row_q4_K /
+ * dequantize_row_q6_K (ggml is not vendored in the reference and no version
+ * is pinned there; the layout below is the QK_K = 256 one).  Parity against
+ * the reference is therefore unpinned; the tests pin these functions with
+ * hand-derived known-answer blocks, the exact-rational closed form of every
+ * element, and a packer that writes blocks from the encoder's side.
+ *
+ * Q4_K (144 bytes): f16 d, f16 dmin, 12 bytes of 6-bit sub-block scales and
+ * mins, 128 bytes of nibbles.  Element 64p + 32h + l (p = 0..3, h = 0..1,
+ * l = 0..31) is nibble h of byte qs[32p + l] (h = 0 the low nibble), in
+ * sub-block j = 2p + h, value f32(d * sc_j) * q - f32(dmin * m_j), where
+ * for j < 4 sc_j = s[j] & 63, m_j = s[j + 4] & 63, and for j >= 4
+ * sc_j = (s[j + 4] & 15) | (s[j - 4] >> 6) << 4,
+ * m_j = (s[j + 4] >> 4) | (s[j] >> 6) << 4.
+ * Q6_K (210 bytes): ql[128] low nibbles, qh[64] high bit pairs, int8
+ * scales[16], f16 d.  Element 128g + 32c + l (g = 0..1, c = 0..3,
+ * l = 0..31) has q = nibble (c >> 1) of ql[64g + 32(c & 1) + l] plus
+ * bits 2c..2c+1 of qh[32g + l] shifted to bits 4..5, value
+ * f32(d * scales[e / 16]) * (q - 32). */
+int mote_oracle_dequantize_kquant_row(const uint8_t* bytes, size_t bytes_len, int format,
+                                      size_t row_elements, float* out);
+
+/* f64 judge of a K-quant linear: out[r * N + n] = sum_k x[r, k] w[n, k] in
+ * binary64 over the decoded weights (products exact in binary64). */
+int mote_oracle_kquant_linear_f64(const float* input, const uint8_t* weights, int format,
+                                  size_t rows, size_t output_features, size_t input_features,
+                                  double* out);
+
 /* --- dense matmul (REF/src/lib.rs:116-156) -------------------------------- */
 int mote_oracle_matmul_f32(const float* lhs, size_t lhs_len, const float* rhs,
                            size_t rhs_len, size_t m, size_t n, size_t k, float* out,
