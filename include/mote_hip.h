@@ -98,6 +98,40 @@ int mote_hip_quantized_linear_q8_0_f32(const void* input, const void* weights, v
 int mote_hip_dequantize_q4_0_f32(const void* weights, void* output, uint64_t rows,
                                  uint64_t input_features, void* stream);
 
+/* ---- K-quants: Q4_K and Q6_K (256-element super-blocks) ------------------ */
+/* [new] The reference defines only their geometry
+ * (crates/mote-types/src/lib.rs:39-74: Q4_K 256 elements in 144 bytes,
+ * 4-byte aligned; Q6_K 256 in 210 bytes, 2-byte aligned; the GGML
+ * ggml-common.h layouts) and plans their block-dot path
+ * (docs/roadmap.md:26-27); it has no kernel, no FFI and no oracle for them
+ * (crates/mote-reference/src/quantized.rs:154-156).  These follow the
+ * Q4_0 entry points' arguments and statuses, with blocks of 256 elements:
+ * null pointer, K % 256 != 0, weights below the format's alignment, an odd
+ * input address or an output below its element alignment -> 1; rows == 0 or
+ * N == 0 -> 0; rows * N > UINT_MAX or K > 2^31 - 1 -> 9; K == 0 writes zeros.
+ * output[rows, N] = input[rows, K] (f16) x weights[N, K]^T, f32
+ * accumulation, one final rounding for the f16 output. */
+int mote_hip_quantized_linear_q4_k_f16(const void* input, const void* weights, void* output,
+                                       uint64_t rows, uint64_t output_features,
+                                       uint64_t input_features, void* stream);
+int mote_hip_quantized_linear_q4_k_f32(const void* input, const void* weights, void* output,
+                                       uint64_t rows, uint64_t output_features,
+                                       uint64_t input_features, void* stream);
+int mote_hip_quantized_linear_q6_k_f16(const void* input, const void* weights, void* output,
+                                       uint64_t rows, uint64_t output_features,
+                                       uint64_t input_features, void* stream);
+int mote_hip_quantized_linear_q6_k_f32(const void* input, const void* weights, void* output,
+                                       uint64_t rows, uint64_t output_features,
+                                       uint64_t input_features, void* stream);
+
+/* [new] On-device decode of rows x K elements to f32 (output 4-byte
+ * aligned), bit-identical to GGML's dequantize_row_q4_K / dequantize_row_q6_K.
+ * Status: null, K % 256 != 0 or misaligned -> 1; empty -> 0. */
+int mote_hip_dequantize_q4_k_f32(const void* weights, void* output, uint64_t rows,
+                                 uint64_t input_features, void* stream);
+int mote_hip_dequantize_q6_k_f32(const void* weights, void* output, uint64_t rows,
+                                 uint64_t input_features, void* stream);
+
 /* ---- Q4_0 dispatch context (per-(M, N, K) plan cache) -------------------- */
 /* [new] Handle pattern of the reference's hipBLASLt plan cache
  * (crates/mote-backend-hip/src/hipblaslt_shim.cpp:326-408): create / destroy

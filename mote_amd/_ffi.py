@@ -53,6 +53,12 @@ SIGNATURES = {
     "mote_hip_quantized_linear_q8_0_f32": (_I, [_P, _P, _P, _U64, _U64, _U64, _P]),
     "mote_hip_q4_0_gate_up_silu_f32": (_I, [_P, _P, _P, _P, _U64, _U64, _U64, _P]),
     "mote_hip_dequantize_q4_0_f32": (_I, [_P, _P, _U64, _U64, _P]),
+    "mote_hip_quantized_linear_q4_k_f16": (_I, [_P, _P, _P, _U64, _U64, _U64, _P]),
+    "mote_hip_quantized_linear_q4_k_f32": (_I, [_P, _P, _P, _U64, _U64, _U64, _P]),
+    "mote_hip_quantized_linear_q6_k_f16": (_I, [_P, _P, _P, _U64, _U64, _U64, _P]),
+    "mote_hip_quantized_linear_q6_k_f32": (_I, [_P, _P, _P, _U64, _U64, _U64, _P]),
+    "mote_hip_dequantize_q4_k_f32": (_I, [_P, _P, _U64, _U64, _P]),
+    "mote_hip_dequantize_q6_k_f32": (_I, [_P, _P, _U64, _U64, _P]),
     "mote_q4_0_dispatch_create": (_I, [ctypes.POINTER(_P)]),
     "mote_q4_0_dispatch_destroy": (None, [_P]),
     "mote_q4_0_dispatch_last_error": (ctypes.c_char_p, [_P]),

@@ -1,0 +1,529 @@
+// K-quant super-block kernels for gfx950: Q4_K and Q6_K weights decoded to
+// f32, and the weight-only linear y[M, N] = x[M, K] (f16) . W[N, K]^T for few
+// tokens (the decode-shaped GEMV).
+//
+// The reference has the geometry of these formats only
+// (crates/mote-types/src/lib.rs:39-74: 256 elements in 144 and 210 bytes, the
+// "ggml-common.h ABI", storage alignment 4 and 2) and neither a kernel nor an
+// oracle for them (crates/mote-reference/src/quantized.rs:154-156).  The
+// layouts are GGML's block_q4_K and block_q6_K:
+//
+//  Q4_K, 144 bytes: f16 d, f16 dmin, scales[12], qs[128].  Element
+//    64p + 32h + l (p = 0..3, h = 0..1, l = 0..31) is nibble h of qs[32p + l]
+//    in sub-block j = 2p + h, value (d sc_j) q - dmin m_j, with the 6-bit sc_j
+//    and m_j packed as: j < 4: sc = s[j] & 63, m = s[j + 4] & 63; j >= 4:
+//    sc = (s[j + 4] & 15) | (s[j - 4] >> 6) << 4,
+//    m = (s[j + 4] >> 4) | (s[j] >> 6) << 4.
+//  Q6_K, 210 bytes: ql[128], qh[64], int8 scales[16], f16 d.  Element
+//    128g + 32c + l (g = 0..1, c = 0..3, l = 0..31) is nibble (c >> 1) of
+//    ql[64g + 32(c & 1) + l] with bits 2c..2c+1 of qh[32g + l] as bits 4..5,
+//    value (d scales[e / 16]) (q - 32).
+//
+// Decode is bit-identical to the oracle: d sc and dmin m are exact in f32 (11
+// + 6 significant bits), so is (d sc) q, and fma((d sc), q, -(dmin m)) is the
+// one rounding of the exact Q4_K value that GGML's two f32 operations give;
+// every Q6_K value (d sc)(q - 32) is exact (at most 23 significant bits).
+//
+// The linear (kq_gemv_kernel): workgroups of four waves, each wave owning R
+// weight rows at a time and a token group of MT tokens (gridDim.y).  The
+// activations of the token group are staged in LDS once per K chunk, in "pair
+// order" (elements [a b c d] stored as [a c b d], so that the dword pairs
+// (e, e + 2) and (e + 1, e + 3) line up with the nibble pairs one AND
+// extracts), together with the f32 sum of every 16 consecutive activations.
+// Eight lanes share a super-block, each taking 16 bytes of its quants (32
+// elements, two scale groups), so a wave streams eight blocks of a row per
+// step with 16-byte loads.  Quantized values enter v_dot2_f32_f16 as binary16
+// subnormals (q 2^-24, products exact in f32), and the per-group offsets (the
+// Q4_K minimum, the Q6_K -32) are applied through the staged group sums:
+//   Q4_K: sum_e x_e (d sc q_e - dmin m) = d sc 2^24 acc - dmin m S
+//   Q6_K: sum_e x_e d sc (q_e - 32)     = d sc (2^24 acc - 32 S).
+// HBM-bound: algorithmic bytes per call are |W| + 2 M K + M N |y|.
+#include "common.hpp"
+#include "q4_0.hpp"
+
+namespace mote::kquant {
+namespace {
+
+enum class Fmt { Q4K, Q6K };
+
+constexpr uint32_t kSuper = 256;
+constexpr int kGemvWaves = 4;
+constexpr int kGemvThreads = kGemvWaves * kWave;
+constexpr uint32_t kLdsBudget = 64 * 1024;  // x and group sums of one token group
+
+template <Fmt F>
+constexpr uint32_t block_bytes() {
+    return F == Fmt::Q4K ? 144u : 210u;
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+}
+
+// Sub-block j's 6-bit scale and min from the three dwords holding the 12
+// scale bytes (s0 = s[0..3], s1 = s[4..7], s2 = s[8..11]).
+__device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t j, uint32_t& sc,
+                                              uint32_t& m) {
+    const uint32_t sh = 8u * (j & 3u);
+    const uint32_t a = __builtin_amdgcn_ubfe(s0, sh, 8), b = __builtin_amdgcn_ubfe(s1, sh, 8);
+    if (j < 4) {
+        sc = a & 63u;
+        m = b & 63u;
+    } else {
+        const uint32_t c = __builtin_amdgcn_ubfe(s2, sh, 8);
+        sc = (c & 15u) | ((a >> 6) << 4);
+        m = (c >> 4) | ((b >> 6) << 4);
+    }
+}
+
+// 16 bytes at a 2-byte-aligned address, read as five dwords from the dword
+// boundary at or below it; the caller guarantees the 20 bytes from there lie
+// inside the object.
+__device__ __forceinline__ u32x4 load16_a2(const uint8_t* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t{3});
+    const uint32_t sh = static_cast<uint32_t>(a & 3u);  // 0 or 2
+    const u32x4_a4 v = *reinterpret_cast<const u32x4_a4*>(q);
+    const uint32_t e = q[4];
+    u32x4 r;
+    r.x = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+    r.y = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+    r.z = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
+    r.w = __builtin_amdgcn_alignbyte(e, v.w, sh);
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// Decode: one thread per 16 consecutive elements of a super-block.
+// ---------------------------------------------------------------------------
+template <bool VEC>
+__device__ __forceinline__ void store16(float* out, const float (&v)[16]) {
+    if constexpr (VEC) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            reinterpret_cast<f32x4*>(out)[i] = f32x4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) out[i] = v[i];
+    }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void decode_q4k_kernel(const uint8_t* __restrict__ w, float* __restrict__ out,
+                                                         uint64_t pieces) {
+    const uint64_t t = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= pieces) return;
+    const uint64_t b = t >> 4;
+    const uint32_t i = static_cast<uint32_t>(t & 15u);  // elements 16i .. 16i + 15
+    const uint8_t* blk = w + b * 144;
+    const u32x4_a4 hdr = *reinterpret_cast<const u32x4_a4*>(blk);
+    const uint32_t p = i >> 2, h = (i >> 1) & 1u, l0 = 16u * (i & 1u);
+    const u32x4_a4 qs = *reinterpret_cast<const u32x4_a4*>(blk + 16 + 32 * p + l0);
+    uint32_t sc, m;
+    q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * p + h, sc, m);
+    const float d1 = half_bits_to_float(hdr.x & 0xffffu) * static_cast<float>(sc);
+    const float m1 = half_bits_to_float(hdr.x >> 16) * static_cast<float>(m);
+    const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const uint32_t nib = (q[k >> 2] >> (8 * (k & 3) + 4 * h)) & 15u;
+        v[k] = __builtin_fmaf(d1, static_cast<float>(nib), -m1);
+    }
+    store16<VEC>(out + t * 16, v);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void decode_q6k_kernel(const uint8_t* __restrict__ w, float* __restrict__ out,
+                                                         uint64_t pieces) {
+    const uint64_t t = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= pieces) return;
+    const uint64_t b = t >> 4;
+    const uint32_t i = static_cast<uint32_t>(t & 15u);  // elements 16i .. 16i + 15
+    const uint8_t* blk = w + b * 210;
+    const uint32_t g = i >> 3, c = (i >> 1) & 3u, l0 = 16u * (i & 1u);
+    const u32x4 ql = load16_a2(blk + 64 * g + 32 * (c & 1u) + l0);
+    const u32x4 qh = load16_a2(blk + 128 + 32 * g + l0);
+    const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(blk + 208));
+    const float ds = d * static_cast<float>(static_cast<int8_t>(blk[192 + i]));
+    const uint32_t lo[4] = {ql.x, ql.y, ql.z, ql.w}, hi[4] = {qh.x, qh.y, qh.z, qh.w};
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const uint32_t sh = 8 * (k & 3);
+        const uint32_t low = (lo[k >> 2] >> (sh + 4 * (c >> 1))) & 15u;
+        const uint32_t high = (hi[k >> 2] >> (sh + 2 * c)) & 3u;
+        v[k] = ds * static_cast<float>(static_cast<int>(low | (high << 4)) - 32);
+    }
+    store16<VEC>(out + t * 16, v);
+}
+
+// ---------------------------------------------------------------------------
+// Linear.
+// ---------------------------------------------------------------------------
+
+// Stages tokens [0, mt) of the token group, elements [k0, k0 + kc), into LDS:
+// xs[t][kc_max / 2] dwords in pair order and gs[t][kc_max / 16] group sums
+// (kc <= kc_max, the row strides of the two arrays).
+template <int MT>
+__device__ __forceinline__ void stage_x(const uint16_t* __restrict__ x, uint32_t K, uint32_t k0, uint32_t kc,
+                                        uint32_t kc_max, int mt, bool x16, uint32_t* xs, float* gs) {
+    const uint32_t per_token = kc / 8;  // 8-element pieces (16 bytes) per token
+    const uint32_t total = static_cast<uint32_t>(mt) * per_token;
+    for (uint32_t idx = threadIdx.x; idx < total; idx += kGemvThreads) {
+        const uint32_t t = idx / per_token, piece = idx - t * per_token;
+        const uint16_t* src = x + static_cast<size_t>(t) * K + k0 + 8 * piece;
+        uint32_t a[4];
+        if (x16) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(src);
+            a[0] = v.x; a[1] = v.y; a[2] = v.z; a[3] = v.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = src[2 * i] | (static_cast<uint32_t>(src[2 * i + 1]) << 16);
+        }
+        // [x0 x1][x2 x3] -> [x0 x2][x1 x3]
+        u32x4 o;
+        o.x = __builtin_amdgcn_perm(a[1], a[0], 0x05040100u);
+        o.y = __builtin_amdgcn_perm(a[1], a[0], 0x07060302u);
+        o.z = __builtin_amdgcn_perm(a[3], a[2], 0x05040100u);
+        o.w = __builtin_amdgcn_perm(a[3], a[2], 0x07060302u);
+        *reinterpret_cast<u32x4*>(xs + t * (kc_max / 2) + 4 * piece) = o;
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s += half_bits_to_float(a[i] & 0xffffu) + half_bits_to_float(a[i] >> 16);
+        // pieces 2q and 2q + 1 (adjacent lanes) form one 16-element group
+        s += dpp<0xB1>(s);
+        if ((piece & 1u) == 0) gs[t * (kc_max / 16) + piece / 2] = s;
+    }
+}
+
+// One block's contribution for every token, lane part `part` (0..7).
+template <Fmt F, int MT>
+struct BlockPart;
+
+template <int MT>
+struct BlockPart<Fmt::Q4K, MT> {
+    u32x4 hdr, qs;
+    __device__ __forceinline__ void load(const uint8_t* blk, uint32_t part) {
+        hdr = *reinterpret_cast<const u32x4_a4*>(blk);
+        qs = *reinterpret_cast<const u32x4_a4*>(blk + 16 + 16 * part);
+    }
+    // e0: chunk-local element of the block's first element.
+    __device__ __forceinline__ void accumulate(uint32_t part, uint32_t e0, int mt, const uint32_t* xs,
+                                               const float* gs, uint32_t xs_stride, uint32_t gs_stride,
+                                               float (&acc)[MT]) const {
+        const uint32_t p = part >> 1, half = part & 1u;
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * p, sc0, m0);
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * p + 1, sc1, m1);
+        const float d = half_bits_to_float(hdr.x & 0xffffu), dmin = half_bits_to_float(hdr.x >> 16);
+        const float a0 = d * static_cast<float>(sc0) * 16777216.0f, a1 = d * static_cast<float>(sc1) * 16777216.0f;
+        const float c0 = dmin * static_cast<float>(m0), c1 = dmin * static_cast<float>(m1);
+        const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
+        uint32_t lo02[4], lo13[4], hi02[4], hi13[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            lo02[w] = q[w] & 0x000F000Fu;
+            lo13[w] = (q[w] >> 8) & 0x000F000Fu;
+            hi02[w] = (q[w] >> 4) & 0x000F000Fu;
+            hi13[w] = (q[w] >> 12) & 0x000F000Fu;
+        }
+        const uint32_t e_lo = e0 + 64 * p + 16 * half, e_hi = e_lo + 32;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (m >= mt) break;
+            const u32x4* xl = reinterpret_cast<const u32x4*>(xs + m * xs_stride + e_lo / 2);
+            const u32x4* xh = reinterpret_cast<const u32x4*>(xs + m * xs_stride + e_hi / 2);
+            const u32x4 l0 = xl[0], l1 = xl[1], h0 = xh[0], h1 = xh[1];
+            const uint32_t xlo[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+            const uint32_t xhi[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+            float sl = 0.0f, sh = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                sl = dot2(lo02[w], xlo[2 * w], sl);
+                sl = dot2(lo13[w], xlo[2 * w + 1], sl);
+                sh = dot2(hi02[w], xhi[2 * w], sh);
+                sh = dot2(hi13[w], xhi[2 * w + 1], sh);
+            }
+            const float g_lo = gs[m * gs_stride + e_lo / 16], g_hi = gs[m * gs_stride + e_hi / 16];
+            float v = acc[m];
+            v = __builtin_fmaf(a0, sl, v);
+            v = __builtin_fmaf(-c0, g_lo, v);
+            v = __builtin_fmaf(a1, sh, v);
+            v = __builtin_fmaf(-c1, g_hi, v);
+            acc[m] = v;
+        }
+    }
+};
+
+template <int MT>
+struct BlockPart<Fmt::Q6K, MT> {
+    u32x4 ql, qh;
+    uint32_t d, s_lo, s_hi;
+    __device__ __forceinline__ void load(const uint8_t* blk, uint32_t part) {
+        const uint32_t g = part >> 2, c4 = part & 3u;
+        ql = load16_a2(blk + 64 * g + 16 * c4);
+        qh = load16_a2(blk + 128 + 32 * g + 16 * (c4 & 1u));
+        s_lo = static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(blk[192 + 8 * g + c4])));
+        s_hi = static_cast<uint32_t>(static_cast<int32_t>(static_cast<int8_t>(blk[196 + 8 * g + c4])));
+        d = *reinterpret_cast<const uint16_t*>(blk + 208);
+    }
+    __device__ __forceinline__ void accumulate(uint32_t part, uint32_t e0, int mt, const uint32_t* xs,
+                                               const float* gs, uint32_t xs_stride, uint32_t gs_stride,
+                                               float (&acc)[MT]) const {
+        const uint32_t g = part >> 2, c4 = part & 3u;
+        const uint32_t sh_lo = 2 * (c4 >> 1), sh_hi = 4 + 2 * (c4 >> 1);
+        const float dd = half_bits_to_float(d);
+        const float ds_lo = dd * static_cast<float>(static_cast<int32_t>(s_lo));
+        const float ds_hi = dd * static_cast<float>(static_cast<int32_t>(s_hi));
+        const float a_lo = ds_lo * 16777216.0f, a_hi = ds_hi * 16777216.0f;
+        const float b_lo = ds_lo * 32.0f, b_hi = ds_hi * 32.0f;
+        const uint32_t l[4] = {ql.x, ql.y, ql.z, ql.w}, h[4] = {qh.x, qh.y, qh.z, qh.w};
+        uint32_t lo02[4], lo13[4], hi02[4], hi13[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t vlo = (l[w] & 0x0F0F0F0Fu) | (((h[w] >> sh_lo) & 0x03030303u) << 4);
+            const uint32_t vhi = ((l[w] >> 4) & 0x0F0F0F0Fu) | (((h[w] >> sh_hi) & 0x03030303u) << 4);
+            lo02[w] = vlo & 0x00FF00FFu;
+            lo13[w] = (vlo >> 8) & 0x00FF00FFu;
+            hi02[w] = vhi & 0x00FF00FFu;
+            hi13[w] = (vhi >> 8) & 0x00FF00FFu;
+        }
+        const uint32_t e_lo = e0 + 128 * g + 16 * c4, e_hi = e_lo + 64;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (m >= mt) break;
+            const u32x4* xl = reinterpret_cast<const u32x4*>(xs + m * xs_stride + e_lo / 2);
+            const u32x4* xh = reinterpret_cast<const u32x4*>(xs + m * xs_stride + e_hi / 2);
+            const u32x4 l0 = xl[0], l1 = xl[1], h0 = xh[0], h1 = xh[1];
+            const uint32_t xlo[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+            const uint32_t xhi[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+            float sl = 0.0f, sh = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                sl = dot2(lo02[w], xlo[2 * w], sl);
+                sl = dot2(lo13[w], xlo[2 * w + 1], sl);
+                sh = dot2(hi02[w], xhi[2 * w], sh);
+                sh = dot2(hi13[w], xhi[2 * w + 1], sh);
+            }
+            const float g_lo = gs[m * gs_stride + e_lo / 16], g_hi = gs[m * gs_stride + e_hi / 16];
+            float v = acc[m];
+            v = __builtin_fmaf(a_lo, sl, v);
+            v = __builtin_fmaf(-b_lo, g_lo, v);
+            v = __builtin_fmaf(a_hi, sh, v);
+            v = __builtin_fmaf(-b_hi, g_hi, v);
+            acc[m] = v;
+        }
+    }
+};
+
+// kc: K chunk (a multiple of 256) whose activations fit the LDS budget.
+template <Fmt F, int MT, int R, typename OutT>
+__global__ __launch_bounds__(kGemvThreads) void kq_gemv_kernel(const uint16_t* __restrict__ x,
+                                                              const uint8_t* __restrict__ w, OutT* __restrict__ y,
+                                                              uint32_t M, uint32_t N, uint32_t K, uint32_t kc_max,
+                                                              uint32_t x16) {
+    extern __shared__ uint32_t lds[];
+    uint32_t* xs = lds;
+    float* gs = reinterpret_cast<float*>(lds + MT * (kc_max / 2));
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t part = lane & 7u, slot = lane >> 3;
+    constexpr uint32_t BB = block_bytes<F>();
+    const size_t row_bytes = static_cast<size_t>(K / kSuper) * BB;
+    const uint32_t rows_per_group = kGemvWaves * R;
+    const uint32_t groups = (N + rows_per_group - 1) / rows_per_group;
+    const uint32_t chunks = (K + kc_max - 1) / kc_max;
+    const uint32_t token_groups = (M + MT - 1) / MT;
+    for (uint32_t tg = blockIdx.y; tg < token_groups; tg += gridDim.y) {
+        const uint32_t m0 = tg * MT;
+        const int mt = static_cast<int>(min(static_cast<uint32_t>(MT), M - m0));
+        const uint16_t* xg = x + static_cast<size_t>(m0) * K;
+        bool staged = false;
+        for (uint32_t rg = blockIdx.x; rg < groups; rg += gridDim.x) {
+            const uint32_t n0 = rg * rows_per_group + static_cast<uint32_t>(wave) * R;
+            float acc[R][MT];
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
+            for (uint32_t c = 0; c < chunks; ++c) {
+                const uint32_t k0 = c * kc_max, kc = min(kc_max, K - k0);
+                if (chunks > 1 || !staged) {
+                    __syncthreads();
+                    stage_x<MT>(xg, K, k0, kc, kc_max, mt, x16 != 0, xs, gs);
+                    __syncthreads();
+                    staged = true;
+                }
+                const uint32_t nb = kc / kSuper;
+                // Two block steps of all R rows are loaded before either is used.
+                for (uint32_t jb = slot; jb < nb; jb += 16) {
+                    const bool second = jb + 8 < nb;
+                    BlockPart<F, MT> bp[2][R];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        if (n0 + r < N) {
+                            const uint8_t* row =
+                                w + static_cast<size_t>(n0 + r) * row_bytes + static_cast<size_t>(k0 / kSuper) * BB;
+                            bp[0][r].load(row + static_cast<size_t>(jb) * BB, part);
+                            if (second) bp[1][r].load(row + static_cast<size_t>(jb + 8) * BB, part);
+                        }
+                    }
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        if (n0 + r < N) {
+                            bp[0][r].accumulate(part, jb * kSuper, mt, xs, gs, kc_max / 2, kc_max / 16, acc[r]);
+                            if (second)
+                                bp[1][r].accumulate(part, (jb + 8) * kSuper, mt, xs, gs, kc_max / 2, kc_max / 16,
+                                                    acc[r]);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                if (n0 + r >= N) continue;
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    if (m >= mt) break;
+                    const float s = wave_sum(acc[r][m]);
+                    if (lane == 0) y[static_cast<size_t>(m0 + m) * N + n0 + r] = to_out<OutT>(s);
+                }
+            }
+        }
+    }
+}
+
+int device_cus() {
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        return n;
+    }();
+    return cus;
+}
+
+constexpr int kRows = 2;
+
+template <Fmt F, int MT, typename OutT>
+hipError_t launch_gemv_mt(const void* x, const void* w, void* y, uint32_t M, uint32_t N, uint32_t K,
+                          hipStream_t stream) {
+    // the largest multiple of 256 whose activations and group sums, 2.25 MT
+    // bytes per element, fit the budget
+    uint32_t kc = kLdsBudget * 4 / (MT * 9) / kSuper * kSuper;
+    if (kc > K) kc = K;
+    const size_t lds = static_cast<size_t>(MT) * (kc / 2) * 4 + static_cast<size_t>(MT) * (kc / 16) * 4;
+    const uint32_t groups = (N + kGemvWaves * kRows - 1) / (kGemvWaves * kRows);
+    size_t fit = (160 * 1024) / (lds > 0 ? lds : 1);  // workgroups whose LDS fits one CU
+    const uint32_t per_cu = static_cast<uint32_t>(fit < 1 ? 1 : (fit > 4 ? 4 : fit));
+    uint32_t gx = K <= kc ? min(groups, static_cast<uint32_t>(device_cus()) * per_cu) : groups;
+    if (gx == 0) gx = 1;
+    const uint32_t token_groups = (M + MT - 1) / MT;
+    const uint32_t gy = token_groups < 65535u ? token_groups : 65535u;
+    const uint32_t x16 = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 ? 1u : 0u;
+    hipLaunchKernelGGL((kq_gemv_kernel<F, MT, kRows, OutT>), dim3(gx, gy), dim3(kGemvThreads), lds, stream,
+                       static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), static_cast<OutT*>(y), M, N,
+                       K, kc, x16);
+    return hipGetLastError();
+}
+
+template <Fmt F, typename OutT>
+hipError_t launch_gemv(const void* x, const void* w, void* y, uint32_t M, uint32_t N, uint32_t K,
+                       hipStream_t stream) {
+    if (M == 1) return launch_gemv_mt<F, 1, OutT>(x, w, y, M, N, K, stream);
+    if (M == 2) return launch_gemv_mt<F, 2, OutT>(x, w, y, M, N, K, stream);
+    if (M <= 4) return launch_gemv_mt<F, 4, OutT>(x, w, y, M, N, K, stream);
+    return launch_gemv_mt<F, 8, OutT>(x, w, y, M, N, K, stream);
+}
+
+template <Fmt F>
+int linear(const void* input, const void* weights, void* output, uint64_t rows, uint64_t n, uint64_t k,
+           bool f16_out, void* stream) {
+    if (!input || !weights || !output || !stream) return hipErrorInvalidValue;
+    if (k % kSuper != 0) return hipErrorInvalidValue;
+    const uintptr_t walign = F == Fmt::Q4K ? 4 : 2;
+    if ((reinterpret_cast<uintptr_t>(weights) & (walign - 1)) != 0 || (reinterpret_cast<uintptr_t>(input) & 1u) != 0 ||
+        (reinterpret_cast<uintptr_t>(output) & (f16_out ? 1u : 3u)) != 0)
+        return hipErrorInvalidValue;
+    if (rows == 0 || n == 0) return hipSuccess;
+    if (rows > UINT_MAX || n > UINT_MAX || rows > UINT_MAX / n) return hipErrorInvalidConfiguration;
+    if (k > 0x7fffffffull) return hipErrorInvalidConfiguration;
+    const auto s = static_cast<hipStream_t>(stream);
+    if (k == 0)
+        return static_cast<int>(q4_0::launch_zero_fill(output, rows * n, f16_out ? q4_0::OutType::F16 : q4_0::OutType::F32, s));
+    const auto M = static_cast<uint32_t>(rows), N = static_cast<uint32_t>(n), K = static_cast<uint32_t>(k);
+    const hipError_t e = f16_out ? launch_gemv<F, _Float16>(input, weights, output, M, N, K, s)
+                                 : launch_gemv<F, float>(input, weights, output, M, N, K, s);
+    return static_cast<int>(e);
+}
+
+template <Fmt F>
+int dequantize(const void* weights, void* output, uint64_t rows, uint64_t k, void* stream) {
+    if (!weights || !output || !stream) return hipErrorInvalidValue;
+    if (k % kSuper != 0) return hipErrorInvalidValue;
+    const uintptr_t walign = F == Fmt::Q4K ? 4 : 2;
+    if ((reinterpret_cast<uintptr_t>(weights) & (walign - 1)) != 0 || (reinterpret_cast<uintptr_t>(output) & 3u) != 0)
+        return hipErrorInvalidValue;
+    if (rows == 0 || k == 0) return hipSuccess;
+    if (rows > (1ull << 40) / k) return hipErrorInvalidConfiguration;
+    const uint64_t pieces = rows * (k / 16);
+    const uint64_t grid = (pieces + 255) / 256;
+    if (grid > 0x7fffffffull) return hipErrorInvalidConfiguration;
+    const bool vec = (reinterpret_cast<uintptr_t>(output) & 15u) == 0;
+    const auto s = static_cast<hipStream_t>(stream);
+    const auto* wp = static_cast<const uint8_t*>(weights);
+    auto* op = static_cast<float*>(output);
+    if constexpr (F == Fmt::Q4K) {
+        if (vec)
+            hipLaunchKernelGGL(decode_q4k_kernel<true>, dim3(static_cast<uint32_t>(grid)), dim3(256), 0, s, wp, op, pieces);
+        else
+            hipLaunchKernelGGL(decode_q4k_kernel<false>, dim3(static_cast<uint32_t>(grid)), dim3(256), 0, s, wp, op, pieces);
+    } else {
+        if (vec)
+            hipLaunchKernelGGL(decode_q6k_kernel<true>, dim3(static_cast<uint32_t>(grid)), dim3(256), 0, s, wp, op, pieces);
+        else
+            hipLaunchKernelGGL(decode_q6k_kernel<false>, dim3(static_cast<uint32_t>(grid)), dim3(256), 0, s, wp, op, pieces);
+    }
+    return static_cast<int>(hipGetLastError());
+}
+
+}  // namespace
+}  // namespace mote::kquant
+
+using mote::kquant::Fmt;
+
+MOTE_EXPORT int mote_hip_quantized_linear_q4_k_f32(const void* input, const void* weights, void* output,
+                                                  uint64_t rows, uint64_t output_features,
+                                                  uint64_t input_features, void* stream) noexcept {
+    return mote::kquant::linear<Fmt::Q4K>(input, weights, output, rows, output_features, input_features, false, stream);
+}
+
+MOTE_EXPORT int mote_hip_quantized_linear_q4_k_f16(const void* input, const void* weights, void* output,
+                                                  uint64_t rows, uint64_t output_features,
+                                                  uint64_t input_features, void* stream) noexcept {
+    return mote::kquant::linear<Fmt::Q4K>(input, weights, output, rows, output_features, input_features, true, stream);
+}
+
+MOTE_EXPORT int mote_hip_quantized_linear_q6_k_f32(const void* input, const void* weights, void* output,
+                                                  uint64_t rows, uint64_t output_features,
+                                                  uint64_t input_features, void* stream) noexcept {
+    return mote::kquant::linear<Fmt::Q6K>(input, weights, output, rows, output_features, input_features, false, stream);
+}
+
+MOTE_EXPORT int mote_hip_quantized_linear_q6_k_f16(const void* input, const void* weights, void* output,
+                                                  uint64_t rows, uint64_t output_features,
+                                                  uint64_t input_features, void* stream) noexcept {
+    return mote::kquant::linear<Fmt::Q6K>(input, weights, output, rows, output_features, input_features, true, stream);
+}
+
+MOTE_EXPORT int mote_hip_dequantize_q4_k_f32(const void* weights, void* output, uint64_t rows,
+                                            uint64_t input_features, void* stream) noexcept {
+    return mote::kquant::dequantize<Fmt::Q4K>(weights, output, rows, input_features, stream);
+}
+
+MOTE_EXPORT int mote_hip_dequantize_q6_k_f32(const void* weights, void* output, uint64_t rows,
+                                            uint64_t input_features, void* stream) noexcept {
+    return mote::kquant::dequantize<Fmt::Q6K>(weights, output, rows, input_features, stream);
+}

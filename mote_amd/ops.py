@@ -50,6 +50,30 @@ def dequantize_q4_0_f32(w, out, rows, k, stream) -> None:
     check(lib().mote_hip_dequantize_q4_0_f32(w, out, rows, k, _s(stream)), "launch Q4_0 decode kernel")
 
 
+def quantized_linear_q4_k_f16(x, w, y, rows, n, k, stream) -> None:
+    check(lib().mote_hip_quantized_linear_q4_k_f16(x, w, y, rows, n, k, _s(stream)), "launch Q4_K linear kernel")
+
+
+def quantized_linear_q4_k_f32(x, w, y, rows, n, k, stream) -> None:
+    check(lib().mote_hip_quantized_linear_q4_k_f32(x, w, y, rows, n, k, _s(stream)), "launch Q4_K linear kernel")
+
+
+def quantized_linear_q6_k_f16(x, w, y, rows, n, k, stream) -> None:
+    check(lib().mote_hip_quantized_linear_q6_k_f16(x, w, y, rows, n, k, _s(stream)), "launch Q6_K linear kernel")
+
+
+def quantized_linear_q6_k_f32(x, w, y, rows, n, k, stream) -> None:
+    check(lib().mote_hip_quantized_linear_q6_k_f32(x, w, y, rows, n, k, _s(stream)), "launch Q6_K linear kernel")
+
+
+def dequantize_q4_k_f32(w, out, rows, k, stream) -> None:
+    check(lib().mote_hip_dequantize_q4_k_f32(w, out, rows, k, _s(stream)), "launch Q4_K decode kernel")
+
+
+def dequantize_q6_k_f32(w, out, rows, k, stream) -> None:
+    check(lib().mote_hip_dequantize_q6_k_f32(w, out, rows, k, _s(stream)), "launch Q6_K decode kernel")
+
+
 def rms_norm_f16(x, weight, y, rows, hidden, eps, stream) -> None:
     check(lib().mote_hip_rms_norm_f16(x, weight, y, rows, hidden, eps, _s(stream)), "launch RMSNorm kernel")
 

@@ -85,6 +85,31 @@ def test_gate_up_and_decode_status_codes(lib):
     assert d(FAKE, FAKE, 4, 0, STREAM) == 0
 
 
+def test_k_quant_status_codes(lib):
+    """Q4_K / Q6_K: the Q4_0 statuses with K % 256 and each format's storage
+    alignment (crates/mote-types/src/lib.rs:67-73: Q4_K 4, Q6_K 2)."""
+    for name, walign in (("q4_k", 4), ("q6_k", 2)):
+        for out, oalign in (("f16", 2), ("f32", 4)):
+            fn = getattr(lib, f"mote_hip_quantized_linear_{name}_{out}")
+            assert fn(None, FAKE, FAKE, 1, 1, 256, STREAM) == 1
+            assert fn(FAKE, FAKE, FAKE, 1, 1, 256, None) == 1
+            assert fn(FAKE, FAKE, FAKE, 1, 1, 288, STREAM) == 1   # K % 256 != 0
+            assert fn(FAKE, FAKE + walign // 2, FAKE, 1, 1, 256, STREAM) == 1  # weights misaligned
+            assert fn(FAKE + 1, FAKE, FAKE, 1, 1, 256, STREAM) == 1  # odd input address
+            assert fn(FAKE, FAKE, FAKE + oalign // 2, 1, 1, 256, STREAM) == 1
+            assert fn(FAKE, FAKE, FAKE, 0, 5, 256, STREAM) == 0
+            assert fn(FAKE, FAKE, FAKE, 5, 0, 256, STREAM) == 0
+            assert fn(FAKE, FAKE, FAKE, 65536, 65536, 256, STREAM) == 9
+            assert fn(FAKE, FAKE, FAKE, 1, 1, 1 << 31, STREAM) == 9
+        d = getattr(lib, f"mote_hip_dequantize_{name}_f32")
+        assert d(None, FAKE, 1, 256, STREAM) == 1
+        assert d(FAKE, FAKE, 1, 128, STREAM) == 1
+        assert d(FAKE + walign // 2, FAKE, 1, 256, STREAM) == 1
+        assert d(FAKE, FAKE + 2, 1, 256, STREAM) == 1
+        assert d(FAKE, FAKE, 0, 256, STREAM) == 0
+        assert d(FAKE, FAKE, 4, 0, STREAM) == 0
+
+
 def test_norm_status_codes(lib):
     r = lib.mote_hip_rms_norm_f16
     assert r(None, FAKE, FAKE, 1, 8, 1e-6, STREAM) == -1
