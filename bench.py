@@ -83,15 +83,21 @@ class LinearCase:
     """Device buffers for one Q4_0 (or Q8_0) linear problem with rotating weight copies."""
 
     def __init__(self, m: int, n: int, k: int, workload: int, x_uniform: bool = False,
-                 gate_up: bool = False, q8_0: bool = False, reference_inputs: bool = False) -> None:
+                 gate_up: bool = False, q8_0: bool = False, reference_inputs: bool = False,
+                 kquant: str | None = None) -> None:
         """`reference_inputs`: the reference benchmark's closed-form inputs
         and weights, through the F16-output entry point it times
-        (crates/mote-backend-hip/benches/quantized_linear.rs:8-13,128-152)."""
+        (crates/mote-backend-hip/benches/quantized_linear.rs:8-13,128-152).
+        `kquant`: "q4_k" or "q6_k" weights through their f32 entry points."""
         self.m, self.n, self.k, self.gate_up, self.q8_0 = m, n, k, gate_up, q8_0
         self.f16_out = reference_inputs
+        self.kquant = kquant
         if reference_inputs:
             self.x = wl.reference_bench_inputs(m, k)
             self.w = wl.reference_bench_q4_0_weights(n, k)
+        elif kquant is not None:
+            self.x = wl.normal_f16(wl.seed_for(workload, 0), m * k)
+            self.w = (wl.q4_k_weights if kquant == "q4_k" else wl.q6_k_weights)(wl.seed_for(workload, 1), n, k)
         else:
             self.x = (wl.uniform_f16 if x_uniform else wl.normal_f16)(wl.seed_for(workload, 0), m * k)
             self.w = (wl.q8_0_weights if q8_0 else wl.q4_0_weights)(wl.seed_for(workload, 1), n, k)
@@ -113,6 +119,9 @@ class LinearCase:
         elif self.q8_0:
             ops.quantized_linear_q8_0_f32(self.xb.ptr, bufs[0].ptr, self.yb.ptr,
                                           self.m, self.n, self.k, stream)
+        elif self.kquant is not None:
+            fn = ops.quantized_linear_q4_k_f32 if self.kquant == "q4_k" else ops.quantized_linear_q6_k_f32
+            fn(self.xb.ptr, bufs[0].ptr, self.yb.ptr, self.m, self.n, self.k, stream)
         elif self.f16_out:
             ops.quantized_linear_q4_0_f16(self.xb.ptr, bufs[0].ptr, self.yb.ptr,
                                           self.m, self.n, self.k, stream)
@@ -121,7 +130,7 @@ class LinearCase:
                                           self.m, self.n, self.k, stream)
 
     def algorithmic_bytes(self) -> int:
-        if self.q8_0:
+        if self.q8_0 or self.kquant is not None:
             return self.w.nbytes + 2 * self.m * self.k + 4 * self.m * self.n
         b = linear_bytes(self.m, self.n, self.k, 2 if self.f16_out else 4)
         return b + (self.w_up.nbytes if self.gate_up else 0)
@@ -279,6 +288,10 @@ SWEEP = (
     # the reference benchmark's cases (rows, N, K), its inputs, the F16-output entry point
     + [("ref bench f16", m, k, n, 0, False, "ref") for m, n, k in
        ((1, 4096, 4096), (1, 11008, 4096), (1, 4096, 11008), (16, 4096, 4096))]
+    # K-quant GEMV (Q4_K, Q6_K): the decode-shaped linears
+    + [(f"{f} {what}", m, k, n, 6, False, f) for f in ("q4_k", "q6_k")
+       for what, m, k, n in (("decode", 1, 4096, 4096), ("up/gate", 1, 4096, 14336), ("down", 1, 14336, 4096),
+                             ("4 tok", 4, 4096, 14336), ("8 tok", 8, 4096, 14336))]
 )
 
 
@@ -368,27 +381,33 @@ class DenseCase:
         self.ctx.close()
 
 
-def run_sweep(stream: Stream, hip: HipRuntime, steps: int, warmup: int) -> None:
+def run_sweep(stream: Stream, hip: HipRuntime, steps: int, warmup: int, only: str | None = None) -> None:
     """One line per configuration; the last column is the kernel variant the
     library's shape heuristic plans for it (the one the default entry points
-    launch)."""
+    launch).  `only`: just the linear configurations whose name contains it."""
     print(f"{'case':<15}{'M':>5}{'K':>7}{'N':>7}{'kernel us':>11}{'eager us':>10}{'GB/s':>9}"
           f"{'%HBM':>7}{'TFLOP/s':>9}{'%MFMA':>7}  kernel", file=sys.stderr)
     planner = ops.Q4_0Dispatch()  # no autotuning: the default entry points' heuristic
     for name, m, k, n, workload, uni, kind in SWEEP:
+        if only is not None and only not in name:
+            continue
+        kq = kind if kind in ("q4_k", "q6_k") else None
         case = LinearCase(m, n, k, workload, x_uniform=uni, gate_up=kind is True, q8_0=kind == "q8",
-                          reference_inputs=kind == "ref")
+                          reference_inputs=kind == "ref", kquant=kq)
         t = time_case(case, stream, hip, steps, warmup)
         us = t["kernel_ms_mean"] * 1e3
         w = case.wb[0]
-        if kind is True:
+        if kq is not None:
+            pass
+        elif kind is True:
             planner.gate_up_silu(case.xb.ptr, w[0].ptr, w[1].ptr, case.yb.ptr, m, n, k, stream)
         elif kind == "q8":
             planner.linear_q8_0(case.xb.ptr, w[0].ptr, case.yb.ptr, m, n, k, stream)
         else:
             planner.linear(case.xb.ptr, w[0].ptr, case.yb.ptr, m, n, k, stream, f16_out=kind == "ref")
         stream.synchronize()
-        variant = planner.plan(m, n, k, gate_up=kind is True, q8_0=kind == "q8", f16_out=kind == "ref")
+        variant = (f"kq_gemv_{kq}" if kq is not None else
+                   planner.plan(m, n, k, gate_up=kind is True, q8_0=kind == "q8", f16_out=kind == "ref"))
         gbs = case.algorithmic_bytes() / (us * 1e-6) / 1e9
         tf = case.flops() / (us * 1e-6) / 1e12
         print(f"{name:<15}{m:>5}{k:>7}{n:>7}{us:>11.2f}{t['eager_ms_per_step'] * 1e3:>10.2f}{gbs:>9.0f}"
@@ -396,6 +415,8 @@ def run_sweep(stream: Stream, hip: HipRuntime, steps: int, warmup: int) -> None:
               file=sys.stderr, flush=True)
         case.free()
     planner.close()
+    if only is not None:
+        return
     for m in (64, 512):
         case = DenseCase(m, 14336, 4096)
         t = time_case(case, stream, hip, steps, max(warmup, 1))
@@ -571,6 +592,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU time budget of the oracle baseline (0 skips it)")
     ap.add_argument("--sweep", action="store_true", help="also time every configuration (stderr)")
+    ap.add_argument("--sweep-only", default=None, metavar="TEXT",
+                    help="time only the sweep configurations whose name contains TEXT, and nothing "
+                         "else (stderr table, no result line)")
     ap.add_argument("--profile-run", action="store_true",
                     help="for rocprofv3 counter passes: one device-to-device copy of one weight "
                          "matrix (the calibration kernel of known size), then 20 calls of the "
@@ -621,6 +645,10 @@ def main() -> int:
         else:
             case = LinearCase(m, n, k, workload=1)
         return profile_run(case, stream, hip)
+    if args.sweep_only is not None:
+        run_sweep(stream, hip, min(args.steps, 50), min(args.warmup, 5), only=args.sweep_only)
+        stream.close()
+        return 0
     case = LinearCase(m, n, k, workload=1)
     print(f"bench: Q4_0 linear M={m} K={k} N={n}, {case.copies} weight copies "
           f"({case.copies * case.w.nbytes / 1e6:.0f} MB), warmup {args.warmup}, steps {args.steps}",

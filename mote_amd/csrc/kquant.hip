@@ -429,9 +429,383 @@ hipError_t launch_gemv_mt(const void* x, const void* w, void* y, uint32_t M, uin
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Few-token GEMV through per-wave LDS rings (kq_ring_kernel).
+//
+// One workgroup of eight waves per CU.  K is cut into S slices of at most 16
+// super-blocks (S = 1, 2, 4 or 8; Q6_K slices are whole multiples of eight
+// blocks so every slice starts on a 16-byte boundary); wave w takes slice
+// w % S of row group w / S, so a workgroup computes 8 / S rows per step.
+// Four lanes share a super-block, each with 64 elements of it: the lane's
+// activations for those elements stay in registers for the whole kernel (32
+// dwords per token in pair order, plus their group sums), and only weights
+// stream.  A wave's slice of a row arrives in its LDS ring by coalesced
+// non-temporal direct-to-LDS 16-byte loads (every lane of every load
+// instruction active, chunk indexes clamped inside the slice, so each row
+// issues exactly LOADS instructions and vmcnt counts rows), two rows ahead of
+// the one computed and never past the wave's last row.  Lane j of a wave keeps the partial sum of step j % 64;
+// every 64 steps the S partials of each row are added in slice order through
+// LDS (bitwise reproducible) and stored.
+//
+// Requires: x and w 16-byte aligned, row bytes a multiple of 16 (Q6_K: K a
+// multiple of 2048), K <= 32768.
+// ---------------------------------------------------------------------------
+constexpr int kRingWaves = 8;
+constexpr int kRingThreads = kRingWaves * kWave;
+constexpr int kRingSlots = 3;
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// LDS store and load of one f32 that the compiler does not see as LDS
+// accesses: with direct-to-LDS loads in flight, any LDS write it knows of
+// makes it wait for all of them before every later LDS read.  Each completes
+// before returning (lgkmcnt(0)).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr)(p)));
+}
+__device__ __forceinline__ void lds_store_f32_sync(uint32_t addr, float v) {
+    asm volatile("ds_write_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" ::"v"(addr), "v"(v));
+}
+__device__ __forceinline__ float lds_load_f32_sync(uint32_t addr) {
+    float r;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(r) : "v"(addr));
+    return r;
+}
+
+template <Fmt F>
+constexpr int ring_loads() {
+    return F == Fmt::Q4K ? 3 : 4;  // 16 blocks = 144 / 210 chunks of 16 bytes
+}
+
+// The lane's activations: 64 elements of its block part for every token, in
+// pair order, and the sums of its scale groups.
+template <Fmt F, int MT>
+struct LaneX {
+    static constexpr int kGroups = F == Fmt::Q4K ? 2 : 4;
+    uint32_t xr[MT][32];
+    float sum[MT][kGroups];
+};
+
+// Element offsets (in the block) of the lane's two 32-element runs.
+template <Fmt F>
+__device__ __forceinline__ void part_runs(uint32_t part, uint32_t& e0, uint32_t& e1) {
+    if constexpr (F == Fmt::Q4K) {
+        e0 = 64 * part;
+        e1 = e0 + 32;
+    } else {
+        e0 = 128 * (part >> 1) + 32 * (part & 1u);
+        e1 = e0 + 64;
+    }
+}
+
+// The lane's 64 activations of every token as loaded (two 32-element runs,
+// 16 dwords each); issued before the first weight rows, used after them.
+template <Fmt F, int MT>
+__device__ __forceinline__ void load_lane_x(const uint16_t* __restrict__ x, uint32_t K, int mt, uint32_t elem0,
+                                            uint32_t part, uint32_t (&raw)[MT][32]) {
+    uint32_t e0, e1;
+    part_runs<F>(part, e0, e1);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const int mm = m < mt ? m : mt - 1;  // tokens past the group re-read the last one
+        const uint16_t* xr = x + static_cast<size_t>(mm) * K + elem0;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(xr + (r ? e1 : e0));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const u32x4 v = src[i];
+                raw[m][16 * r + 4 * i + 0] = v.x; raw[m][16 * r + 4 * i + 1] = v.y;
+                raw[m][16 * r + 4 * i + 2] = v.z; raw[m][16 * r + 4 * i + 3] = v.w;
+            }
+        }
+    }
+}
+
+// Pair order and the group sums (32 elements for Q4_K, 16 for Q6_K).
+template <Fmt F, int MT>
+__device__ __forceinline__ void order_lane_x(const uint32_t (&raw)[MT][32], LaneX<F, MT>& lx) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            // [x0 x1][x2 x3] -> [x0 x2][x1 x3]
+            lx.xr[m][2 * i] = __builtin_amdgcn_perm(raw[m][2 * i + 1], raw[m][2 * i], 0x05040100u);
+            lx.xr[m][2 * i + 1] = __builtin_amdgcn_perm(raw[m][2 * i + 1], raw[m][2 * i], 0x07060302u);
+        }
+        constexpr int per = 32 / LaneX<F, MT>::kGroups;  // dwords of raw per group
+#pragma unroll
+        for (int g = 0; g < LaneX<F, MT>::kGroups; ++g) {
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < per; ++i) s = dot2(raw[m][g * per + i], kOnePair, s);
+            lx.sum[m][g] = s;
+        }
+    }
+}
+
+// sum over the lane's 64 elements of x * w for every token, from the block at
+// `blk` in LDS.
+template <Fmt F, int MT>
+__device__ __forceinline__ void ring_part_dot(uint32_t slot, uint32_t blk_off, uint32_t part,
+                                              const LaneX<F, MT>& lx, float (&out)[MT]) {
+    if constexpr (F == Fmt::Q4K) {
+        // header, then the lane's 32 nibble bytes; LDS address `slot + blk_off`
+        u32x4 hdr, qa, qb;
+        const uint32_t ah = slot + blk_off, aq = ah + 16 + 32 * part;
+        asm volatile(
+            "ds_read_b128 %0, %3\n\t"
+            "ds_read_b128 %1, %4\n\t"
+            "ds_read_b128 %2, %4 offset:16\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(hdr), "=&v"(qa), "=&v"(qb)  // early clobber: no output may share an address register
+            : "v"(ah), "v"(aq));
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * part, sc0, m0);
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * part + 1, sc1, m1);
+        const float d = half_bits_to_float(hdr.x & 0xffffu), dmin = half_bits_to_float(hdr.x >> 16);
+        const float a0 = d * static_cast<float>(sc0) * 16777216.0f, a1 = d * static_cast<float>(sc1) * 16777216.0f;
+        const float c0 = dmin * static_cast<float>(m0), c1 = dmin * static_cast<float>(m1);
+        const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                lo = dot2(q[w] & 0x000F000Fu, lx.xr[m][2 * w], lo);
+                lo = dot2((q[w] >> 8) & 0x000F000Fu, lx.xr[m][2 * w + 1], lo);
+                hi = dot2((q[w] >> 4) & 0x000F000Fu, lx.xr[m][16 + 2 * w], hi);
+                hi = dot2((q[w] >> 12) & 0x000F000Fu, lx.xr[m][16 + 2 * w + 1], hi);
+            }
+            float v = a0 * lo;
+            v = __builtin_fmaf(-c0, lx.sum[m][0], v);
+            v = __builtin_fmaf(a1, hi, v);
+            out[m] = __builtin_fmaf(-c1, lx.sum[m][1], v);
+        }
+    } else {
+        const uint32_t g = part >> 1, c = part & 1u;
+        // ql (32 bytes), qh (32 bytes) and the scale bytes 8g + 2c + {0, 1, 4, 5}
+        // start at 2-byte offsets: each is read as dwords from the dword
+        // boundary below it and realigned
+        const uint32_t b = slot + blk_off;
+        const uint32_t oq = b + 64 * g + 32 * c, oh = b + 128 + 32 * g, os = b + 192 + 8 * g + 2 * c;
+        u32x2 l01, l23, l45, l67, h01, h23, h45, h67, s01;
+        uint32_t l8, h8, s2, dbits;
+        asm volatile(
+            "ds_read2_b32 %0, %13 offset1:1\n\t"
+            "ds_read2_b32 %1, %13 offset0:2 offset1:3\n\t"
+            "ds_read2_b32 %2, %13 offset0:4 offset1:5\n\t"
+            "ds_read2_b32 %3, %13 offset0:6 offset1:7\n\t"
+            "ds_read_b32 %8, %13 offset:32\n\t"
+            "ds_read2_b32 %4, %14 offset1:1\n\t"
+            "ds_read2_b32 %5, %14 offset0:2 offset1:3\n\t"
+            "ds_read2_b32 %6, %14 offset0:4 offset1:5\n\t"
+            "ds_read2_b32 %7, %14 offset0:6 offset1:7\n\t"
+            "ds_read_b32 %9, %14 offset:32\n\t"
+            "ds_read2_b32 %10, %15 offset1:1\n\t"
+            "ds_read_b32 %11, %15 offset:8\n\t"
+            "ds_read_u16 %12, %16 offset:208\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(l01), "=&v"(l23), "=&v"(l45), "=&v"(l67), "=&v"(h01), "=&v"(h23), "=&v"(h45), "=&v"(h67),
+              "=&v"(l8), "=&v"(h8), "=&v"(s01), "=&v"(s2), "=&v"(dbits)  // early clobber, as above
+            : "v"(oq & ~3u), "v"(oh & ~3u), "v"(os & ~3u), "v"(b));
+        const uint32_t lv[9] = {l01.x, l01.y, l23.x, l23.y, l45.x, l45.y, l67.x, l67.y, l8};
+        const uint32_t hv[9] = {h01.x, h01.y, h23.x, h23.y, h45.x, h45.y, h67.x, h67.y, h8};
+        const uint32_t sv[3] = {s01.x, s01.y, s2};
+        uint32_t ql[8], qh[8], sc[2];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            ql[i] = __builtin_amdgcn_alignbyte(lv[i + 1], lv[i], oq & 2u);
+            qh[i] = __builtin_amdgcn_alignbyte(hv[i + 1], hv[i], oh & 2u);
+        }
+        sc[0] = __builtin_amdgcn_alignbyte(sv[1], sv[0], os & 2u);
+        sc[1] = __builtin_amdgcn_alignbyte(sv[2], sv[1], os & 2u);
+        const float d = half_bits_to_float(dbits);
+        // scales 8g + 2c + {0, 1} (low runs) in sc[0] bytes 0-1; 8g + 4 + 2c + {0, 1} in sc[1] bytes 0-1
+        const float ds[4] = {
+            d * static_cast<float>(static_cast<int8_t>(sc[0] & 0xffu)),
+            d * static_cast<float>(static_cast<int8_t>((sc[0] >> 8) & 0xffu)),
+            d * static_cast<float>(static_cast<int8_t>(sc[1] & 0xffu)),
+            d * static_cast<float>(static_cast<int8_t>((sc[1] >> 8) & 0xffu)),
+        };
+        const uint32_t sh_lo = 2 * c, sh_hi = 4 + 2 * c;
+        uint32_t v02[2][8], v13[2][8];
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            const uint32_t vlo = (ql[w] & 0x0F0F0F0Fu) | (((qh[w] >> sh_lo) & 0x03030303u) << 4);
+            const uint32_t vhi = ((ql[w] >> 4) & 0x0F0F0F0Fu) | (((qh[w] >> sh_hi) & 0x03030303u) << 4);
+            v02[0][w] = vlo & 0x00FF00FFu;
+            v13[0][w] = (vlo >> 8) & 0x00FF00FFu;
+            v02[1][w] = vhi & 0x00FF00FFu;
+            v13[1][w] = (vhi >> 8) & 0x00FF00FFu;
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float v = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+#pragma unroll
+                for (int gi = 0; gi < 2; ++gi) {
+                    float a = 0.0f;
+#pragma unroll
+                    for (int w = 4 * gi; w < 4 * gi + 4; ++w) {
+                        a = dot2(v02[r][w], lx.xr[m][16 * r + 2 * w], a);
+                        a = dot2(v13[r][w], lx.xr[m][16 * r + 2 * w + 1], a);
+                    }
+                    const float dsg = ds[2 * r + gi];
+                    v = __builtin_fmaf(dsg * 16777216.0f, a, v);
+                    v = __builtin_fmaf(-32.0f * dsg, lx.sum[m][2 * r + gi], v);
+                }
+            }
+            out[m] = v;
+        }
+    }
+}
+
+template <Fmt F, int MT, int S, typename OutT>
+__global__ __launch_bounds__(kRingThreads) void kq_ring_kernel(const uint16_t* __restrict__ x,
+                                                              const uint8_t* __restrict__ w, OutT* __restrict__ y,
+                                                              uint32_t M, uint32_t N, uint32_t K, uint32_t slice_blocks) {
+    constexpr int LOADS = ring_loads<F>();
+    constexpr uint32_t kSlot = LOADS * 1024;
+    constexpr uint32_t BB = block_bytes<F>();
+    constexpr int RW = kRingWaves / S;
+    __shared__ __attribute__((aligned(16))) uint8_t ring_lds[kRingWaves][kRingSlots][kSlot];
+    __shared__ float part_lds[kRingWaves][kWave];
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t s = static_cast<uint32_t>(wave % S), rw = static_cast<uint32_t>(wave / S);
+    const uint32_t nb = K / kSuper;
+    const uint32_t b0 = min(s * slice_blocks, nb), b1 = min(b0 + slice_blocks, nb);
+    // this wave's slice of a row in 16-byte chunks; an empty slice (possible
+    // for the last Q6_K slices) loads the row's first chunk and drops it
+    // (all its lanes are idle)
+    const uint32_t chunks = b1 > b0 ? (b1 - b0) * BB / 16 : 1u;
+    const size_t row_bytes = static_cast<size_t>(nb) * BB;
+    const uint32_t blk = lane >> 2, part = lane & 3u;
+    const bool active = b0 + blk < b1;
+    const uint32_t keep = active ? 0xFFFFFFFFu : 0u;  // NaN-safe drop of idle lanes
+    uint8_t* ring = &ring_lds[wave][0][0];
+    const uint32_t row_steps = (N + RW - 1) / RW;
+
+    for (uint32_t tg = blockIdx.y; tg * MT < M; tg += gridDim.y) {
+        const uint32_t m0 = tg * MT;
+        const int mt = static_cast<int>(min(static_cast<uint32_t>(MT), M - m0));
+        const uint32_t steps = blockIdx.x < row_steps ? (row_steps - 1 - blockIdx.x) / gridDim.x + 1 : 0;
+        auto row_of = [&](uint32_t t) { return (blockIdx.x + t * gridDim.x) * RW + rw; };
+        auto load_row = [&](uint32_t t, uint32_t slot) {
+            const uint32_t n = min(row_of(t), N - 1);  // past the end: re-read a row, never used
+            const uint8_t* src = w + static_cast<size_t>(n) * row_bytes + static_cast<size_t>(b1 > b0 ? b0 : 0) * BB;
+#pragma unroll
+            for (int i = 0; i < LOADS; ++i) {
+                const uint32_t c = min(64u * static_cast<uint32_t>(i) + lane, chunks - 1);
+                __builtin_amdgcn_global_load_lds(src + 16u * c, (lds_ptr)(ring + slot * kSlot + 1024u * i), 16, 0,
+                                                 2 /* non-temporal */);
+            }
+        };
+        if (steps == 0) continue;  // uniform per workgroup
+        __syncthreads();  // the previous token group's ring reads are done
+        LaneX<F, MT> lx;
+        {
+            uint32_t raw[MT][32];
+            load_lane_x<F, MT>(x + static_cast<size_t>(m0) * K, K, mt, min(b0 + blk, nb - 1) * kSuper, part, raw);
+            __builtin_amdgcn_sched_barrier(0);
+            load_row(0, 0);
+            if (steps > 1) load_row(1, 1);
+            __builtin_amdgcn_sched_barrier(0);
+            order_lane_x<F, MT>(raw, lx);
+        }
+        float mine[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) mine[m] = 0.0f;
+        for (uint32_t t = 0; t < steps; ++t) {
+            // Rows are loaded only up to the last step, so the count of loads
+            // still allowed in flight once row t has landed shrinks at the end.
+            if (t + 2 < steps) {
+                load_row(t + 2, (t + 2) % kRingSlots);
+                __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * 2));
+            } else if (t + 1 < steps) {
+                __builtin_amdgcn_s_waitcnt(0x0F70 | LOADS);
+            } else {
+                __builtin_amdgcn_s_waitcnt(0x0F70);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            float part_sum[MT];
+            ring_part_dot<F, MT>(lds_addr(ring + (t % kRingSlots) * kSlot), blk * BB, part, lx, part_sum);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const float v = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, part_sum[m]) & keep);
+                const float tot = wave_sum(v);
+                mine[m] = lane == (t & 63u) ? tot : mine[m];
+            }
+            if ((t & 63u) == 63u || t + 1 == steps) {
+                const uint32_t first = t & ~63u, count = (t & 63u) + 1;
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    if (m >= mt) break;
+                    float total = mine[m];
+                    if constexpr (S > 1) {
+                        lds_store_f32_sync(lds_addr(&part_lds[wave][lane]), mine[m]);
+                        __builtin_amdgcn_s_barrier();
+                        total = 0.0f;
+#pragma unroll
+                        for (int k = 0; k < S; ++k) total += lds_load_f32_sync(lds_addr(&part_lds[rw * S + k][lane]));
+                        __builtin_amdgcn_s_barrier();
+                    }
+                    const uint32_t n = row_of(first + lane);
+                    if (s == 0 && lane < count && n < N) y[static_cast<size_t>(m0 + m) * N + n] = to_out<OutT>(total);
+                }
+            }
+        }
+    }
+}
+
+template <Fmt F>
+bool ring_supported(const void* x, const void* w, uint32_t K) {
+    const uint32_t nb = K / kSuper;
+    if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0 || (reinterpret_cast<uintptr_t>(w) & 15u) != 0) return false;
+    if (nb == 0 || nb > 128) return false;
+    return F == Fmt::Q4K || nb % 8 == 0;
+}
+
+template <Fmt F, int MT, int S, typename OutT>
+hipError_t launch_ring_s(const void* x, const void* w, void* y, uint32_t M, uint32_t N, uint32_t K,
+                         uint32_t slice_blocks, hipStream_t stream) {
+    constexpr uint32_t RW = kRingWaves / S;
+    const uint32_t row_steps = (N + RW - 1) / RW;
+    uint32_t gx = static_cast<uint32_t>(device_cus());
+    if (gx > row_steps) gx = row_steps;
+    const uint32_t groups = (M + MT - 1) / MT;
+    const uint32_t gy = groups < 65535u ? groups : 65535u;
+    hipLaunchKernelGGL((kq_ring_kernel<F, MT, S, OutT>), dim3(gx, gy), dim3(kRingThreads), 0, stream,
+                       static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), static_cast<OutT*>(y), M, N, K,
+                       slice_blocks);
+    return hipGetLastError();
+}
+
+template <Fmt F, int MT, typename OutT>
+hipError_t launch_ring_mt(const void* x, const void* w, void* y, uint32_t M, uint32_t N, uint32_t K,
+                          hipStream_t stream) {
+    const uint32_t nb = K / kSuper;
+    uint32_t S = 1;
+    while ((nb + S - 1) / S > 16) S *= 2;
+    uint32_t sb = (nb + S - 1) / S;
+    if (F == Fmt::Q6K) sb = (sb + 7) / 8 * 8;
+    switch (S) {
+        case 1: return launch_ring_s<F, MT, 1, OutT>(x, w, y, M, N, K, sb, stream);
+        case 2: return launch_ring_s<F, MT, 2, OutT>(x, w, y, M, N, K, sb, stream);
+        case 4: return launch_ring_s<F, MT, 4, OutT>(x, w, y, M, N, K, sb, stream);
+        default: return launch_ring_s<F, MT, 8, OutT>(x, w, y, M, N, K, sb, stream);
+    }
+}
+
 template <Fmt F, typename OutT>
 hipError_t launch_gemv(const void* x, const void* w, void* y, uint32_t M, uint32_t N, uint32_t K,
                        hipStream_t stream) {
+    if (ring_supported<F>(x, w, K)) {
+        if (M == 1) return launch_ring_mt<F, 1, OutT>(x, w, y, M, N, K, stream);
+        if (M == 2) return launch_ring_mt<F, 2, OutT>(x, w, y, M, N, K, stream);
+        return launch_ring_mt<F, 4, OutT>(x, w, y, M, N, K, stream);
+    }
     if (M == 1) return launch_gemv_mt<F, 1, OutT>(x, w, y, M, N, K, stream);
     if (M == 2) return launch_gemv_mt<F, 2, OutT>(x, w, y, M, N, K, stream);
     if (M <= 4) return launch_gemv_mt<F, 4, OutT>(x, w, y, M, N, K, stream);

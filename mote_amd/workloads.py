@@ -97,6 +97,48 @@ def q8_0_weights(seed: int, rows: int, cols: int, std: float = 0.02) -> np.ndarr
     return out.reshape(-1)
 
 
+Q4_K_BLOCK_BYTES, Q6_K_BLOCK_BYTES, K_SUPER = 144, 210, 256
+
+
+def _random_blocks(seed: int, blocks: int, block_bytes: int) -> np.ndarray:
+    words = (block_bytes + 7) // 8
+    draws = splitmix64(seed, words * blocks) if blocks else np.zeros(0, np.uint64)
+    raw = draws.astype("<u8").view(np.uint8).reshape(blocks, words * 8)
+    return np.ascontiguousarray(raw[:, :block_bytes])
+
+
+def q4_k_weights(seed: int, rows: int, cols: int, std: float = 0.002) -> np.ndarray:
+    """GGML Q4_K bytes for a ``[rows, cols]`` matrix (144-byte blocks of 256
+    elements): per block d and dmin ``|N(0, std)|`` in f16, then 12 scale
+    bytes and 128 nibble bytes uniform (every byte pattern is a valid block)."""
+    if cols % K_SUPER:
+        raise ValueError("cols must be a multiple of 256")
+    blocks = rows * (cols // K_SUPER)
+    out = _random_blocks(seed, blocks, Q4_K_BLOCK_BYTES)
+    draws = splitmix64(seed ^ 0x5EED, 4 * blocks).reshape(blocks, 4) if blocks else np.zeros((0, 4), np.uint64)
+    u = uniform01(draws)
+    d = np.abs(std * _box_muller(u[:, 0], u[:, 1])).astype(np.float16).view(np.uint16)
+    dmin = np.abs(std * _box_muller(u[:, 2], u[:, 3])).astype(np.float16).view(np.uint16)
+    out[:, 0:2] = d.astype("<u2").view(np.uint8).reshape(blocks, 2)
+    out[:, 2:4] = dmin.astype("<u2").view(np.uint8).reshape(blocks, 2)
+    return out.reshape(-1)
+
+
+def q6_k_weights(seed: int, rows: int, cols: int, std: float = 0.0005) -> np.ndarray:
+    """GGML Q6_K bytes for a ``[rows, cols]`` matrix (210-byte blocks of 256
+    elements): 128 + 64 quant bytes and 16 int8 scales uniform, d
+    ``|N(0, std)|`` in f16 in the last two bytes."""
+    if cols % K_SUPER:
+        raise ValueError("cols must be a multiple of 256")
+    blocks = rows * (cols // K_SUPER)
+    out = _random_blocks(seed, blocks, Q6_K_BLOCK_BYTES)
+    draws = splitmix64(seed ^ 0x5EED, 2 * blocks).reshape(blocks, 2) if blocks else np.zeros((0, 2), np.uint64)
+    u = uniform01(draws)
+    d = np.abs(std * _box_muller(u[:, 0], u[:, 1])).astype(np.float16).view(np.uint16)
+    out[:, 208:210] = d.astype("<u2").view(np.uint8).reshape(blocks, 2)
+    return out.reshape(-1)
+
+
 def reference_bench_q4_0_weights(rows: int, cols: int) -> np.ndarray:
     """The closed-form Q4_0 matrix of the reference's own benchmark
     (crates/mote-backend-hip/benches/quantized_linear.rs:134-152): block b of

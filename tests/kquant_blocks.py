@@ -133,29 +133,3 @@ def random_q6_k(rng: np.random.Generator, blocks: int, scale_bits=None):
         out.append(pack_q6_k(d_bits, scales, q))
         params.append((d_bits, scales, q))
     return np.concatenate(out), params
-
-
-def model_like_q4_k(seed: int, n: int, k: int) -> np.ndarray:
-    """Q4_K weights [n, k] with the magnitudes of real checkpoints: d and dmin
-    around 2^-9 .. 2^-6, uniform 6-bit scales / mins and nibbles.  Built with
-    numpy in bulk (random bytes for the scale and nibble fields are valid
-    Q4_K blocks)."""
-    rng = np.random.default_rng(seed)
-    blocks = n * (k // SUPER)
-    out = rng.integers(0, 256, (blocks, Q4_K_BYTES), dtype=np.uint8)
-    d = (rng.uniform(2.0 ** -9, 2.0 ** -6, blocks) * rng.choice([-1.0, 1.0], blocks)).astype(np.float16)
-    dmin = rng.uniform(2.0 ** -10, 2.0 ** -7, blocks).astype(np.float16)
-    out[:, 0:2] = d.view(np.uint8).reshape(blocks, 2)
-    out[:, 2:4] = dmin.view(np.uint8).reshape(blocks, 2)
-    return out.reshape(-1)
-
-
-def model_like_q6_k(seed: int, n: int, k: int) -> np.ndarray:
-    """Q6_K weights [n, k] with d around 2^-13 .. 2^-10 and uniform int8
-    scales, 6-bit values (any bytes are a valid Q6_K block)."""
-    rng = np.random.default_rng(seed)
-    blocks = n * (k // SUPER)
-    out = rng.integers(0, 256, (blocks, Q6_K_BYTES), dtype=np.uint8)
-    d = (rng.uniform(2.0 ** -13, 2.0 ** -10, blocks) * rng.choice([-1.0, 1.0], blocks)).astype(np.float16)
-    out[:, 208:210] = d.view(np.uint8).reshape(blocks, 2)
-    return out.reshape(-1)

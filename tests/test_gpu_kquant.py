@@ -23,7 +23,7 @@ import numpy as np
 import pytest
 
 from helpers import bits_to_f32
-from kquant_blocks import Q4_K_BYTES, Q6_K_BYTES, SUPER, model_like_q4_k, model_like_q6_k, random_q4_k, random_q6_k
+from kquant_blocks import Q4_K_BYTES, Q6_K_BYTES, SUPER, random_q4_k, random_q6_k
 from mote_amd import ops, workloads as wl
 from mote_amd.device import DeviceBuffer
 
@@ -107,15 +107,15 @@ def _judge(oracle, name, x_bits, w, m, n, k):
     return y64, max_w, max_x
 
 
-def _run(stream, name, x_bits, w, m, n, k, f16_out=False, w_offset=0):
-    xb = DeviceBuffer(x_bits.nbytes)
-    xb.upload(x_bits)
+def _run(stream, name, x_bits, w, m, n, k, f16_out=False, w_offset=0, x_offset=0):
+    xb = DeviceBuffer(x_bits.nbytes + x_offset)
+    xb.upload(x_bits, offset=x_offset)
     wb = DeviceBuffer(w.nbytes + w_offset)
     wb.upload(w, offset=w_offset)
     out_bytes = m * n * (2 if f16_out else 4)
     yb = DeviceBuffer(out_bytes)
     yb.upload(np.full(out_bytes, 0xA5, dtype=np.uint8))  # sentinel: every element must be written
-    FORMATS[name][3 if f16_out else 2](xb.ptr, wb.ptr + w_offset, yb.ptr, m, n, k, stream)
+    FORMATS[name][3 if f16_out else 2](xb.ptr + x_offset, wb.ptr + w_offset, yb.ptr, m, n, k, stream)
     stream.synchronize()
     y = yb.download(np.uint16 if f16_out else np.float32)
     return (bits_to_f32(y) if f16_out else y).reshape(m, n).astype(np.float64)
@@ -145,6 +145,14 @@ SHAPES = [
     (2, 96, 14336),
     (8, 40, 14336),
     (1, 24, 36864),
+    # the ring kernel's K slices: 2, 4 and 8 ways, Q6_K slices padded to 8
+    # blocks (10 blocks per slice -> an empty fourth slice at K = 10240)
+    (1, 33, 8192),
+    (3, 70, 10240),
+    (2, 45, 20480),
+    (1, 18, 28672),
+    (4, 1000, 4096),
+    (5, 12, 6144),
 ]
 
 
@@ -152,13 +160,26 @@ SHAPES = [
 @pytest.mark.parametrize("m,n,k", SHAPES)
 def test_linear(stream, oracle, name, m, n, k):
     seed = 600 + m * 7 + n + k
-    w = (model_like_q4_k if name == "q4_k" else model_like_q6_k)(seed, n, k)
+    w = (wl.q4_k_weights if name == "q4_k" else wl.q6_k_weights)(seed, n, k)
     x = wl.normal_f16(wl.seed_for(31, seed), m * k)
     y64, max_w, max_x = _judge(oracle, name, x, w, m, n, k)
     y = _run(stream, name, x, w, m, n, k)
     _check(y, y64, k, max_w, max_x, what=f"{name} {m}x{n}x{k} f32")
     y16 = _run(stream, name, x, w, m, n, k, f16_out=True)
     _check(y16, y64, k, max_w, max_x, 2.0 ** -11, what=f"{name} {m}x{n}x{k} f16")
+
+
+@pytest.mark.parametrize("name", list(FORMATS))
+@pytest.mark.parametrize("m,n,k", [(1, 300, 4096), (2, 64, 14336), (4, 50, 8192), (3, 20, 2048)])
+def test_linear_unaligned_activations(stream, oracle, name, m, n, k):
+    """Activations off the 16-byte grid take the LDS-staged kernel instead of
+    the ring kernel (which loads a lane's activations 16 bytes at a time):
+    the same shapes judged the same way."""
+    seed = 700 + m + n + k
+    w = (wl.q4_k_weights if name == "q4_k" else wl.q6_k_weights)(seed, n, k)
+    x = wl.normal_f16(wl.seed_for(34, seed), m * k)
+    y64, max_w, max_x = _judge(oracle, name, x, w, m, n, k)
+    _check(_run(stream, name, x, w, m, n, k, x_offset=2), y64, k, max_w, max_x, what=f"{name} x at 2 mod 16")
 
 
 @pytest.mark.parametrize("name", list(FORMATS))
@@ -175,7 +196,7 @@ def test_linear_every_finite_scale(stream, oracle, name):
 
 def test_q6_k_weights_at_two_byte_offset(stream, oracle):
     m, n, k = 2, 50, 1280
-    w = model_like_q6_k(611, n, k)
+    w = wl.q6_k_weights(611, n, k)
     x = wl.normal_f16(wl.seed_for(33, 1), m * k)
     y64, max_w, max_x = _judge(oracle, "q6_k", x, w, m, n, k)
     _check(_run(stream, "q6_k", x, w, m, n, k, w_offset=2), y64, k, max_w, max_x, what="q6_k at 2 mod 4")
