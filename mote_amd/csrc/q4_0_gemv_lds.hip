@@ -24,7 +24,7 @@
 // Grid: one workgroup of 8 waves per CU (more measured slower: the LDS ring of
 // 16 waves per CU puts too many rows in flight); wave g walks rows g, g + T,
 // ... (T waves in the grid).  R ring slots, D rows in flight ahead of the
-// one being computed.  Measured on MI355X (K = 4096): N = 14336 7.27 us
+// one being computed, none past the wave's last row.  Measured on MI355X (K = 4096): N = 14336 7.27 us
 // (the pair-load kernel: 7.62), 11008 6.23 (7.07), 6144 4.62 (5.14), 4096
 // 3.90 (4.22), 1024 3.12 (3.51).
 #include "common.hpp"
@@ -98,7 +98,7 @@ template <int R, int D, int LOADS, typename OutT>
 __global__ __launch_bounds__(kThreads) void gemv_lds_kernel(const uint16_t* __restrict__ x,
                                                            const uint8_t* __restrict__ w, OutT* __restrict__ y,
                                                            uint32_t N, uint32_t K, uint32_t total_groups) {
-    static_assert(D >= 1 && D < R, "the ring holds the rows in flight and the one computed");
+    static_assert(D >= 1 && D <= 2 && D < R, "the ring holds the rows in flight and the one computed");
     extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];     // [waves][R][row bytes]
     __shared__ __attribute__((aligned(16))) uint8_t xs[kMaxK * 2];        // x, contiguous
     const int tid = static_cast<int>(threadIdx.x);
@@ -114,9 +114,8 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_kernel(const uint16_t* __re
     const uint32_t pc = min(static_cast<uint32_t>(lane), npairs - 1);
     const uint32_t keep = static_cast<uint32_t>(lane) < npairs ? 0xFFFFFFFFu : 0u;  // NaN-safe drop of idle lanes
 
-    // Row jj of this wave (clamped to its last row: loads past it re-read a
-    // row and are never used) into ring slot `slot`: chunk 64 i + lane per
-    // instruction, the last instruction's lanes past the row idle.
+    // Row jj (< nrows) of this wave into ring slot `slot`: chunk 64 i + lane
+    // per instruction, the last instruction's lanes past the row idle.
     auto load_row = [&](uint32_t jj, uint32_t slot) {
         const uint8_t* src = w + static_cast<size_t>(min(g + jj * total_groups, last)) * row_bytes;
 #pragma unroll
@@ -137,11 +136,18 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_kernel(const uint16_t* __re
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int d = 0; d < D; ++d) load_row(static_cast<uint32_t>(d), static_cast<uint32_t>(d));
+    for (int d = 0; d < D; ++d)
+        if (static_cast<uint32_t>(d) < nrows) load_row(static_cast<uint32_t>(d), static_cast<uint32_t>(d));
     __builtin_amdgcn_sched_barrier(0);
-    // vmcnt counts in issue order: at most D rows' loads outstanding means
-    // this wave's x chunk has landed; the barrier then covers every wave's.
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * D));
+    // vmcnt counts in issue order: no more than this wave's first rows'
+    // loads outstanding means its x chunk has landed; the barrier then covers
+    // every wave's.
+    if (nrows >= static_cast<uint32_t>(D))
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * D));
+    else if (D > 1 && nrows == 1)
+        __builtin_amdgcn_s_waitcnt(0x0F70 | LOADS);
+    else
+        __builtin_amdgcn_s_waitcnt(0x0F70);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 
@@ -169,8 +175,16 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_kernel(const uint16_t* __re
     // rows and at the end.
     float mine = 0.0f;
     for (uint32_t j = 0; j < nrows; ++j) {
-        load_row(j + D, (j + D) % R);
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * D));  // row j has landed (D rows' loads left)
+        // Rows are loaded only up to the wave's last, so the loads left in
+        // flight once row j has landed shrink at the end (D <= 2).
+        if (j + D < nrows) {
+            load_row(j + D, (j + D) % R);
+            __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * D));
+        } else if (D > 1 && j + 1 < nrows) {
+            __builtin_amdgcn_s_waitcnt(0x0F70 | LOADS);
+        } else {
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+        }
         const uint32_t* pr = reinterpret_cast<const uint32_t*>(ring + (j % R) * row_bytes + pc * kPairBytes);
         uint32_t raw[9];
 #pragma unroll
@@ -184,9 +198,6 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_kernel(const uint16_t* __re
                 y[g + (first + static_cast<uint32_t>(lane)) * total_groups] = to_out<OutT>(1048576.0f * mine);
         }
     }
-    // The loads issued past the last row still write this workgroup's LDS:
-    // they land before the waves exit.
-    __builtin_amdgcn_s_waitcnt(0x0F70);
 }
 
 template <int R, int D>
