@@ -143,6 +143,12 @@ int mote_q4_0_dispatch_create(void** handle);
 void mote_q4_0_dispatch_destroy(void* handle);
 const char* mote_q4_0_dispatch_last_error(void* handle);
 int mote_q4_0_dispatch_set_autotune(void* handle, int enabled);
+/* Split K (K parts of one tile computed by different workgroups): enabled,
+ * the tiles kernel adds the parts itself, the last workgroup of a tile to
+ * finish summing them in part order (write-through partial stores and a
+ * per-tile arrival counter); disabled (the default, faster on MI355X), a
+ * second kernel adds them in the same order.  Results are bit-identical. */
+int mote_q4_0_dispatch_set_splitk_fold(void* handle, int enabled);
 /* Forces one variant by name (NULL or "" clears); tests use it to run every
  * kernel on the same problem. */
 int mote_q4_0_dispatch_force_variant(void* handle, const char* name);

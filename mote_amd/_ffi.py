@@ -63,6 +63,7 @@ SIGNATURES = {
     "mote_q4_0_dispatch_destroy": (None, [_P]),
     "mote_q4_0_dispatch_last_error": (ctypes.c_char_p, [_P]),
     "mote_q4_0_dispatch_set_autotune": (_I, [_P, _I]),
+    "mote_q4_0_dispatch_set_splitk_fold": (_I, [_P, _I]),
     "mote_q4_0_dispatch_force_variant": (_I, [_P, ctypes.c_char_p]),
     "mote_q4_0_dispatch_linear": (_I, [_P, _P, _P, _P, _U64, _U64, _U64, _I, _P]),
     "mote_q4_0_dispatch_linear_q8_0": (_I, [_P, _P, _P, _P, _U64, _U64, _U64, _I, _P]),

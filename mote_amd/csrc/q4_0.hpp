@@ -24,7 +24,17 @@ struct Problem {
     // the stream's buffer from the library's scratch pool.
     float* scratch = nullptr;
     size_t scratch_bytes = 0;
+    // Split K: the tiles kernel adds the K parts itself (the last workgroup
+    // of a tile to finish) instead of a second kernel.  Off by default: on
+    // MI355X the fold measured slower (its workgroups wait for their
+    // write-through partial stores and the arrival atomic before exiting).
+    bool splitk_fold = false;
 };
+
+// Split-K scratch layout: kSplitKCounterBytes of per-tile arrival counters
+// (zero between calls: the workgroup that adds a tile's parts resets its
+// counter) followed by the partial tiles.
+constexpr size_t kSplitKCounterBytes = 64 * 1024;
 
 enum class Kind : int { Gemv = 0, Mfma = 1, Generic = 2, GateUpMfma = 3, GateUpGeneric = 4, GemvRows = 5,
                         GemvStream = 6, SkinnyMfma = 7, Q8Stream = 8, Q8Generic = 9, GateUpSkinny = 10,

@@ -47,6 +47,7 @@ struct Dispatcher {
     std::mutex mutex;
     std::map<Key, const Variant*> plans;
     bool autotune = false;
+    bool splitk_fold = false;
     std::string forced;
     std::string last_error;
 };
@@ -504,8 +505,10 @@ int fail(Dispatcher* d, hipError_t status, const std::string& message) {
     return static_cast<int>(status);
 }
 
-int run(Dispatcher& d, const Problem& p, Op op) {
+int run(Dispatcher& d, const Problem& problem, Op op) {
     std::lock_guard<std::mutex> lock(d.mutex);
+    Problem p = problem;
+    p.splitk_fold = d.splitk_fold;
     const Variant* v = nullptr;
     if (!d.forced.empty()) {
         v = find_variant(d.forced);
@@ -546,8 +549,10 @@ int run(Dispatcher& d, const Problem& p, Op op) {
 // The launch of the entry point that allocates nothing: the cached plan, or
 // on the first call of a shape the shape heuristic (never the autotuner,
 // which would create events and synchronise), then the launch.
-int run_no_alloc(Dispatcher& d, const Problem& p) {
+int run_no_alloc(Dispatcher& d, const Problem& problem) {
     std::lock_guard<std::mutex> lock(d.mutex);
+    Problem p = problem;
+    p.splitk_fold = d.splitk_fold;
     const Variant* v = nullptr;
     if (!d.forced.empty()) {
         v = find_variant(d.forced);
@@ -802,6 +807,14 @@ MOTE_EXPORT int mote_q4_0_dispatch_set_autotune(void* handle, int enabled) noexc
     if (!d) return hipErrorInvalidValue;
     std::lock_guard<std::mutex> lock(d->mutex);
     d->autotune = enabled != 0;
+    return 0;
+}
+
+MOTE_EXPORT int mote_q4_0_dispatch_set_splitk_fold(void* handle, int enabled) noexcept {
+    auto* d = static_cast<mote::q4_0::Dispatcher*>(handle);
+    if (!d) return hipErrorInvalidValue;
+    std::lock_guard<std::mutex> lock(d->mutex);
+    d->splitk_fold = enabled != 0;
     return 0;
 }
 

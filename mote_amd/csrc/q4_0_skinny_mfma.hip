@@ -52,6 +52,38 @@ __device__ __forceinline__ uint32_t pick(const uint32_t* x, int a, int b) {
     return __builtin_amdgcn_perm(x[b >> 1], x[a >> 1], hi | lo);
 }
 
+// Split-K epilogue: y[i] = sum over the K parts of part[k][i], in part order
+// (deterministic), converted to the output type; gate/up (GU): silu of the
+// gate sum times the up sum, the up planes following the kparts gate planes.
+// Up to kMaxParts parts every load of an element is issued before the first
+// add (one memory latency instead of one per part); more parts loop.
+constexpr uint32_t kMaxParts = 16;
+
+// SYS: the loads are system-scope (they miss in every cache and read what the
+// write-through partial stores of other workgroups left in memory).
+template <bool SYS = false>
+__device__ __forceinline__ float load_part(const float* p, uint64_t i) {
+    if constexpr (SYS) return __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return p[i];
+}
+
+template <bool SYS = false>
+__device__ __forceinline__ float sum_parts(const float* __restrict__ p, uint32_t kparts, uint64_t count, uint64_t i) {
+    if (kparts > kMaxParts) {
+        float s = load_part<SYS>(p, i);
+        for (uint32_t k = 1; k < kparts; ++k) s += load_part<SYS>(p, static_cast<uint64_t>(k) * count + i);
+        return s;
+    }
+    float v[kMaxParts];
+#pragma unroll
+    for (uint32_t k = 0; k < kMaxParts; ++k) v[k] = k < kparts ? load_part<SYS>(p, static_cast<uint64_t>(k) * count + i) : 0.0f;
+    float s = v[0];
+#pragma unroll
+    for (uint32_t k = 1; k < kMaxParts; ++k)
+        if (k < kparts) s += v[k];
+    return s;
+}
+
 template <int KS, int STEPS, int MT, int D, int RT, bool TR, typename OutT, int LAZY = 0, bool XC = false,
           bool GU = false, bool Q8 = false, bool XW = false, bool SK = false>
 __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __restrict__ x,
@@ -61,7 +93,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
                                                              uint32_t N, uint32_t K,
                                                              uint32_t token_groups, uint32_t items,
                                                              uint32_t groups_per_xcd, float* __restrict__ kpartial,
-                                                             uint32_t kparts) {
+                                                             uint32_t kparts, uint32_t* __restrict__ tile_count) {
     // Transposed loads: wave-private staging of the raw pairs, [row tile][row]
     // [pair of the slice], rows padded by one dword so the 16 rows read by an
     // MFMA operand fall on distinct banks.
@@ -110,7 +142,10 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     // token group and one K part.  Split K (SK): K is cut into kparts parts of
     // KS x STEPS x 256; each item writes its part's partial sums to
     // `kpartial` ([kparts][M][N] f32; gate/up: the gate planes, then the up
-    // planes), which a second kernel adds in part order.
+    // planes), which are added in part order either by the last workgroup of
+    // the tile to finish (tile_count non-null: one arrival counter per
+    // (row tile, token group), zero on entry and left zero) or by a second
+    // kernel.
     static_assert(!GU || RT == 2, "gate/up items are one gate and one up row tile");
     constexpr uint32_t kItemRows = GU ? 16u : 16u * RT;
     const uint32_t combos = token_groups * kparts;
@@ -180,6 +215,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     // (every CU needs all of x; with weight loads queued ahead of it, its
     // broadcast took twice as long).
     static_assert(!XW || LAZY > 0, "x first is a variant of the deferred reduction");
+    static_assert(!SK || LAZY > 0, "split K adds its parts in the deferred reduction's epilogue");
     if constexpr (!XW) load_item(first, buf0);
     // Activations of this wave's K slice for the workgroup's MT token tiles.
     // Tokens past M read row M - 1: a token only feeds its own output column
@@ -383,8 +419,19 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
     auto store = [&](uint32_t m, uint32_t n, int tile, int row, int tok) {
         if constexpr (SK) {
             float* dst = kpartial + (static_cast<size_t>(kpart) * M + m) * N + n;
-            dst[0] = tile_sum(tile, row, tok);
-            if constexpr (GU) dst[static_cast<size_t>(kparts) * M * N] = tile_sum(tile + MT, row, tok);
+            const float g = tile_sum(tile, row, tok);
+            const float u = GU ? tile_sum(tile + MT, row, tok) : 0.0f;
+            float* dst_u = dst + static_cast<size_t>(kparts) * M * N;
+            if (tile_count != nullptr) {
+                // folded epilogue: system-scope stores write through every
+                // cache, so the workgroup that adds the parts can read them
+                // from memory without a cache writeback
+                __hip_atomic_store(dst, g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                if constexpr (GU) __hip_atomic_store(dst_u, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            } else {
+                dst[0] = g;
+                if constexpr (GU) dst_u[0] = u;
+            }
         } else {
             float v = tile_sum(tile, row, tok);
             if constexpr (GU) v = silu(v) * tile_sum(tile + MT, row, tok);
@@ -475,6 +522,60 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
                 if (n < N && m < M) store(m, n, (i * RT + rt) * MT + mt, row, tok);
             }
         }
+        if constexpr (SK) {
+            if (tile_count != nullptr) {  // uniform
+                // This workgroup's partial tiles are stored with system-scope
+                // (write-through) stores: once every wave's stores have
+                // completed (vmcnt 0, then the barrier) they are in memory,
+                // and the workgroup counts itself in at each of its items'
+                // tiles with a system-scope atomic.  The last of a tile's
+                // kparts workgroups reads the parts with system-scope loads,
+                // adds them in part order (as the second kernel would) and
+                // resets the tile's counter for the next call.  (Agent-scope
+                // release and acquire fences would instead write back and
+                // invalidate the whole L2 of the XCD, per wave: measured over
+                // six times slower than the second kernel.)
+                __shared__ uint32_t last_of[LAZY];
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are done
+                __syncthreads();
+                const uint32_t tok_group = combo % token_groups;
+                if (tid < LAZY) {
+                    const uint32_t it = first + static_cast<uint32_t>(tid) * groups;
+                    uint32_t last = 0;
+                    if (it < items) {
+                        const uint32_t old = __hip_atomic_fetch_add(&tile_count[(it / combos) * token_groups + tok_group],
+                                                                    1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                        last = old + 1u == kparts ? 1u : 0u;
+                    }
+                    last_of[tid] = last;
+                }
+                __syncthreads();
+                uint32_t any = 0;
+#pragma unroll
+                for (int i = 0; i < LAZY; ++i) any |= last_of[i];
+                if (any != 0) {  // uniform
+                    const uint64_t count = static_cast<uint64_t>(M) * N;
+#pragma unroll
+                    for (int i = 0; i < LAZY; ++i) {
+                        if (last_of[i] == 0) continue;  // uniform
+                        const uint32_t it = first + static_cast<uint32_t>(i) * groups;
+                        for (int o = tid; o < static_cast<int>(kItemRows) * 16 * MT; o += KS * 64) {
+                            const uint32_t n = rows_of(it) + static_cast<uint32_t>(o) % kItemRows;
+                            const uint32_t m = tok0 + static_cast<uint32_t>(o) / kItemRows;
+                            if (n >= N || m >= M) continue;
+                            const uint64_t e = static_cast<uint64_t>(m) * N + n;
+                            float v = sum_parts<true>(kpartial, kparts, count, e);
+                            if constexpr (GU)
+                                v = silu(v) * sum_parts<true>(kpartial + static_cast<uint64_t>(kparts) * count, kparts, count, e);
+                            y[e] = to_out<OutT>(v);
+                        }
+                        if (tid == 0)
+                            __hip_atomic_store(&tile_count[(it / combos) * token_groups + tok_group], 0u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_SYSTEM);
+                    }
+                }
+            }
+        }
     } else if constexpr (TR && D == 1) {
         // The stage frees the registers as soon as an item is written to LDS,
         // so one register buffer already keeps the next item in flight.
@@ -498,29 +599,6 @@ __global__ __launch_bounds__(KS * 64) void skinny_mfma_kernel(const uint16_t* __
                 process(item + groups, buf1, item + 3 * groups, std::true_type{});
         }
     }
-}
-
-// Split-K epilogue: y[i] = sum over the K parts of part[k][i], in part order
-// (deterministic), converted to the output type; gate/up (GU): silu of the
-// gate sum times the up sum, the up planes following the kparts gate planes.
-// Up to kMaxParts parts every load of an element is issued before the first
-// add (one memory latency instead of one per part); more parts loop.
-constexpr uint32_t kMaxParts = 16;
-
-__device__ __forceinline__ float sum_parts(const float* __restrict__ p, uint32_t kparts, uint64_t count, uint64_t i) {
-    if (kparts > kMaxParts) {
-        float s = p[i];
-        for (uint32_t k = 1; k < kparts; ++k) s += p[static_cast<uint64_t>(k) * count + i];
-        return s;
-    }
-    float v[kMaxParts];
-#pragma unroll
-    for (uint32_t k = 0; k < kMaxParts; ++k) v[k] = k < kparts ? p[static_cast<uint64_t>(k) * count + i] : 0.0f;
-    float s = v[0];
-#pragma unroll
-    for (uint32_t k = 1; k < kMaxParts; ++k)
-        if (k < kparts) s += v[k];
-    return s;
 }
 
 template <typename OutT, bool GU>
@@ -565,35 +643,45 @@ hipError_t launch_skinny(const Problem& p) {
     const uint32_t per_xcd = groups / 8u;
     const dim3 grid(groups), block(KS * 64);
     float* part = nullptr;
+    uint32_t* counters = nullptr;
+    bool fold = false;
     const uint64_t count = static_cast<uint64_t>(p.M) * p.N;
-    // Split K: the stream's scratch lock is held until both kernels are queued
-    // (the lease goes out of scope at return).
+    // Split K: the stream's scratch lock is held until every kernel of the
+    // call is queued (the lease goes out of scope at return).
     ScratchPool::Lease lease;
     if constexpr (SK) {
-        const size_t need = count * kparts * (GU ? 2 : 1) * sizeof(float);
+        const size_t need = kSplitKCounterBytes + count * kparts * (GU ? 2 : 1) * sizeof(float);
+        uint8_t* base = nullptr;
         if (p.scratch != nullptr) {  // the caller's buffer: too small is an error, before any launch
             if (need > p.scratch_bytes) return hipErrorOutOfMemory;
-            part = p.scratch;
+            base = reinterpret_cast<uint8_t*>(p.scratch);
         } else {
             const hipError_t e = acquire_scratch(p.stream, need, &lease);
             if (e != hipSuccess) return e;
-            part = static_cast<float*>(lease.ptr());
+            base = static_cast<uint8_t*>(lease.ptr());
+            if (lease.fresh()) {  // a new buffer: its counters start at zero
+                const hipError_t z = launch_zero_fill(base, kSplitKCounterBytes / 4, OutType::F32, p.stream);
+                if (z != hipSuccess) return z;
+            }
         }
+        part = reinterpret_cast<float*>(base + kSplitKCounterBytes);
+        fold = p.splitk_fold && static_cast<uint64_t>(row_tiles) * token_groups <= kSplitKCounterBytes / 4;
+        if (fold) counters = reinterpret_cast<uint32_t*>(base);
     }
     if (p.out == OutType::F32) {
         hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, float, LAZY, XC, GU, Q8, XW, SK>), grid,
                            block, 0, p.stream, static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<const uint8_t*>(p.w_up), static_cast<float*>(p.y), p.M, p.N, p.K,
-                           token_groups, items, per_xcd, part, kparts);
+                           token_groups, items, per_xcd, part, kparts, counters);
     } else {
         hipLaunchKernelGGL((skinny_mfma_kernel<KS, STEPS, MT, D, RT, TR, _Float16, LAZY, XC, GU, Q8, XW, SK>), grid,
                            block, 0, p.stream, static_cast<const uint16_t*>(p.x), static_cast<const uint8_t*>(p.w),
                            static_cast<const uint8_t*>(p.w_up), static_cast<_Float16*>(p.y), p.M, p.N, p.K,
-                           token_groups, items, per_xcd, part, kparts);
+                           token_groups, items, per_xcd, part, kparts, counters);
     }
     if constexpr (SK) {
         const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
+        if (e != hipSuccess || fold) return e;
         const uint64_t blocks64 = (count + 255) / 256;
         const dim3 rgrid(static_cast<uint32_t>(blocks64 < 2048 ? blocks64 : 2048)), rblock(256);
         if (p.out == OutType::F32)
@@ -630,8 +718,8 @@ hipError_t launch_skinny(const Problem& p) {
     Variant{"q8_skinny_k" #KS "_s" #STEPS "_t" #MT "_d1_l" #L SUFFIX "_w", Kind::Q8Skinny, KS, STEPS, MT, \
             &launch_skinny<KS, STEPS, MT, 1, 1, 1, true, L, XC, false, true, true>}
 // Split K (_sk): K any multiple of KS x STEPS x 256, cut into that many
-// parts; partial tiles in a per-stream scratch buffer, added by a second
-// kernel.
+// parts; partial tiles in a per-stream scratch buffer, added in part order by
+// the last workgroup of each tile (or, with the fold off, a second kernel).
 #define MOTE_SKINNY_SK(KS, STEPS, MT, L, SUFFIX)                                                   \
     Variant{"skinny_mfma_k" #KS "_s" #STEPS "_t" #MT "_d1_g1_r1_tr_l" #L SUFFIX "_w_sk", Kind::SkinnyMfma, KS, \
             STEPS, MT, &launch_skinny<KS, STEPS, MT, 1, 1, 1, true, L, true, false, false, true, true>}

@@ -53,12 +53,16 @@ class ScratchPool {
        public:
         void* ptr() const { return ptr_; }
         bool held() const { return lock_.owns_lock(); }
+        // Whether this acquire allocated the buffer (its contents are then
+        // undefined; the caller clears what must start at zero).
+        bool fresh() const { return fresh_; }
 
        private:
         friend class ScratchPool;
         std::shared_ptr<Entry> entry_;
         std::unique_lock<std::mutex> lock_;
         void* ptr_ = nullptr;
+        bool fresh_ = false;
     };
 
     // Blocks while another lease of the same (device, stream) is held.
@@ -72,6 +76,7 @@ class ScratchPool {
             entry = slot;
         }
         std::unique_lock<std::mutex> lock(entry->mu);
+        lease->fresh_ = false;
         if (entry->size < bytes) {
             std::size_t want = std::size_t{1} << 20;
             while (want < bytes) want <<= 1;
@@ -81,6 +86,7 @@ class ScratchPool {
             if (entry->ptr != nullptr) entry->retired.push_back(entry->ptr);
             entry->ptr = fresh;
             entry->size = want;
+            lease->fresh_ = true;
         }
         lease->ptr_ = entry->ptr;
         lease->entry_ = std::move(entry);

@@ -131,6 +131,9 @@ class Q4_0Dispatch:
     def set_autotune(self, enabled: bool) -> None:
         self._check(lib().mote_q4_0_dispatch_set_autotune(self.handle, int(enabled)), "set autotune")
 
+    def set_splitk_fold(self, enabled: bool) -> None:
+        self._check(lib().mote_q4_0_dispatch_set_splitk_fold(self.handle, int(enabled)), "set split-K fold")
+
     def force(self, name: str | None) -> None:
         self._check(
             lib().mote_q4_0_dispatch_force_variant(self.handle, name.encode() if name else None),

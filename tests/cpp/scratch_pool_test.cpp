@@ -123,17 +123,20 @@ void test_growth_retires_and_release_frees_everything() {
         {
             ScratchPool::Lease l;
             CHECK(pool.acquire(0, s, 1, &l) == 0);
+            CHECK(l.fresh());  // allocated by this acquire
             first = l.ptr();
         }
         {
             ScratchPool::Lease l;  // fits the 1 MiB minimum: same buffer
             CHECK(pool.acquire(0, s, 1u << 20, &l) == 0);
             CHECK(l.ptr() == first);
+            CHECK(!l.fresh());
         }
         {
             ScratchPool::Lease l;  // grows: a new buffer, the old one retired
             CHECK(pool.acquire(0, s, (1u << 20) + 1, &l) == 0);
             CHECK(l.ptr() != first);
+            CHECK(l.fresh());
         }
         CHECK(g_allocs - allocs0 == 2);
         CHECK(g_frees - frees0 == 0);

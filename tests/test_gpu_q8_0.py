@@ -216,7 +216,8 @@ def test_every_q8_prefill_variant(stream, oracle, variant):
 
 @pytest.mark.parametrize("m,k,n", [(1, 4096, 14336), (1, 14336, 4096), (2, 4096, 4096), (4, 4096, 6144),
                                    (3, 4096, 4096), (8, 4096, 4096), (16, 4096, 14336), (32, 4096, 14336),
-                                   (64, 4096, 14336), (128, 4096, 14336), (512, 4096, 14336)])
+                                   (64, 4096, 14336), (128, 4096, 14336), (512, 4096, 14336),
+                                   (3, 8192, 8192), (3, 14336, 4096)])
 def test_llama_shapes_through_the_default_entry_points(stream, oracle, m, k, n):
     x = normal_x(wl.seed_for(22, m), m, k)
     w = weights(wl.seed_for(22, n), n, k)

@@ -2,11 +2,14 @@
 K slice: the MLP down projection, K = 14336, among others; the fused gate/up at
 K = 8192) against the oracle.
 
-The split-K tiles cut K into parts, write each part's partial tile to a
-per-stream scratch buffer and add the parts in a second kernel, in part order;
-the products are rounded once to binary16 before the MFMA, so the check is the
+The split-K tiles cut K into parts and write each part's partial tile to a
+per-stream scratch buffer; a second kernel adds the parts in part order, or,
+with the fold turned on on a dispatch handle, the last workgroup of a tile to
+finish (counted by a per-tile arrival counter) does, in the same order.  The
+products are rounded once to binary16 before the MFMA, so the check is the
 path's tolerance (|y - y64| <= 1e-3 |y64| or <= 2e-3 sqrt(K) max|d| max|x|,
-y64 the f64-accumulated oracle), and two runs must agree bit for bit.
+y64 the f64-accumulated oracle); two runs, and the two epilogues, must agree
+bit for bit.
 """
 
 from __future__ import annotations
@@ -60,6 +63,36 @@ def test_every_split_k_variant(stream, oracle, variant):
     assert np.array_equal(y, run_linear(stream, x, w, m, n, k, dispatch=d)), "split-K result differs between runs"
     y16 = run_linear(stream, x, w, m, n, k, dispatch=d, f16_out=True)
     check_against_oracle(oracle, y16, x, w, m, n, k, f16_out=True, what=f"{variant} f16")
+
+
+@pytest.mark.parametrize("variant", SPLIT_K + Q8_SPLIT_K + GATE_UP_SPLIT_K)
+def test_fold_matches_the_second_kernel(stream, variant):
+    """The folded epilogue and the second kernel add the same parts in the
+    same order: bitwise equal outputs, over consecutive calls of different
+    shapes on one stream (each call must leave every tile counter at zero for
+    the next; the last call repeats the first)."""
+    fold, kernel = ops.Q4_0Dispatch(), ops.Q4_0Dispatch()
+    fold.force(variant)
+    fold.set_splitk_fold(True)
+    kernel.force(variant)
+    span = _slice(variant)
+    for i, (m, n, parts) in enumerate([(3, 100, 2), (17, 130, 3), (64, 80, 7), (33, 1000, 2), (3, 100, 2)]):
+        k = span * parts
+        x = normal_x(wl.seed_for(46, m), m, k)
+        f16_out = i == 1
+        if variant.startswith("gateup_"):
+            wg, wu = q4_weights(wl.seed_for(46, 100 + n), n, k), q4_weights(wl.seed_for(46, 200 + n), n, k)
+            a = run_gate_up(stream, x, wg, wu, m, n, k, dispatch=fold, f16_out=f16_out)
+            b = run_gate_up(stream, x, wg, wu, m, n, k, dispatch=kernel, f16_out=f16_out)
+        elif variant.startswith("q8_"):
+            w = q8.weights(wl.seed_for(46, 300 + n), n, k)
+            a = q8.run(stream, x, w, m, n, k, dispatch=fold, f16_out=f16_out)
+            b = q8.run(stream, x, w, m, n, k, dispatch=kernel, f16_out=f16_out)
+        else:
+            w = q4_weights(wl.seed_for(46, 400 + n), n, k)
+            a = run_linear(stream, x, w, m, n, k, dispatch=fold, f16_out=f16_out)
+            b = run_linear(stream, x, w, m, n, k, dispatch=kernel, f16_out=f16_out)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{variant} {m}x{n}x{k}: the epilogues differ"
 
 
 @pytest.mark.parametrize("m", [2, 3, 8, 16, 32, 64])
