@@ -98,7 +98,7 @@ template <int R, int D, int LOADS, typename OutT>
 __global__ __launch_bounds__(kThreads) void gemv_lds_kernel(const uint16_t* __restrict__ x,
                                                            const uint8_t* __restrict__ w, OutT* __restrict__ y,
                                                            uint32_t N, uint32_t K, uint32_t total_groups) {
-    static_assert(D >= 1 && D <= 2 && D < R, "the ring holds the rows in flight and the one computed");
+    static_assert(D >= 1 && D <= 3 && D < R, "the ring holds the rows in flight and the one computed");
     extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];     // [waves][R][row bytes]
     __shared__ __attribute__((aligned(16))) uint8_t xs[kMaxK * 2];        // x, contiguous
     const int tid = static_cast<int>(threadIdx.x);
@@ -135,19 +135,21 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_kernel(const uint16_t* __re
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
+    // Waits until at most `rows` rows' loads (rows <= D, wave-uniform) are
+    // outstanding (vmcnt counts in issue order).
+    auto wait_rows = [&](uint32_t rows) {
+        if (rows >= 3 && D >= 3) __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * 3));
+        else if (rows == 2 && D >= 2) __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * 2));
+        else if (rows == 1) __builtin_amdgcn_s_waitcnt(0x0F70 | LOADS);
+        else __builtin_amdgcn_s_waitcnt(0x0F70);
+    };
 #pragma unroll
     for (int d = 0; d < D; ++d)
         if (static_cast<uint32_t>(d) < nrows) load_row(static_cast<uint32_t>(d), static_cast<uint32_t>(d));
     __builtin_amdgcn_sched_barrier(0);
-    // vmcnt counts in issue order: no more than this wave's first rows'
-    // loads outstanding means its x chunk has landed; the barrier then covers
-    // every wave's.
-    if (nrows >= static_cast<uint32_t>(D))
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * D));
-    else if (D > 1 && nrows == 1)
-        __builtin_amdgcn_s_waitcnt(0x0F70 | LOADS);
-    else
-        __builtin_amdgcn_s_waitcnt(0x0F70);
+    // no more than this wave's first rows' loads outstanding means its x
+    // chunk has landed; the barrier then covers every wave's
+    wait_rows(nrows < static_cast<uint32_t>(D) ? nrows : static_cast<uint32_t>(D));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 
@@ -176,14 +178,12 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_kernel(const uint16_t* __re
     float mine = 0.0f;
     for (uint32_t j = 0; j < nrows; ++j) {
         // Rows are loaded only up to the wave's last, so the loads left in
-        // flight once row j has landed shrink at the end (D <= 2).
+        // flight once row j has landed shrink at the end.
         if (j + D < nrows) {
             load_row(j + D, (j + D) % R);
             __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * D));
-        } else if (D > 1 && j + 1 < nrows) {
-            __builtin_amdgcn_s_waitcnt(0x0F70 | LOADS);
         } else {
-            __builtin_amdgcn_s_waitcnt(0x0F70);
+            wait_rows(nrows - 1 - j);
         }
         const uint32_t* pr = reinterpret_cast<const uint32_t*>(ring + (j % R) * row_bytes + pc * kPairBytes);
         uint32_t raw[9];
