@@ -295,6 +295,28 @@ SWEEP = (
 )
 
 
+class CopyRowsCase:
+    """The probe library's row copy (one 256-thread workgroup per row), the
+    smallest kernel of the norm's launch shape."""
+
+    def __init__(self, probe, rows: int, row_bytes: int) -> None:
+        self.probe, self.rows, self.row_bytes = probe, rows, row_bytes
+        self.src = DeviceBuffer(rows * row_bytes)
+        self.src.upload(np.arange(rows * row_bytes, dtype=np.uint32).astype(np.uint8))
+        self.dst = DeviceBuffer(rows * row_bytes)
+
+    def launch(self, i: int, stream: Stream) -> None:
+        _ffi.check(self.probe.mote_probe_copy_rows(self.src.ptr, self.dst.ptr, self.rows, self.row_bytes,
+                                                   stream.handle), "copy probe")
+
+    def algorithmic_bytes(self) -> int:
+        return 2 * self.rows * self.row_bytes
+
+    def free(self) -> None:
+        self.src.free()
+        self.dst.free()
+
+
 class NormRopeCase:
     """RMSNorm, fused add + RMSNorm or q/k RoPE on the decoder-step shape: 32
     tokens, hidden 4096 (f16, eps 1e-5, weight f16(1 + 0.1 N(0,1))); RoPE on 32
@@ -427,6 +449,17 @@ def run_sweep(stream: Stream, hip: HipRuntime, steps: int, warmup: int, only: st
               f"{gbs:>9.0f}{100 * gbs / HBM_PEAK_GBS:>6.1f}%{tf:>9.1f}{100 * tf / MFMA_F16_PEAK_TFLOPS:>6.1f}%  "
               f"mote_hipblaslt_matmul_f16_f32", file=sys.stderr, flush=True)
         case.free()
+    # The floor under these launch-bound kernels: a plain copy of RMSNorm's
+    # bytes (32 rows of 8 KiB in and out) by one 256-thread workgroup per row.
+    probe = load_probe()
+    floor = CopyRowsCase(probe, NormRopeCase.TOKENS, NormRopeCase.HIDDEN * 2)
+    t = time_case(floor, stream, hip, steps, warmup)
+    us = t["kernel_ms_mean"] * 1e3
+    gbs = floor.algorithmic_bytes() / (us * 1e-6) / 1e9
+    print(f"{'copy floor':<15}{floor.rows:>5}{0:>7}{NormRopeCase.HIDDEN:>7}{us:>11.2f}{t['eager_ms_per_step'] * 1e3:>10.2f}"
+          f"{gbs:>9.0f}{100 * gbs / HBM_PEAK_GBS:>6.1f}%{0.0:>9.1f}{0.0:>6.1f}%  mote_probe_copy_rows",
+          file=sys.stderr, flush=True)
+    floor.free()
     entry = {"rmsnorm": "mote_hip_rms_norm_f16", "fused add+rmsnorm": "mote_hip_fused_add_rms_norm_f16",
              "rope q+k": "mote_hip_rope_qk_f16"}
     for kind in ("rmsnorm", "fused add+rmsnorm", "rope q+k"):
@@ -468,6 +501,8 @@ def load_probe():
     P, U32 = ctypes.c_void_p, ctypes.c_uint32
     probe.mote_probe_read_u128.restype = ctypes.c_int
     probe.mote_probe_read_u128.argtypes = [P, ctypes.c_size_t, U32, U32, U32, ctypes.c_int, P, P]
+    probe.mote_probe_copy_rows.restype = ctypes.c_int
+    probe.mote_probe_copy_rows.argtypes = [P, P, U32, U32, P]
     return probe
 
 

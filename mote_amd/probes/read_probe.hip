@@ -67,6 +67,16 @@ hipError_t by_threads(uint32_t threads, uint32_t in_flight, const void* data, ui
     }
 }
 
+// The smallest kernel of the decoder-step neighbours' shape: one 256-thread
+// workgroup per row copying its bytes (16 bytes per thread and round), no
+// arithmetic.  Its graph-replayed duration is the floor under RMSNorm and
+// RoPE at these sizes.
+__global__ __launch_bounds__(256) void copy_rows_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                        uint32_t chunks_per_row) {
+    const size_t base = static_cast<size_t>(blockIdx.x) * chunks_per_row;
+    for (uint32_t c = threadIdx.x; c < chunks_per_row; c += 256) dst[base + c] = src[base + c];
+}
+
 }  // namespace
 }  // namespace mote
 
@@ -85,4 +95,18 @@ MOTE_EXPORT int mote_probe_read_u128(const void* data, size_t bytes, uint32_t gr
     const uint64_t n16 = bytes / 16;
     return static_cast<int>(non_temporal ? mote::by_threads<true>(threads, in_flight, data, n16, grid, sink, s)
                                          : mote::by_threads<false>(threads, in_flight, data, n16, grid, sink, s));
+}
+
+// Copies rows x row_bytes bytes (row_bytes a multiple of 16, both pointers
+// 16-byte aligned, no overlap) with one 256-thread workgroup per row.
+// Status: hipError_t (1 for a bad argument).
+MOTE_EXPORT int mote_probe_copy_rows(const void* src, void* dst, uint32_t rows, uint32_t row_bytes,
+                                     void* stream) noexcept {
+    if (src == nullptr || dst == nullptr || stream == nullptr || row_bytes % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(src) % 16 != 0 || reinterpret_cast<uintptr_t>(dst) % 16 != 0)
+        return hipErrorInvalidValue;
+    if (rows == 0 || row_bytes == 0) return hipSuccess;
+    hipLaunchKernelGGL(mote::copy_rows_kernel, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const mote::u32x4*>(src), static_cast<mote::u32x4*>(dst), row_bytes / 16);
+    return static_cast<int>(hipGetLastError());
 }

@@ -209,6 +209,13 @@ def test_read_probe_is_a_separate_library(lib):
     assert fn(FAKE, 16, 1, 300, 2, 0, FAKE, STREAM) == 1
     assert fn(FAKE, 16, 1, 256, 3, 1, FAKE, STREAM) == 1
     assert fn(FAKE, 0, 1, 256, 2, 0, FAKE, STREAM) == 0  # nothing to read
+    copy = probe.mote_probe_copy_rows
+    copy.restype = ctypes.c_int
+    copy.argtypes = [P, P, U32, U32, P]
+    assert copy(None, FAKE, 1, 16, STREAM) == 1
+    assert copy(FAKE, FAKE, 1, 24, STREAM) == 1  # row bytes not a multiple of 16
+    assert copy(FAKE + 8, FAKE, 1, 16, STREAM) == 1  # misaligned
+    assert copy(FAKE, FAKE, 0, 16, STREAM) == 0  # nothing to copy
 
 
 def test_python_wrappers_raise_hip_error(lib):
