@@ -203,7 +203,98 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
     // Scales past binary16 range go through the scaled MFMA (common.hpp).
     constexpr uint32_t kBig = Q8 ? kQ8BigScale : kQ4BigScale;
     constexpr float kDown = Q8 ? kQ8BigDown : kQ4BigDown;
+    // The step of the 32 x 32 Q4_0 tiles with staging waves, software
+    // pipelined: its four k groups (block, half) run as read -> dequantise ->
+    // MFMA stages one group apart, so the LDS reads and the vector-ALU
+    // dequantisation of group g + 1 issue while the matrix core works on
+    // group g (measured 2-3 % faster than the step below at 128-512 tokens).
+    auto mma_step_pipe = [&](int buf) {
+        constexpr int NG = 4;
+        uint32_t scales[NW][TN];
+        uint32_t q[2][NW][TN];
+        f16x8 a[2][TM];
+        f16x8 b[2][NW][TN];
+        auto read_b = [&](int grp, uint32_t (&dst)[NW][TN]) {
+            const int blk = grp >> 1, g = 2 * (grp & 1) + lgrp;
+#pragma unroll
+            for (int s = 0; s < NW; ++s)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    dst[s][j] = *reinterpret_cast<const uint32_t*>(
+                        &ws[s][buf][b_base + j * T * kWRow + 4 + blk * 16 + g * 4]);
+        };
+        auto read_a = [&](int grp, f16x8 (&dst)[TM]) {
+            const int blk = grp >> 1, g = 2 * (grp & 1) + lgrp;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+                dst[i] = *reinterpret_cast<const f16x8*>(&xs[buf][a_base + i * T * kXRow + blk * 64 + g * 16]);
+        };
+        auto dequant = [&](int grp, const uint32_t (&qq)[NW][TN], f16x8 (&dst)[NW][TN]) {
+            const int blk = grp >> 1;
+#pragma unroll
+            for (int s = 0; s < NW; ++s)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const f16x2 d = as_h2(__builtin_amdgcn_perm(scales[s][j], scales[s][j],
+                                                                blk ? 0x03020302u : 0x01000100u));
+                    dst[s][j] = dequant8(qq[s][j], d, dq.c1024, dq.c64);
+                }
+        };
+#pragma unroll
+        for (int s = 0; s < NW; ++s)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                scales[s][j] = *reinterpret_cast<const uint32_t*>(&ws[s][buf][b_base + j * T * kWRow]);
+        read_b(0, q[0]);
+        read_a(0, a[0]);
+        bool big = false;
+#pragma unroll
+        for (int s = 0; s < NW; ++s)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) big = big || big_scales<kBig>(scales[s][j]);
+        // the scaled MFMA of a step with a scale past binary16 range, as below
+        const bool big_step = wave_any(big);
+        if (__builtin_expect(big_step, 0)) {
+            const f16x2 dd = {static_cast<_Float16>(kDown), static_cast<_Float16>(kDown)};
+#pragma unroll
+            for (int s = 0; s < NW; ++s)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    scales[s][j] = __builtin_bit_cast(uint32_t, as_h2(scales[s][j]) * dd);
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) acc[s][i][j] *= kDown;
+                }
+        }
+        dequant(0, q[0], b[0]);
+#pragma unroll
+        for (int grp = 0; grp < NG; ++grp) {
+            const int cur = grp & 1, nxt = cur ^ 1;
+            if (grp + 1 < NG) {
+                read_b(grp + 1, q[nxt]);
+                read_a(grp + 1, a[nxt]);
+            }
+#pragma unroll
+            for (int s = 0; s < NW; ++s)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) acc[s][i][j] = mfma(a[cur][i], b[cur][s][j], acc[s][i][j]);
+            if (grp + 1 < NG) dequant(grp + 1, q[nxt], b[nxt]);
+        }
+        if (__builtin_expect(big_step, 0)) {
+#pragma unroll
+            for (int s = 0; s < NW; ++s)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) acc[s][i][j] *= 1.0f / kDown;
+        }
+    };
     auto mma_step = [&](int buf) {
+        if constexpr (SPEC && T32 && !Q8) {
+            mma_step_pipe(buf);
+            return;
+        }
         uint32_t scales[NW][TN];
         bool big = false;
 #pragma unroll

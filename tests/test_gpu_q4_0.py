@@ -340,7 +340,8 @@ def test_every_skinny_mfma_variant(stream, oracle, variant):
 def test_every_mfma_variant(stream, oracle, variant):
     d = ops.Q4_0Dispatch()
     d.force(variant)
-    for m, n, k in [(70, 200, 512), (130, 67, 1024), (64, 128, 64)]:
+    # K = 448: seven steps, not a multiple of the staging waves' prefetch depth
+    for m, n, k in [(70, 200, 512), (130, 67, 1024), (64, 128, 64), (96, 160, 448)]:
         x = normal_x(wl.seed_for(10, m), m, k)
         w = weights(wl.seed_for(10, 100 + n), n, k)
         y = run_linear(stream, x, w, m, n, k, dispatch=d)
