@@ -14,8 +14,12 @@
 // inside each wave and through LDS across the four waves in a fixed order
 // (deterministic), and the same registers produce the output: every read
 // precedes the barrier and every write follows it, so input == output (and
-// input == residual for the fused op) is race free.  Other rows (e.g. hidden
-// 513) use a strided two-pass loop with the same reduction.
+// input == residual for the fused op) is race free.  A thread's loads (input,
+// residual, weights) are all issued before any is waited for, unguarded
+// (indices past the row re-read its last chunk and are not used): guarded by
+// a branch each, the compiler waited for each load before issuing the next,
+// and at 32 x 4096 RMSNorm took 2.26 us against 2.06 us.  Other rows (e.g.
+// hidden 513) use a strided two-pass loop with the same reduction.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -68,35 +72,51 @@ __global__ __launch_bounds__(256) void norm_vec_kernel(const u32x4* input, u32x4
     u32x4* res = FUSED ? residual + row * chunks : nullptr;
     u32x4* out = output + row * chunks;
 
+    // Unconditional loads (indices past the row re-read its last chunk and
+    // are not used), weights included, all in flight before the reduction.
+    u32x4 wreg[CPT], xreg[CPT], rreg[CPT];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const uint32_t idx = min(threadIdx.x + 256u * c, chunks - 1);
+        xreg[c] = in[idx];
+        if constexpr (FUSED) rreg[c] = res[idx];
+        wreg[c] = weight[idx];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the arithmetic
     float v[CPT][8];
     float partial = 0.0f;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
-        const uint32_t idx = threadIdx.x + 256u * c;
-        if (idx < chunks) {
-            unpack8(in[idx], v[c]);
-            if constexpr (FUSED) {
-                float r[8];
-                unpack8(res[idx], r);
+        const bool live = threadIdx.x + 256u * c < chunks;
+        unpack8(xreg[c], v[c]);
+        if constexpr (FUSED) {
+            float r[8];
+            unpack8(rreg[c], r);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] + r[i];
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) partial = __builtin_fmaf(v[c][i], v[c][i], partial);
+            for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] + r[i];
         }
+        float sq = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sq = __builtin_fmaf(v[c][i], v[c][i], sq);
+        partial += live ? sq : 0.0f;
     }
     const float sum = block_sum(partial, lds);
     const float inv_rms = 1.0f / sqrtf(sum / hidden + epsilon);
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
+        float wv[8], o[8];
+        unpack8(wreg[c], wv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = (v[c][i] * inv_rms) * wv[i];
+        xreg[c] = pack8(o);
+        if constexpr (FUSED) rreg[c] = pack8(v[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
         const uint32_t idx = threadIdx.x + 256u * c;
         if (idx < chunks) {
-            float wv[8], o[8];
-            unpack8(weight[idx], wv);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) o[i] = (v[c][i] * inv_rms) * wv[i];
-            out[idx] = pack8(o);
-            if constexpr (FUSED) res[idx] = pack8(v[c]);
+            out[idx] = xreg[c];
+            if constexpr (FUSED) res[idx] = rreg[c];
         }
     }
 }

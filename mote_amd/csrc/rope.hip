@@ -41,7 +41,10 @@ __device__ __forceinline__ f16x2 rotate(float a, float b, float c, float s) {
 }
 
 // Vector path: items per vector = R/8 rotation quads + tail/4 copy quads.
-template <uint32_t LAYOUT>
+// Idx is the index type: 32-bit when every item index fits (the divisions
+// that locate an item's vector and token are then hardware 32-bit ones, not
+// the multi-instruction 64-bit sequence in front of every load).
+template <uint32_t LAYOUT, typename Idx>
 __global__ __launch_bounds__(256) void rope_vec_kernel(const _Float16* in_a, const _Float16* in_b,
                                                        const float* __restrict__ cos_t,
                                                        const float* __restrict__ sin_t,
@@ -52,16 +55,16 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(const _Float16* in_a, con
     const uint32_t freq = rotary_dim / 2;
     const uint32_t rot_items = freq / 4;
     const uint32_t items = rot_items + (head_dim - rotary_dim) / 4;
-    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256;
-    for (uint64_t it = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; it < total_items;
+    const Idx stride = static_cast<Idx>(gridDim.x) * 256;
+    for (Idx it = static_cast<Idx>(blockIdx.x) * 256 + threadIdx.x; it < static_cast<Idx>(total_items);
          it += stride) {
-        const uint64_t vec = it / items;
+        const Idx vec = it / items;
         const uint32_t item = static_cast<uint32_t>(it - vec * items);
-        const bool is_a = vec < vectors_a;
-        const uint64_t local = is_a ? vec : vec - vectors_a;
+        const bool is_a = vec < static_cast<Idx>(vectors_a);
+        const Idx local = is_a ? vec : vec - static_cast<Idx>(vectors_a);
         const uint64_t token = local / (is_a ? heads_a : heads_b);
-        const _Float16* src = (is_a ? in_a : in_b) + local * head_dim;
-        _Float16* dst = (is_a ? out_a : out_b) + local * head_dim;
+        const _Float16* src = (is_a ? in_a : in_b) + static_cast<uint64_t>(local) * head_dim;
+        _Float16* dst = (is_a ? out_a : out_b) + static_cast<uint64_t>(local) * head_dim;
         if (item >= rot_items) {
             const uint32_t e = rotary_dim + (item - rot_items) * 4;
             *reinterpret_cast<u32x2*>(dst + e) = *reinterpret_cast<const u32x2*>(src + e);
@@ -169,16 +172,19 @@ int launch(const void* in_a, const void* in_b, const void* cos_t, const void* si
     const auto* c = static_cast<const float*>(cos_t);
     const auto* s = static_cast<const float*>(sin_t);
     const uint64_t heads_b = g.heads_b == 0 ? 1 : g.heads_b;  // divisor of never-taken k path
+    // 32-bit indices when the last item index plus one grid stride fits
+    const bool narrow = total + static_cast<uint64_t>(grid.x) * 256 <= 0xffffffffull;
+    auto launch_vec = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, block, 0, stream, ia, ib, c, s, oa, ob, vectors_a, total,
+                           static_cast<uint32_t>(g.heads_a), static_cast<uint32_t>(heads_b),
+                           static_cast<uint32_t>(g.head_dim), static_cast<uint32_t>(g.rotary_dim));
+    };
     if (vec && g.layout == kHalfSplit) {
-        hipLaunchKernelGGL(rope_vec_kernel<kHalfSplit>, grid, block, 0, stream, ia, ib, c, s, oa, ob,
-                           vectors_a, total, static_cast<uint32_t>(g.heads_a),
-                           static_cast<uint32_t>(heads_b), static_cast<uint32_t>(g.head_dim),
-                           static_cast<uint32_t>(g.rotary_dim));
+        if (narrow) launch_vec(rope_vec_kernel<kHalfSplit, uint32_t>);
+        else launch_vec(rope_vec_kernel<kHalfSplit, uint64_t>);
     } else if (vec) {
-        hipLaunchKernelGGL(rope_vec_kernel<kInterleaved>, grid, block, 0, stream, ia, ib, c, s, oa,
-                           ob, vectors_a, total, static_cast<uint32_t>(g.heads_a),
-                           static_cast<uint32_t>(heads_b), static_cast<uint32_t>(g.head_dim),
-                           static_cast<uint32_t>(g.rotary_dim));
+        if (narrow) launch_vec(rope_vec_kernel<kInterleaved, uint32_t>);
+        else launch_vec(rope_vec_kernel<kInterleaved, uint64_t>);
     } else {
         hipLaunchKernelGGL(rope_scalar_kernel, grid, block, 0, stream, ia, ib, c, s, oa, ob,
                            vectors_a, total, g.heads_a, heads_b, g.head_dim,
