@@ -639,6 +639,17 @@ hipError_t launch_skinny(const Problem& p) {
     uint32_t groups = static_cast<uint32_t>(cus) * G;
     if (groups > items) groups = items;
     if (LAZY > 0 && groups < (items + LAZY - 1) / LAZY) groups = (items + LAZY - 1) / LAZY;  // <= LAZY items each
+    if constexpr (LAZY > 0 && !SK && G == 1) {
+        // Balanced: as few items per workgroup as one workgroup per CU allows,
+        // and no more workgroups than that count needs (every workgroup loads
+        // all of its token group's x, so a workgroup with fewer items than the
+        // busiest adds x traffic without shortening the kernel): at 16 x 4096
+        // x 14 336, 224 workgroups of 4 items took 11.3 us against 12.1 us for
+        // 256 of 3 or 4; at 16 x 4096 x 6144, 192 of 2 took 7.2 against 7.9 us.
+        uint32_t ipw = (items + cus - 1) / static_cast<uint32_t>(cus);
+        if (ipw > static_cast<uint32_t>(LAZY)) ipw = LAZY;
+        groups = (items + ipw - 1) / ipw;
+    }
     groups = (groups + unit - 1) / unit * unit;
     const uint32_t per_xcd = groups / 8u;
     const dim3 grid(groups), block(KS * 64);
