@@ -146,6 +146,23 @@ uint64_t prefill_tiles(const Problem& p, uint32_t bm, uint32_t bn) {
     return static_cast<uint64_t>((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
 }
 
+// The tile `base` with the most block pairs per step (barrier) up to max_kp
+// that K allows (`<base>_k<kp>`), else `base` itself.  More k per step
+// amortises the step's barrier and operand ramp: measured on MI355X at K =
+// 4096, N = 14 336, 128 x 256 with 2 pairs 69.7 us against 73.5 at 512
+// tokens, 128 x 128 with 2 pairs 45.0 against 47.4 at 256, 64 x 128 with 4
+// pairs 26.0-27.4 against 38.8 at 128 (gate/up 130.6 against 137.6 us at 512
+// tokens, 88.3 against 117.8 us at 64 x 8192 x 28 672).
+const Variant* deepest_step(const char* base, const Problem& p, int max_kp) {
+    char name[80];
+    for (int kp = max_kp; kp >= 2; kp /= 2) {
+        std::snprintf(name, sizeof name, "%s_k%d", base, kp);
+        const Variant* v = by_name(name);
+        if (v && prefill_supports(*v, p)) return v;
+    }
+    return by_name(base);
+}
+
 // Skinny GEMM (3 <= M <= 64, K = 4096) on the matrix cores, transposed weight
 // loads; null when the K slicing does not fit.  One (16-row, token-group) item
 // per step of a workgroup, with the reduction deferred over up to 4 items (16
@@ -363,6 +380,14 @@ const Variant* heuristic(const Problem& p, Op op) {
             const Variant* v = by_name(name);
             if (v && gemv_stream_supports(*v, p)) return v;
         }
+        if (fast && p.M > 48 && p.M <= 64 && prefill_tiles(p, 64, 128) < 200 &&
+            prefill_tiles(p, 64, 64) >= 200) {
+            // 49-64 tokens where 64 x 128 tiles are too few: 64 x 64 tiles of
+            // 2 x 2 waves, 4 block pairs per step (64 x 4096 x 14 336: 30.8
+            // us, against 35.6 us on the skinny tiles)
+            const Variant* v = by_name("gateup_mfma_x32s_m64_n64_w2_k4");
+            if (v && prefill_supports(*v, p)) return v;
+        }
         if (fast && p.M <= 64) {
             if (const Variant* v = skinny_gate_up_heuristic(p)) return v;
             if (const Variant* v = split_k_heuristic(p, op)) return v;
@@ -372,9 +397,10 @@ const Variant* heuristic(const Problem& p, Op op) {
             // about one per CU (256 tokens: 72.7-75.4 us, 512: 139.5-144.6 us,
             // against 84.5 and 164 us for 16 x 16 tiles); up to 64 tokens
             // the 64 x 128 tiles (64 x 8192 x 28672: 119.4 us, against 150.3
-            // us for 128 x 128 tiles).
-            if (p.M <= 64 && prefill_tiles(p, 64, 128) >= 200) return by_name("gateup_mfma_x32s_m64_n128_w1");
-            if (prefill_tiles(p, 128, 128) >= 200) return by_name("gateup_mfma_x32s_m128_n128_w1");
+            // us for 128 x 128 tiles); each with the deepest step K allows.
+            if (p.M <= 64 && prefill_tiles(p, 64, 128) >= 200)
+                return deepest_step("gateup_mfma_x32s_m64_n128_w1", p, 4);
+            if (prefill_tiles(p, 128, 128) >= 200) return deepest_step("gateup_mfma_x32s_m128_n128_w1", p, 2);
             return by_name(p.M >= 128 ? "gateup_mfma_r_m128_n64" : "gateup_mfma_r_m64_n64");
         }
         return by_name("gateup_generic");
@@ -392,12 +418,15 @@ const Variant* heuristic(const Problem& p, Op op) {
         // N = 14336: 128 x 256 at 512 tokens, 68-72 us; 128 x 128 at 256
         // tokens, 46.5-47.1 us; 64 x 128 at 128 tokens, 39.8 us; the 16 x 16
         // tiles took 83, 59.4 and 46.1 us).
+        // Each x32s tile with the deepest step K allows (2 block pairs for
+        // the 128-row tiles, 4 for 64 x 128: what fits the LDS).
         static const char* const order[] = {"mfma_x32s_m128_n256_w1", "mfma_x32s_m128_n128_w1",
                                             "mfma_x32s_m64_n128_w1", "mfma_r_m64_n128", "mfma_r_m64_n64"};
+        static const int max_kp[] = {2, 2, 4, 1, 1};
         const Variant* best = nullptr;
         uint64_t best_tiles = 0;
-        for (const char* name : order) {
-            const Variant* v = by_name(name);
+        for (int i = 0; i < 5; ++i) {
+            const Variant* v = max_kp[i] > 1 ? deepest_step(order[i], p, max_kp[i]) : by_name(order[i]);
             const uint64_t tiles = static_cast<uint64_t>((p.M + v->p0 - 1) / v->p0) *
                                    ((p.N + v->p1 - 1) / v->p1);
             if (tiles >= 200) return v;

@@ -48,10 +48,8 @@
 namespace mote::q4_0 {
 namespace {
 
-constexpr int kXRow = 144;  // LDS bytes per activation row and step (128 + 16 padding)
-
 template <int BM, int BN, bool GATE_UP, typename OutT, bool Q8 = false, int WM = 2, bool T32 = false,
-          bool SPEC = false>
+          bool SPEC = false, int KP = 1>
 __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_t* __restrict__ x,
                                                       const uint8_t* __restrict__ wg,
                                                       const uint8_t* __restrict__ wu,
@@ -63,15 +61,22 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
     constexpr int T = T32 ? 32 : 16;          // MFMA tile edge
     constexpr int TM = BM / (WM * T);         // MFMA tiles per wave along M
     constexpr int TN = BN / (WN * T);         // along N
-    constexpr int XC = BM * 8 / 256;          // 16-byte activation chunks per thread and step
-    constexpr int WI = (BN + 255) / 256;      // weight rows per thread and step (per matrix)
+    // KP block pairs (64 k each) per step and barrier (KP > 1: the pipelined
+    // 32 x 32 Q4_0 step with staging waves only).
+    static_assert(KP == 1 || (SPEC && T32 && !Q8), "several pairs per step: pipelined Q4_0 tiles");
+    constexpr int kXRow = 128 * KP + 16;      // LDS bytes per activation row and step (+16: banks)
+    constexpr int XC = BM * 8 * KP / 256;     // 16-byte activation chunks per thread and step
+    constexpr int WI = (BN * KP + 255) / 256; // weight (row, pair) units per thread and step (per matrix)
     static_assert((WM == 1 || WM == 2 || WM == 4) && TM >= 1 && TN >= 1 && BM % (WM * T) == 0 &&
                       BN % (WN * T) == 0 && XC >= 1, "tile shape");
     using Acc = std::conditional_t<T32, f32x16, f32x4>;
     constexpr int kAccRows = T32 ? 16 : 4;    // accumulator registers per lane and tile
     static_assert(!(Q8 && GATE_UP), "the fused gate/up is a Q4_0 operation");
     constexpr int kDw = Q8 ? 17 : 9;         // dwords of a staged block pair
-    constexpr int kWRow = kDw * 4;           // LDS bytes per weight row and step
+    // LDS bytes per weight row and step: KP staged pairs, plus a dword when
+    // that keeps the row stride odd in dwords (the 32 rows of an operand on
+    // distinct banks)
+    constexpr int kWRow = (kDw * KP + (KP % 2 == 0 ? 1 : 0)) * 4;
     constexpr uint32_t kPB = Q8 ? kQ8PairBytes : kPairBytes;
 
     __shared__ __attribute__((aligned(16))) uint8_t xs[2][BM * kXRow];
@@ -93,51 +98,57 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
     const int wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const uint32_t npairs = K >> 6;
+    const uint32_t nsteps = npairs / KP;
     const size_t row_bytes = static_cast<size_t>(npairs) * kPB;
     const uint8_t* wsrc[NW] = {wg};
     if constexpr (GATE_UP) wsrc[1] = wu;
 
     // Activation chunks: thread c of the tile copies 16 bytes (8 halves) of
-    // row c / 8; chunk c % 8 holds elements 8 (c % 4) .. + 7 of block (c % 8) / 4.
+    // row c / (8 KP): pair (c / 8) % KP of the step, whose chunk c % 8 holds
+    // elements 8 (c % 4) .. + 7 of block (c % 8) / 4.
     const uint16_t* xptr[XC];
     int xoff[XC];
 #pragma unroll
     for (int j = 0; j < XC; ++j) {
         const int c = tid + 256 * j;
-        const int row = c >> 3, chunk = c & 7;
+        const int row = c / (8 * KP), pair = (c / 8) % KP, chunk = c & 7;
         const uint32_t m = min(m0 + row, M - 1);
-        xptr[j] = x + static_cast<size_t>(m) * K + chunk * 8;
+        xptr[j] = x + static_cast<size_t>(m) * K + pair * 64 + chunk * 8;
         const int blk = chunk >> 2, kin = (chunk & 3) * 8;
         if constexpr (Q8)  // k group chunk % 4: both halves together
             xoff[j] = row * kXRow + blk * 64 + (chunk & 3) * 16;
         else
-            xoff[j] = row * kXRow + blk * 64 + ((kin & 15) >> 2) * 16 + (kin >= 16 ? 8 : 0);
+            xoff[j] = row * kXRow + pair * 128 + blk * 64 + ((kin & 15) >> 2) * 16 + (kin >= 16 ? 8 : 0);
     }
-    // Weight rows: thread t copies the step's block pair of rows t, t + 256, ...
+    // Weight units: thread t copies unit t, t + 256, ... of the step, unit u
+    // being block pair u % KP of row u / KP.
     const uint8_t* wptr[NW][WI];
     bool wlive[WI];
+    int woff[WI];
 #pragma unroll
     for (int j = 0; j < WI; ++j) {
-        const int row = tid + 256 * j;
-        wlive[j] = row < BN;
-        const uint32_t n = min(n0 + static_cast<uint32_t>(wlive[j] ? row : 0), N - 1);
+        const int u = tid + 256 * j;
+        wlive[j] = u < BN * KP;
+        const int row = wlive[j] ? u / KP : 0, pair = wlive[j] ? u % KP : 0;
+        woff[j] = row * kWRow + pair * kDw * 4;
+        const uint32_t n = min(n0 + static_cast<uint32_t>(row), N - 1);
 #pragma unroll
-        for (int s = 0; s < NW; ++s) wptr[s][j] = wsrc[s] + static_cast<size_t>(n) * row_bytes;
+        for (int s = 0; s < NW; ++s) wptr[s][j] = wsrc[s] + static_cast<size_t>(n) * row_bytes + pair * kPB;
     }
 
     u32x4 xreg[XC];
     uint32_t wreg[NW][WI][kDw];
     auto load_stage = [&](uint32_t kp) {
-        kp = min(kp, npairs - 1);  // past the end: a cached re-read, never used
+        kp = min(kp, nsteps - 1);  // past the end: a cached re-read, never used
 #pragma unroll
         for (int j = 0; j < XC; ++j)
-            xreg[j] = *reinterpret_cast<const u32x4*>(xptr[j] + static_cast<size_t>(kp) * 64);
+            xreg[j] = *reinterpret_cast<const u32x4*>(xptr[j] + static_cast<size_t>(kp) * 64 * KP);
 #pragma unroll
         for (int s = 0; s < NW; ++s)
 #pragma unroll
             for (int j = 0; j < WI; ++j)
                 if (wlive[j]) {
-                    const uint8_t* src = wptr[s][j] + static_cast<size_t>(kp) * kPB;
+                    const uint8_t* src = wptr[s][j] + static_cast<size_t>(kp) * kPB * KP;
                     if constexpr (Q8)
                         load_pair_q8(src, wreg[s][j]);
                     else
@@ -162,7 +173,7 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
             for (int j = 0; j < WI; ++j) {
                 if (!wlive[j]) continue;
                 const uint32_t (&d)[kDw] = wreg[s][j];
-                uint32_t* dst = reinterpret_cast<uint32_t*>(&ws[s][buf][(tid + 256 * j) * kWRow]);
+                uint32_t* dst = reinterpret_cast<uint32_t*>(&ws[s][buf][woff[j]]);
                 if constexpr (Q8) {
                     dst[0] = __builtin_amdgcn_perm(d[8], d[0], 0x07060100u);  // d0 (bytes 0-1) | d1 (bytes 34-35)
 #pragma unroll
@@ -209,61 +220,74 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
     // dequantisation of group g + 1 issue while the matrix core works on
     // group g (measured 2-3 % faster than the step below at 128-512 tokens).
     auto mma_step_pipe = [&](int buf) {
-        constexpr int NG = 4;
-        uint32_t scales[NW][TN];
+        // group grp: pair grp / 4 of the step, block (grp / 2) % 2 of the
+        // pair, half grp % 2 of the block
+        constexpr int NG = 4 * KP;
+        uint32_t scales[KP][NW][TN];
         uint32_t q[2][NW][TN];
         f16x8 a[2][TM];
         f16x8 b[2][NW][TN];
         auto read_b = [&](int grp, uint32_t (&dst)[NW][TN]) {
-            const int blk = grp >> 1, g = 2 * (grp & 1) + lgrp;
+            const int pair = grp >> 2, blk = (grp >> 1) & 1, g = 2 * (grp & 1) + lgrp;
 #pragma unroll
             for (int s = 0; s < NW; ++s)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
                     dst[s][j] = *reinterpret_cast<const uint32_t*>(
-                        &ws[s][buf][b_base + j * T * kWRow + 4 + blk * 16 + g * 4]);
+                        &ws[s][buf][b_base + j * T * kWRow + pair * kDw * 4 + 4 + blk * 16 + g * 4]);
         };
         auto read_a = [&](int grp, f16x8 (&dst)[TM]) {
-            const int blk = grp >> 1, g = 2 * (grp & 1) + lgrp;
+            const int pair = grp >> 2, blk = (grp >> 1) & 1, g = 2 * (grp & 1) + lgrp;
 #pragma unroll
             for (int i = 0; i < TM; ++i)
-                dst[i] = *reinterpret_cast<const f16x8*>(&xs[buf][a_base + i * T * kXRow + blk * 64 + g * 16]);
+                dst[i] = *reinterpret_cast<const f16x8*>(
+                    &xs[buf][a_base + i * T * kXRow + pair * 128 + blk * 64 + g * 16]);
         };
         auto dequant = [&](int grp, const uint32_t (&qq)[NW][TN], f16x8 (&dst)[NW][TN]) {
-            const int blk = grp >> 1;
+            const int pair = grp >> 2, blk = (grp >> 1) & 1;
 #pragma unroll
             for (int s = 0; s < NW; ++s)
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
-                    const f16x2 d = as_h2(__builtin_amdgcn_perm(scales[s][j], scales[s][j],
+                    const f16x2 d = as_h2(__builtin_amdgcn_perm(scales[pair][s][j], scales[pair][s][j],
                                                                 blk ? 0x03020302u : 0x01000100u));
                     dst[s][j] = dequant8(qq[s][j], d, dq.c1024, dq.c64);
                 }
         };
 #pragma unroll
-        for (int s = 0; s < NW; ++s)
+        for (int p = 0; p < KP; ++p)
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
-                scales[s][j] = *reinterpret_cast<const uint32_t*>(&ws[s][buf][b_base + j * T * kWRow]);
+            for (int s = 0; s < NW; ++s)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    scales[p][s][j] = *reinterpret_cast<const uint32_t*>(
+                        &ws[s][buf][b_base + j * T * kWRow + p * kDw * 4]);
         read_b(0, q[0]);
         read_a(0, a[0]);
         bool big = false;
 #pragma unroll
-        for (int s = 0; s < NW; ++s)
+        for (int p = 0; p < KP; ++p)
 #pragma unroll
-            for (int j = 0; j < TN; ++j) big = big || big_scales<kBig>(scales[s][j]);
+            for (int s = 0; s < NW; ++s)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) big = big || big_scales<kBig>(scales[p][s][j]);
         // the scaled MFMA of a step with a scale past binary16 range, as below
         const bool big_step = wave_any(big);
         if (__builtin_expect(big_step, 0)) {
             const f16x2 dd = {static_cast<_Float16>(kDown), static_cast<_Float16>(kDown)};
 #pragma unroll
+            for (int p = 0; p < KP; ++p)
+#pragma unroll
+                for (int s = 0; s < NW; ++s)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        scales[p][s][j] = __builtin_bit_cast(uint32_t, as_h2(scales[p][s][j]) * dd);
+#pragma unroll
             for (int s = 0; s < NW; ++s)
 #pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    scales[s][j] = __builtin_bit_cast(uint32_t, as_h2(scales[s][j]) * dd);
+                for (int i = 0; i < TM; ++i)
 #pragma unroll
-                    for (int i = 0; i < TM; ++i) acc[s][i][j] *= kDown;
-                }
+                    for (int j = 0; j < TN; ++j) acc[s][i][j] *= kDown;
         }
         dequant(0, q[0], b[0]);
 #pragma unroll
@@ -380,8 +404,8 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
     __syncthreads();
     if constexpr (SPEC) {
         if (stager) {
-            for (uint32_t kp = 0; kp < npairs; ++kp) {
-                if (kp + 1 < npairs) {  // uniform
+            for (uint32_t kp = 0; kp < nsteps; ++kp) {
+                if (kp + 1 < nsteps) {  // uniform
                     store_stage(static_cast<int>(kp & 1u) ^ 1);
                     load_stage(kp + 2);
                 }
@@ -389,14 +413,14 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
             }
             return;  // the compute waves hold the results
         }
-        for (uint32_t kp = 0; kp < npairs; ++kp) {
+        for (uint32_t kp = 0; kp < nsteps; ++kp) {
             mma_step(static_cast<int>(kp & 1u));
             __syncthreads();
         }
     } else {
-        for (uint32_t kp = 0; kp < npairs; ++kp) {
+        for (uint32_t kp = 0; kp < nsteps; ++kp) {
             const int buf = static_cast<int>(kp & 1u);
-            if (kp + 1 < npairs) {  // uniform
+            if (kp + 1 < nsteps) {  // uniform
                 store_stage(buf ^ 1);
                 load_stage(kp + 2);
             }
@@ -424,8 +448,10 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
     }
 }
 
-template <int BM, int BN, bool GATE_UP, bool Q8 = false, int WM = 2, bool T32 = false, bool SPEC = false>
+template <int BM, int BN, bool GATE_UP, bool Q8 = false, int WM = 2, bool T32 = false, bool SPEC = false,
+          int KP = 1>
 hipError_t launch_prefill(const Problem& p) {
+    if (p.K % (64u * KP) != 0) return hipErrorInvalidValue;
     const uint32_t m_tiles = (p.M + BM - 1) / BM;
     const uint32_t n_tiles = (p.N + BN - 1) / BN;
     const uint64_t total64 = static_cast<uint64_t>(m_tiles) * n_tiles;
@@ -437,10 +463,10 @@ hipError_t launch_prefill(const Problem& p) {
     const auto* wg = static_cast<const uint8_t*>(p.w);
     const auto* wu = static_cast<const uint8_t*>(p.w_up);
     if (p.out == OutType::F32) {
-        hipLaunchKernelGGL((prefill_kernel<BM, BN, GATE_UP, float, Q8, WM, T32, SPEC>), grid, block, 0, p.stream, x, wg, wu,
+        hipLaunchKernelGGL((prefill_kernel<BM, BN, GATE_UP, float, Q8, WM, T32, SPEC, KP>), grid, block, 0, p.stream, x, wg, wu,
                            static_cast<float*>(p.y), p.M, p.N, p.K, m_tiles, total, per_xcd);
     } else {
-        hipLaunchKernelGGL((prefill_kernel<BM, BN, GATE_UP, _Float16, Q8, WM, T32, SPEC>), grid, block, 0, p.stream, x, wg,
+        hipLaunchKernelGGL((prefill_kernel<BM, BN, GATE_UP, _Float16, Q8, WM, T32, SPEC, KP>), grid, block, 0, p.stream, x, wg,
                            wu, static_cast<_Float16*>(p.y), p.M, p.N, p.K, m_tiles, total, per_xcd);
     }
     return hipGetLastError();
@@ -459,6 +485,13 @@ hipError_t launch_prefill(const Problem& p) {
 #define MOTE_PREFILL_X32S(BM, BN, WM)                                                                \
     Variant{"mfma_x32s_m" #BM "_n" #BN "_w" #WM, Kind::Mfma, BM, BN, 1,                              \
             &launch_prefill<BM, BN, false, false, WM, true, true>}
+// ... with KP block pairs per step (p2 = KP: K a multiple of 64 KP).
+#define MOTE_PREFILL_X32SK(BM, BN, WM, KP)                                                           \
+    Variant{"mfma_x32s_m" #BM "_n" #BN "_w" #WM "_k" #KP, Kind::Mfma, BM, BN, KP,                    \
+            &launch_prefill<BM, BN, false, false, WM, true, true, KP>}
+#define MOTE_PREFILL_GU_X32SK(BM, BN, WM, KP)                                                        \
+    Variant{"gateup_mfma_x32s_m" #BM "_n" #BN "_w" #WM "_k" #KP, Kind::GateUpMfma, BM, BN, KP,       \
+            &launch_prefill<BM, BN, true, false, WM, true, true, KP>}
 #define MOTE_PREFILL_GU_X32S(BM, BN, WM)                                                             \
     Variant{"gateup_mfma_x32s_m" #BM "_n" #BN "_w" #WM, Kind::GateUpMfma, BM, BN, 1,                 \
             &launch_prefill<BM, BN, true, false, WM, true, true>}
@@ -476,6 +509,10 @@ const Variant kPrefill[] = {
     MOTE_PREFILL_Q8(64, 64),
     MOTE_PREFILL_X32(128, 128, 1),
     MOTE_PREFILL_X32S(128, 128, 1), MOTE_PREFILL_X32S(64, 128, 1), MOTE_PREFILL_X32S(128, 256, 1),
+    MOTE_PREFILL_X32SK(128, 128, 1, 2), MOTE_PREFILL_X32SK(64, 128, 1, 2), MOTE_PREFILL_X32SK(128, 256, 1, 2),
+    MOTE_PREFILL_X32SK(64, 128, 1, 4), MOTE_PREFILL_X32SK(64, 64, 2, 4), MOTE_PREFILL_X32SK(64, 64, 2, 2),
+    MOTE_PREFILL_GU_X32SK(128, 128, 1, 2), MOTE_PREFILL_GU_X32SK(64, 128, 1, 2),
+    MOTE_PREFILL_GU_X32SK(64, 128, 1, 4), MOTE_PREFILL_GU_X32SK(64, 64, 2, 4),
     MOTE_PREFILL_GU_X32S(128, 128, 1), MOTE_PREFILL_GU_X32S(64, 128, 1),
     MOTE_PREFILL_Q8_X32S(128, 128, 1), MOTE_PREFILL_Q8_X32S(128, 256, 1),
 };
@@ -486,6 +523,8 @@ const Variant kPrefill[] = {
 #undef MOTE_PREFILL_X32
 #undef MOTE_PREFILL_X32S
 #undef MOTE_PREFILL_GU_X32S
+#undef MOTE_PREFILL_X32SK
+#undef MOTE_PREFILL_GU_X32SK
 #undef MOTE_PREFILL_Q8_X32S
 
 }  // namespace
@@ -498,9 +537,9 @@ const Variant* prefill_variants(int* count) {
 // K a multiple of 64, x 16-byte and the weights (and the up matrix of a
 // gate/up) dword aligned; any M and N (partial tiles are masked).
 bool prefill_supports(const Variant& v, const Problem& p) {
-    (void)v;
     const bool up_ok = p.w_up == nullptr || reinterpret_cast<uintptr_t>(p.w_up) % 4 == 0;
-    return p.K % 64 == 0 && p.K > 0 && up_ok && reinterpret_cast<uintptr_t>(p.w) % 4 == 0 &&
+    const uint32_t step = 64u * static_cast<uint32_t>(v.p2 > 0 ? v.p2 : 1);
+    return p.K % step == 0 && p.K > 0 && up_ok && reinterpret_cast<uintptr_t>(p.w) % 4 == 0 &&
            reinterpret_cast<uintptr_t>(p.x) % 16 == 0;
 }
 

@@ -41,8 +41,10 @@ LINEAR = [
     ((24, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l4_c_w"),
     ((32, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l4_c_w"),
     ((64, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l8_c_w"),
-    ((256, 4096, 14336), "mfma_x32s_m128_n128_w1"),
-    ((512, 4096, 14336), "mfma_x32s_m128_n256_w1"),
+    ((128, 4096, 14336), "mfma_x32s_m64_n128_w1_k4"),
+    ((256, 4096, 14336), "mfma_x32s_m128_n128_w1_k2"),
+    ((512, 4096, 14336), "mfma_x32s_m128_n256_w1_k2"),
+    ((256, 4160, 14336), "mfma_x32s_m128_n128_w1"),  # 65 block pairs: one pair per step
 ]
 
 
@@ -78,7 +80,9 @@ def test_gate_up_and_q8_plans(d):
     assert d.select(1, 14336, 4096, gate_up=True) == "gateup_stream_p1_d1_g1"
     assert d.select(2, 14336, 4096, gate_up=True) == "gateup_stream_p1_m2_d1q_g1"
     assert d.select(16, 14336, 4096, gate_up=True).startswith("gateup_skinny_")
-    assert d.select(256, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m128_n128_w1"
+    assert d.select(256, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m128_n128_w1_k2"
+    assert d.select(64, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m64_n64_w2_k4"
+    assert d.select(64, 28672, 8192, gate_up=True) == "gateup_mfma_x32s_m64_n128_w1_k4"
     assert d.select(1, 14336, 4096, q8_0=True) == "q8_stream_d1_g1"
     assert d.select(16, 14336, 4096, q8_0=True).startswith("q8_skinny_")
     assert d.select(512, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m128_n256_w1"

@@ -340,8 +340,12 @@ def test_every_skinny_mfma_variant(stream, oracle, variant):
 def test_every_mfma_variant(stream, oracle, variant):
     d = ops.Q4_0Dispatch()
     d.force(variant)
-    # K = 448: seven steps, not a multiple of the staging waves' prefetch depth
-    for m, n, k in [(70, 200, 512), (130, 67, 1024), (64, 128, 64), (96, 160, 448)]:
+    # `_k<P>` tiles take P block pairs (64 P of K) per step: the shapes they
+    # can run, plus K = 768 (12 pairs: 6 or 3 steps); K = 448 is seven steps
+    # of one pair
+    kp = int(variant.rsplit("_k", 1)[1]) if "_x32s_" in variant and "_k" in variant.rsplit("_w", 1)[1] else 1
+    shapes = [(70, 200, 512), (130, 67, 1024), (64, 128, 64), (96, 160, 448), (96, 160, 768)]
+    for m, n, k in [sh for sh in shapes if sh[2] % (64 * kp) == 0]:
         x = normal_x(wl.seed_for(10, m), m, k)
         w = weights(wl.seed_for(10, 100 + n), n, k)
         y = run_linear(stream, x, w, m, n, k, dispatch=d)
