@@ -380,6 +380,14 @@ const Variant* heuristic(const Problem& p, Op op) {
             const Variant* v = by_name(name);
             if (v && gemv_stream_supports(*v, p)) return v;
         }
+        if (fast && p.M > 16 && p.M <= 64 && prefill_tiles(p, 64, 128) >= 200) {
+            // 17-64 tokens with at least 200 64 x 128 tiles (wide gate/up,
+            // e.g. 28 672 rows): those tiles with 4 block pairs per step beat
+            // the split-K skinny tiles (32 x 8192 x 28 672: 91.0 against 96.6
+            // us; 48 tokens: 91.8 against 152.0 us)
+            const Variant* v = by_name("gateup_mfma_x32s_m64_n128_w1_k4");
+            if (v && prefill_supports(*v, p)) return v;
+        }
         if (fast && p.M > 48 && p.M <= 64 && prefill_tiles(p, 64, 128) < 200 &&
             prefill_tiles(p, 64, 64) >= 200) {
             // 49-64 tokens where 64 x 128 tiles are too few: 64 x 64 tiles of
