@@ -350,8 +350,15 @@ const Variant* heuristic(const Problem& p, Op op) {
             // (measured on MI355X at K = 4096, N = 14336: 256 tokens 67-69 us,
             // 512 tokens 112 us, against 79 and 126 us for 16 x 16 MFMA
             // tiles), the 64 x 64 tiles below (128 tokens: 56.7 us).
-            if (prefill_tiles(p, 128, 256) >= 200) return by_name("q8_mfma_x32s_m128_n256_w1");
-            if (prefill_tiles(p, 128, 128) >= 200) return by_name("q8_mfma_x32s_m128_n128_w1");
+            // Each with the deepest step K allows: 2 block pairs per step at
+            // 256 tokens 65.0 us (67.8 with one); the 64 x 128 tiles with 4
+            // pairs at 128 tokens 40.8 us (61.5 on the 64 x 64 16 x 16 tiles).
+            if (prefill_tiles(p, 128, 256) >= 200) return deepest_step("q8_mfma_x32s_m128_n256_w1", p, 2);
+            if (prefill_tiles(p, 128, 128) >= 200) return deepest_step("q8_mfma_x32s_m128_n128_w1", p, 2);
+            if (prefill_tiles(p, 64, 128) >= 200) {
+                const Variant* v = deepest_step("q8_mfma_x32s_m64_n128_w1", p, 4);
+                if (v && prefill_supports(*v, p)) return v;
+            }
             return by_name("q8_mfma_r_m64_n64");
         }
         return by_name("q8_generic");

@@ -63,7 +63,7 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
     constexpr int TN = BN / (WN * T);         // along N
     // KP block pairs (64 k each) per step and barrier (KP > 1: the pipelined
     // 32 x 32 Q4_0 step with staging waves only).
-    static_assert(KP == 1 || (SPEC && T32 && !Q8), "several pairs per step: pipelined Q4_0 tiles");
+    static_assert(KP == 1 || (SPEC && T32), "several pairs per step: the pipelined step");
     constexpr int kXRow = 128 * KP + 16;      // LDS bytes per activation row and step (+16: banks)
     constexpr int XC = BM * 8 * KP / 256;     // 16-byte activation chunks per thread and step
     constexpr int WI = (BN * KP + 255) / 256; // weight (row, pair) units per thread and step (per matrix)
@@ -116,7 +116,7 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
         xptr[j] = x + static_cast<size_t>(m) * K + pair * 64 + chunk * 8;
         const int blk = chunk >> 2, kin = (chunk & 3) * 8;
         if constexpr (Q8)  // k group chunk % 4: both halves together
-            xoff[j] = row * kXRow + blk * 64 + (chunk & 3) * 16;
+            xoff[j] = row * kXRow + pair * 128 + blk * 64 + (chunk & 3) * 16;
         else
             xoff[j] = row * kXRow + pair * 128 + blk * 64 + ((kin & 15) >> 2) * 16 + (kin >= 16 ? 8 : 0);
     }
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
     // Scales past binary16 range go through the scaled MFMA (common.hpp).
     constexpr uint32_t kBig = Q8 ? kQ8BigScale : kQ4BigScale;
     constexpr float kDown = Q8 ? kQ8BigDown : kQ4BigDown;
-    // The step of the 32 x 32 Q4_0 tiles with staging waves, software
+    // The step of the 32 x 32 tiles with staging waves (Q4_0 and Q8_0), software
     // pipelined: its four k groups (block, half) run as read -> dequantise ->
     // MFMA stages one group apart, so the LDS reads and the vector-ALU
     // dequantisation of group g + 1 issue while the matrix core works on
@@ -223,18 +223,24 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
         // group grp: pair grp / 4 of the step, block (grp / 2) % 2 of the
         // pair, half grp % 2 of the block
         constexpr int NG = 4 * KP;
+        constexpr int QW = Q8 ? 2 : 1;   // weight dwords per lane and group
+        constexpr int NB = Q8 ? 2 : 1;   // binary16 operands per weight operand (Q8_0: hi + lo)
         uint32_t scales[KP][NW][TN];
-        uint32_t q[2][NW][TN];
+        uint32_t q[2][NW][TN][QW];
         f16x8 a[2][TM];
-        f16x8 b[2][NW][TN];
-        auto read_b = [&](int grp, uint32_t (&dst)[NW][TN]) {
+        f16x8 b[2][NW][TN][NB];
+        auto read_b = [&](int grp, uint32_t (&dst)[NW][TN][QW]) {
             const int pair = grp >> 2, blk = (grp >> 1) & 1, g = 2 * (grp & 1) + lgrp;
 #pragma unroll
             for (int s = 0; s < NW; ++s)
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    dst[s][j] = *reinterpret_cast<const uint32_t*>(
-                        &ws[s][buf][b_base + j * T * kWRow + pair * kDw * 4 + 4 + blk * 16 + g * 4]);
+                for (int j = 0; j < TN; ++j) {
+                    // Q4_0: nibble dword g of the block; Q8_0: its bytes 8g .. 8g + 7
+                    const uint32_t* src = reinterpret_cast<const uint32_t*>(
+                        &ws[s][buf][b_base + j * T * kWRow + pair * kDw * 4 + 4 + blk * (16 * QW) + g * (4 * QW)]);
+#pragma unroll
+                    for (int w = 0; w < QW; ++w) dst[s][j][w] = src[w];
+                }
         };
         auto read_a = [&](int grp, f16x8 (&dst)[TM]) {
             const int pair = grp >> 2, blk = (grp >> 1) & 1, g = 2 * (grp & 1) + lgrp;
@@ -243,7 +249,7 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
                 dst[i] = *reinterpret_cast<const f16x8*>(
                     &xs[buf][a_base + i * T * kXRow + pair * 128 + blk * 64 + g * 16]);
         };
-        auto dequant = [&](int grp, const uint32_t (&qq)[NW][TN], f16x8 (&dst)[NW][TN]) {
+        auto dequant = [&](int grp, const uint32_t (&qq)[NW][TN][QW], f16x8 (&dst)[NW][TN][NB]) {
             const int pair = grp >> 2, blk = (grp >> 1) & 1;
 #pragma unroll
             for (int s = 0; s < NW; ++s)
@@ -251,7 +257,13 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
                 for (int j = 0; j < TN; ++j) {
                     const f16x2 d = as_h2(__builtin_amdgcn_perm(scales[pair][s][j], scales[pair][s][j],
                                                                 blk ? 0x03020302u : 0x01000100u));
-                    dst[s][j] = dequant8(qq[s][j], d, dq.c1024, dq.c64);
+                    if constexpr (Q8) {
+                        const F16x8Pair v = dequant8_q8(qq[s][j][0], qq[s][j][QW - 1], d, dq.q8);
+                        dst[s][j][0] = v.hi;
+                        dst[s][j][NB - 1] = v.lo;
+                    } else {
+                        dst[s][j][0] = dequant8(qq[s][j][0], d, dq.c1024, dq.c64);
+                    }
                 }
         };
 #pragma unroll
@@ -302,7 +314,9 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
 #pragma unroll
-                    for (int i = 0; i < TM; ++i) acc[s][i][j] = mfma(a[cur][i], b[cur][s][j], acc[s][i][j]);
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int h = 0; h < NB; ++h) acc[s][i][j] = mfma(a[cur][i], b[cur][s][j][h], acc[s][i][j]);
             if (grp + 1 < NG) dequant(grp + 1, q[nxt], b[nxt]);
         }
         if (__builtin_expect(big_step, 0)) {
@@ -315,7 +329,7 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
         }
     };
     auto mma_step = [&](int buf) {
-        if constexpr (SPEC && T32 && !Q8) {
+        if constexpr (SPEC && T32) {
             mma_step_pipe(buf);
             return;
         }
@@ -492,6 +506,9 @@ hipError_t launch_prefill(const Problem& p) {
 #define MOTE_PREFILL_GU_X32SK(BM, BN, WM, KP)                                                        \
     Variant{"gateup_mfma_x32s_m" #BM "_n" #BN "_w" #WM "_k" #KP, Kind::GateUpMfma, BM, BN, KP,       \
             &launch_prefill<BM, BN, true, false, WM, true, true, KP>}
+#define MOTE_PREFILL_Q8_X32SK(BM, BN, WM, KP)                                                        \
+    Variant{"q8_mfma_x32s_m" #BM "_n" #BN "_w" #WM "_k" #KP, Kind::Q8Prefill, BM, BN, KP,            \
+            &launch_prefill<BM, BN, false, true, WM, true, true, KP>}
 #define MOTE_PREFILL_GU_X32S(BM, BN, WM)                                                             \
     Variant{"gateup_mfma_x32s_m" #BM "_n" #BN "_w" #WM, Kind::GateUpMfma, BM, BN, 1,                 \
             &launch_prefill<BM, BN, true, false, WM, true, true>}
@@ -515,6 +532,8 @@ const Variant kPrefill[] = {
     MOTE_PREFILL_GU_X32SK(64, 128, 1, 4), MOTE_PREFILL_GU_X32SK(64, 64, 2, 4),
     MOTE_PREFILL_GU_X32S(128, 128, 1), MOTE_PREFILL_GU_X32S(64, 128, 1),
     MOTE_PREFILL_Q8_X32S(128, 128, 1), MOTE_PREFILL_Q8_X32S(128, 256, 1),
+    MOTE_PREFILL_Q8_X32SK(128, 128, 1, 2), MOTE_PREFILL_Q8_X32SK(128, 256, 1, 2),
+    MOTE_PREFILL_Q8_X32SK(64, 128, 1, 2), MOTE_PREFILL_Q8_X32SK(64, 128, 1, 4),
 };
 
 #undef MOTE_PREFILL
@@ -524,6 +543,7 @@ const Variant kPrefill[] = {
 #undef MOTE_PREFILL_X32S
 #undef MOTE_PREFILL_GU_X32S
 #undef MOTE_PREFILL_X32SK
+#undef MOTE_PREFILL_Q8_X32SK
 #undef MOTE_PREFILL_GU_X32SK
 #undef MOTE_PREFILL_Q8_X32S
 

@@ -87,7 +87,10 @@ def test_gate_up_and_q8_plans(d):
     assert d.select(16, 28672, 8192, gate_up=True).startswith("gateup_skinny_")
     assert d.select(1, 14336, 4096, q8_0=True) == "q8_stream_d1_g1"
     assert d.select(16, 14336, 4096, q8_0=True).startswith("q8_skinny_")
-    assert d.select(512, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m128_n256_w1"
+    assert d.select(512, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m128_n256_w1_k2"
+    assert d.select(256, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m128_n128_w1_k2"
+    assert d.select(128, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m64_n128_w1_k4"
+    assert d.select(128, 14336, 4160, q8_0=True) == "q8_mfma_r_m64_n64"
 
 
 def test_forced_variant_and_bad_shapes(d):

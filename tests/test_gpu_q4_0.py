@@ -13,6 +13,7 @@ the f64-accumulated oracle.  Outputs rounded to f16 get an extra 2^-11 |y64|.
 from __future__ import annotations
 
 import functools
+import re
 
 import numpy as np
 import pytest
@@ -343,7 +344,7 @@ def test_every_mfma_variant(stream, oracle, variant):
     # `_k<P>` tiles take P block pairs (64 P of K) per step: the shapes they
     # can run, plus K = 768 (12 pairs: 6 or 3 steps); K = 448 is seven steps
     # of one pair
-    kp = int(variant.rsplit("_k", 1)[1]) if "_x32s_" in variant and "_k" in variant.rsplit("_w", 1)[1] else 1
+    kp = int(re.search(r"_k(\d+)$", variant).group(1)) if re.search(r"_k(\d+)$", variant) else 1
     shapes = [(70, 200, 512), (130, 67, 1024), (64, 128, 64), (96, 160, 448), (96, 160, 768)]
     for m, n, k in [sh for sh in shapes if sh[2] % (64 * kp) == 0]:
         x = normal_x(wl.seed_for(10, m), m, k)

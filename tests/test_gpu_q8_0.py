@@ -12,6 +12,7 @@ through the C ABI of libmote_hip.so.
 from __future__ import annotations
 
 import functools
+import re
 
 import numpy as np
 import pytest
@@ -200,10 +201,14 @@ def test_every_q8_skinny_variant(stream, oracle, variant):
 @pytest.mark.parametrize("variant", _variants("q8_mfma_"))
 def test_every_q8_prefill_variant(stream, oracle, variant):
     """Prefill tiles over Q8_0 pairs (64 or more tokens): M and N ragged
-    against the tiles, K of one pair and K = 4160 (65 pairs), f32 and f16."""
+    against the tiles, K of one pair and K = 4160 (65 pairs), f32 and f16;
+    `_k<P>` tiles (P pairs per step) the shapes whose K they divide, plus
+    K = 768 (12 pairs)."""
     d = ops.Q4_0Dispatch()
     d.force(variant)
-    for m, n, k in [(70, 200, 512), (130, 67, 1024), (64, 128, 64), (65, 33, 4160)]:
+    kp = int(re.search(r"_k(\d+)$", variant).group(1)) if re.search(r"_k(\d+)$", variant) else 1
+    shapes = [(70, 200, 512), (130, 67, 1024), (64, 128, 64), (65, 33, 4160), (96, 160, 768)]
+    for m, n, k in [sh for sh in shapes if sh[2] % (64 * kp) == 0]:
         x = normal_x(wl.seed_for(25, m), m, k)
         w = weights(wl.seed_for(25, 100 + n), n, k)
         y = run(stream, x, w, m, n, k, dispatch=d)
