@@ -413,7 +413,10 @@ const Variant* heuristic(const Problem& p, Op op) {
             // against 84.5 and 164 us for 16 x 16 tiles); up to 64 tokens
             // the 64 x 128 tiles (64 x 8192 x 28672: 119.4 us, against 150.3
             // us for 128 x 128 tiles); each with the deepest step K allows.
-            if (p.M <= 64 && prefill_tiles(p, 64, 128) >= 200)
+            // (up to 128 tokens where 128 x 128 tiles are too few: 128 x 4096
+            // x 14 336 in 45.7 us with 4 pairs per step, against 78.0 us on
+            // the 16 x 16 tiles)
+            if (p.M <= 128 && prefill_tiles(p, 64, 128) >= 200 && (p.M <= 64 || prefill_tiles(p, 128, 128) < 200))
                 return deepest_step("gateup_mfma_x32s_m64_n128_w1", p, 4);
             if (prefill_tiles(p, 128, 128) >= 200) return deepest_step("gateup_mfma_x32s_m128_n128_w1", p, 2);
             return by_name(p.M >= 128 ? "gateup_mfma_r_m128_n64" : "gateup_mfma_r_m64_n64");

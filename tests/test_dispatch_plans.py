@@ -84,6 +84,8 @@ def test_gate_up_and_q8_plans(d):
     assert d.select(64, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m64_n64_w2_k4"
     assert d.select(64, 28672, 8192, gate_up=True) == "gateup_mfma_x32s_m64_n128_w1_k4"
     assert d.select(32, 28672, 8192, gate_up=True) == "gateup_mfma_x32s_m64_n128_w1_k4"
+    assert d.select(128, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m64_n128_w1_k4"
+    assert d.select(192, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m128_n128_w1_k2"
     assert d.select(16, 28672, 8192, gate_up=True).startswith("gateup_skinny_")
     assert d.select(1, 14336, 4096, q8_0=True) == "q8_stream_d1_g1"
     assert d.select(16, 14336, 4096, q8_0=True).startswith("q8_skinny_")
