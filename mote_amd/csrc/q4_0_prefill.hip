@@ -103,15 +103,18 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
     const uint8_t* wsrc[NW] = {wg};
     if constexpr (GATE_UP) wsrc[1] = wu;
 
-    // Activation chunks: thread c of the tile copies 16 bytes (8 halves) of
-    // row c / (8 KP): pair (c / 8) % KP of the step, whose chunk c % 8 holds
-    // elements 8 (c % 4) .. + 7 of block (c % 8) / 4.
+    // Activation chunks: chunk c of the tile is 16 bytes (8 halves) of row
+    // (c / 8) % BM, pair (c / 8) / BM of the step, whose chunk c % 8 holds
+    // elements 8 (c % 4) .. + 7 of block (c % 8) / 4.  One store instruction
+    // covers one pair of consecutive rows, whose 16-byte row padding spreads
+    // them over the banks (the two pairs of a row lie 128 bytes apart, on the
+    // same banks).
     const uint16_t* xptr[XC];
     int xoff[XC];
 #pragma unroll
     for (int j = 0; j < XC; ++j) {
         const int c = tid + 256 * j;
-        const int row = c / (8 * KP), pair = (c / 8) % KP, chunk = c & 7;
+        const int row = (c >> 3) % BM, pair = (c >> 3) / BM, chunk = c & 7;
         const uint32_t m = min(m0 + row, M - 1);
         xptr[j] = x + static_cast<size_t>(m) * K + pair * 64 + chunk * 8;
         const int blk = chunk >> 2, kin = (chunk & 3) * 8;
@@ -121,7 +124,12 @@ __global__ __launch_bounds__(SPEC ? 512 : 256) void prefill_kernel(const uint16_
             xoff[j] = row * kXRow + pair * 128 + blk * 64 + ((kin & 15) >> 2) * 16 + (kin >= 16 ? 8 : 0);
     }
     // Weight units: thread t copies unit t, t + 256, ... of the step, unit u
-    // being block pair u % KP of row u / KP.
+    // being block pair u % KP of row u / KP: a load instruction reads KP
+    // neighbouring pairs of 64 / KP rows.  (One pair of 64 consecutive rows
+    // per instruction would keep the LDS stores free of bank conflicts, but
+    // measured slower with 4 pairs per step: 30.2 against 27.6 us at 128 x
+    // 4096 x 14 336, 110.6 against 95.3 us for the gate/up at 64 x 8192 x
+    // 28 672; level with 2.)
     const uint8_t* wptr[NW][WI];
     bool wlive[WI];
     int woff[WI];
