@@ -466,6 +466,28 @@ const Variant* heuristic(const Problem& p, Op op) {
             const Variant* v = by_name(rows_per_wave >= 3 ? "rowlds_r3d2" : "rowlds_r2d1");
             if (v && gemv_lds_supports(*v, p)) return v;
         }
+        // K past 4096: rows split over S waves through the LDS ring where
+        // each row group owns 8 rows or more and the slices fill 90 % of
+        // their load instructions, or 12 rows or more (measured on MI355X:
+        // 14336 x 4096 7.90 us, 13824 x 5120 8.90, 5120 x 13824 10.40,
+        // 8192 x 28672 22.2, 28672 x 8192 22.2, against 8.04, 9.30, 10.63,
+        // 22.6 and 23.8 us for the streaming GEMV below; that one stays ahead
+        // at 11008 x 4096, 7.23 us against 7.46, ties at 8192 x 8192, 8.21
+        // us, and leads with fewer rows, 14336 x 1024 4.54 us against 4.78).
+        if (p.K > 4096 && p.K % 256 == 0) {
+            uint32_t s = 2;
+            while (s < 8 && p.K > 4096u * s) s *= 2;
+            const uint32_t span = (p.K / 64 + s - 1) / s;
+            const uint32_t chunks = (span * 36 + 15) / 16, loads = (chunks + 63) / 64;
+            const uint64_t rows_per_group = p.N / (static_cast<uint64_t>(device_cus()) * (8u / s));
+            const bool full = 10u * chunks >= 9u * 64u * loads;
+            if ((rows_per_group >= 8 && full) || rows_per_group >= 12) {
+                char name[32];
+                std::snprintf(name, sizeof name, "rowlds_s%u_r3d2_g1", s);
+                const Variant* v = by_name(name);
+                if (v && gemv_lds_supports(*v, p)) return v;
+            }
+        }
         // Measured on MI355X (graph replays, weights rotated past the MALL):
         // the persistent pipelined GEMV, with rows split over S waves for
         // K > 4096 (4096 x 14336: 7.3 us; 14336 x 4096: 8.0 us, against

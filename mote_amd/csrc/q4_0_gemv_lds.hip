@@ -200,6 +200,181 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_kernel(const uint16_t* __re
     }
 }
 
+// LDS slot of a slice of `span` pairs: the 16-byte chunks that overlap it
+// wherever it starts (a multiple of 4 bytes into a chunk).
+__host__ __device__ constexpr uint32_t slot_size(uint32_t span) { return (span * kPairBytes + 15u) / 16u * 16u + 16u; }
+
+// Load instructions per slice of a row split over s waves: enough for the
+// widest slice, and 0 (unsupported) unless every slice's last instruction
+// keeps at least one lane (the wait counts assume LOADS loads per row, and the
+// other instructions load whole).
+inline uint32_t split_loads(uint32_t s, uint32_t k) {
+    const uint32_t npairs = k / 64, span = (npairs + s - 1) / s;
+    uint32_t lo = 0xFFFFFFFFu, hi = 0;
+    for (uint32_t i = 0; i < s; ++i) {
+        if (i * span >= npairs) return 0;
+        const uint32_t b0 = i * span * kPairBytes, count = npairs - i * span < span ? npairs - i * span : span;
+        const uint32_t chunks = (b0 + count * kPairBytes + 15u) / 16u - b0 / 16u;
+        lo = chunks < lo ? chunks : lo;
+        hi = chunks > hi ? chunks : hi;
+    }
+    const uint32_t loads = (hi + 63u) / 64u;
+    return loads >= 1 && loads <= 3 && lo > 64u * (loads - 1) ? loads : 0;
+}
+
+// Dynamic LDS of the split-row kernel: the waves' rings, then x in 8 KB steps.
+__host__ __device__ constexpr size_t split_lds_bytes(uint32_t s, uint32_t r, uint32_t k) {
+    return static_cast<size_t>(kWaves) * r * slot_size((k / 64 + s - 1) / s) + (k + 4095u) / 4096u * 8192u;
+}
+
+// Rows split over S waves (K past 4096, up to about 4096 S): wave w of a
+// workgroup reads slice w % S of its row group's rows -- pairs [s span,
+// min((s + 1) span, K / 64)) with span = ceil(K / (64 S)), the pair
+// assignment of the split-row streaming GEMV -- through its own ring, and
+// lane l owns pair l of the slice.  A slice starts 36 s span bytes into a row
+// (rows start on 16-byte boundaries, K % 256 == 0), so its loads cover the
+// 16-byte chunks that overlap it and its pairs sit (36 s span) % 16 bytes
+// into the ring slot.  x is staged once per workgroup in LDS by direct-to-LDS
+// loads (thread t loads 16-byte chunks t, t + 512, ..., clamped, into 8 KB
+// steps), issued before the first rows; each lane then reads its pair's 128
+// bytes (measured on MI355X at 14336 x 4096: 7.85 us, against 8.69 us with
+// every lane loading its pair's x into registers, twice the L2 traffic).
+// The slice sums are added in slice order through LDS, as in the streaming
+// GEMV, so the two agree bit for bit; that addition sits behind workgroup
+// barriers, so every wave runs the row count of its workgroup's first row
+// group (the largest), and a group with one row fewer re-reads its last row
+// once and does not store it.
+template <int S, int R, int D, int LOADS, typename OutT>
+__global__ __launch_bounds__(kThreads) void gemv_lds_split_kernel(const uint16_t* __restrict__ x,
+                                                                 const uint8_t* __restrict__ w,
+                                                                 OutT* __restrict__ y, uint32_t N, uint32_t K,
+                                                                 uint32_t total_groups) {
+    static_assert(S == 2 || S == 4 || S == 8, "whole row groups per workgroup");
+    static_assert(D >= 1 && D <= 3 && D < R, "the ring holds the rows in flight and the one computed");
+    constexpr uint32_t kGroups = kWaves / S;
+    // [waves][R][slot bytes], then x in 8 KB steps
+    extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
+    __shared__ float red[kThreads];  // slice sums of 64 rows
+    const int tid = static_cast<int>(threadIdx.x);
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const uint32_t slice = static_cast<uint32_t>(wave) % S;
+    const uint32_t npairs = K >> 6;
+    const uint32_t span = (npairs + S - 1) / S;
+    const uint32_t first_pair = slice * span;
+    const uint32_t count = min(span, npairs - first_pair);  // >= 1: every slice holds pairs
+    const size_t row_bytes = static_cast<size_t>(npairs) * kPairBytes;  // a multiple of 16
+    const uint32_t b0 = first_pair * kPairBytes;
+    const uint32_t c0 = b0 >> 4;
+    const uint32_t chunks = (b0 + count * kPairBytes + 15u) / 16u - c0;
+    const uint32_t slot_bytes = slot_size(span);
+    uint8_t* ring = ring_lds + static_cast<uint32_t>(wave) * R * slot_bytes;
+    const uint32_t g = blockIdx.x * kGroups + static_cast<uint32_t>(wave) / S;
+    const uint32_t nrows = g < N ? (N - 1 - g) / total_groups + 1 : 0;
+    const uint32_t last = g < N ? g + (nrows - 1) * total_groups : N - 1;
+    // the grid has no workgroup without a row: its first group's g < N
+    const uint32_t trips = (N - 1 - blockIdx.x * kGroups) / total_groups + 1;
+    const uint32_t pc = min(static_cast<uint32_t>(lane), count - 1);
+    const uint32_t keep = static_cast<uint32_t>(lane) < count ? 0xFFFFFFFFu : 0u;  // NaN-safe drop of idle lanes
+    const uint8_t* wslice = w + 16u * c0;
+
+    // Chunks of row jj's slice (jj < trips) into ring slot `slot`; the last
+    // instruction's lanes past the slice idle (lane 0 always loads).
+    auto load_row = [&](uint32_t jj, uint32_t slot) {
+        const uint8_t* src = wslice + static_cast<size_t>(min(g + jj * total_groups, last)) * row_bytes;
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const uint32_t c = 64u * static_cast<uint32_t>(i) + static_cast<uint32_t>(lane);
+            if (i + 1 < LOADS || c < chunks)
+                __builtin_amdgcn_global_load_lds(src + 16u * c, (lds_ptr)(ring + slot * slot_bytes + 1024u * i), 16,
+                                                 0, 2 /* non-temporal */);
+        }
+    };
+    auto wait_rows = [&](uint32_t rows) {
+        if (rows >= 3 && D >= 3) __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * 3));
+        else if (rows == 2 && D >= 2) __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * 2));
+        else if (rows == 1) __builtin_amdgcn_s_waitcnt(0x0F70 | LOADS);
+        else __builtin_amdgcn_s_waitcnt(0x0F70);
+    };
+
+    // x first, then the first rows; loads retire in order, so once only those
+    // rows are outstanding this wave's x chunks have landed, and after the
+    // barrier every wave's have.
+    const uint32_t xsteps = (K + 4095u) / 4096u;
+    uint8_t* xs = ring_lds + kWaves * R * slot_bytes;
+    for (uint32_t i = 0; i < xsteps; ++i) {
+        const uint32_t c = min(512u * i + static_cast<uint32_t>(tid), K / 8u - 1u);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(x) + 16u * c,
+                                         (lds_ptr)(xs + 8192u * i + 1024u * static_cast<uint32_t>(wave)), 16, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        if (static_cast<uint32_t>(d) < trips) load_row(static_cast<uint32_t>(d), static_cast<uint32_t>(d));
+    __builtin_amdgcn_sched_barrier(0);
+    wait_rows(trips < static_cast<uint32_t>(D) ? trips : static_cast<uint32_t>(D));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+
+    XPair xv;
+    {
+        uint32_t xr[32];
+        const uint8_t* xslot = xs + (first_pair + pc) * 128u;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(xslot + i * 16);
+            xr[4 * i + 0] = v.x; xr[4 * i + 1] = v.y; xr[4 * i + 2] = v.z; xr[4 * i + 3] = v.w;
+        }
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            s0 = dot2(xr[i], kOnePair, s0);
+            s1 = dot2(xr[16 + i], kOnePair, s1);
+        }
+        xv.c0 = (-8.0f / 1048576.0f) * s0;
+        xv.c1 = (-8.0f / 1048576.0f) * s1;
+        order_x(xr, xv);
+    }
+
+    // Lane j % 64 holds the slice sum of row j; every 64 rows and at the end
+    // slice 0 adds the other slices' sums (in slice order) and stores.
+    float mine = 0.0f;
+    auto flush = [&](uint32_t first, uint32_t n) {
+        red[tid] = mine;
+        __syncthreads();
+        float t = mine;
+        if (slice == 0) {
+#pragma unroll
+            for (int r = 1; r < S; ++r) t += red[(wave + r) * 64 + lane];
+        }
+        __syncthreads();
+        if (slice == 0 && static_cast<uint32_t>(lane) < n)
+            y[g + (first + static_cast<uint32_t>(lane)) * total_groups] = to_out<OutT>(1048576.0f * t);
+    };
+    const uint32_t pair_offset = (b0 & 15u) + pc * kPairBytes;
+    for (uint32_t j = 0; j < trips; ++j) {
+        if (j + D < trips) {
+            load_row(j + D, (j + D) % R);
+            __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * D));
+        } else {
+            wait_rows(trips - 1 - j);
+        }
+        const uint32_t* pr = reinterpret_cast<const uint32_t*>(ring + (j % R) * slot_bytes + pair_offset);
+        uint32_t raw[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) raw[i] = pr[i];
+        const float part = 0.0f + __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pair_dot(raw, xv)) & keep);
+        const float s = wave_sum(part);
+        mine = static_cast<uint32_t>(lane) == (j & 63u) ? s : mine;
+        if ((j & 63u) == 63u) {  // uniform over the workgroup
+            const uint32_t first = j - 63u;
+            flush(first, nrows > first ? min(nrows - first, 64u) : 0u);
+        }
+    }
+    const uint32_t base = trips & ~63u;
+    if (base < trips) flush(base, nrows > base ? nrows - base : 0u);
+}
+
 template <int R, int D>
 hipError_t launch_gemv_lds(const Problem& p) {
     static const int cus = [] {
@@ -238,11 +413,54 @@ hipError_t launch_gemv_lds(const Problem& p) {
     return hipGetLastError();
 }
 
-// p0 = ring slots, p1 = rows in flight.
+template <int S, int R, int D, int G>
+hipError_t launch_gemv_lds_split(const Problem& p) {
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        return n;
+    }();
+    constexpr uint32_t kGroups = kWaves / S;
+    const uint32_t loads = split_loads(S, p.K);
+    uint32_t groups = static_cast<uint32_t>(cus) * G;
+    const uint32_t need = (p.N + kGroups - 1) / kGroups;  // no workgroup without a row
+    if (groups > need) groups = need;
+    const size_t lds = split_lds_bytes(S, R, p.K);
+    const dim3 grid(groups), block(kThreads);
+    const auto* x = static_cast<const uint16_t*>(p.x);
+    const auto* w = static_cast<const uint8_t*>(p.w);
+    const uint32_t total = groups * kGroups;
+#define MOTE_LDS_LAUNCH(L)                                                                                      \
+    do {                                                                                                        \
+        if (p.out == OutType::F32)                                                                              \
+            hipLaunchKernelGGL((gemv_lds_split_kernel<S, R, D, L, float>), grid, block, lds, p.stream, x, w,   \
+                               static_cast<float*>(p.y), p.N, p.K, total);                                    \
+        else                                                                                                    \
+            hipLaunchKernelGGL((gemv_lds_split_kernel<S, R, D, L, _Float16>), grid, block, lds, p.stream, x, w, \
+                               static_cast<_Float16*>(p.y), p.N, p.K, total);                                 \
+    } while (0)
+    switch (loads) {
+        case 1: MOTE_LDS_LAUNCH(1); break;
+        case 2: MOTE_LDS_LAUNCH(2); break;
+        case 3: MOTE_LDS_LAUNCH(3); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef MOTE_LDS_LAUNCH
+    return hipGetLastError();
+}
+
+// p0 = ring slots, p1 = rows in flight, p2 = waves per row (0: one).
 const Variant kLds[] = {
     Variant{"rowlds_r2d1", Kind::GemvLds, 2, 1, 0, &launch_gemv_lds<2, 1>},
     Variant{"rowlds_r3d1", Kind::GemvLds, 3, 1, 0, &launch_gemv_lds<3, 1>},
     Variant{"rowlds_r3d2", Kind::GemvLds, 3, 2, 0, &launch_gemv_lds<3, 2>},
+#define MOTE_LDS_SPLIT(S, R, D, G) \
+    Variant{"rowlds_s" #S "_r" #R "d" #D "_g" #G, Kind::GemvLds, R, D, S, &launch_gemv_lds_split<S, R, D, G>}
+    MOTE_LDS_SPLIT(2, 3, 2, 1), MOTE_LDS_SPLIT(4, 2, 1, 1), MOTE_LDS_SPLIT(4, 3, 2, 1), MOTE_LDS_SPLIT(4, 4, 3, 1),
+    MOTE_LDS_SPLIT(8, 3, 2, 1),
+#undef MOTE_LDS_SPLIT
 };
 
 }  // namespace
@@ -252,13 +470,19 @@ const Variant* gemv_lds_variants(int* count) {
     return kLds;
 }
 
-// One token, K a multiple of 256 from 256 to 4096 (rows start on 16-byte
-// boundaries), weights and x 16-byte aligned (the direct-to-LDS loads move
+// One token, K a multiple of 256 (rows start on 16-byte boundaries) up to
+// 4096 (one pair per lane), or with rows split over S waves up to 64 pairs per
+// slice, every slice non-empty, and the rings and x within the workgroup's
+// 160 KB of LDS; weights and x 16-byte aligned (the direct-to-LDS loads move
 // aligned 16-byte chunks).
 bool gemv_lds_supports(const Variant& v, const Problem& p) {
-    (void)v;
-    return p.M == 1 && p.K % 256 == 0 && p.K >= 256 && p.K <= kMaxK && reinterpret_cast<uintptr_t>(p.w) % 16 == 0 &&
-           reinterpret_cast<uintptr_t>(p.x) % 16 == 0 && p.w_up == nullptr;
+    if (p.M != 1 || p.K % 256 != 0 || p.K == 0 || p.w_up != nullptr || reinterpret_cast<uintptr_t>(p.w) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(p.x) % 16 != 0)
+        return false;
+    if (v.p2 <= 1) return p.K <= kMaxK;
+    const uint32_t s = static_cast<uint32_t>(v.p2), npairs = p.K / 64, span = (npairs + s - 1) / s;
+    return span <= 64 && (s - 1) * span < npairs && split_loads(s, p.K) != 0 &&
+           split_lds_bytes(s, static_cast<uint32_t>(v.p0), p.K) + kThreads * sizeof(float) <= 160u * 1024u;
 }
 
 }  // namespace mote::q4_0

@@ -28,10 +28,15 @@ LINEAR = [
     ((1, 4096, 6144), "rowlds_r3d2"),
     ((1, 1024, 4096), "rowlds_r2d1"),
     ((1, 4160, 4096), "stream_s2_d1_g2"),
-    ((1, 14336, 4096), "stream_s4_d1q_g2"),
+    ((1, 14336, 4096), "rowlds_s4_r3d2_g1"),
+    ((1, 13824, 5120), "rowlds_s4_r3d2_g1"),
+    ((1, 5120, 13824), "rowlds_s2_r3d2_g1"),
+    ((1, 8192, 28672), "rowlds_s2_r3d2_g1"),
+    ((1, 14336, 1024), "stream_s4_d1q_g1"),
+    ((1, 8192, 8192), "stream_s2_d1_g2"),
     ((1, 11008, 4096), "stream_s4_d1q_g2"),
     ((1, 4096, 11008), "rowlds_r3d2"),
-    ((1, 28672, 8192), "stream_s8_d1_g2"),
+    ((1, 28672, 8192), "rowlds_s8_r3d2_g1"),
     ((2, 4096, 14336), "stream_m2_d1q_g1"),
     ((2, 14336, 4096), "stream_s4_m2_d1q_g1"),
     ((3, 8192, 8192), "stream_s2_m3_d1q_g1"),

@@ -7,9 +7,21 @@ per row with the last one partly idle (K = 256 ... 4096), N below one
 workgroup, ragged N, and N = 140001 at K = 256, where each wave owns more
 than 64 rows and stores its register-held sums mid-loop; f32 and f16
 outputs.  The arithmetic is the pair-load streaming GEMV's, so the outputs
-must equal it bit for bit, and the oracle's tolerance holds too."""
+must equal it bit for bit, and the oracle's tolerance holds too.
+
+The variants with rows split over S waves (``rowlds_s<S>_...``, K a multiple
+of 256 with at most 64 pairs per slice) run slices of one to three load
+instructions, slices that start 4, 8 and 12 bytes into a 16-byte chunk
+(K = 3328, 4352, 11008, 13824 ...), a last slice shorter than the others
+(K = 6400 and 2304 at S = 8), N below one workgroup's row groups, ragged N
+(row groups of one workgroup with different row counts), the down
+projection's 14336 x 4096, and more than 64 rows per group (the slice sums
+are added through LDS mid-loop); they must equal the split-row streaming
+GEMV with the same S bit for bit."""
 
 from __future__ import annotations
+
+import re
 
 import numpy as np
 import pytest
@@ -23,13 +35,29 @@ SHAPES = [(1, 256), (7, 1024), (257, 1792), (130, 2048), (61, 3072), (1000, 3584
           (14336, 4096), (140001, 256)]
 
 
+SPLIT_SHAPES = {
+    2: [(1, 512), (7, 2048), (257, 4352), (61, 6144), (1000, 7424), (4099, 8192), (70001, 768)],
+    4: [(1, 1024), (5, 3328), (257, 5376), (130, 8192), (61, 11008), (4099, 14336), (4096, 14336), (33, 16384),
+        (70001, 1280)],
+    8: [(1, 2048), (3, 6400), (257, 10240), (130, 13824), (4099, 28672), (1000, 32768), (40001, 2304)],
+}
+REFERENCE = {1: "stream_d1_g2", 2: "stream_s2_d1_g1", 4: "stream_s4_d1q_g1", 8: "stream_s8_d1_g1"}
+
+
+def _split(variant: str) -> int:
+    m = re.match(r"rowlds_s(\d+)_", variant)
+    return int(m.group(1)) if m else 1
+
+
 @pytest.mark.parametrize("variant", [v for v in ops.variant_names() if v.startswith("rowlds_")])
 def test_every_rowlds_variant(stream, oracle, variant):
+    split = _split(variant)
     d = ops.Q4_0Dispatch()
     d.force(variant)
     ref = ops.Q4_0Dispatch()
-    ref.force("stream_d1_g2")
-    for n, k in SHAPES:
+    ref.force(REFERENCE[split])
+    for n, k in SHAPES if split == 1 else SPLIT_SHAPES[split]:
+        print(f"{variant} 1x{n}x{k}", flush=True)
         x = normal_x(wl.seed_for(17, k), 1, k)
         w = weights(wl.seed_for(17, 100 + n), n, k)
         cols = None if n < 5000 else sample_columns(n, 512)
@@ -41,13 +69,20 @@ def test_every_rowlds_variant(stream, oracle, variant):
                                  what=f"{variant} 1x{n}x{k}{' f16' if f16_out else ''}")
 
 
-def test_rowlds_rejects_what_it_cannot_run(stream):
-    """K not a multiple of 256, K past 4096 and two tokens fall outside the
-    variant: forcing it is an error, never a silent misread."""
+@pytest.mark.parametrize("variant,shapes", [
+    ("rowlds_r2d1", [(1, 64, 192), (1, 64, 4352), (2, 64, 1024)]),
+    ("rowlds_s4_r3d2_g1", [(1, 64, 3200), (1, 64, 17408), (2, 64, 14336)]),
+    ("rowlds_s8_r3d2_g1", [(1, 64, 1792), (1, 64, 14592), (1, 64, 33024)]),
+])
+def test_rowlds_rejects_what_it_cannot_run(stream, variant, shapes):
+    """K not a multiple of 256, more than 64 pairs per slice, slices whose
+    last load instruction would be idle (K = 1792 and 14592 at S = 8) and two
+    tokens fall outside the variant: forcing it is an error, never a silent
+    misread."""
     d = ops.Q4_0Dispatch()
-    d.force("rowlds_r2d1")
+    d.force(variant)
     from mote_amd import HipError
-    for m, n, k in [(1, 64, 192), (1, 64, 4352), (2, 64, 1024)]:
+    for m, n, k in shapes:
         x = normal_x(wl.seed_for(17, 1), m, k)
         w = weights(wl.seed_for(17, 2), n, k)
         with pytest.raises(HipError):
