@@ -1,6 +1,6 @@
-// Decode GEMV (M = 1) over GGML Q4_0 for K a multiple of 256 up to 4096, with
-// the weight rows streamed through a per-wave LDS ring by CDNA4's
-// direct-to-LDS loads.
+// Decode GEMV (M = 1) over GGML Q4_0 for K a multiple of 256, with the weight
+// rows streamed through a per-wave LDS ring by CDNA4's direct-to-LDS loads:
+// whole rows for K up to 4096, rows split over 2, 4 or 8 waves past that.
 //
 // Computes y[n] = sum_k x[k] * w[n, k] for f16 x [1, K] and Q4_0 w [N, K], the
 // operation of crates/mote-backend-hip/src/quantized_linear.hip:13-52 (oracle
