@@ -38,7 +38,8 @@ constexpr size_t kSplitKCounterBytes = 64 * 1024;
 
 enum class Kind : int { Gemv = 0, Mfma = 1, Generic = 2, GateUpMfma = 3, GateUpGeneric = 4, GemvRows = 5,
                         GemvStream = 6, SkinnyMfma = 7, Q8Stream = 8, Q8Generic = 9, GateUpSkinny = 10,
-                        GateUpStream = 11, Q8Skinny = 12, Q8Prefill = 13, GemvLds = 14 };
+                        GateUpStream = 11, Q8Skinny = 12, Q8Prefill = 13, GemvLds = 14,
+                        Q8Lds = 15 };
 
 struct Variant {
     const char* name;

@@ -74,8 +74,8 @@ bool kind_matches(const Variant& v, Op op) {
         return v.kind == Kind::GateUpMfma || v.kind == Kind::GateUpSkinny || v.kind == Kind::GateUpStream ||
                v.kind == Kind::GateUpGeneric;
     if (op == Op::LinearQ8)
-        return v.kind == Kind::Q8Stream || v.kind == Kind::Q8Skinny || v.kind == Kind::Q8Prefill ||
-               v.kind == Kind::Q8Generic;
+        return v.kind == Kind::Q8Stream || v.kind == Kind::Q8Lds || v.kind == Kind::Q8Skinny ||
+               v.kind == Kind::Q8Prefill || v.kind == Kind::Q8Generic;
     return v.kind == Kind::Gemv || v.kind == Kind::GemvRows || v.kind == Kind::GemvStream ||
            v.kind == Kind::GemvLds || v.kind == Kind::SkinnyMfma || v.kind == Kind::Mfma || v.kind == Kind::Generic;
 }
@@ -84,7 +84,8 @@ bool supports(const Variant& v, const Problem& p) {
     switch (v.kind) {
         case Kind::Gemv: return gemv_supports(v, p);
         case Kind::GemvRows: return gemv_rows_supports(v, p);
-        case Kind::GemvLds: return gemv_lds_supports(v, p);
+        case Kind::GemvLds:
+        case Kind::Q8Lds: return gemv_lds_supports(v, p);
         case Kind::GemvStream:
         case Kind::GateUpStream:
         case Kind::Q8Stream: return gemv_stream_supports(v, p);
@@ -114,7 +115,7 @@ std::vector<const Variant*> candidates(const Problem& p, Op op) {
         if (generic && fast_eligible(p)) continue;
         const bool vector_alu = v->kind == Kind::Gemv || v->kind == Kind::GemvRows || v->kind == Kind::GemvLds ||
                                 v->kind == Kind::GemvStream || v->kind == Kind::Q8Stream ||
-                                v->kind == Kind::GateUpStream;
+                                v->kind == Kind::GateUpStream || v->kind == Kind::Q8Lds;
         if (vector_alu && p.M >= 64) continue;
         const bool skinny = v->kind == Kind::SkinnyMfma || v->kind == Kind::GateUpSkinny || v->kind == Kind::Q8Skinny;
         if (skinny && p.M > 64) continue;
@@ -321,6 +322,31 @@ const Variant* split_k_heuristic(const Problem& p, Op op) {
 const Variant* heuristic(const Problem& p, Op op) {
     const bool fast = fast_eligible(p);
     if (op == Op::LinearQ8) {
+        // K a multiple of 256: Q8_0 rows through the per-wave LDS ring
+        // (q4_0_gemv_lds.hip), one to three tokens per row read up to K =
+        // 4096, one token with rows split over S waves above.  Measured on
+        // MI355X against the streaming GEMV (or, for three tokens, the skinny
+        // tiles): 1 x 4096 x 4096 4.88 us (5.71), x 14336 11.09 (12.46), 2 x
+        // 4096 x 14336 12.10 (13.52), 3 x 4096 x 14336 13.17 (14.66), 14336 x
+        // 4096 11.41 (12.24), 28672 x 8192 37.95 (41.06).  Four tokens stay
+        // on the streaming GEMV (4 x 4096 x 4096: 6.78 us against 8.17).
+        if (fast && p.K % 256 == 0 && (p.M <= 3 && p.K <= 4096)) {
+            char name[32];
+            if (p.M == 1)
+                std::snprintf(name, sizeof name, "q8_rowlds_r2d1");
+            else
+                std::snprintf(name, sizeof name, "q8_rowlds_m%u_r2d1", p.M);
+            const Variant* v = by_name(name);
+            if (v && gemv_lds_supports(*v, p)) return v;
+        }
+        if (fast && p.K % 256 == 0 && p.M == 1 && p.K > 4096) {
+            uint32_t split = 2;
+            while (split < 8 && p.K > 4096u * split) split *= 2;
+            char name[32];
+            std::snprintf(name, sizeof name, "q8_rowlds_s%u_r2d1", split);
+            const Variant* v = by_name(name);
+            if (v && gemv_lds_supports(*v, p)) return v;
+        }
         // The streaming GEMV over Q8_0 pairs for 1, 2 or 4 tokens (rows split
         // over S waves above K = 4096; one workgroup per CU measured fastest
         // for Q8_0's 68-byte pairs at every Llama shape), the generic kernel

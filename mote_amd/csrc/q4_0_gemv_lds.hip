@@ -28,6 +28,7 @@
 // (the pair-load kernel: 7.62), 11008 6.23 (7.07), 6144 4.62 (5.14), 4096
 // 3.90 (4.22), 1024 3.12 (3.51).
 #include "common.hpp"
+#include "gemv_formats.hpp"
 #include "q4_0.hpp"
 
 namespace mote::q4_0 {
@@ -35,77 +36,31 @@ namespace {
 
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * kWave;
-constexpr uint32_t kSubLo = 0x000F000Fu;  // low nibbles of bytes 0 and 2: n * 2^-24
-constexpr uint32_t kSubHi = 0x00F000F0u;  // high nibbles of bytes 0 and 2: n * 2^-20
 constexpr uint32_t kMaxK = 4096;
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
-__device__ __forceinline__ uint32_t pick(const uint32_t* x, int a, int b) {
-    const uint32_t lo = (a & 1) ? 0x0302u : 0x0100u;
-    const uint32_t hi = (b & 1) ? 0x07060000u : 0x05040000u;
-    return __builtin_amdgcn_perm(x[b >> 1], x[a >> 1], hi | lo);
-}
+// s_waitcnt immediate that waits until at most n vector memory loads are
+// outstanding (vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt not waited).
+constexpr int vm_wait(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
 
-// x of a pair in the order of the nibble operands, and the start values of
-// the two blocks' sums (-8 2^-20 times the block's sum of x).
-struct XPair {
-    uint32_t xp[32];
-    float c0, c1;
-};
-
-__device__ __forceinline__ void order_x(const uint32_t (&xr)[32], XPair& xv) {
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-        const int base = (q < 4) ? 0 : 32;
-        const int e0 = base + pair_byte_element(q, 0), e1 = base + pair_byte_element(q, 1);
-        const int e2 = base + pair_byte_element(q, 2), e3 = base + pair_byte_element(q, 3);
-        xv.xp[4 * q + 0] = pick(xr, e0 + 16, e2 + 16);  // hi02
-        xv.xp[4 * q + 1] = pick(xr, e0, e2);            // lo02
-        xv.xp[4 * q + 2] = pick(xr, e1, e3);            // lo13
-        xv.xp[4 * q + 3] = pick(xr, e1 + 16, e3 + 16);  // hi13
-    }
-}
-
-// sum_k x_k (n_k - 8) d of the two blocks of a pair, divided by 2^20.
-__device__ __forceinline__ float pair_dot(const uint32_t (&raw)[9], const XPair& x) {
-    uint32_t q[8];
-    q[0] = pair_q0(raw);
-    q[1] = raw[1]; q[2] = raw[2]; q[3] = raw[3];
-    q[4] = raw[5]; q[5] = raw[6]; q[6] = raw[7]; q[7] = raw[8];
-    const float d0 = half_lo_to_float(raw[0]);
-    const float d1 = half_hi_to_float(raw[4]);
-    float lo0 = 0.0f, hi0 = x.c0, lo1 = 0.0f, hi1 = x.c1;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t a = q[i], b = q[4 + i];
-        const uint32_t a8 = a >> 8, b8 = b >> 8;
-        hi0 = dot2(a & kSubHi, x.xp[4 * i + 0], hi0);
-        lo0 = dot2(a & kSubLo, x.xp[4 * i + 1], lo0);
-        lo0 = dot2(a8 & kSubLo, x.xp[4 * i + 2], lo0);
-        hi0 = dot2(a8 & kSubHi, x.xp[4 * i + 3], hi0);
-        hi1 = dot2(b & kSubHi, x.xp[16 + 4 * i + 0], hi1);
-        lo1 = dot2(b & kSubLo, x.xp[16 + 4 * i + 1], lo1);
-        lo1 = dot2(b8 & kSubLo, x.xp[16 + 4 * i + 2], lo1);
-        hi1 = dot2(b8 & kSubHi, x.xp[16 + 4 * i + 3], hi1);
-    }
-    const float acc = d0 * __builtin_fmaf(lo0, 16.0f, hi0);
-    return __builtin_fmaf(d1, __builtin_fmaf(lo1, 16.0f, hi1), acc);
-}
-
-// LOADS: 16-byte chunks of a row / 64, rounded up (1 for K <= 1792, 2 up to
-// 3584, 3 up to 4096).
-template <int R, int D, int LOADS, typename OutT>
+// F: the weight format (FmtQ4: 36-byte Q4_0 block pairs, FmtQ8: 68-byte Q8_0
+// pairs); MT: tokens, every row read once for all of them (the pair's
+// operands unpacked once and shared by the tokens' dot chains).  LOADS:
+// 16-byte chunks of a row / 64, rounded up (Q4_0: 1 for K <= 1792, 2 up to
+// 3584, 3 up to 4096; Q8_0: up to 5).
+template <class F, int MT, int R, int D, int LOADS, typename OutT>
 __global__ __launch_bounds__(kThreads) void gemv_lds_kernel(const uint16_t* __restrict__ x,
                                                            const uint8_t* __restrict__ w, OutT* __restrict__ y,
                                                            uint32_t N, uint32_t K, uint32_t total_groups) {
     static_assert(D >= 1 && D <= 3 && D < R, "the ring holds the rows in flight and the one computed");
-    extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];     // [waves][R][row bytes]
-    __shared__ __attribute__((aligned(16))) uint8_t xs[kMaxK * 2];        // x, contiguous
+    static_assert(MT >= 1 && MT <= 4, "tokens per row read");
+    extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];  // [waves][R][row bytes]
+    __shared__ __attribute__((aligned(16))) uint8_t xs[MT * kMaxK * 2];  // x of token m at 8 KB m
     const int tid = static_cast<int>(threadIdx.x);
     const int wave = tid >> 6;
     const int lane = tid & 63;
     const uint32_t npairs = K >> 6;
-    const uint32_t row_bytes = npairs * kPairBytes;  // a multiple of 16: K % 256 == 0
+    const uint32_t row_bytes = npairs * F::kPairBytes;  // a multiple of 16: K % 256 == 0
     const uint32_t chunks = row_bytes >> 4;
     uint8_t* ring = ring_lds + static_cast<uint32_t>(wave) * R * row_bytes;
     const uint32_t g = blockIdx.x * kWaves + static_cast<uint32_t>(wave);
@@ -127,36 +82,41 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_kernel(const uint16_t* __re
         }
     };
 
-    // x first: thread t loads 16-byte chunk t (clamped) to xs + 16 t, and
-    // every wave's x load is issued before any weight load of the workgroup.
+    // x first: thread t loads 16-byte chunk t (clamped) of every token to xs
+    // + 8 KB m + 16 t, and every wave's x loads are issued before any weight
+    // load of the workgroup.
     const uint32_t xc = min(static_cast<uint32_t>(tid), npairs * 8 - 1);
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(x) + 16u * xc,
-                                     (lds_ptr)(xs + 1024u * static_cast<uint32_t>(wave)), 16, 0, 0);
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(x) + static_cast<size_t>(m) * K * 2 + 16u * xc,
+                                         (lds_ptr)(xs + m * kMaxK * 2 + 1024u * static_cast<uint32_t>(wave)), 16, 0,
+                                         0);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     // Waits until at most `rows` rows' loads (rows <= D, wave-uniform) are
     // outstanding (vmcnt counts in issue order).
     auto wait_rows = [&](uint32_t rows) {
-        if (rows >= 3 && D >= 3) __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * 3));
-        else if (rows == 2 && D >= 2) __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * 2));
-        else if (rows == 1) __builtin_amdgcn_s_waitcnt(0x0F70 | LOADS);
-        else __builtin_amdgcn_s_waitcnt(0x0F70);
+        if (rows >= 3 && D >= 3) __builtin_amdgcn_s_waitcnt(vm_wait(LOADS * 3));
+        else if (rows == 2 && D >= 2) __builtin_amdgcn_s_waitcnt(vm_wait(LOADS * 2));
+        else if (rows == 1) __builtin_amdgcn_s_waitcnt(vm_wait(LOADS));
+        else __builtin_amdgcn_s_waitcnt(vm_wait(0));
     };
 #pragma unroll
     for (int d = 0; d < D; ++d)
         if (static_cast<uint32_t>(d) < nrows) load_row(static_cast<uint32_t>(d), static_cast<uint32_t>(d));
     __builtin_amdgcn_sched_barrier(0);
     // no more than this wave's first rows' loads outstanding means its x
-    // chunk has landed; the barrier then covers every wave's
+    // chunks have landed; the barrier then covers every wave's
     wait_rows(nrows < static_cast<uint32_t>(D) ? nrows : static_cast<uint32_t>(D));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 
-    XPair xv;
-    {
+    XPair xv[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
         uint32_t xr[32];
-        const uint8_t* slot = xs + pc * 128u;
+        const uint8_t* slot = xs + m * kMaxK * 2 + pc * 128u;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const u32x4 v = *reinterpret_cast<const u32x4*>(slot + i * 16);
@@ -168,63 +128,82 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_kernel(const uint16_t* __re
             s0 = dot2(xr[i], kOnePair, s0);
             s1 = dot2(xr[16 + i], kOnePair, s1);
         }
-        xv.c0 = (-8.0f / 1048576.0f) * s0;
-        xv.c1 = (-8.0f / 1048576.0f) * s1;
-        order_x(xr, xv);
+        xv[m].c0 = F::kStart * s0;
+        xv[m].c1 = F::kStart * s1;
+        F::order_x(xr, xv[m]);
     }
 
     // Row sums stay in lanes (lane j % 64 holds row j) and are stored every 64
     // rows and at the end.
-    float mine = 0.0f;
+    float mine[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) mine[m] = 0.0f;
     for (uint32_t j = 0; j < nrows; ++j) {
         // Rows are loaded only up to the wave's last, so the loads left in
         // flight once row j has landed shrink at the end.
         if (j + D < nrows) {
             load_row(j + D, (j + D) % R);
-            __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * D));
+            __builtin_amdgcn_s_waitcnt(vm_wait(LOADS * D));
         } else {
             wait_rows(nrows - 1 - j);
         }
-        const uint32_t* pr = reinterpret_cast<const uint32_t*>(ring + (j % R) * row_bytes + pc * kPairBytes);
-        uint32_t raw[9];
+        const uint32_t* pr = reinterpret_cast<const uint32_t*>(ring + (j % R) * row_bytes + pc * F::kPairBytes);
+        uint32_t raw[F::kDwords];
 #pragma unroll
-        for (int i = 0; i < 9; ++i) raw[i] = pr[i];
-        const float part = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pair_dot(raw, xv)) & keep);
-        const float s = wave_sum(part);
-        mine = static_cast<uint32_t>(lane) == (j & 63u) ? s : mine;
+        for (int i = 0; i < F::kDwords; ++i) raw[i] = pr[i];
+        float part[MT];
+        if constexpr (MT == 1) {
+            part[0] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, F::dot(raw, xv[0])) & keep);
+        } else {
+            Unpacked wu;
+            F::unpack(raw, wu);
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                part[m] = 0.0f + __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, F::dot(wu, xv[m])) & keep);
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const float s = wave_sum(part[m]);
+            mine[m] = static_cast<uint32_t>(lane) == (j & 63u) ? s : mine[m];
+        }
         if ((j & 63u) == 63u || j + 1 == nrows) {
             const uint32_t first = j & ~63u;
-            if (static_cast<uint32_t>(lane) <= (j & 63u))
-                y[g + (first + static_cast<uint32_t>(lane)) * total_groups] = to_out<OutT>(1048576.0f * mine);
+            if (static_cast<uint32_t>(lane) <= (j & 63u)) {
+                OutT* yr = y + g + (first + static_cast<uint32_t>(lane)) * total_groups;
+#pragma unroll
+                for (int m = 0; m < MT; ++m) yr[static_cast<size_t>(m) * N] = to_out<OutT>(F::kFinal * mine[m]);
+            }
         }
     }
 }
 
 // LDS slot of a slice of `span` pairs: the 16-byte chunks that overlap it
 // wherever it starts (a multiple of 4 bytes into a chunk).
-__host__ __device__ constexpr uint32_t slot_size(uint32_t span) { return (span * kPairBytes + 15u) / 16u * 16u + 16u; }
+__host__ __device__ constexpr uint32_t slot_size(uint32_t span, uint32_t pair_bytes) {
+    return (span * pair_bytes + 15u) / 16u * 16u + 16u;
+}
 
 // Load instructions per slice of a row split over s waves: enough for the
 // widest slice, and 0 (unsupported) unless every slice's last instruction
 // keeps at least one lane (the wait counts assume LOADS loads per row, and the
 // other instructions load whole).
-inline uint32_t split_loads(uint32_t s, uint32_t k) {
+inline uint32_t split_loads(uint32_t s, uint32_t k, uint32_t pair_bytes) {
     const uint32_t npairs = k / 64, span = (npairs + s - 1) / s;
     uint32_t lo = 0xFFFFFFFFu, hi = 0;
     for (uint32_t i = 0; i < s; ++i) {
         if (i * span >= npairs) return 0;
-        const uint32_t b0 = i * span * kPairBytes, count = npairs - i * span < span ? npairs - i * span : span;
-        const uint32_t chunks = (b0 + count * kPairBytes + 15u) / 16u - b0 / 16u;
+        const uint32_t b0 = i * span * pair_bytes, count = npairs - i * span < span ? npairs - i * span : span;
+        const uint32_t chunks = (b0 + count * pair_bytes + 15u) / 16u - b0 / 16u;
         lo = chunks < lo ? chunks : lo;
         hi = chunks > hi ? chunks : hi;
     }
     const uint32_t loads = (hi + 63u) / 64u;
-    return loads >= 1 && loads <= 3 && lo > 64u * (loads - 1) ? loads : 0;
+    return loads >= 1 && loads <= 5 && lo > 64u * (loads - 1) ? loads : 0;
 }
 
 // Dynamic LDS of the split-row kernel: the waves' rings, then x in 8 KB steps.
-__host__ __device__ constexpr size_t split_lds_bytes(uint32_t s, uint32_t r, uint32_t k) {
-    return static_cast<size_t>(kWaves) * r * slot_size((k / 64 + s - 1) / s) + (k + 4095u) / 4096u * 8192u;
+__host__ __device__ constexpr size_t split_lds_bytes(uint32_t s, uint32_t r, uint32_t k, uint32_t pair_bytes) {
+    return static_cast<size_t>(kWaves) * r * slot_size((k / 64 + s - 1) / s, pair_bytes) + (k + 4095u) / 4096u * 8192u;
 }
 
 // Rows split over S waves (K past 4096, up to about 4096 S): wave w of a
@@ -244,7 +223,7 @@ __host__ __device__ constexpr size_t split_lds_bytes(uint32_t s, uint32_t r, uin
 // barriers, so every wave runs the row count of its workgroup's first row
 // group (the largest), and a group with one row fewer re-reads its last row
 // once and does not store it.
-template <int S, int R, int D, int LOADS, typename OutT>
+template <class F, int S, int R, int D, int LOADS, typename OutT>
 __global__ __launch_bounds__(kThreads) void gemv_lds_split_kernel(const uint16_t* __restrict__ x,
                                                                  const uint8_t* __restrict__ w,
                                                                  OutT* __restrict__ y, uint32_t N, uint32_t K,
@@ -263,11 +242,11 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_split_kernel(const uint16_t
     const uint32_t span = (npairs + S - 1) / S;
     const uint32_t first_pair = slice * span;
     const uint32_t count = min(span, npairs - first_pair);  // >= 1: every slice holds pairs
-    const size_t row_bytes = static_cast<size_t>(npairs) * kPairBytes;  // a multiple of 16
-    const uint32_t b0 = first_pair * kPairBytes;
+    const size_t row_bytes = static_cast<size_t>(npairs) * F::kPairBytes;  // a multiple of 16
+    const uint32_t b0 = first_pair * F::kPairBytes;
     const uint32_t c0 = b0 >> 4;
-    const uint32_t chunks = (b0 + count * kPairBytes + 15u) / 16u - c0;
-    const uint32_t slot_bytes = slot_size(span);
+    const uint32_t chunks = (b0 + count * F::kPairBytes + 15u) / 16u - c0;
+    const uint32_t slot_bytes = slot_size(span, F::kPairBytes);
     uint8_t* ring = ring_lds + static_cast<uint32_t>(wave) * R * slot_bytes;
     const uint32_t g = blockIdx.x * kGroups + static_cast<uint32_t>(wave) / S;
     const uint32_t nrows = g < N ? (N - 1 - g) / total_groups + 1 : 0;
@@ -291,10 +270,10 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_split_kernel(const uint16_t
         }
     };
     auto wait_rows = [&](uint32_t rows) {
-        if (rows >= 3 && D >= 3) __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * 3));
-        else if (rows == 2 && D >= 2) __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * 2));
-        else if (rows == 1) __builtin_amdgcn_s_waitcnt(0x0F70 | LOADS);
-        else __builtin_amdgcn_s_waitcnt(0x0F70);
+        if (rows >= 3 && D >= 3) __builtin_amdgcn_s_waitcnt(vm_wait(LOADS * 3));
+        else if (rows == 2 && D >= 2) __builtin_amdgcn_s_waitcnt(vm_wait(LOADS * 2));
+        else if (rows == 1) __builtin_amdgcn_s_waitcnt(vm_wait(LOADS));
+        else __builtin_amdgcn_s_waitcnt(vm_wait(0));
     };
 
     // x first, then the first rows; loads retire in order, so once only those
@@ -331,9 +310,9 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_split_kernel(const uint16_t
             s0 = dot2(xr[i], kOnePair, s0);
             s1 = dot2(xr[16 + i], kOnePair, s1);
         }
-        xv.c0 = (-8.0f / 1048576.0f) * s0;
-        xv.c1 = (-8.0f / 1048576.0f) * s1;
-        order_x(xr, xv);
+        xv.c0 = F::kStart * s0;
+        xv.c1 = F::kStart * s1;
+        F::order_x(xr, xv);
     }
 
     // Lane j % 64 holds the slice sum of row j; every 64 rows and at the end
@@ -349,21 +328,21 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_split_kernel(const uint16_t
         }
         __syncthreads();
         if (slice == 0 && static_cast<uint32_t>(lane) < n)
-            y[g + (first + static_cast<uint32_t>(lane)) * total_groups] = to_out<OutT>(1048576.0f * t);
+            y[g + (first + static_cast<uint32_t>(lane)) * total_groups] = to_out<OutT>(F::kFinal * t);
     };
-    const uint32_t pair_offset = (b0 & 15u) + pc * kPairBytes;
+    const uint32_t pair_offset = (b0 & 15u) + pc * F::kPairBytes;
     for (uint32_t j = 0; j < trips; ++j) {
         if (j + D < trips) {
             load_row(j + D, (j + D) % R);
-            __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * D));
+            __builtin_amdgcn_s_waitcnt(vm_wait(LOADS * D));
         } else {
             wait_rows(trips - 1 - j);
         }
         const uint32_t* pr = reinterpret_cast<const uint32_t*>(ring + (j % R) * slot_bytes + pair_offset);
-        uint32_t raw[9];
+        uint32_t raw[F::kDwords];
 #pragma unroll
-        for (int i = 0; i < 9; ++i) raw[i] = pr[i];
-        const float part = 0.0f + __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pair_dot(raw, xv)) & keep);
+        for (int i = 0; i < F::kDwords; ++i) raw[i] = pr[i];
+        const float part = 0.0f + __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, F::dot(raw, xv)) & keep);
         const float s = wave_sum(part);
         mine = static_cast<uint32_t>(lane) == (j & 63u) ? s : mine;
         if ((j & 63u) == 63u) {  // uniform over the workgroup
@@ -375,7 +354,7 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_split_kernel(const uint16_t
     if (base < trips) flush(base, nrows > base ? nrows - base : 0u);
 }
 
-template <int R, int D>
+template <class F, int MT, int R, int D>
 hipError_t launch_gemv_lds(const Problem& p) {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -384,7 +363,7 @@ hipError_t launch_gemv_lds(const Problem& p) {
             n = 256;
         return n;
     }();
-    const uint32_t row_bytes = p.K / 64 * kPairBytes;
+    const uint32_t row_bytes = p.K / 64 * F::kPairBytes;
     const uint32_t loads = (row_bytes / 16 + 63) / 64;
     uint32_t groups = static_cast<uint32_t>(cus);
     const uint32_t need = (p.N + kWaves - 1) / kWaves;  // no workgroup without a row
@@ -394,26 +373,35 @@ hipError_t launch_gemv_lds(const Problem& p) {
     const auto* x = static_cast<const uint16_t*>(p.x);
     const auto* w = static_cast<const uint8_t*>(p.w);
     const uint32_t total = groups * kWaves;
-#define MOTE_LDS_LAUNCH(L)                                                                                      \
-    do {                                                                                                        \
-        if (p.out == OutType::F32)                                                                              \
-            hipLaunchKernelGGL((gemv_lds_kernel<R, D, L, float>), grid, block, lds, p.stream, x, w,            \
-                               static_cast<float*>(p.y), p.N, p.K, total);                                    \
-        else                                                                                                    \
-            hipLaunchKernelGGL((gemv_lds_kernel<R, D, L, _Float16>), grid, block, lds, p.stream, x, w,         \
-                               static_cast<_Float16*>(p.y), p.N, p.K, total);                                 \
+#define MOTE_LDS_LAUNCH(L)                                                                                       \
+    do {                                                                                                         \
+        if (p.out == OutType::F32)                                                                               \
+            hipLaunchKernelGGL((gemv_lds_kernel<F, MT, R, D, L, float>), grid, block, lds, p.stream, x, w,      \
+                               static_cast<float*>(p.y), p.N, p.K, total);                                     \
+        else                                                                                                     \
+            hipLaunchKernelGGL((gemv_lds_kernel<F, MT, R, D, L, _Float16>), grid, block, lds, p.stream, x, w,   \
+                               static_cast<_Float16*>(p.y), p.N, p.K, total);                                  \
     } while (0)
     switch (loads) {
         case 1: MOTE_LDS_LAUNCH(1); break;
         case 2: MOTE_LDS_LAUNCH(2); break;
         case 3: MOTE_LDS_LAUNCH(3); break;
+        case 4:
+        case 5:  // Q8_0 rows past 3584 elements
+            if constexpr (F::kPairBytes > kPairBytes) {
+                if (loads == 4) MOTE_LDS_LAUNCH(4);
+                else MOTE_LDS_LAUNCH(5);
+                break;
+            } else {
+                return hipErrorInvalidValue;
+            }
         default: return hipErrorInvalidValue;
     }
 #undef MOTE_LDS_LAUNCH
     return hipGetLastError();
 }
 
-template <int S, int R, int D, int G>
+template <class F, int S, int R, int D, int G>
 hipError_t launch_gemv_lds_split(const Problem& p) {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -423,11 +411,11 @@ hipError_t launch_gemv_lds_split(const Problem& p) {
         return n;
     }();
     constexpr uint32_t kGroups = kWaves / S;
-    const uint32_t loads = split_loads(S, p.K);
+    const uint32_t loads = split_loads(S, p.K, F::kPairBytes);
     uint32_t groups = static_cast<uint32_t>(cus) * G;
     const uint32_t need = (p.N + kGroups - 1) / kGroups;  // no workgroup without a row
     if (groups > need) groups = need;
-    const size_t lds = split_lds_bytes(S, R, p.K);
+    const size_t lds = split_lds_bytes(S, R, p.K, F::kPairBytes);
     const dim3 grid(groups), block(kThreads);
     const auto* x = static_cast<const uint16_t*>(p.x);
     const auto* w = static_cast<const uint8_t*>(p.w);
@@ -435,32 +423,52 @@ hipError_t launch_gemv_lds_split(const Problem& p) {
 #define MOTE_LDS_LAUNCH(L)                                                                                      \
     do {                                                                                                        \
         if (p.out == OutType::F32)                                                                              \
-            hipLaunchKernelGGL((gemv_lds_split_kernel<S, R, D, L, float>), grid, block, lds, p.stream, x, w,   \
+            hipLaunchKernelGGL((gemv_lds_split_kernel<F, S, R, D, L, float>), grid, block, lds, p.stream, x, w,   \
                                static_cast<float*>(p.y), p.N, p.K, total);                                    \
         else                                                                                                    \
-            hipLaunchKernelGGL((gemv_lds_split_kernel<S, R, D, L, _Float16>), grid, block, lds, p.stream, x, w, \
+            hipLaunchKernelGGL((gemv_lds_split_kernel<F, S, R, D, L, _Float16>), grid, block, lds, p.stream, x, w, \
                                static_cast<_Float16*>(p.y), p.N, p.K, total);                                 \
     } while (0)
     switch (loads) {
         case 1: MOTE_LDS_LAUNCH(1); break;
         case 2: MOTE_LDS_LAUNCH(2); break;
         case 3: MOTE_LDS_LAUNCH(3); break;
+        case 4:
+        case 5:  // Q8_0 slices past 42 pairs
+            if constexpr (F::kPairBytes > kPairBytes) {
+                if (loads == 4) MOTE_LDS_LAUNCH(4);
+                else MOTE_LDS_LAUNCH(5);
+                break;
+            } else {
+                return hipErrorInvalidValue;
+            }
         default: return hipErrorInvalidValue;
     }
 #undef MOTE_LDS_LAUNCH
     return hipGetLastError();
 }
 
-// p0 = ring slots, p1 = rows in flight, p2 = waves per row (0: one).
+// p0 = ring slots, p1 = rows in flight, p2 = waves per row (0: one);
+// tokens = the exact M of the multi-token variants.
 const Variant kLds[] = {
-    Variant{"rowlds_r2d1", Kind::GemvLds, 2, 1, 0, &launch_gemv_lds<2, 1>},
-    Variant{"rowlds_r3d1", Kind::GemvLds, 3, 1, 0, &launch_gemv_lds<3, 1>},
-    Variant{"rowlds_r3d2", Kind::GemvLds, 3, 2, 0, &launch_gemv_lds<3, 2>},
+    Variant{"rowlds_r2d1", Kind::GemvLds, 2, 1, 0, &launch_gemv_lds<FmtQ4, 1, 2, 1>},
+    Variant{"rowlds_r3d1", Kind::GemvLds, 3, 1, 0, &launch_gemv_lds<FmtQ4, 1, 3, 1>},
+    Variant{"rowlds_r3d2", Kind::GemvLds, 3, 2, 0, &launch_gemv_lds<FmtQ4, 1, 3, 2>},
+#define MOTE_LDS_Q8(MT, R, D)                                                          \
+    Variant{MT == 1 ? "q8_rowlds_r" #R "d" #D : "q8_rowlds_m" #MT "_r" #R "d" #D, Kind::Q8Lds, R, D, 0,     \
+            &launch_gemv_lds<FmtQ8, MT, R, D>, MT}
+    MOTE_LDS_Q8(1, 2, 1), MOTE_LDS_Q8(1, 3, 2), MOTE_LDS_Q8(2, 2, 1), MOTE_LDS_Q8(2, 3, 2), MOTE_LDS_Q8(3, 2, 1),
+    MOTE_LDS_Q8(4, 2, 1),
+#undef MOTE_LDS_Q8
 #define MOTE_LDS_SPLIT(S, R, D, G) \
-    Variant{"rowlds_s" #S "_r" #R "d" #D "_g" #G, Kind::GemvLds, R, D, S, &launch_gemv_lds_split<S, R, D, G>}
+    Variant{"rowlds_s" #S "_r" #R "d" #D "_g" #G, Kind::GemvLds, R, D, S, &launch_gemv_lds_split<FmtQ4, S, R, D, G>}
     MOTE_LDS_SPLIT(2, 3, 2, 1), MOTE_LDS_SPLIT(4, 2, 1, 1), MOTE_LDS_SPLIT(4, 3, 2, 1), MOTE_LDS_SPLIT(4, 4, 3, 1),
     MOTE_LDS_SPLIT(8, 3, 2, 1),
 #undef MOTE_LDS_SPLIT
+#define MOTE_LDS_SPLIT_Q8(S, R, D)                                            \
+    Variant{"q8_rowlds_s" #S "_r" #R "d" #D, Kind::Q8Lds, R, D, S, &launch_gemv_lds_split<FmtQ8, S, R, D, 1>}
+    MOTE_LDS_SPLIT_Q8(2, 2, 1), MOTE_LDS_SPLIT_Q8(4, 2, 1), MOTE_LDS_SPLIT_Q8(4, 3, 2), MOTE_LDS_SPLIT_Q8(8, 2, 1),
+#undef MOTE_LDS_SPLIT_Q8
 };
 
 }  // namespace
@@ -470,19 +478,25 @@ const Variant* gemv_lds_variants(int* count) {
     return kLds;
 }
 
-// One token, K a multiple of 256 (rows start on 16-byte boundaries) up to
-// 4096 (one pair per lane), or with rows split over S waves up to 64 pairs per
-// slice, every slice non-empty, and the rings and x within the workgroup's
-// 160 KB of LDS; weights and x 16-byte aligned (the direct-to-LDS loads move
-// aligned 16-byte chunks).
+// The variant's tokens (one, or 2-4 for the multi-token rings), K a multiple
+// of 256 (rows start on 16-byte boundaries) up to 4096 (one pair per lane),
+// or one token with rows split over S waves, up to 64 pairs per slice, every
+// slice non-empty; the rings and x within the workgroup's 160 KB of LDS;
+// weights and x 16-byte aligned (the direct-to-LDS loads move aligned 16-byte
+// chunks).
 bool gemv_lds_supports(const Variant& v, const Problem& p) {
-    if (p.M != 1 || p.K % 256 != 0 || p.K == 0 || p.w_up != nullptr || reinterpret_cast<uintptr_t>(p.w) % 16 != 0 ||
-        reinterpret_cast<uintptr_t>(p.x) % 16 != 0)
+    const uint32_t tokens = v.tokens > 0 ? static_cast<uint32_t>(v.tokens) : 1u;
+    if (p.M != tokens || p.K % 256 != 0 || p.K == 0 || p.w_up != nullptr ||
+        reinterpret_cast<uintptr_t>(p.w) % 16 != 0 || reinterpret_cast<uintptr_t>(p.x) % 16 != 0)
         return false;
-    if (v.p2 <= 1) return p.K <= kMaxK;
+    const uint32_t pair_bytes = v.kind == Kind::Q8Lds ? 68u : kPairBytes;
+    if (v.p2 <= 1)
+        return p.K <= kMaxK && static_cast<size_t>(kWaves) * v.p0 * (p.K / 64 * pair_bytes) +
+                                       tokens * kMaxK * 2 <= 160u * 1024u;
     const uint32_t s = static_cast<uint32_t>(v.p2), npairs = p.K / 64, span = (npairs + s - 1) / s;
-    return span <= 64 && (s - 1) * span < npairs && split_loads(s, p.K) != 0 &&
-           split_lds_bytes(s, static_cast<uint32_t>(v.p0), p.K) + kThreads * sizeof(float) <= 160u * 1024u;
+    return tokens == 1 && span <= 64 && (s - 1) * span < npairs && split_loads(s, p.K, pair_bytes) != 0 &&
+           split_lds_bytes(s, static_cast<uint32_t>(v.p0), p.K, pair_bytes) + kThreads * sizeof(float) <=
+               160u * 1024u;
 }
 
 }  // namespace mote::q4_0

@@ -92,7 +92,15 @@ def test_gate_up_and_q8_plans(d):
     assert d.select(128, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m64_n128_w1_k4"
     assert d.select(192, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m128_n128_w1_k2"
     assert d.select(16, 28672, 8192, gate_up=True).startswith("gateup_skinny_")
-    assert d.select(1, 14336, 4096, q8_0=True) == "q8_stream_d1_g1"
+    assert d.select(1, 14336, 4096, q8_0=True) == "q8_rowlds_r2d1"
+    assert d.select(1, 4096, 4096, q8_0=True) == "q8_rowlds_r2d1"
+    assert d.select(2, 14336, 4096, q8_0=True) == "q8_rowlds_m2_r2d1"
+    assert d.select(3, 14336, 4096, q8_0=True) == "q8_rowlds_m3_r2d1"
+    assert d.select(4, 14336, 4096, q8_0=True) == "q8_stream_m4_d1q_g1"
+    assert d.select(1, 4096, 14336, q8_0=True) == "q8_rowlds_s4_r2d1"
+    assert d.select(1, 8192, 28672, q8_0=True) == "q8_rowlds_s8_r2d1"
+    assert d.select(1, 28672, 8192, q8_0=True) == "q8_rowlds_s2_r2d1"
+    assert d.select(1, 4096, 4160, q8_0=True) == "q8_stream_s2_d1_g1"  # K % 256 != 0
     assert d.select(16, 14336, 4096, q8_0=True).startswith("q8_skinny_")
     assert d.select(512, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m128_n256_w1_k2"
     assert d.select(256, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m128_n128_w1_k2"

@@ -148,7 +148,7 @@ def test_one_hot_activations_read_back_the_decode_exactly(stream, oracle, varian
             assert np.array_equal(y[t].view(np.uint32), decoded[:, j].view(np.uint32)), (variant, j)
 
 
-@pytest.mark.parametrize("variant", STREAM_AND_GENERIC)
+@pytest.mark.parametrize("variant", [v for v in STREAM_AND_GENERIC if not v.startswith("q8_rowlds_")])
 def test_every_q8_variant(stream, oracle, variant):
     """Ragged N, idle lanes (K below a slot's 4096), K filling every slot and
     one pair past a slot boundary, N = 140001 at K = 64 (register flush past 64
@@ -253,7 +253,7 @@ def test_exact_properties_at_full_size(stream, m, k, n):
     w = weights(wl.seed_for(24, n), n, k)
     d = ops.Q4_0Dispatch()
     y = run(stream, x, w, m, n, k, dispatch=d)
-    assert d.plan(m, n, k, q8_0=True).startswith("q8_stream")
+    assert d.plan(m, n, k, q8_0=True).startswith(("q8_stream", "q8_rowlds"))  # the vector-ALU GEMVs
     assert np.array_equal(y, run(stream, x, w, m, n, k, dispatch=d)), "non-deterministic"
     x2 = f16_bits(bits_to_f32(x) * 2.0)
     assert np.array_equal(run(stream, x2, w, m, n, k, dispatch=d), 2.0 * y)

@@ -1,6 +1,7 @@
 """GPU parity of the decode GEMV that streams rows through a per-wave LDS ring
-(q4_0_gemv_lds.hip: coalesced non-temporal direct-to-LDS loads, M = 1, K a
-multiple of 256 up to 4096).
+(q4_0_gemv_lds.hip: coalesced non-temporal direct-to-LDS loads, M = 1 to 4,
+K a multiple of 256 up to 4096, Q4_0 and Q8_0; one token past K = 4096 with
+rows split over waves).
 
 Every variant runs row lengths that need one, two and three load instructions
 per row with the last one partly idle (K = 256 ... 4096), N below one
@@ -42,10 +43,19 @@ SPLIT_SHAPES = {
     8: [(1, 2048), (3, 6400), (257, 10240), (130, 13824), (4099, 28672), (1000, 32768), (40001, 2304)],
 }
 REFERENCE = {1: "stream_d1_g2", 2: "stream_s2_d1_g1", 4: "stream_s4_d1q_g1", 8: "stream_s8_d1_g1"}
+# the Q8_0 streaming GEMV reading each row once for every token, or with rows
+# split over S waves
+Q8_REFERENCE = {1: "q8_stream_d1_g1", 2: "q8_stream_m2_d1q_g1", 4: "q8_stream_m4_d1q_g1"}
+Q8_SPLIT_REFERENCE = {2: "q8_stream_s2_d1_g1", 4: "q8_stream_s4_d1_g1", 8: "q8_stream_s8_d1_g1"}
 
 
 def _split(variant: str) -> int:
     m = re.match(r"rowlds_s(\d+)_", variant)
+    return int(m.group(1)) if m else 1
+
+
+def _tokens(variant: str) -> int:
+    m = re.search(r"rowlds_m(\d+)_", variant)
     return int(m.group(1)) if m else 1
 
 
@@ -69,21 +79,59 @@ def test_every_rowlds_variant(stream, oracle, variant):
                                  what=f"{variant} 1x{n}x{k}{' f16' if f16_out else ''}")
 
 
+@pytest.mark.parametrize("variant", [v for v in ops.variant_names() if v.startswith("q8_rowlds_")])
+def test_every_q8_rowlds_variant(stream, oracle, variant):
+    """Q8_0 through the ring (68-byte pairs, up to five load instructions per
+    row or slice), one token with rows whole or split over S waves, or 2-4
+    tokens per row read: the shapes above, bit for bit the Q8_0 streaming GEMV
+    of the same shape of work (three tokens, which no streaming variant reads
+    at K <= 4096: each token bit for bit the one-token ring), and within the
+    oracle's tolerance."""
+    from test_gpu_q8_0 import check as check_q8, run as run_q8, weights as q8_weights
+
+    split, tokens = _split(variant.removeprefix("q8_")), _tokens(variant)
+    d = ops.Q4_0Dispatch()
+    d.force(variant)
+    ref = ops.Q4_0Dispatch()
+    ref.force(Q8_SPLIT_REFERENCE[split] if split > 1 else Q8_REFERENCE.get(tokens, "q8_rowlds_r2d1"))
+    per_token = split == 1 and tokens not in Q8_REFERENCE
+    for n, k in SHAPES if split == 1 else SPLIT_SHAPES[split]:
+        print(f"{variant} {tokens}x{n}x{k}", flush=True)
+        x = normal_x(wl.seed_for(19, k), tokens, k)
+        w = q8_weights(wl.seed_for(19, 100 + n), n, k)
+        cols = None if n < 5000 else sample_columns(n, 512)
+        for f16_out in (False, True):
+            y = run_q8(stream, x, w, tokens, n, k, dispatch=d, f16_out=f16_out)
+            if per_token:
+                want = np.concatenate([run_q8(stream, x[t * k:(t + 1) * k], w, 1, n, k, dispatch=ref,
+                                              f16_out=f16_out) for t in range(tokens)])
+            else:
+                want = run_q8(stream, x, w, tokens, n, k, dispatch=ref, f16_out=f16_out)
+            assert np.array_equal(y.view(np.uint32), want.view(np.uint32)), (variant, n, k, f16_out)
+            check_q8(oracle, y, x, w, tokens, n, k, columns=cols, f16_out=f16_out,
+                     what=f"{variant} {tokens}x{n}x{k}{' f16' if f16_out else ''}")
+
+
 @pytest.mark.parametrize("variant,shapes", [
     ("rowlds_r2d1", [(1, 64, 192), (1, 64, 4352), (2, 64, 1024)]),
     ("rowlds_s4_r3d2_g1", [(1, 64, 3200), (1, 64, 17408), (2, 64, 14336)]),
     ("rowlds_s8_r3d2_g1", [(1, 64, 1792), (1, 64, 14592), (1, 64, 33024)]),
+    ("q8_rowlds_m2_r2d1", [(1, 64, 1024), (3, 64, 1024), (2, 64, 4352), (2, 64, 192)]),
+    ("q8_rowlds_s8_r2d1", [(1, 64, 7424), (1, 64, 33024), (2, 64, 28672)]),
 ])
 def test_rowlds_rejects_what_it_cannot_run(stream, variant, shapes):
     """K not a multiple of 256, more than 64 pairs per slice, slices whose
     last load instruction would be idle (K = 1792 and 14592 at S = 8) and two
     tokens fall outside the variant: forcing it is an error, never a silent
     misread."""
+    from mote_amd import HipError
+    from test_gpu_q8_0 import run as run_q8, weights as q8_weights
+
+    q8 = variant.startswith("q8_")
     d = ops.Q4_0Dispatch()
     d.force(variant)
-    from mote_amd import HipError
     for m, n, k in shapes:
         x = normal_x(wl.seed_for(17, 1), m, k)
-        w = weights(wl.seed_for(17, 2), n, k)
+        w = (q8_weights if q8 else weights)(wl.seed_for(17, 2), n, k)
         with pytest.raises(HipError):
-            run_linear(stream, x, w, m, n, k, dispatch=d)
+            (run_q8 if q8 else run_linear)(stream, x, w, m, n, k, dispatch=d)
