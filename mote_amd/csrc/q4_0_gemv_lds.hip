@@ -1,10 +1,12 @@
-// Decode GEMV (M = 1) over GGML Q4_0 for K a multiple of 256, with the weight
+// Decode GEMV over GGML Q4_0 and Q8_0 for K a multiple of 256, with the weight
 // rows streamed through a per-wave LDS ring by CDNA4's direct-to-LDS loads:
-// whole rows for K up to 4096, rows split over 2, 4 or 8 waves past that.
+// whole rows for K up to 4096 (one token; Q8_0 also two or three tokens per
+// row read), rows split over 2, 4 or 8 waves past that (one token).
 //
-// Computes y[n] = sum_k x[k] * w[n, k] for f16 x [1, K] and Q4_0 w [N, K], the
-// operation of crates/mote-backend-hip/src/quantized_linear.hip:13-52 (oracle
-// crates/mote-reference/src/quantized.rs:89-144) at one token.
+// Computes y[m, n] = sum_k x[m, k] * w[n, k] for f16 x [M, K] and quantized
+// w [N, K], the operation of crates/mote-backend-hip/src/
+// quantized_linear.hip:13-52 (oracle crates/mote-reference/src/
+// quantized.rs:89-144; Q8_0 decode at :191-195).
 //
 // Why: a wave that loads its lanes' 36-byte block pairs directly issues three
 // strided instructions per row, each touching every cache line of the row, so
