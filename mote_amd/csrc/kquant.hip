@@ -661,7 +661,13 @@ __device__ __forceinline__ void ring_part_dot(uint32_t slot, uint32_t blk_off, u
     }
 }
 
-template <Fmt F, int MT, int S, typename OutT>
+// XL: the token group's activations are staged once per workgroup in LDS by
+// direct-to-LDS loads (thread t loads 16-byte chunks t, t + 512, ... of each
+// token, clamped, into 8 KB steps), issued before the first rows, and each
+// lane reads its runs there after a barrier.  Without it every wave loads its
+// lanes' activations from global memory: at one slice per row (K <= 4096 for
+// Q4_K) the eight waves of a workgroup fetch the same x eight times.
+template <Fmt F, int MT, int S, typename OutT, bool XL>
 __global__ __launch_bounds__(kRingThreads) void kq_ring_kernel(const uint16_t* __restrict__ x,
                                                               const uint8_t* __restrict__ w, OutT* __restrict__ y,
                                                               uint32_t M, uint32_t N, uint32_t K, uint32_t slice_blocks) {
@@ -671,6 +677,7 @@ __global__ __launch_bounds__(kRingThreads) void kq_ring_kernel(const uint16_t* _
     constexpr int RW = kRingWaves / S;
     __shared__ __attribute__((aligned(16))) uint8_t ring_lds[kRingWaves][kRingSlots][kSlot];
     __shared__ float part_lds[kRingWaves][kWave];
+    extern __shared__ __attribute__((aligned(16))) uint8_t x_lds[];  // XL: [MT][ceil(K / 4096) 8 KB]
     const int wave = static_cast<int>(threadIdx.x) >> 6;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t s = static_cast<uint32_t>(wave % S), rw = static_cast<uint32_t>(wave / S);
@@ -705,7 +712,48 @@ __global__ __launch_bounds__(kRingThreads) void kq_ring_kernel(const uint16_t* _
         if (steps == 0) continue;  // uniform per workgroup
         __syncthreads();  // the previous token group's ring reads are done
         LaneX<F, MT> lx;
-        {
+        if constexpr (XL) {
+            const uint32_t xsteps = (K + 4095u) / 4096u, xstride = xsteps * 8192u;
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const int mm = m < mt ? m : mt - 1;  // tokens past the group re-read the last one
+                const uint8_t* src = reinterpret_cast<const uint8_t*>(x + static_cast<size_t>(m0 + mm) * K);
+                for (uint32_t i = 0; i < xsteps; ++i) {
+                    const uint32_t c = min(512u * i + threadIdx.x, K / 8u - 1u);
+                    __builtin_amdgcn_global_load_lds(
+                        src + 16u * c, (lds_ptr)(x_lds + m * xstride + 8192u * i + 1024u * static_cast<uint32_t>(wave)),
+                        16, 0, 0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            load_row(0, 0);
+            if (steps > 1) load_row(1, 1);
+            __builtin_amdgcn_sched_barrier(0);
+            // loads retire in order: with only the rows outstanding this
+            // wave's x chunks have landed, and after the barrier every wave's
+            if (steps > 1) __builtin_amdgcn_s_waitcnt(0x0F70 | (LOADS * 2));
+            else __builtin_amdgcn_s_waitcnt(0x0F70 | LOADS);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            uint32_t raw[MT][32];
+            uint32_t e0, e1;
+            part_runs<F>(part, e0, e1);
+            const uint32_t elem0 = min(b0 + blk, nb - 1) * kSuper;
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    const uint8_t* run = x_lds + m * xstride + 2u * (elem0 + (r ? e1 : e0));
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const u32x4 v = *reinterpret_cast<const u32x4*>(run + 16 * i);
+                        raw[m][16 * r + 4 * i + 0] = v.x; raw[m][16 * r + 4 * i + 1] = v.y;
+                        raw[m][16 * r + 4 * i + 2] = v.z; raw[m][16 * r + 4 * i + 3] = v.w;
+                    }
+                }
+            }
+            order_lane_x<F, MT>(raw, lx);
+        } else {
             uint32_t raw[MT][32];
             load_lane_x<F, MT>(x + static_cast<size_t>(m0) * K, K, mt, min(b0 + blk, nb - 1) * kSuper, part, raw);
             __builtin_amdgcn_sched_barrier(0);
@@ -776,9 +824,20 @@ hipError_t launch_ring_s(const void* x, const void* w, void* y, uint32_t M, uint
     if (gx > row_steps) gx = row_steps;
     const uint32_t groups = (M + MT - 1) / MT;
     const uint32_t gy = groups < 65535u ? groups : 65535u;
-    hipLaunchKernelGGL((kq_ring_kernel<F, MT, S, OutT>), dim3(gx, gy), dim3(kRingThreads), 0, stream,
-                       static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), static_cast<OutT*>(y), M, N, K,
-                       slice_blocks);
+    // x through LDS where several row groups share a slice and the staged
+    // tokens fit beside the rings (static: rings and partial sums)
+    constexpr size_t kStatic = sizeof(uint8_t) * kRingWaves * kRingSlots * ring_loads<F>() * 1024 +
+                               sizeof(float) * kRingWaves * kWave;
+    const size_t xl = static_cast<size_t>(MT) * ((K + 4095u) / 4096u) * 8192u;
+    const auto* xp = static_cast<const uint16_t*>(x);
+    const auto* wp = static_cast<const uint8_t*>(w);
+    auto* yp = static_cast<OutT*>(y);
+    if (RW > 1 && kStatic + xl <= 160u * 1024u)
+        hipLaunchKernelGGL((kq_ring_kernel<F, MT, S, OutT, true>), dim3(gx, gy), dim3(kRingThreads), xl, stream, xp,
+                           wp, yp, M, N, K, slice_blocks);
+    else
+        hipLaunchKernelGGL((kq_ring_kernel<F, MT, S, OutT, false>), dim3(gx, gy), dim3(kRingThreads), 0, stream, xp,
+                           wp, yp, M, N, K, slice_blocks);
     return hipGetLastError();
 }
 
