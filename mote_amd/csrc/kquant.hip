@@ -824,15 +824,19 @@ hipError_t launch_ring_s(const void* x, const void* w, void* y, uint32_t M, uint
     if (gx > row_steps) gx = row_steps;
     const uint32_t groups = (M + MT - 1) / MT;
     const uint32_t gy = groups < 65535u ? groups : 65535u;
-    // x through LDS where several row groups share a slice and the staged
-    // tokens fit beside the rings (static: rings and partial sums)
+    // Q4_K: x through LDS where several row groups share a slice and the
+    // staged tokens fit beside the rings (static: rings and partial sums).
+    // Measured on MI355X: 1 x 4096 x 14336 9.05 -> 8.53 us, 2 tokens 12.23
+    // -> 11.10, 8 tokens 33.2 -> 30.4, 14336 x 4096 10.35 -> 9.86.  Q6_K keeps
+    // the per-wave loads: staged, its 2-8 token passes ran 3-5 % slower
+    // (4 x 4096 x 14336: 19.2 against 18.7 us) and one token gained 0-2 %.
     constexpr size_t kStatic = sizeof(uint8_t) * kRingWaves * kRingSlots * ring_loads<F>() * 1024 +
                                sizeof(float) * kRingWaves * kWave;
     const size_t xl = static_cast<size_t>(MT) * ((K + 4095u) / 4096u) * 8192u;
     const auto* xp = static_cast<const uint16_t*>(x);
     const auto* wp = static_cast<const uint8_t*>(w);
     auto* yp = static_cast<OutT*>(y);
-    if (RW > 1 && kStatic + xl <= 160u * 1024u)
+    if (F == Fmt::Q4K && RW > 1 && kStatic + xl <= 160u * 1024u)
         hipLaunchKernelGGL((kq_ring_kernel<F, MT, S, OutT, true>), dim3(gx, gy), dim3(kRingThreads), xl, stream, xp,
                            wp, yp, M, N, K, slice_blocks);
     else
