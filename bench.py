@@ -272,6 +272,9 @@ SWEEP = (
      ("mlp down", 1, 14336, 4096, 1, False, False)]
     + [("skinny", m, 4096, n, 2, False, False) for n in (4096, 6144, 14336) for m in (2, 4, 8, 16, 32)]
     + [("prefill", m, 4096, 14336, 4, False, False) for m in (64, 256, 512)]
+    # prefill beyond one dispatch wave of tiles, and the q/o projection's N = 4096
+    + [("prefill", m, 4096, 14336, 4, False, False) for m in (384, 1024)]
+    + [("prefill o proj", m, 4096, 4096, 4, False, False) for m in (128, 256, 512)]
     + [("down split-K", m, 14336, 4096, 2, False, False) for m in (2, 4, 16, 32, 64)]
     + [("70b o split-K", m, 8192, 8192, 2, False, False) for m in (16, 64)]
     + [("70b down", m, 28672, 8192, 2, False, False) for m in (1, 2, 16, 64)]
@@ -283,6 +286,7 @@ SWEEP = (
        ("q8_0 4 tok", 4, 4096, 14336, 5, False, "q8")]
     + [("q8_0 skinny", m, 4096, 14336, 5, False, "q8") for m in (8, 16, 32, 64)]
     + [("q8_0 prefill", m, 4096, 14336, 5, False, "q8") for m in (256, 512)]
+    + [("q8_0 prefill o proj", 256, 4096, 4096, 5, False, "q8")]
     + [("3 tok o proj", 3, 8192, 8192, 2, False, False), ("3 tok down", 3, 14336, 4096, 2, False, False),
        ("q8_0 3 tok", 3, 8192, 8192, 5, False, "q8"), ("3 tok gate/up", 3, 8192, 28672, 4, False, True)]
     # the reference benchmark's cases (rows, N, K), its inputs, the F16-output entry point

@@ -164,6 +164,42 @@ const Variant* deepest_step(const char* base, const Problem& p, int max_kp) {
     return by_name(base);
 }
 
+// A prefill tile: the variant family, the deepest step to try, and the
+// measured time of one dispatch wave of such tiles (one per CU) at K = 4096.
+struct TileCost {
+    const char* base;
+    int max_kp;
+    float wave_us;
+};
+
+// The tile minimising the modelled time, dispatch waves (ceil(tiles / CUs):
+// a partial last wave costs a whole one) times the wave time; ties go to the
+// earlier (larger) tile.  Null when K allows none of them a multi-pair step.  Measured on MI355X, the model picks the fastest
+// tile at every shape timed (64-1024 tokens, N = 4096-14 336, K = 4096 and
+// 14 336); e.g. 256 x 4096 x 4096 on 64 x 64 tiles in 18.9 us (the rule
+// "first tile with >= 200 tiles" fell to the 16 x 16 tiles: 39.5 us), 384 x
+// 4096 x 14 336 on 128 x 256 tiles in 59.4 us (128 x 128: 80.4 us).
+template <int N>
+const Variant* cheapest_tiles(const Problem& p, const TileCost (&cand)[N]) {
+    const uint64_t cus = static_cast<uint64_t>(device_cus());
+    const Variant* best = nullptr;
+    float best_us = 0.0f;
+    for (const TileCost& c : cand) {
+        const Variant* v = deepest_step(c.base, p, c.max_kp);
+        // the wave times hold for multi-pair steps; where K allows only one
+        // pair per step the caller's rule decides (the 16 x 16 tiles measure
+        // as fast there: Q8_0 128 x 4160 x 14 336 62.5 us against 64.5)
+        if (!v || v == by_name(c.base) || !prefill_supports(*v, p)) continue;
+        const uint64_t waves = (prefill_tiles(p, static_cast<uint32_t>(v->p0), static_cast<uint32_t>(v->p1)) + cus - 1) / cus;
+        const float us = static_cast<float>(waves) * c.wave_us;
+        if (!best || us < best_us) {
+            best = v;
+            best_us = us;
+        }
+    }
+    return best;
+}
+
 // Skinny GEMM (3 <= M <= 64, K = 4096) on the matrix cores, transposed weight
 // loads; null when the K slicing does not fit.  One (16-row, token-group) item
 // per step of a workgroup, with the reduction deferred over up to 4 items (16
@@ -379,12 +415,14 @@ const Variant* heuristic(const Problem& p, Op op) {
             // Each with the deepest step K allows: 2 block pairs per step at
             // 256 tokens 65.0 us (67.8 with one); the 64 x 128 tiles with 4
             // pairs at 128 tokens 40.8 us (61.5 on the 64 x 64 16 x 16 tiles).
-            if (prefill_tiles(p, 128, 256) >= 200) return deepest_step("q8_mfma_x32s_m128_n256_w1", p, 2);
-            if (prefill_tiles(p, 128, 128) >= 200) return deepest_step("q8_mfma_x32s_m128_n128_w1", p, 2);
-            if (prefill_tiles(p, 64, 128) >= 200) {
-                const Variant* v = deepest_step("q8_mfma_x32s_m64_n128_w1", p, 4);
-                if (v && prefill_supports(*v, p)) return v;
-            }
+            // The tile by dispatch waves and wave time (K = 4096: 128 x 256
+            // 96 us, 128 x 128 56 us, 64 x 128 36 us; e.g. 256 x 4096 x 4096
+            // in 32.8 us on 64 x 128 tiles against 50.3 on the 16 x 16 tiles,
+            // 384 x 4096 x 14 336 in 96.3 us on 128 x 256 against 118.7).
+            static const TileCost kQ8Tiles[] = {{"q8_mfma_x32s_m128_n256_w1", 2, 96.0f},
+                                                {"q8_mfma_x32s_m128_n128_w1", 2, 56.0f},
+                                                {"q8_mfma_x32s_m64_n128_w1", 4, 36.0f}};
+            if (const Variant* v = cheapest_tiles(p, kQ8Tiles)) return v;
             return by_name("q8_mfma_r_m64_n64");
         }
         return by_name("q8_generic");
@@ -442,6 +480,15 @@ const Variant* heuristic(const Problem& p, Op op) {
             // (up to 128 tokens where 128 x 128 tiles are too few: 128 x 4096
             // x 14 336 in 45.7 us with 4 pairs per step, against 78.0 us on
             // the 16 x 16 tiles)
+            // Above 64 tokens the tile by dispatch waves and wave time (K =
+            // 4096: 128 x 128 64 us, 64 x 128 42 us, 64 x 64 30 us; e.g.
+            // 256 x 4096 x 4096 in 32.0 us on 64 x 64 tiles against 77.0 on
+            // the 16 x 16 tiles, 512 x 4096 x 4096 in 46.7 us on 64 x 128).
+            static const TileCost kGateUpTiles[] = {{"gateup_mfma_x32s_m128_n128_w1", 2, 64.0f},
+                                                    {"gateup_mfma_x32s_m64_n128_w1", 4, 42.0f},
+                                                    {"gateup_mfma_x32s_m64_n64_w2", 4, 30.0f}};
+            if (p.M > 64)
+                if (const Variant* v = cheapest_tiles(p, kGateUpTiles)) return v;
             if (p.M <= 128 && prefill_tiles(p, 64, 128) >= 200 && (p.M <= 64 || prefill_tiles(p, 128, 128) < 200))
                 return deepest_step("gateup_mfma_x32s_m64_n128_w1", p, 4);
             if (prefill_tiles(p, 128, 128) >= 200) return deepest_step("gateup_mfma_x32s_m128_n128_w1", p, 2);
@@ -463,7 +510,14 @@ const Variant* heuristic(const Problem& p, Op op) {
         // tokens, 46.5-47.1 us; 64 x 128 at 128 tokens, 39.8 us; the 16 x 16
         // tiles took 83, 59.4 and 46.1 us).
         // Each x32s tile with the deepest step K allows (2 block pairs for
-        // the 128-row tiles, 4 for 64 x 128: what fits the LDS).
+        // the 128-row tiles, 4 for 64 x 128 and 64 x 64: what fits the LDS),
+        // chosen by dispatch waves and wave time (K = 4096: 128 x 256 60 us,
+        // 128 x 128 40 us, 64 x 128 25 us, 64 x 64 18 us).
+        static const TileCost kTiles[] = {{"mfma_x32s_m128_n256_w1", 2, 60.0f},
+                                          {"mfma_x32s_m128_n128_w1", 2, 40.0f},
+                                          {"mfma_x32s_m64_n128_w1", 4, 25.0f},
+                                          {"mfma_x32s_m64_n64_w2", 4, 18.0f}};
+        if (const Variant* v = cheapest_tiles(p, kTiles)) return v;
         static const char* const order[] = {"mfma_x32s_m128_n256_w1", "mfma_x32s_m128_n128_w1",
                                             "mfma_x32s_m64_n128_w1", "mfma_r_m64_n128", "mfma_r_m64_n64"};
         static const int max_kp[] = {2, 2, 4, 1, 1};

@@ -48,6 +48,13 @@ LINEAR = [
     ((64, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l8_c_w"),
     ((128, 4096, 14336), "mfma_x32s_m64_n128_w1_k4"),
     ((256, 4096, 14336), "mfma_x32s_m128_n128_w1_k2"),
+    ((384, 4096, 14336), "mfma_x32s_m128_n256_w1_k2"),
+    ((1024, 4096, 14336), "mfma_x32s_m128_n256_w1_k2"),
+    ((128, 4096, 4096), "mfma_x32s_m64_n64_w2_k4"),
+    ((256, 4096, 4096), "mfma_x32s_m64_n64_w2_k4"),
+    ((512, 4096, 4096), "mfma_x32s_m64_n128_w1_k4"),
+    ((512, 4096, 6144), "mfma_x32s_m128_n128_w1_k2"),
+    ((256, 14336, 4096), "mfma_x32s_m64_n64_w2_k4"),
     ((512, 4096, 14336), "mfma_x32s_m128_n256_w1_k2"),
     ((256, 4160, 14336), "mfma_x32s_m128_n128_w1"),  # 65 block pairs: one pair per step
 ]
@@ -106,6 +113,12 @@ def test_gate_up_and_q8_plans(d):
     assert d.select(256, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m128_n128_w1_k2"
     assert d.select(128, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m64_n128_w1_k4"
     assert d.select(128, 14336, 4160, q8_0=True) == "q8_mfma_r_m64_n64"
+    # prefill tiles by dispatch waves x wave time
+    assert d.select(256, 4096, 4096, q8_0=True) == "q8_mfma_x32s_m64_n128_w1_k4"
+    assert d.select(384, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m128_n256_w1_k2"
+    assert d.select(256, 4096, 4096, gate_up=True) == "gateup_mfma_x32s_m64_n64_w2_k4"
+    assert d.select(512, 4096, 4096, gate_up=True) == "gateup_mfma_x32s_m64_n128_w1_k4"
+    assert d.select(256, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m128_n128_w1_k2"
 
 
 def test_forced_variant_and_bad_shapes(d):
