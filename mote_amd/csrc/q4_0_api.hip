@@ -227,7 +227,11 @@ const Variant* skinny_heuristic(const Problem& p) {
     // (A one-item 8-wave tile for <= 4 tokens and <= 1 item per CU measured
     // 2-3 % slower than the 16-wave tile below: 3 / 4 x 4096 x 4096 in 5.70 /
     // 5.81 us against 5.57 / 5.65 us.)
-    if (per16 <= 4)
+    // (Three 16-token tiles at three or more items per workgroup run the
+    // 32-token items instead: 36 / 48 x 4096 x 4096 in 9.9 us against 12.7 /
+    // 14.3 us; with two items per workgroup the 16-token tiles stay ahead,
+    // 48 x 4096 x 2048 in 6.8 against 8.6 us.)
+    if (per16 <= 4 && !((p.M + 15) / 16 == 3 && per16 >= 3))
         name = "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w";
     else if (p.M <= 16)
         name = "skinny_mfma_k8_s2_t1_d1_g1_r1_tr_l8_c_w";
@@ -245,6 +249,7 @@ const Variant* skinny_heuristic(const Problem& p) {
 const Variant* skinny_gate_up_heuristic(const Problem& p) {
     const uint64_t cus = static_cast<uint64_t>(device_cus());
     const uint64_t per16 = ((p.N + 15) / 16 * ((p.M + 15) / 16) + cus - 1) / cus;
+    const uint64_t per32 = ((p.N + 15) / 16 * ((p.M + 31) / 32) + cus - 1) / cus;
     const char* name;
     if (p.M <= 16 && per16 <= 1)
         name = "gateup_skinny_k8_s2_t1_d1";
@@ -254,8 +259,8 @@ const Variant* skinny_gate_up_heuristic(const Problem& p) {
         name = "gateup_skinny_k8_s2_t1_d1_l8_c_w";
     else if (p.M <= 32)
         name = "gateup_skinny_k8_s2_t2_d1_l4_c_w";
-    else
-        name = "gateup_skinny_k8_s2_t2_d1_c";
+    else  // up to 4 items per workgroup the lazy 32-token tile (48 x 4096 x 4096: 14.2 against 15.4 us)
+        name = per32 <= 4 ? "gateup_skinny_k8_s2_t2_d1_l4_c_w" : "gateup_skinny_k8_s2_t2_d1_c";
     const Variant* v = by_name(name);
     return v && skinny_mfma_supports(*v, p) ? v : nullptr;
 }
@@ -269,12 +274,13 @@ const Variant* skinny_gate_up_heuristic(const Problem& p) {
 const Variant* skinny_q8_heuristic(const Problem& p) {
     const uint64_t cus = static_cast<uint64_t>(device_cus());
     const uint64_t per16 = ((p.N + 15) / 16 * ((p.M + 15) / 16) + cus - 1) / cus;
+    const uint64_t per32 = ((p.N + 15) / 16 * ((p.M + 31) / 32) + cus - 1) / cus;
     const char* name;
     if (p.M <= 32 && per16 <= 4)
         name = p.M <= 8 ? "q8_skinny_k16_s1_t1_d1_l4_w" : "q8_skinny_k16_s1_t1_d1_l4_c_w";
     else if (p.M <= 16)
         name = "q8_skinny_k8_s2_t1_d1_l8_c_w";
-    else if (p.M <= 32)
+    else if (p.M <= 32 || per32 <= 4)  // 48 x 4096 x 4096: 12.5 against 13.1 us on the one below
         name = "q8_skinny_k8_s2_t2_d1_l4_c_w";
     else
         name = "q8_skinny_k16_s1_t2_d1_c";

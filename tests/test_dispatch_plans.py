@@ -46,6 +46,9 @@ LINEAR = [
     ((24, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l4_c_w"),
     ((32, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l4_c_w"),
     ((64, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l8_c_w"),
+    ((48, 4096, 4096), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l4_c_w"),
+    ((48, 4096, 2048), "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w"),
+    ((56, 4096, 4096), "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w"),
     ((128, 4096, 14336), "mfma_x32s_m64_n128_w1_k4"),
     ((256, 4096, 14336), "mfma_x32s_m128_n128_w1_k2"),
     ((384, 4096, 14336), "mfma_x32s_m128_n256_w1_k2"),
@@ -113,6 +116,9 @@ def test_gate_up_and_q8_plans(d):
     assert d.select(256, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m128_n128_w1_k2"
     assert d.select(128, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m64_n128_w1_k4"
     assert d.select(128, 14336, 4160, q8_0=True) == "q8_mfma_r_m64_n64"
+    assert d.select(48, 4096, 4096, gate_up=True) == "gateup_skinny_k8_s2_t2_d1_l4_c_w"
+    assert d.select(48, 4096, 4096, q8_0=True) == "q8_skinny_k8_s2_t2_d1_l4_c_w"
+    assert d.select(64, 14336, 4096, q8_0=True) == "q8_skinny_k16_s1_t2_d1_c"
     # prefill tiles by dispatch waves x wave time
     assert d.select(256, 4096, 4096, q8_0=True) == "q8_mfma_x32s_m64_n128_w1_k4"
     assert d.select(384, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m128_n256_w1_k2"
