@@ -329,13 +329,24 @@ const Variant* split_k_heuristic(const Problem& p, Op op) {
     const bool k4 = p.K % 4096 == 0;
     const char* name;
     if (op == Op::LinearQ8) {
-        // 8 items per workgroup where K is a multiple of 4096 (3 x 8192 x 8192:
-        // 17.6 us against 19.4 us with 4), else 4 (3 x 14336 x 4096: 18.3 us
-        // against 24.0 us with 8)
+        // Measured on MI355X: where K is a multiple of 4096, parts of 2048
+        // with 8 items per workgroup, 32-token items above 16 tokens (24 /
+        // 32 x 8192 x 28672: 71.0 / 75.7 us against 91.1 / 93.4 with 16-token
+        // items); otherwise parts of 1024 up to 16 tokens (4 / 16 x 14336 x
+        // 4096: 17.7 / 18.6 us against 18.4 / 19.8 with parts of 2048) and
+        // parts of 2048 with 8 items per workgroup above (24 / 32 x 14336 x
+        // 4096: 27.2 / 28.2 us against 30.1 / 31.0 with 4)
         if (p.M > 32)
             name = "q8_skinny_k8_s1_t2_d1_l8_c_w_sk";
-        else
-            name = k4 ? "q8_skinny_k8_s1_t1_d1_l8_c_w_sk" : "q8_skinny_k8_s1_t1_d1_l4_c_w_sk";
+        else if (k4)
+            name = p.M > 16 ? "q8_skinny_k8_s1_t2_d1_l8_c_w_sk" : "q8_skinny_k8_s1_t1_d1_l8_c_w_sk";
+        else if (p.M > 16)
+            name = "q8_skinny_k8_s1_t1_d1_l8_c_w_sk";
+        else {
+            const Variant* v = by_name("q8_skinny_k4_s1_t1_d1_l8_c_w_sk");
+            if (v && skinny_mfma_supports(*v, p)) return v;
+            name = "q8_skinny_k8_s1_t1_d1_l4_c_w_sk";
+        }
     } else if (op == Op::GateUp) {
         if (p.M > 32) return nullptr;  // the prefill tiles
         if (p.M > 16)
@@ -407,6 +418,13 @@ const Variant* heuristic(const Problem& p, Op op) {
                 std::snprintf(name, sizeof name, "q8_stream_s%u_d1_g1", split);
             const Variant* v = by_name(name);
             if (v && gemv_stream_supports(*v, p)) return v;
+        }
+        if (fast && p.M > 32 && p.M <= 64 && p.K > 4096 && prefill_tiles(p, 64, 128) >= 200) {
+            // as for Q4_0: 33-64 tokens past K = 4096 on at least 200 64 x
+            // 128 tiles (48 x 8192 x 28672: 81.4 us against 119.3 us on the
+            // split-K skinny tiles)
+            const Variant* v = by_name("q8_mfma_x32s_m64_n128_w1_k4");
+            if (v && prefill_supports(*v, p)) return v;
         }
         if (fast && p.M <= 64) {
             if (const Variant* v = skinny_q8_heuristic(p)) return v;
@@ -493,8 +511,18 @@ const Variant* heuristic(const Problem& p, Op op) {
             static const TileCost kGateUpTiles[] = {{"gateup_mfma_x32s_m128_n128_w1", 2, 64.0f},
                                                     {"gateup_mfma_x32s_m64_n128_w1", 4, 42.0f},
                                                     {"gateup_mfma_x32s_m64_n64_w2", 4, 30.0f}};
-            if (p.M > 64)
-                if (const Variant* v = cheapest_tiles(p, kGateUpTiles)) return v;
+            if (p.M > 64) {
+                if (const Variant* v = cheapest_tiles(p, kGateUpTiles)) {
+                    // three or more waves of 64 x 128 tiles: 2 block pairs
+                    // per step (384 x 4096 x 14 336: 115.4 us against 130.1
+                    // with 4; 192 x 8192 x 28 672: 228.1 against 241.9)
+                    const Variant* k2 = by_name("gateup_mfma_x32s_m64_n128_w1_k2");
+                    const uint64_t waves = (prefill_tiles(p, 64, 128) + device_cus() - 1) / device_cus();
+                    if (v == by_name("gateup_mfma_x32s_m64_n128_w1_k4") && waves >= 3 && k2 && prefill_supports(*k2, p))
+                        return k2;
+                    return v;
+                }
+            }
             if (p.M <= 128 && prefill_tiles(p, 64, 128) >= 200 && (p.M <= 64 || prefill_tiles(p, 128, 128) < 200))
                 return deepest_step("gateup_mfma_x32s_m64_n128_w1", p, 4);
             if (prefill_tiles(p, 128, 128) >= 200) return deepest_step("gateup_mfma_x32s_m128_n128_w1", p, 2);
@@ -503,6 +531,15 @@ const Variant* heuristic(const Problem& p, Op op) {
         return by_name("gateup_generic");
     }
     if (!fast) return by_name("generic");
+    if (p.M > 32 && p.M <= 64 && p.K > 4096 && prefill_tiles(p, 64, 128) >= 200) {
+        // 33-64 tokens past K = 4096 with at least 200 64 x 128 tiles (wide
+        // rows, e.g. 28 672): those tiles with 4 block pairs per step beat
+        // the split-K skinny tiles (measured on MI355X: 40 / 48 / 64 x 8192 x
+        // 28672 in 51.8 / 52.3 / 51.3 us against 80.0 / 81.0 / 81.6 us; at
+        // 8192 x 8192, 64 x 128 tiles too few, the skinny tiles stay ahead)
+        const Variant* v = by_name("mfma_x32s_m64_n128_w1_k4");
+        if (v && prefill_supports(*v, p)) return v;
+    }
     if (p.M == 64) {
         // 64 tokens still run as a skinny GEMM (faster than the prefill tiles).
         const Variant* v = skinny_heuristic(p);

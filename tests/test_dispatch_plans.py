@@ -47,6 +47,10 @@ LINEAR = [
     ((32, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l4_c_w"),
     ((64, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l8_c_w"),
     ((48, 4096, 4096), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l4_c_w"),
+    ((40, 8192, 28672), "mfma_x32s_m64_n128_w1_k4"),
+    ((64, 8192, 28672), "mfma_x32s_m64_n128_w1_k4"),
+    ((32, 8192, 28672), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l8_c_w_sk"),
+    ((64, 8192, 8192), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l8_c_w_sk"),
     ((48, 4096, 2048), "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w"),
     ((56, 4096, 4096), "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w"),
     ((128, 4096, 14336), "mfma_x32s_m64_n128_w1_k4"),
@@ -119,6 +123,11 @@ def test_gate_up_and_q8_plans(d):
     assert d.select(48, 4096, 4096, gate_up=True) == "gateup_skinny_k8_s2_t2_d1_l4_c_w"
     assert d.select(48, 4096, 4096, q8_0=True) == "q8_skinny_k8_s2_t2_d1_l4_c_w"
     assert d.select(64, 14336, 4096, q8_0=True) == "q8_skinny_k16_s1_t2_d1_c"
+    assert d.select(48, 28672, 8192, q8_0=True) == "q8_mfma_x32s_m64_n128_w1_k4"
+    assert d.select(24, 28672, 8192, q8_0=True) == "q8_skinny_k8_s1_t2_d1_l8_c_w_sk"
+    assert d.select(16, 4096, 14336, q8_0=True) == "q8_skinny_k4_s1_t1_d1_l8_c_w_sk"
+    assert d.select(32, 4096, 14336, q8_0=True) == "q8_skinny_k8_s1_t1_d1_l8_c_w_sk"
+    assert d.select(384, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m64_n128_w1_k2"
     # prefill tiles by dispatch waves x wave time
     assert d.select(256, 4096, 4096, q8_0=True) == "q8_mfma_x32s_m64_n128_w1_k4"
     assert d.select(384, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m128_n256_w1_k2"

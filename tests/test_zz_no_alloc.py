@@ -58,10 +58,10 @@ def test_two_calls_in_a_row_second_smaller(stream, oracle):
 
 
 def test_partial_tiles_beyond_the_array_are_rejected_before_launch(stream):
-    """64 tokens x N = 32768 x K = 16384 on the split-K tiles (four K parts of
-    4096) needs 64 x 32768 x 4 x 4 bytes = 32 MiB > 16 MiB: status 2, output
+    """64 tokens x N = 24576 x K = 16384 on the split-K tiles (four K parts of
+    4096) needs 64 x 24576 x 4 x 4 bytes = 24 MiB > 16 MiB: status 2, output
     untouched."""
-    m, n, k = 64, 32768, 16384
+    m, n, k = 64, 24576, 16384
     d = ops.Q4_0Dispatch()
     assert d.select(m, n, k).endswith("_sk")
     xb, wb = DeviceBuffer(m * k * 2), DeviceBuffer(n * (k // 32) * 18)
