@@ -200,6 +200,12 @@ const Variant* cheapest_tiles(const Problem& p, const TileCost (&cand)[N]) {
     return best;
 }
 
+// The Q4_0 linear's prefill tiles and their wave times at K = 4096.
+const TileCost kTiles[] = {{"mfma_x32s_m128_n256_w1", 2, 60.0f},
+                           {"mfma_x32s_m128_n128_w1", 2, 40.0f},
+                           {"mfma_x32s_m64_n128_w1", 4, 25.0f},
+                           {"mfma_x32s_m64_n64_w2", 4, 18.0f}};
+
 // Skinny GEMM (3 <= M <= 64, K = 4096) on the matrix cores, transposed weight
 // loads; null when the K slicing does not fit.  One (16-row, token-group) item
 // per step of a workgroup, with the reduction deferred over up to 4 items (16
@@ -310,10 +316,12 @@ const Variant* split_k_heuristic(const Problem& p, Op op) {
         // 2048 takes the one-slice tiles).
         if (op == Op::Linear && p.K == 2048) return nullptr;
         if (op == Op::GateUp && p.M > 32) return nullptr;  // the prefill tiles
-        // 16-token items up to 32 tokens (measured on MI355X: 32 x 3072 x
-        // 8192 in 14.6 us against 21.3 us with 32-token items; 4 x 5120 x
-        // 5120 in 10.9 us against 15.5 us on the vector-ALU GEMV)
-        const bool t2 = p.M > 32;
+        // 16-token items (measured on MI355X: 32 x 3072 x 8192 in 14.6 us
+        // against 21.3 us with 32-token items, 48 / 64 x 5120 x 5120 in 18.0
+        // / 22.2 against 24.8 / 26.0; 4 x 5120 x 5120 in 10.9 us against 15.5
+        // us on the vector-ALU GEMV); the gate/up takes 32-token items above
+        // 16 tokens (32 x 5120 x 13824: 48.3 us against 55.5)
+        const bool t2 = op == Op::GateUp && p.M > 16;
         const char* name = op == Op::LinearQ8 ? (t2 ? "q8_skinny_k4_s1_t2_d1_l8_c_w_sk" : "q8_skinny_k4_s1_t1_d1_l8_c_w_sk")
                            : op == Op::GateUp ? (t2 ? "gateup_skinny_k4_s1_t2_d1_l8_c_w_sk" : "gateup_skinny_k4_s1_t1_d1_l8_c_w_sk")
                                               : (t2 ? "skinny_mfma_k4_s1_t2_d1_g1_r1_tr_l8_c_w_sk"
@@ -531,14 +539,15 @@ const Variant* heuristic(const Problem& p, Op op) {
         return by_name("gateup_generic");
     }
     if (!fast) return by_name("generic");
-    if (p.M > 32 && p.M <= 64 && p.K > 4096 && prefill_tiles(p, 64, 128) >= 200) {
-        // 33-64 tokens past K = 4096 with at least 200 64 x 128 tiles (wide
-        // rows, e.g. 28 672): those tiles with 4 block pairs per step beat
-        // the split-K skinny tiles (measured on MI355X: 40 / 48 / 64 x 8192 x
-        // 28672 in 51.8 / 52.3 / 51.3 us against 80.0 / 81.0 / 81.6 us; at
-        // 8192 x 8192, 64 x 128 tiles too few, the skinny tiles stay ahead)
-        const Variant* v = by_name("mfma_x32s_m64_n128_w1_k4");
-        if (v && prefill_supports(*v, p)) return v;
+    if (p.M > 32 && p.M <= 64 && (p.K > 4096 || p.M == 64) && prefill_tiles(p, 64, 64) >= 200) {
+        // 33-64 tokens past K = 4096 (64 from K = 4096) with at least 200
+        // 64 x 64 tiles (wide rows): the prefill tiles beat the skinny ones
+        // (measured on MI355X: 40 / 48 / 64 x 8192 x 28672 on 64 x 128 tiles
+        // in 51.8 / 52.3 / 51.3 us against 80.0 / 81.0 / 81.6 us split K; 40
+        // x 5120 x 13824 on 64 x 64 tiles in 22.7 us against 31.5; 64 x 4096
+        // x 14336 in 17.5 against 18.6).  With fewer tiles (64 x 8192 x 8192,
+        // 64 x 14336 x 4096) the skinny tiles stay ahead.
+        if (const Variant* v = cheapest_tiles(p, kTiles)) return v;
     }
     if (p.M == 64) {
         // 64 tokens still run as a skinny GEMM (faster than the prefill tiles).
@@ -556,10 +565,6 @@ const Variant* heuristic(const Problem& p, Op op) {
         // the 128-row tiles, 4 for 64 x 128 and 64 x 64: what fits the LDS),
         // chosen by dispatch waves and wave time (K = 4096: 128 x 256 60 us,
         // 128 x 128 40 us, 64 x 128 25 us, 64 x 64 18 us).
-        static const TileCost kTiles[] = {{"mfma_x32s_m128_n256_w1", 2, 60.0f},
-                                          {"mfma_x32s_m128_n128_w1", 2, 40.0f},
-                                          {"mfma_x32s_m64_n128_w1", 4, 25.0f},
-                                          {"mfma_x32s_m64_n64_w2", 4, 18.0f}};
         if (const Variant* v = cheapest_tiles(p, kTiles)) return v;
         static const char* const order[] = {"mfma_x32s_m128_n256_w1", "mfma_x32s_m128_n128_w1",
                                             "mfma_x32s_m64_n128_w1", "mfma_r_m64_n128", "mfma_r_m64_n64"};
@@ -650,12 +655,17 @@ const Variant* heuristic(const Problem& p, Op op) {
     // (4096 x 14336: 9.2 us against 11.9 us on the matrix cores).  From 3
     // tokens: the skinny GEMM of skinny_heuristic, then any skinny variant
     // whose K slicing fits, then the vector-ALU GEMV.
-    if (p.M == 2 || (p.M == 3 && p.K > 4096 && p.K <= 16384)) {
+    if (p.M == 2 || (p.M == 3 && p.K > 4096 && p.K <= 16384) ||
+        (p.M == 4 && p.K > 4096 && p.K <= 16384 && p.K % 1024 != 0)) {
         // Rows split over S waves past K = 4096, one workgroup per CU
         // (measured on MI355X: 8192 x 8192 in 9.35 us, 14336 x 4096 in 9.35
         // us, 28672 x 8192 in 26.0 us, against 11.8, 11.8 and 31.4 us for the
         // split-K tiles; three tokens, 8192 x 8192 in 11.1 us and 14336 x
-        // 4096 in 11.6 us, against 11.9 and 11.8 us).
+        // 4096 in 11.6 us, against 11.9 and 11.8 us; four tokens where K
+        // takes no split-K slicing, 11008 x 4096 in 13.4 us and 13824 x 5120
+        // in 15.7 us, against 24.0 and 48.2 us on the vector-ALU GEMV, while
+        // where it does the split-K tiles stay ahead, 14336 x 4096 12.1 us
+        // against 13.6).
         uint32_t split = 1;
         while (split < 8 && p.K > 4096u * split) split *= 2;
         char name[32];
@@ -673,8 +683,14 @@ const Variant* heuristic(const Problem& p, Op op) {
         const Variant* v = by_name(name);
         if (v && skinny_mfma_supports(*v, p)) return v;
     }
+    // 12 tokens and more with no K slicing (K % 1024 != 0, e.g. 11 008 and
+    // 13 824): the prefill tiles (measured on MI355X: 16 x 11008 x 4096 in
+    // 40.4 us, 32 x 13824 x 5120 in 50.5 us, against 59.0 and 181.3 us on
+    // the vector-ALU GEMV; 8 tokens 40.4 / 50.0 against 32.7 / 50.8)
+    if (p.M >= 12)
+        if (const Variant* v = cheapest_tiles(p, kTiles)) return v;
     if (p.M == 2) return by_name("gemv_r4_t2_k1");
-    return by_name("gemv_r4_t4_k1");
+    return by_name(p.M >= 8 ? "gemv_r4_t2_k1" : "gemv_r4_t4_k1");
 }
 
 hipError_t time_variant(const Variant& v, const Problem& p, float* ms) {

@@ -317,7 +317,7 @@ const Variant kStream[] = {
     MOTE_STREAM_S(8, 1, 1), MOTE_STREAM_S(8, 1, 2),
     MOTE_STREAM_M(3, 1, 1), MOTE_STREAM_M(4, 1, 1), MOTE_STREAM_MQ(2, 1, 1),
     MOTE_STREAM_SMQ(2, 2, 1), MOTE_STREAM_SMQ(4, 2, 1), MOTE_STREAM_SMQ(8, 2, 1),
-    MOTE_STREAM_SMQ(2, 3, 1), MOTE_STREAM_SMQ(4, 3, 1),
+    MOTE_STREAM_SMQ(2, 3, 1), MOTE_STREAM_SMQ(4, 3, 1), MOTE_STREAM_SMQ(2, 4, 1), MOTE_STREAM_SMQ(4, 4, 1),
     MOTE_Q8("d1_g1", 1, 1), MOTE_Q8("d1_g2", 1, 2), MOTE_Q8("s2_d1_g1", 2, 1), MOTE_Q8("s4_d1_g1", 4, 1),
     MOTE_Q8("s8_d1_g1", 8, 1),
     MOTE_Q8_SM(2, 2), MOTE_Q8_SM(4, 2), MOTE_Q8_SM(8, 2), MOTE_Q8_SM(2, 3), MOTE_Q8_SM(4, 3), MOTE_Q8_M(2, 1), MOTE_Q8_M(4, 1),

@@ -45,7 +45,15 @@ LINEAR = [
     ((16, 4096, 14336), "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w"),
     ((24, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l4_c_w"),
     ((32, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l4_c_w"),
-    ((64, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l8_c_w"),
+    ((64, 4096, 14336), "mfma_x32s_m64_n64_w2_k4"),
+    ((40, 4096, 14336), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l8_c_w"),
+    ((40, 5120, 13824), "mfma_x32s_m64_n64_w2_k4"),
+    ((48, 5120, 5120), "skinny_mfma_k4_s1_t1_d1_g1_r1_tr_l8_c_w_sk"),
+    ((4, 11008, 4096), "stream_s4_m4_d1q_g1"),
+    ((4, 13824, 5120), "stream_s4_m4_d1q_g1"),
+    ((4, 14336, 4096), "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l4_c_w_sk"),
+    ((16, 11008, 4096), "mfma_x32s_m64_n64_w2_k4"),
+    ((8, 11008, 4096), "gemv_r4_t2_k1"),
     ((48, 4096, 4096), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l4_c_w"),
     ((40, 8192, 28672), "mfma_x32s_m64_n128_w1_k4"),
     ((64, 8192, 28672), "mfma_x32s_m64_n128_w1_k4"),
