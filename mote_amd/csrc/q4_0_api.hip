@@ -200,6 +200,11 @@ const Variant* cheapest_tiles(const Problem& p, const TileCost (&cand)[N]) {
     return best;
 }
 
+// The Q8_0 linear's prefill tiles and their wave times at K = 4096.
+const TileCost kQ8Tiles[] = {{"q8_mfma_x32s_m128_n256_w1", 2, 96.0f},
+                             {"q8_mfma_x32s_m128_n128_w1", 2, 56.0f},
+                             {"q8_mfma_x32s_m64_n128_w1", 4, 36.0f}};
+
 // The Q4_0 linear's prefill tiles and their wave times at K = 4096.
 const TileCost kTiles[] = {{"mfma_x32s_m128_n256_w1", 2, 60.0f},
                            {"mfma_x32s_m128_n128_w1", 2, 40.0f},
@@ -416,7 +421,10 @@ const Variant* heuristic(const Problem& p, Op op) {
             uint32_t split = 1;
             while (split < 8 && p.K > 4096u * split) split *= 2;
             char name[32];
-            if ((p.M == 2 || p.M == 3) && split > 1)  // 3 x 8192 x 8192: 15.2 us (split-K tiles 17.6)
+            // four tokens past K = 4096 where no split-K slicing fits (K %
+            // 1024 != 0): rows split over S waves as for two and three
+            const bool m4_split = p.M == 4 && split > 1 && split <= 4 && p.K % 1024 != 0;
+            if (((p.M == 2 || p.M == 3) && split > 1) || m4_split)  // 3 x 8192 x 8192: 15.2 us (split-K tiles 17.6)
                 std::snprintf(name, sizeof name, "q8_stream_s%u_m%u_d1q_g1", split, p.M);
             else if (p.M > 1)
                 std::snprintf(name, sizeof name, "q8_stream_m%u_d1q_g1", p.M);
@@ -424,6 +432,16 @@ const Variant* heuristic(const Problem& p, Op op) {
                 std::snprintf(name, sizeof name, "q8_stream_d1_g1");
             else
                 std::snprintf(name, sizeof name, "q8_stream_s%u_d1_g1", split);
+            const Variant* v = by_name(name);
+            if (v && gemv_stream_supports(*v, p)) return v;
+        }
+        if (fast && p.M >= 5 && p.M <= 16 && p.K > 4096 && p.K <= 16384 && p.K % 1024 != 0) {
+            // 5-16 tokens where K takes no split-K slicing: passes of up to
+            // four tokens on the split-row streaming GEMV (a four-token pass
+            // at 11008 x 4096 in 14.9 us; 8 tokens took 76.3 us on the
+            // prefill tiles and 89.5 us on the generic kernel)
+            char name[40];
+            std::snprintf(name, sizeof name, "q8_stream_s%u_m4x_d1q_g1", p.K > 8192 ? 4u : 2u);
             const Variant* v = by_name(name);
             if (v && gemv_stream_supports(*v, p)) return v;
         }
@@ -451,12 +469,13 @@ const Variant* heuristic(const Problem& p, Op op) {
             // 96 us, 128 x 128 56 us, 64 x 128 36 us; e.g. 256 x 4096 x 4096
             // in 32.8 us on 64 x 128 tiles against 50.3 on the 16 x 16 tiles,
             // 384 x 4096 x 14 336 in 96.3 us on 128 x 256 against 118.7).
-            static const TileCost kQ8Tiles[] = {{"q8_mfma_x32s_m128_n256_w1", 2, 96.0f},
-                                                {"q8_mfma_x32s_m128_n128_w1", 2, 56.0f},
-                                                {"q8_mfma_x32s_m64_n128_w1", 4, 36.0f}};
             if (const Variant* v = cheapest_tiles(p, kQ8Tiles)) return v;
             return by_name("q8_mfma_r_m64_n64");
         }
+        // tokens with no K slicing (K % 1024 != 0, e.g. 11 008, 13 824): the
+        // prefill tiles, where K allows their multi-pair steps
+        if (fast && p.M >= 4)
+            if (const Variant* v = cheapest_tiles(p, kQ8Tiles)) return v;
         return by_name("q8_generic");
     }
     if (op == Op::GateUp) {
@@ -673,6 +692,17 @@ const Variant* heuristic(const Problem& p, Op op) {
             std::snprintf(name, sizeof name, "%s", "stream_m2_d1q_g1");
         else
             std::snprintf(name, sizeof name, "stream_s%u_m%u_d1q_g1", split, p.M);
+        const Variant* v = by_name(name);
+        if (v && gemv_stream_supports(*v, p)) return v;
+    }
+    if (p.M >= 5 && p.M <= 11 && p.K > 4096 && p.K <= 16384 && p.K % 1024 != 0) {
+        // 5-11 tokens where K takes no split-K slicing: passes of up to four
+        // tokens on the split-row streaming GEMV (each pass reads the
+        // weights once; measured on MI355X: a four-token pass at 11008 x
+        // 4096 13.4 us, against 32.7 us for 8 tokens on the vector-ALU GEMV
+        // and 40.4 us on the prefill tiles)
+        char name[32];
+        std::snprintf(name, sizeof name, "stream_s%u_m4x_d1q_g1", p.K > 8192 ? 4u : 2u);
         const Variant* v = by_name(name);
         if (v && gemv_stream_supports(*v, p)) return v;
     }

@@ -268,6 +268,32 @@ hipError_t launch_gemv_stream(const Problem& p) {
     return hipGetLastError();
 }
 
+// 5-16 tokens as passes of at most four tokens each (rows split over S
+// waves), every pass reading the weights once: for K with no split-K slicing
+// (K % 1024 != 0, e.g. 11 008, 13 824), where the alternatives are the
+// vector-ALU GEMV or the prefill tiles.
+template <int S, class F>
+hipError_t launch_gemv_stream_groups(const Problem& p) {
+    const size_t out_bytes = p.out == OutType::F32 ? 4 : 2;
+    for (uint32_t m0 = 0; m0 < p.M;) {
+        const uint32_t mt = p.M - m0 < 4u ? p.M - m0 : 4u;
+        Problem q = p;
+        q.M = mt;
+        q.x = static_cast<const uint16_t*>(p.x) + static_cast<size_t>(m0) * p.K;
+        q.y = static_cast<uint8_t*>(p.y) + static_cast<size_t>(m0) * p.N * out_bytes;
+        hipError_t e;
+        switch (mt) {
+            case 4: e = launch_gemv_stream<1, S, 1, 1, 4, false, F>(q); break;
+            case 3: e = launch_gemv_stream<1, S, 1, 1, 3, false, F>(q); break;
+            case 2: e = launch_gemv_stream<1, S, 1, 1, 2, false, F>(q); break;
+            default: e = launch_gemv_stream<1, S, 1, 1, 1, false, F>(q); break;
+        }
+        if (e != hipSuccess) return e;
+        m0 += mt;
+    }
+    return hipSuccess;
+}
+
 // p0 = 64-pair capacity of a row (K <= 4096 p0), p1 = rows in flight,
 // p2 = workgroups per CU.
 #define MOTE_STREAM(D, G) \
@@ -320,7 +346,12 @@ const Variant kStream[] = {
     MOTE_STREAM_SMQ(2, 3, 1), MOTE_STREAM_SMQ(4, 3, 1), MOTE_STREAM_SMQ(2, 4, 1), MOTE_STREAM_SMQ(4, 4, 1),
     MOTE_Q8("d1_g1", 1, 1), MOTE_Q8("d1_g2", 1, 2), MOTE_Q8("s2_d1_g1", 2, 1), MOTE_Q8("s4_d1_g1", 4, 1),
     MOTE_Q8("s8_d1_g1", 8, 1),
-    MOTE_Q8_SM(2, 2), MOTE_Q8_SM(4, 2), MOTE_Q8_SM(8, 2), MOTE_Q8_SM(2, 3), MOTE_Q8_SM(4, 3), MOTE_Q8_M(2, 1), MOTE_Q8_M(4, 1),
+    MOTE_Q8_SM(2, 2), MOTE_Q8_SM(4, 2), MOTE_Q8_SM(8, 2), MOTE_Q8_SM(2, 3), MOTE_Q8_SM(4, 3), MOTE_Q8_SM(2, 4), MOTE_Q8_SM(4, 4),
+    // tokens = -4: 5-16 tokens in passes of four
+    Variant{"q8_stream_s2_m4x_d1q_g1", Kind::Q8Stream, 2, 1, 1, &launch_gemv_stream_groups<2, FmtQ8>, -4},
+    Variant{"q8_stream_s4_m4x_d1q_g1", Kind::Q8Stream, 4, 1, 1, &launch_gemv_stream_groups<4, FmtQ8>, -4},
+    Variant{"stream_s2_m4x_d1q_g1", Kind::GemvStream, 2, 1, 1, &launch_gemv_stream_groups<2, FmtQ4>, -4},
+    Variant{"stream_s4_m4x_d1q_g1", Kind::GemvStream, 4, 1, 1, &launch_gemv_stream_groups<4, FmtQ4>, -4}, MOTE_Q8_M(2, 1), MOTE_Q8_M(4, 1),
     MOTE_STREAM_GU(1, 1), MOTE_STREAM_GU(1, 2),
     MOTE_STREAM_GU_MQ(1, 2), MOTE_STREAM_GU_SMQ(2, 2), MOTE_STREAM_GU_SMQ(4, 2), MOTE_STREAM_GU_SMQ(8, 2),
     MOTE_STREAM_GU_SMQ(2, 1), MOTE_STREAM_GU_SMQ(4, 1), MOTE_STREAM_GU_SMQ(8, 1),
@@ -352,6 +383,14 @@ const Variant* gemv_stream_variants(int* count) {
 // most 4096 per 64-pair slot of a row, x 16-byte and w (and the up matrix of a
 // gate/up) dword aligned.
 bool gemv_stream_supports(const Variant& v, const Problem& p) {
+    if (v.tokens < 0) {  // passes of -tokens tokens: 5-16 tokens, each pass as that many
+        if (p.M < 5 || p.M > 16) return false;
+        Variant pass = v;
+        pass.tokens = -v.tokens;
+        Problem q = p;
+        q.M = static_cast<uint32_t>(pass.tokens);
+        return gemv_stream_supports(pass, q);
+    }
     const uint32_t tokens = v.tokens > 0 ? static_cast<uint32_t>(v.tokens) : 1u;
     const bool up_ok = v.kind != Kind::GateUpStream ||
                        (p.w_up != nullptr && reinterpret_cast<uintptr_t>(p.w_up) % 4 == 0);

@@ -53,7 +53,9 @@ LINEAR = [
     ((4, 13824, 5120), "stream_s4_m4_d1q_g1"),
     ((4, 14336, 4096), "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l4_c_w_sk"),
     ((16, 11008, 4096), "mfma_x32s_m64_n64_w2_k4"),
-    ((8, 11008, 4096), "gemv_r4_t2_k1"),
+    ((8, 11008, 4096), "stream_s4_m4x_d1q_g1"),
+    ((5, 5376, 4096), "stream_s2_m4x_d1q_g1"),
+    ((12, 11008, 4096), "mfma_x32s_m64_n64_w2_k4"),
     ((48, 4096, 4096), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l4_c_w"),
     ((40, 8192, 28672), "mfma_x32s_m64_n128_w1_k4"),
     ((64, 8192, 28672), "mfma_x32s_m64_n128_w1_k4"),
@@ -136,6 +138,10 @@ def test_gate_up_and_q8_plans(d):
     assert d.select(16, 4096, 14336, q8_0=True) == "q8_skinny_k4_s1_t1_d1_l8_c_w_sk"
     assert d.select(32, 4096, 14336, q8_0=True) == "q8_skinny_k8_s1_t1_d1_l8_c_w_sk"
     assert d.select(384, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m64_n128_w1_k2"
+    assert d.select(4, 4096, 11008, q8_0=True) == "q8_stream_s4_m4_d1q_g1"
+    assert d.select(8, 4096, 11008, q8_0=True) == "q8_stream_s4_m4x_d1q_g1"
+    assert d.select(16, 5120, 13824, q8_0=True) == "q8_stream_s4_m4x_d1q_g1"
+    assert d.select(32, 5120, 13824, q8_0=True) == "q8_mfma_x32s_m64_n128_w1_k4"
     # prefill tiles by dispatch waves x wave time
     assert d.select(256, 4096, 4096, q8_0=True) == "q8_mfma_x32s_m64_n128_w1_k4"
     assert d.select(384, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m128_n256_w1_k2"

@@ -281,7 +281,7 @@ def test_every_rows_variant(stream, oracle, variant):
         check_against_oracle(oracle, y16, x, w, m, n, k, f16_out=True, what=f"{variant} f16 {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("variant", _variants("stream_"))
+@pytest.mark.parametrize("variant", [v for v in _variants("stream_") if "_m4x_" not in v])
 def test_every_stream_variant(stream, oracle, variant):
     """Persistent pipelined GEMV: N below one workgroup, ragged N, idle lanes
     (K < 4096), and N = 140001 at K = 64, where waves own more than 64 rows
