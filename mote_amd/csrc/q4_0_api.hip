@@ -320,13 +320,16 @@ const Variant* split_k_heuristic(const Problem& p, Op op) {
         // gate/up at K = 2048, which no plain slicing fits (a linear at K =
         // 2048 takes the one-slice tiles).
         if (op == Op::Linear && p.K == 2048) return nullptr;
-        if (op == Op::GateUp && p.M > 32) return nullptr;  // the prefill tiles
         // 16-token items (measured on MI355X: 32 x 3072 x 8192 in 14.6 us
         // against 21.3 us with 32-token items, 48 / 64 x 5120 x 5120 in 18.0
         // / 22.2 against 24.8 / 26.0; 4 x 5120 x 5120 in 10.9 us against 15.5
         // us on the vector-ALU GEMV); the gate/up takes 32-token items above
-        // 16 tokens (32 x 5120 x 13824: 48.3 us against 55.5)
-        const bool t2 = op == Op::GateUp && p.M > 16;
+        // 32 tokens, and above 16 where the 16-token items exceed 4096 (32 x
+        // 5120 x 13824: 48.6 us against 55.5; 32 x 5120 x 5120, 3200 items:
+        // 24.1 us against 27.4; 48 / 64 x 5120 x 5120: 32.0 / 33.2 us, where
+        // the 16 x 16 prefill tiles took 68.6)
+        const uint64_t items1k = static_cast<uint64_t>((p.N + 15) / 16) * ((p.M + 15) / 16) * (p.K / 1024);
+        const bool t2 = op == Op::GateUp && (p.M > 32 || (p.M > 16 && items1k > 4096));
         const char* name = op == Op::LinearQ8 ? (t2 ? "q8_skinny_k4_s1_t2_d1_l8_c_w_sk" : "q8_skinny_k4_s1_t1_d1_l8_c_w_sk")
                            : op == Op::GateUp ? (t2 ? "gateup_skinny_k4_s1_t2_d1_l8_c_w_sk" : "gateup_skinny_k4_s1_t1_d1_l8_c_w_sk")
                                               : (t2 ? "skinny_mfma_k4_s1_t2_d1_g1_r1_tr_l8_c_w_sk"
@@ -423,7 +426,10 @@ const Variant* heuristic(const Problem& p, Op op) {
             char name[32];
             // four tokens past K = 4096 where no split-K slicing fits (K %
             // 1024 != 0): rows split over S waves as for two and three
-            const bool m4_split = p.M == 4 && split > 1 && split <= 4 && p.K % 1024 != 0;
+            // (also where split K would take parts of 1024, K % 2048 != 0:
+            // 4 x 5120 x 5120 in 10.9 us against 12.7, x 13824 21.1 against
+            // 24.8)
+            const bool m4_split = p.M == 4 && split > 1 && split <= 4 && p.K % 2048 != 0;
             if (((p.M == 2 || p.M == 3) && split > 1) || m4_split)  // 3 x 8192 x 8192: 15.2 us (split-K tiles 17.6)
                 std::snprintf(name, sizeof name, "q8_stream_s%u_m%u_d1q_g1", split, p.M);
             else if (p.M > 1)
@@ -445,12 +451,11 @@ const Variant* heuristic(const Problem& p, Op op) {
             const Variant* v = by_name(name);
             if (v && gemv_stream_supports(*v, p)) return v;
         }
-        if (fast && p.M > 32 && p.M <= 64 && p.K > 4096 && prefill_tiles(p, 64, 128) >= 200) {
-            // as for Q4_0: 33-64 tokens past K = 4096 on at least 200 64 x
-            // 128 tiles (48 x 8192 x 28672: 81.4 us against 119.3 us on the
-            // split-K skinny tiles)
-            const Variant* v = by_name("q8_mfma_x32s_m64_n128_w1_k4");
-            if (v && prefill_supports(*v, p)) return v;
+        if (fast && p.M > 32 && p.M <= 64 && p.K > 4096 && prefill_tiles(p, 64, 64) >= 200) {
+            // as for Q4_0: 33-64 tokens past K = 4096 on wide rows (48 x 8192
+            // x 28672: 81.4 us against 119.3 us on the split-K skinny tiles;
+            // 64 x 5120 x 13824: 46.8 against 57.4)
+            if (const Variant* v = cheapest_tiles(p, kQ8Tiles)) return v;
         }
         if (fast && p.M <= 64) {
             if (const Variant* v = skinny_q8_heuristic(p)) return v;
@@ -510,11 +515,13 @@ const Variant* heuristic(const Problem& p, Op op) {
             const Variant* v = by_name("gateup_mfma_x32s_m64_n128_w1_k4");
             if (v && prefill_supports(*v, p)) return v;
         }
-        if (fast && p.M > 48 && p.M <= 64 && prefill_tiles(p, 64, 128) < 200 &&
-            prefill_tiles(p, 64, 64) >= 200) {
-            // 49-64 tokens where 64 x 128 tiles are too few: 64 x 64 tiles of
+        if (fast && p.M > 32 && p.M <= 64 && prefill_tiles(p, 64, 128) < 200 &&
+            prefill_tiles(p, 64, 64) >= (p.M > 48 ? 160u : 200u)) {
+            // 33-64 tokens where 64 x 128 tiles are too few: 64 x 64 tiles of
             // 2 x 2 waves, 4 block pairs per step (64 x 4096 x 14 336: 30.8
-            // us, against 35.6 us on the skinny tiles)
+            // us, against 35.6 us on the skinny tiles; 64 x 5120 x 13824: 39.9
+            // us, where 48 tokens took 71.8 us on the 16 x 16 tiles; 64 x 4096
+            // x 11008, 172 tiles: 29.1 us against 31.7 on the skinny tiles)
             const Variant* v = by_name("gateup_mfma_x32s_m64_n64_w2_k4");
             if (v && prefill_supports(*v, p)) return v;
         }

@@ -142,6 +142,13 @@ def test_gate_up_and_q8_plans(d):
     assert d.select(8, 4096, 11008, q8_0=True) == "q8_stream_s4_m4x_d1q_g1"
     assert d.select(16, 5120, 13824, q8_0=True) == "q8_stream_s4_m4x_d1q_g1"
     assert d.select(32, 5120, 13824, q8_0=True) == "q8_mfma_x32s_m64_n128_w1_k4"
+    assert d.select(4, 5120, 5120, q8_0=True) == "q8_stream_s2_m4_d1q_g1"
+    assert d.select(64, 13824, 5120, q8_0=True) == "q8_mfma_x32s_m64_n128_w1_k4"
+    assert d.select(48, 5120, 5120, gate_up=True) == "gateup_skinny_k4_s1_t2_d1_l8_c_w_sk"
+    assert d.select(32, 5120, 5120, gate_up=True) == "gateup_skinny_k4_s1_t1_d1_l8_c_w_sk"
+    assert d.select(32, 13824, 5120, gate_up=True) == "gateup_skinny_k4_s1_t2_d1_l8_c_w_sk"
+    assert d.select(48, 13824, 5120, gate_up=True) == "gateup_mfma_x32s_m64_n64_w2_k4"
+    assert d.select(64, 11008, 4096, gate_up=True) == "gateup_mfma_x32s_m64_n64_w2_k4"
     # prefill tiles by dispatch waves x wave time
     assert d.select(256, 4096, 4096, q8_0=True) == "q8_mfma_x32s_m64_n128_w1_k4"
     assert d.select(384, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m128_n256_w1_k2"
