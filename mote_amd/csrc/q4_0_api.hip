@@ -768,7 +768,13 @@ int run(Dispatcher& d, const Problem& problem, Op op) {
             const Variant* chosen = nullptr;
             if (d.autotune) {
                 float best = 0.0f;
-                for (const Variant* c : candidates(p, op)) {
+                // the shape heuristic's pick is always among those timed (it
+                // may be of a kind the list leaves out for this M, e.g. the
+                // prefill tiles for 12-63 tokens where K has no slicing)
+                std::vector<const Variant*> cands = candidates(p, op);
+                const Variant* h = heuristic(p, op);
+                if (h && std::find(cands.begin(), cands.end(), h) == cands.end()) cands.push_back(h);
+                for (const Variant* c : cands) {
                     float ms = 0.0f;
                     const hipError_t err = time_variant(*c, p, &ms);
                     if (err != hipSuccess)

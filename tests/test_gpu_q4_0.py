@@ -505,3 +505,20 @@ def test_autotuned_dispatch_caches_a_plan(stream, oracle):
     y = run_linear(stream, x, w, m, n, k, dispatch=d)
     assert d.plan(m, n, k) in ops.variant_names()
     check_against_oracle(oracle, y, x, w, m, n, k)
+
+
+def test_autotuner_times_the_heuristic_pick(stream, oracle):
+    """16 tokens at K = 11008 (no K slicing): the heuristic takes the prefill
+    tiles, a kind the autotuner's own list holds only from 64 tokens; the
+    autotuner times that pick beside its list, so its plan is a variant of
+    the list or that pick, and the result is within the oracle's tolerance."""
+    m, k, n = 16, 11008, 512
+    x = normal_x(wl.seed_for(1, 2), m, k)
+    w = weights(wl.seed_for(0, 3), n, k)
+    plain = ops.Q4_0Dispatch()
+    run_linear(stream, x, w, m, n, k, dispatch=plain)
+    assert plain.plan(m, n, k).startswith("mfma_")
+    d = ops.Q4_0Dispatch(autotune=True)
+    y = run_linear(stream, x, w, m, n, k, dispatch=d)
+    assert d.plan(m, n, k) in ops.variant_names()
+    check_against_oracle(oracle, y, x, w, m, n, k)
