@@ -370,15 +370,30 @@ const Variant* split_k_heuristic(const Problem& p, Op op) {
         else
             name = items2k > 4 * 512 ? "gateup_skinny_k8_s1_t1_d1_l8_c_w_sk" : "gateup_skinny_k8_s1_t1_d1_l4_c_w_sk";
     } else if (p.M > 16) {
+        // where K is a multiple of 4096, by 32-token items of 2048 (measured
+        // on MI355X at K = 8192: N = 2048, 32 tokens, 512 items, 16-token
+        // items with 4 per workgroup in 9.3 us against 10.8 with 32-token
+        // items and 8; 48 / 64 tokens, 1024 items, 4 per workgroup; N = 3072,
+        // 48 / 64 tokens, 1536 items, 13.7 / 14.5 us with 8 against 15.3 /
+        // 15.4 for the 2-step items)
         if (!k4)
             name = p.M > 32 ? "skinny_mfma_k8_s1_t2_d1_g1_r1_tr_l8_c_w_sk" : "skinny_mfma_k8_s1_t2_d1_g1_r1_tr_l4_c_w_sk";
-        else if (p.M <= 32 && items2k_t2 <= 8 * 256)
+        else if (p.M <= 32 && items2k_t2 <= 512)
+            name = "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l4_c_w_sk";
+        else if (items2k_t2 <= 1024)
+            name = "skinny_mfma_k8_s1_t2_d1_g1_r1_tr_l4_c_w_sk";
+        else if (items2k_t2 <= 8 * 256 && (p.M <= 32 || items2k_t2 < 2048))
             name = "skinny_mfma_k8_s1_t2_d1_g1_r1_tr_l8_c_w_sk";
         else
             name = "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l8_c_w_sk";
     } else if (k4) {
-        name = items4k > 4 * cus ? "skinny_mfma_k8_s2_t1_d1_g1_r1_tr_l8_c_w_sk"
-                                 : "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w_sk";
+        // parts of 4096 from two items per CU, parts of 2048 below (4 / 8 / 16
+        // x 8192 x 3072, 384 items of 4096: 7.7 / 7.6 / 8.4 us against 8.2 /
+        // 8.4 / 9.0; 4 x 8192 x 8192, 1024 items: 12.2 against 12.5)
+        name = items4k > 4 * cus   ? "skinny_mfma_k8_s2_t1_d1_g1_r1_tr_l8_c_w_sk"
+               : items4k >= 2 * cus ? "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w_sk"
+               : items2k > 4 * 512  ? "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l8_c_w_sk"
+                                    : "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l4_c_w_sk";
     } else {
         name = items2k > 4 * 512 ? "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l8_c_w_sk"
                                  : "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l4_c_w_sk";
@@ -565,14 +580,24 @@ const Variant* heuristic(const Problem& p, Op op) {
         return by_name("gateup_generic");
     }
     if (!fast) return by_name("generic");
-    if (p.M > 32 && p.M <= 64 && (p.K > 4096 || p.M == 64) && prefill_tiles(p, 64, 64) >= 200) {
+    if (p.M > 32 && p.M <= 64 && (p.K > 4096 || p.M == 64) &&
+        prefill_tiles(p, 64, 64) >= (p.K > 4096 ? 160u : 200u)) {
         // 33-64 tokens past K = 4096 (64 from K = 4096) with at least 200
         // 64 x 64 tiles (wide rows): the prefill tiles beat the skinny ones
         // (measured on MI355X: 40 / 48 / 64 x 8192 x 28672 on 64 x 128 tiles
         // in 51.8 / 52.3 / 51.3 us against 80.0 / 81.0 / 81.6 us split K; 40
         // x 5120 x 13824 on 64 x 64 tiles in 22.7 us against 31.5; 64 x 4096
-        // x 14336 in 17.5 against 18.6).  With fewer tiles (64 x 8192 x 8192,
-        // 64 x 14336 x 4096) the skinny tiles stay ahead.
+        // x 14336 in 17.5 against 18.6; 48 / 64 x 8192 x 10240, 160 tiles,
+        // 32.6 / 33.2 us against 35.1 / 39.7).  With fewer tiles (64 x 8192 x
+        // 8192, 64 x 14336 x 4096), or 160-199 at K = 4096 (64 x 4096 x
+        // 11008: 18.8 against 17.8), the skinny tiles stay ahead.
+        if (const Variant* v = cheapest_tiles(p, kTiles)) return v;
+    }
+    if (p.M > 48 && p.M <= 64 && p.K > 2048 && p.K < 4096) {
+        // 49-64 tokens at 2048 < K < 4096, where the skinny tiles split K in
+        // parts of 1024 or not at all: the prefill tiles (64 x 3072 x 8192 in
+        // 13.6 us against 19.0 on the split-K tiles; 64 x 3072 x 5120 13.5
+        // against 14.5)
         if (const Variant* v = cheapest_tiles(p, kTiles)) return v;
     }
     if (p.M == 64) {
@@ -681,8 +706,9 @@ const Variant* heuristic(const Problem& p, Op op) {
     // (4096 x 14336: 9.2 us against 11.9 us on the matrix cores).  From 3
     // tokens: the skinny GEMM of skinny_heuristic, then any skinny variant
     // whose K slicing fits, then the vector-ALU GEMV.
+    const bool mid_k = (p.M == 3 || p.M == 4) && p.K > 2048 && p.K < 4096;
     if (p.M == 2 || (p.M == 3 && p.K > 4096 && p.K <= 16384) ||
-        (p.M == 4 && p.K > 4096 && p.K <= 16384 && p.K % 1024 != 0)) {
+        (p.M == 4 && p.K > 4096 && p.K <= 16384 && p.K % 1024 != 0) || mid_k) {
         // Rows split over S waves past K = 4096, one workgroup per CU
         // (measured on MI355X: 8192 x 8192 in 9.35 us, 14336 x 4096 in 9.35
         // us, 28672 x 8192 in 26.0 us, against 11.8, 11.8 and 31.4 us for the
@@ -691,11 +717,18 @@ const Variant* heuristic(const Problem& p, Op op) {
         // takes no split-K slicing, 11008 x 4096 in 13.4 us and 13824 x 5120
         // in 15.7 us, against 24.0 and 48.2 us on the vector-ALU GEMV, while
         // where it does the split-K tiles stay ahead, 14336 x 4096 12.1 us
-        // against 13.6).
+        // against 13.6).  Three or four tokens at 2048 < K < 4096, where
+        // the skinny tiles take K in parts of 1024 or no slicing fits: the
+        // streaming GEMV reading each row once for all tokens (3 / 4 x 3072 x
+        // 8192 in 6.6 / 7.7 us against 10.3 / 10.4 on the split-K tiles; 3 /
+        // 4 x 3584 x 18944 in 11.6 / 13.9 against 28.1 / 28.6 on the
+        // vector-ALU GEMV).
         uint32_t split = 1;
         while (split < 8 && p.K > 4096u * split) split *= 2;
         char name[32];
-        if (split == 1)
+        if (split == 1 && p.M > 2)
+            std::snprintf(name, sizeof name, "%s", p.M == 3 ? "stream_m3_d1_g1" : "stream_m4_d1_g1");
+        else if (split == 1)
             std::snprintf(name, sizeof name, "%s", "stream_m2_d1q_g1");
         else
             std::snprintf(name, sizeof name, "stream_s%u_m%u_d1q_g1", split, p.M);
@@ -713,6 +746,14 @@ const Variant* heuristic(const Problem& p, Op op) {
         const Variant* v = by_name(name);
         if (v && gemv_stream_supports(*v, p)) return v;
     }
+    if (p.M >= 5 && p.M <= 11 && p.K > 2048 && p.K < 4096 && p.K % 1024 != 0 && p.N >= 8192) {
+        // the same with whole rows below K = 4096 (6 / 8 / 11 x 3584 x 18944
+        // in 23.4 / 28.2 / 39.6 us against 38.9 / 49.9 / 66.9 on the
+        // vector-ALU GEMV; with fewer rows, 6 x 3584 x 4608, that one stays
+        // ahead: 12.1 against 13.2)
+        const Variant* v = by_name("stream_m4x_d1q_g1");
+        if (v && gemv_stream_supports(*v, p)) return v;
+    }
     if (const Variant* v = skinny_heuristic(p)) return v;
     if (const Variant* v = split_k_heuristic(p, op)) return v;
     // one K slice of 2048 or 1024 (K that no split fits)
@@ -726,8 +767,11 @@ const Variant* heuristic(const Problem& p, Op op) {
     // the vector-ALU GEMV; 8 tokens 40.4 / 50.0 against 32.7 / 50.8)
     if (p.M >= 12)
         if (const Variant* v = cheapest_tiles(p, kTiles)) return v;
-    if (p.M == 2) return by_name("gemv_r4_t2_k1");
-    return by_name(p.M >= 8 ? "gemv_r4_t2_k1" : "gemv_r4_t4_k1");
+    // the vector-ALU GEMV one token per pass from 3 tokens (measured on
+    // MI355X: 3 / 5 / 11 x 18944 x 3584 in 24.8 / 36.3 / 66.9 us against 28.3
+    // / 39.8 / 72.6 with two tokens per pass and 58.6 at 5 with four; 8 x
+    // 3584 x 4608: 14.6 against 16.0)
+    return by_name(p.M == 2 ? "gemv_r4_t2_k1" : "gemv_r4_t1_k1");
 }
 
 hipError_t time_variant(const Variant& v, const Problem& p, float* ms) {

@@ -268,10 +268,10 @@ hipError_t launch_gemv_stream(const Problem& p) {
     return hipGetLastError();
 }
 
-// 5-16 tokens as passes of at most four tokens each (rows split over S
-// waves), every pass reading the weights once: for K with no split-K slicing
-// (K % 1024 != 0, e.g. 11 008, 13 824), where the alternatives are the
-// vector-ALU GEMV or the prefill tiles.
+// 5-16 tokens as passes of at most four tokens each (rows whole, S = 1, or
+// split over S waves), every pass reading the weights once: for K with no
+// split-K slicing (K % 1024 != 0, e.g. 3584, 11 008, 13 824), where the
+// alternatives are the vector-ALU GEMV or the prefill tiles.
 template <int S, class F>
 hipError_t launch_gemv_stream_groups(const Problem& p) {
     const size_t out_bytes = p.out == OutType::F32 ? 4 : 2;
@@ -350,6 +350,7 @@ const Variant kStream[] = {
     // tokens = -4: 5-16 tokens in passes of four
     Variant{"q8_stream_s2_m4x_d1q_g1", Kind::Q8Stream, 2, 1, 1, &launch_gemv_stream_groups<2, FmtQ8>, -4},
     Variant{"q8_stream_s4_m4x_d1q_g1", Kind::Q8Stream, 4, 1, 1, &launch_gemv_stream_groups<4, FmtQ8>, -4},
+    Variant{"stream_m4x_d1q_g1", Kind::GemvStream, 1, 1, 1, &launch_gemv_stream_groups<1, FmtQ4>, -4},
     Variant{"stream_s2_m4x_d1q_g1", Kind::GemvStream, 2, 1, 1, &launch_gemv_stream_groups<2, FmtQ4>, -4},
     Variant{"stream_s4_m4x_d1q_g1", Kind::GemvStream, 4, 1, 1, &launch_gemv_stream_groups<4, FmtQ4>, -4}, MOTE_Q8_M(2, 1), MOTE_Q8_M(4, 1),
     MOTE_STREAM_GU(1, 1), MOTE_STREAM_GU(1, 2),

@@ -74,6 +74,26 @@ LINEAR = [
     ((256, 14336, 4096), "mfma_x32s_m64_n64_w2_k4"),
     ((512, 4096, 14336), "mfma_x32s_m128_n256_w1_k2"),
     ((256, 4160, 14336), "mfma_x32s_m128_n128_w1"),  # 65 block pairs: one pair per step
+    # 3-4 tokens at 2048 < K < 4096: each row read once for all tokens
+    ((3, 3072, 8192), "stream_m3_d1_g1"),
+    ((4, 3584, 18944), "stream_m4_d1_g1"),
+    # 5-11 tokens at K = 3584 (no K slicing): passes of four tokens on wide N,
+    # the one-token-per-pass vector-ALU GEMV on narrow N and past K = 16384
+    ((6, 3584, 18944), "stream_m4x_d1q_g1"),
+    ((11, 3584, 18944), "stream_m4x_d1q_g1"),
+    ((6, 3584, 4608), "gemv_r4_t1_k1"),
+    ((3, 18944, 3584), "gemv_r4_t1_k1"),
+    ((5, 18944, 3584), "gemv_r4_t1_k1"),
+    # K = 8192 on narrow N: parts of 2048, 4 items per workgroup
+    ((4, 8192, 3072), "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l4_c_w_sk"),
+    ((16, 8192, 8192), "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w_sk"),
+    ((32, 8192, 2048), "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l4_c_w_sk"),
+    ((48, 8192, 2048), "skinny_mfma_k8_s1_t2_d1_g1_r1_tr_l4_c_w_sk"),
+    ((64, 8192, 3072), "skinny_mfma_k8_s1_t2_d1_g1_r1_tr_l8_c_w_sk"),
+    # 160 64 x 64 tiles past K = 4096 (the 70B fused q/k/v)
+    ((48, 8192, 10240), "mfma_x32s_m64_n64_w2_k4"),
+    ((64, 4096, 11008), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l8_c_w"),
+    ((64, 3072, 8192), "mfma_x32s_m64_n64_w2_k4"),
 ]
 
 

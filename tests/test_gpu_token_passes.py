@@ -1,6 +1,7 @@
 """GPU parity of the streaming GEMV run as passes of up to four tokens
-(`stream_s<S>_m4x_d1q_g1`, `q8_stream_s<S>_m4x_d1q_g1`: 5-16 tokens, rows
-split over S waves, for K with no split-K slicing such as 11 008 and 13 824).
+(`stream_m4x_d1q_g1`, `stream_s<S>_m4x_d1q_g1`, `q8_stream_s<S>_m4x_d1q_g1`:
+5-16 tokens, rows whole or split over S waves, for K with no split-K slicing
+such as 3584, 11 008 and 13 824).
 
 Each pass computes its tokens exactly as the one-token split-row GEMV does (the
 operands of a pair are unpacked once and fed to every token's dot chain in
@@ -23,20 +24,22 @@ from test_gpu_q4_0 import check_against_oracle, normal_x, run_linear, sample_col
 pytestmark = pytest.mark.gpu
 
 CASES = [(5, 300, 11008), (6, 257, 13824), (7, 64, 8320), (8, 4096, 11008), (9, 130, 5376), (12, 33, 16384),
-         (16, 700, 13824), (6, 96, 6144), (13, 40, 7424), (8, 1000, 8192)]
+         (16, 700, 13824), (6, 96, 6144), (13, 40, 7424), (8, 1000, 8192),
+         (5, 300, 3584), (7, 129, 2560), (9, 1000, 3584), (16, 64, 4096)]
 
 
 def _split(variant: str) -> int:
-    return int(re.search(r"_s(\d+)_m4x_", variant).group(1))
+    m = re.search(r"_s(\d+)_m4x_", variant)
+    return int(m.group(1)) if m else 1
 
 
-@pytest.mark.parametrize("variant", ["stream_s2_m4x_d1q_g1", "stream_s4_m4x_d1q_g1"])
+@pytest.mark.parametrize("variant", ["stream_m4x_d1q_g1", "stream_s2_m4x_d1q_g1", "stream_s4_m4x_d1q_g1"])
 def test_q4_0_token_passes(stream, oracle, variant):
     split = _split(variant)
     d = ops.Q4_0Dispatch()
     d.force(variant)
     one = ops.Q4_0Dispatch()
-    one.force("stream_s4_d1q_g1" if split == 4 else "stream_s2_d1_g1")
+    one.force({1: "stream_d1q_g1", 2: "stream_s2_d1_g1", 4: "stream_s4_d1q_g1"}[split])
     for m, n, k in CASES:
         if not (4096 * (split // 2) < k <= 4096 * split):
             continue

@@ -58,10 +58,10 @@ def test_two_calls_in_a_row_second_smaller(stream, oracle):
 
 
 def test_partial_tiles_beyond_the_array_are_rejected_before_launch(stream):
-    """64 tokens x N = 12288 x K = 32768 on the split-K tiles (eight K parts
-    of 4096; fewer than 200 64 x 64 tiles, so no prefill tiles) needs 64 x
-    12288 x 8 x 4 bytes = 24 MiB > 16 MiB: status 2, output untouched."""
-    m, n, k = 64, 12288, 32768
+    """64 tokens x N = 9216 x K = 32768 on the split-K tiles (eight K parts
+    of 4096; 144 64 x 64 tiles, too few for the prefill tiles) needs 64 x
+    9216 x 8 x 4 bytes = 18 MiB > 16 MiB: status 2, output untouched."""
+    m, n, k = 64, 9216, 32768
     d = ops.Q4_0Dispatch()
     assert d.select(m, n, k).endswith("_sk")
     xb, wb = DeviceBuffer(m * k * 2), DeviceBuffer(n * (k // 32) * 18)
