@@ -327,9 +327,9 @@ const Variant* split_k_heuristic(const Problem& p, Op op) {
         // 32 tokens, and above 16 where the 16-token items exceed 4096 (32 x
         // 5120 x 13824: 48.6 us against 55.5; 32 x 5120 x 5120, 3200 items:
         // 24.1 us against 27.4; 48 / 64 x 5120 x 5120: 32.0 / 33.2 us, where
-        // the 16 x 16 prefill tiles took 68.6)
+        // the 16 x 16 prefill tiles took 68.6; 32 x 2048 x 8192: 14.0 against 16.0)
         const uint64_t items1k = static_cast<uint64_t>((p.N + 15) / 16) * ((p.M + 15) / 16) * (p.K / 1024);
-        const bool t2 = op == Op::GateUp && (p.M > 32 || (p.M > 16 && items1k > 4096));
+        const bool t2 = op == Op::GateUp && (p.M > 32 || (p.M > 16 && (items1k > 4096 || p.K == 2048)));
         const char* name = op == Op::LinearQ8 ? (t2 ? "q8_skinny_k4_s1_t2_d1_l8_c_w_sk" : "q8_skinny_k4_s1_t1_d1_l8_c_w_sk")
                            : op == Op::GateUp ? (t2 ? "gateup_skinny_k4_s1_t2_d1_l8_c_w_sk" : "gateup_skinny_k4_s1_t1_d1_l8_c_w_sk")
                                               : (t2 ? "skinny_mfma_k4_s1_t2_d1_g1_r1_tr_l8_c_w_sk"
@@ -456,11 +456,13 @@ const Variant* heuristic(const Problem& p, Op op) {
             const Variant* v = by_name(name);
             if (v && gemv_stream_supports(*v, p)) return v;
         }
-        if (fast && p.M >= 5 && p.M <= 16 && p.K > 4096 && p.K <= 16384 && p.K % 1024 != 0) {
+        if (fast && p.M >= 5 && p.M <= 16 && p.K > 2048 && p.K <= 16384 && p.K % 1024 != 0) {
             // 5-16 tokens where K takes no split-K slicing: passes of up to
             // four tokens on the split-row streaming GEMV (a four-token pass
             // at 11008 x 4096 in 14.9 us; 8 tokens took 76.3 us on the
-            // prefill tiles and 89.5 us on the generic kernel)
+            // prefill tiles and 89.5 us on the generic kernel; rows split 2
+            // ways also below K = 4096: 6 / 8 x 3584 x 4608 in 18.2 / 21.4 us
+            // against 27.9 on the prefill tiles)
             char name[40];
             std::snprintf(name, sizeof name, "q8_stream_s%u_m4x_d1q_g1", p.K > 8192 ? 4u : 2u);
             const Variant* v = by_name(name);
@@ -494,7 +496,9 @@ const Variant* heuristic(const Problem& p, Op op) {
         }
         // tokens with no K slicing (K % 1024 != 0, e.g. 11 008, 13 824): the
         // prefill tiles, where K allows their multi-pair steps
-        if (fast && p.M >= 4)
+        // (past K = 16384 the generic kernel: 4 / 6 x 18944 x 3584 in 69 /
+        // 102 us against 127 us on the tiles)
+        if (fast && p.M >= 4 && p.K <= 16384)
             if (const Variant* v = cheapest_tiles(p, kQ8Tiles)) return v;
         return by_name("q8_generic");
     }
@@ -502,7 +506,7 @@ const Variant* heuristic(const Problem& p, Op op) {
         // Up to 64 tokens the skinny gate/up; above, the prefill tiles with
         // raw Q4_0 weights staged in LDS (measured on MI355X at N = 14336,
         // K = 4096: 1.4x-1.8x faster than dequantised f16 weight tiles).
-        if (fast && (p.M == 1 || p.M == 2 || (p.M == 3 && p.K > 4096 && p.K <= 16384))) {
+        if (fast && (p.M == 1 || p.M == 2 || (p.M == 3 && p.K > 2048 && p.K <= 16384 && p.K != 4096))) {
             // One or two tokens: the streaming GEMV reading both rows per
             // step (and, for two tokens, each row once for both), rows split
             // over S waves past K = 4096 (measured on MI355X: one token,
@@ -512,7 +516,10 @@ const Variant* heuristic(const Problem& p, Op op) {
             // 21.7 us on the skinny tiles; three tokens for 4096 < K <=
             // 16384, rows split up to 4 ways, 8192 x 28672 in 54.4 us against
             // 65.4 us).
-            uint32_t split = 1;
+            // (three tokens at 2048 < K < 4096 with rows split 2 ways: 3 x
+            // 3584 x 18944 in 35.2 us, where the generic kernel took 89.1; 3
+            // x 3072 x 8192 16.5 against 18.6 split K)
+            uint32_t split = p.M == 3 ? 2 : 1;
             while (split < 8 && p.K > 4096u * split) split *= 2;
             char name[40];
             if (split == 1)
@@ -531,13 +538,20 @@ const Variant* heuristic(const Problem& p, Op op) {
             if (v && prefill_supports(*v, p)) return v;
         }
         if (fast && p.M > 32 && p.M <= 64 && prefill_tiles(p, 64, 128) < 200 &&
-            prefill_tiles(p, 64, 64) >= (p.M > 48 ? 160u : 200u)) {
+            (prefill_tiles(p, 64, 64) >= (p.M > 48 ? 160u : 200u) || (p.M > 48 && p.K < 4096))) {
             // 33-64 tokens where 64 x 128 tiles are too few: 64 x 64 tiles of
             // 2 x 2 waves, 4 block pairs per step (64 x 4096 x 14 336: 30.8
             // us, against 35.6 us on the skinny tiles; 64 x 5120 x 13824: 39.9
             // us, where 48 tokens took 71.8 us on the 16 x 16 tiles; 64 x 4096
-            // x 11008, 172 tiles: 29.1 us against 31.7 on the skinny tiles)
-            const Variant* v = by_name("gateup_mfma_x32s_m64_n64_w2_k4");
+            // x 11008, 172 tiles: 29.1 us against 31.7 on the skinny tiles;
+            // below K = 4096, where the skinny tiles split K in parts of
+            // 1024, 64 x 2048 / 3072 x 8192 in 16.5 / 22.4 us against 23.3 /
+            // 33.8).  Where the 64 x 64 tiles would take two dispatch waves
+            // and the 64 x 128 tiles one, the latter (64 x 3584 x 18944: 40.4
+            // us against 53.5)
+            const bool two_waves = prefill_tiles(p, 64, 64) > static_cast<uint64_t>(device_cus());
+            const Variant* v = two_waves ? deepest_step("gateup_mfma_x32s_m64_n128_w1", p, 4)
+                                         : by_name("gateup_mfma_x32s_m64_n64_w2_k4");
             if (v && prefill_supports(*v, p)) return v;
         }
         if (fast && p.M <= 64) {

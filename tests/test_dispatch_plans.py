@@ -186,3 +186,18 @@ def test_forced_variant_and_bad_shapes(d):
     for shape in [(0, 1, 32), (1, 0, 32), (1, 1, 0), (1, 1, 33)]:
         with pytest.raises(HipError):
             d.select(*shape)
+
+
+def test_plans_below_k_4096_and_past_16384(d):
+    """Gate/up: three tokens at 2048 < K < 4096 on the stream with rows split
+    2 ways (K = 4096 keeps the one-slice skinny tiles), 49-64 tokens below K =
+    4096 on 64 x 64 tiles, 32-token items at K = 2048 above 16 tokens.  Q8_0:
+    5-16 tokens at K = 3584 as four-token passes, and past K = 16384 with no K
+    slicing the generic kernel rather than the tiles."""
+    assert d.select(3, 18944, 3584, gate_up=True) == "gateup_stream_s2_m3_d1q_g1"
+    assert d.select(3, 14336, 4096, gate_up=True).startswith("gateup_skinny_k16_")
+    assert d.select(64, 8192, 3072, gate_up=True) == "gateup_mfma_x32s_m64_n64_w2_k4"
+    assert d.select(32, 8192, 2048, gate_up=True) == "gateup_skinny_k4_s1_t2_d1_l8_c_w_sk"
+    assert d.select(64, 18944, 3584, gate_up=True).startswith("gateup_mfma_x32s_m64_n128_w1")
+    assert d.select(6, 4608, 3584, q8_0=True) == "q8_stream_s2_m4x_d1q_g1"
+    assert d.select(4, 3584, 18944, q8_0=True) == "q8_generic"
