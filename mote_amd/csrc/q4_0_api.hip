@@ -376,7 +376,12 @@ const Variant* split_k_heuristic(const Problem& p, Op op) {
         // items and 8; 48 / 64 tokens, 1024 items, 4 per workgroup; N = 3072,
         // 48 / 64 tokens, 1536 items, 13.7 / 14.5 us with 8 against 15.3 /
         // 15.4 for the 2-step items)
-        if (!k4)
+        // (other K: 16-token items at 33-48 tokens and past 4096 rows, 32 / 48 x
+        // 14336 x 5120 in 21.8 / 28.7 us against 24.7 / 36.6, 48 x 14336 x
+        // 3584 21.6 against 25.6)
+        if (!k4 && (p.M > 32 ? p.M <= 48 : p.N > 4096))
+            name = "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l4_c_w_sk";
+        else if (!k4)
             name = p.M > 32 ? "skinny_mfma_k8_s1_t2_d1_g1_r1_tr_l8_c_w_sk" : "skinny_mfma_k8_s1_t2_d1_g1_r1_tr_l4_c_w_sk";
         else if (p.M <= 32 && items2k_t2 <= 512)
             name = "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l4_c_w_sk";
@@ -395,7 +400,9 @@ const Variant* split_k_heuristic(const Problem& p, Op op) {
                : items2k > 4 * 512  ? "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l8_c_w_sk"
                                     : "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l4_c_w_sk";
     } else {
-        name = items2k > 4 * 512 ? "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l8_c_w_sk"
+        // 4 items per workgroup up to 4096 items (4 / 16 x 14336 x 5120, 2240
+        // items: 13.9 / 15.8 us against 18.6 / 20.2 with 8)
+        name = items2k > 8 * 512 ? "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l8_c_w_sk"
                                  : "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l4_c_w_sk";
     }
     const Variant* v = by_name(name);

@@ -94,6 +94,9 @@ LINEAR = [
     ((48, 8192, 10240), "mfma_x32s_m64_n64_w2_k4"),
     ((64, 4096, 11008), "skinny_mfma_k8_s2_t2_d1_g1_r1_tr_l8_c_w"),
     ((64, 3072, 8192), "mfma_x32s_m64_n64_w2_k4"),
+    # K = 14336 on 5120 / 3584 rows: 16-token items, 4 per workgroup
+    ((4, 14336, 5120), "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l4_c_w_sk"),
+    ((48, 14336, 3584), "skinny_mfma_k8_s1_t1_d1_g1_r1_tr_l4_c_w_sk"),
 ]
 
 
