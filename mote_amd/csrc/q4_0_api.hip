@@ -450,8 +450,10 @@ const Variant* heuristic(const Problem& p, Op op) {
             // 1024 != 0): rows split over S waves as for two and three
             // (also where split K would take parts of 1024, K % 2048 != 0:
             // 4 x 5120 x 5120 in 10.9 us against 12.7, x 13824 21.1 against
-            // 24.8)
-            const bool m4_split = p.M == 4 && split > 1 && split <= 4 && p.K % 2048 != 0;
+            // 24.8; and at 8192 < K <= 16384 whatever K's slicing: 4 x 14336 x
+            // 4096 / 5120 / 6144 in 15.7 / 18.2 / 21.0 us against 17.5 / 24.7 /
+            // 27.5 on the split-K tiles)
+            const bool m4_split = p.M == 4 && split > 1 && split <= 4 && (p.K % 2048 != 0 || split == 4);
             if (((p.M == 2 || p.M == 3) && split > 1) || m4_split)  // 3 x 8192 x 8192: 15.2 us (split-K tiles 17.6)
                 std::snprintf(name, sizeof name, "q8_stream_s%u_m%u_d1q_g1", split, p.M);
             else if (p.M > 1)

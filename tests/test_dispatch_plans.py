@@ -204,3 +204,4 @@ def test_plans_below_k_4096_and_past_16384(d):
     assert d.select(64, 18944, 3584, gate_up=True).startswith("gateup_mfma_x32s_m64_n128_w1")
     assert d.select(6, 4608, 3584, q8_0=True) == "q8_stream_s2_m4x_d1q_g1"
     assert d.select(4, 3584, 18944, q8_0=True) == "q8_generic"
+    assert d.select(4, 4096, 14336, q8_0=True) == "q8_stream_s4_m4_d1q_g1"
