@@ -137,7 +137,8 @@ int mote_hip_dequantize_q6_k_f32(const void* weights, void* output, uint64_t row
  * (crates/mote-backend-hip/src/hipblaslt_shim.cpp:326-408): create / destroy
  * / last_error, a mutex-guarded map from (M, N, K, op, output type) to the
  * kernel variant, chosen on first use by a shape heuristic or, with autotune
- * on, by timing every eligible variant on the caller's stream.  Statuses are
+ * on, by timing every eligible variant and the heuristic's own pick on the
+ * caller's stream.  Statuses are
  * hipError_t values; on failure last_error describes the cause. */
 int mote_q4_0_dispatch_create(void** handle);
 void mote_q4_0_dispatch_destroy(void* handle);
