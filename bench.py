@@ -24,7 +24,11 @@ entry point ``mote_hip_quantized_linear_q4_0_f32`` of ``libmote_hip.so``.
   kernel durations of a rocprofv3 kernel trace).
 * ``roofline.traffic`` is the HBM traffic per launch measured by rocprofv3
   counters, read from the committed summary under ``profiles/`` (null when
-  absent).
+  absent); the line says so in ``roofline.traffic_source``.
+* ``reference_statistics`` (and ``kernel_us_median`` / ``kernel_us_spread_pct``)
+  are the reference benchmark's statistics: 5 warm-ups, 9 samples of 20
+  calls, median and spread (max - min) / median, each sample one replay of a
+  graph of 20 captured calls timed by events on the launch stream.
 * ``cpu_baseline`` times the single-threaded C restatement of the reference's
   CPU oracle (``quantized_linear_f32``, crates/mote-reference/src/
   quantized.rs:89-144) on the same inputs for a bounded number of calls, and
@@ -209,6 +213,57 @@ def time_case(case: LinearCase, stream: Stream, hip: HipRuntime, steps: int, war
         "kernel_ms_mean": gpu_ms / calls,
         "eager_ms_per_step": eager_wall_s * 1e3 / steps,
         "eager_gpu_ms_per_step": eager_gpu_ms / steps,
+    }
+
+
+REF_WARMUPS, REF_SAMPLES, REF_BATCH = 5, 9, 20
+
+
+def reference_statistics(case: LinearCase, stream: Stream, hip: HipRuntime) -> dict:
+    """The reference benchmark's statistics (crates/mote-backend-hip/benches/
+    quantized_linear.rs:14-16,51-62): 5 warm-ups, then 9 samples of 20 calls,
+    the median µs per call and the spread (max - min) / median.  Here the 20
+    calls of a sample are one replay of a captured graph (rotating weight
+    copies, as every call of this benchmark), timed by HIP events on the launch
+    stream; the host clock around the same replay (synchronised, as the
+    reference's Instant pair) is reported beside it."""
+    exe = hip.capture(stream, lambda: [case.launch(i, stream) for i in range(REF_BATCH)])
+    start, stop = hip.create(), hip.create()
+    try:
+        t0 = time.perf_counter()
+        while True:  # the same settling as the timed replays of time_case
+            hip.launch_graph(exe, stream)
+            stream.synchronize()
+            if time.perf_counter() - t0 >= SETTLE_S:
+                break
+        for _ in range(REF_WARMUPS):
+            hip.launch_graph(exe, stream)
+        stream.synchronize()
+        dev, host = [], []
+        for _ in range(REF_SAMPLES):
+            t0 = time.perf_counter()
+            hip.record(start, stream)
+            hip.launch_graph(exe, stream)
+            hip.record(stop, stream)
+            stream.synchronize()
+            host.append((time.perf_counter() - t0) * 1e6 / REF_BATCH)
+            dev.append(hip.elapsed_ms(start, stop) * 1e3 / REF_BATCH)
+    finally:
+        hip.destroy_graph(exe)
+        hip.destroy(start)
+        hip.destroy(stop)
+    dev.sort()
+    host.sort()
+    med, hmed = dev[REF_SAMPLES // 2], host[REF_SAMPLES // 2]
+    return {
+        "warmups": REF_WARMUPS, "samples": REF_SAMPLES, "calls_per_sample": REF_BATCH,
+        "kernel_us_median": round(med, 3),
+        "kernel_us_min": round(dev[0], 3),
+        "kernel_us_max": round(dev[-1], 3),
+        "spread_pct": round((dev[-1] - dev[0]) / med * 100.0, 2),
+        "host_us_median": round(hmed, 3),
+        "host_spread_pct": round((host[-1] - host[0]) / hmed * 100.0, 2),
+        "clock": "HIP events on the launch stream around one graph replay of 20 captured calls per sample",
     }
 
 
@@ -693,6 +748,7 @@ def main() -> int:
           f"({case.copies * case.w.nbytes / 1e6:.0f} MB), warmup {args.warmup}, steps {args.steps}",
           file=sys.stderr, flush=True)
     t = time_case(case, stream, hip, args.steps, args.warmup)
+    stats = reference_statistics(case, stream, hip)
     nbytes = case.algorithmic_bytes()
     value = nbytes / (t["ms_per_step"] * 1e-3) / 1e9
     achieved = nbytes / (t["kernel_ms_mean"] * 1e-3) / 1e9
@@ -712,6 +768,9 @@ def main() -> int:
         "ms_per_step": round(t["ms_per_step"], 6),
         "us_per_call": round(t["ms_per_step"] * 1e3, 3),
         "kernel_us": round(t["kernel_ms_mean"] * 1e3, 3),
+        "kernel_us_median": stats["kernel_us_median"],
+        "kernel_us_spread_pct": stats["spread_pct"],
+        "reference_statistics": stats,
         "eager_us_per_call": round(t["eager_ms_per_step"] * 1e3, 3),
         "issue": "HIP graph of `steps` captured C-ABI calls, replayed 3 times",
         "higher_is_better": True,
@@ -735,6 +794,9 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": read_traffic(),
+            "traffic_source": ("rocprofv3 FETCH_SIZE + WRITE_SIZE passes of this workload, copy-calibrated, "
+                               "read from profiles/q4_0_gemv_m1_k4096_n14336_traffic.md (not measured in "
+                               "this run)"),
         },
         "cpu_baseline": cpu,
     }

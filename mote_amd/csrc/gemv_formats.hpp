@@ -25,6 +25,68 @@ struct XPair {
     float c0, c1;  // start values of the two blocks' sums (format's kStart times sum of x)
 };
 
+// ---------------------------------------------------------------------------
+// Rows whose sum is not finite.
+//
+// The dot chains below multiply a block's scale into the block's sum,
+// d * sum x (n - 8); the reference multiplies it into every element first,
+// v = (n - 8) d, and then sums x v (crates/mote-reference/src/quantized.rs:
+// 181,187-188; Q8_0 v d at :191-195).  For finite scales and activations the
+// two agree to rounding: no intermediate of either can overflow (|x v| <=
+// 65504 * 128 * 65504 per element).  They part only when a scale is infinite
+// or an activation is not finite: with d = inf the reference's v is NaN for
+// n = 8 and x v is NaN for x = 0, and products of both signs give
+// inf - inf = NaN, where d * sum is +-inf unless the sum is 0.  In every such
+// case the factored sum is itself not finite, so a wave whose reduced row (or
+// row-slice) sum is not finite -- a test of the wave-uniform value on the
+// scalar unit -- recomputes its share of the row element by element with the
+// reference's operations (exact_pair below), and the NaN and infinities land
+// where the reference puts them.  Ordinary weights never take that branch.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool not_finite(float v) {
+    return (__builtin_bit_cast(uint32_t, v) & 0x7F800000u) == 0x7F800000u;
+}
+
+__device__ __forceinline__ float f16_bits_to_float(uint16_t bits) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+}
+
+// sum over the 64 elements of the Q4_0 block pair at `pair` (global memory,
+// 2-byte aligned) of x * ((n - 8) d), each product and sum in f32: the
+// reference's per-element arithmetic.  Rolled loops: the code only runs for
+// rows that hold a non-finite scale or activation.
+__device__ inline float q4_0_exact_pair(const uint8_t* pair, const uint16_t* x) {
+    float acc = 0.0f;
+#pragma unroll 1
+    for (int b = 0; b < 2; ++b) {
+        const uint8_t* blk = pair + 18 * b;
+        const float d = f16_bits_to_float(*reinterpret_cast<const uint16_t*>(blk));
+#pragma unroll 1
+        for (int j = 0; j < 16; ++j) {
+            const uint32_t q = blk[2 + j];
+            const float lo = static_cast<float>(static_cast<int>(q & 15u) - 8) * d;
+            const float hi = static_cast<float>(static_cast<int>(q >> 4) - 8) * d;
+            acc += f16_bits_to_float(x[32 * b + j]) * lo;
+            acc += f16_bits_to_float(x[32 * b + 16 + j]) * hi;
+        }
+    }
+    return acc;
+}
+
+// The same for a Q8_0 block pair (two 34-byte blocks, value v d).
+__device__ inline float q8_0_exact_pair(const uint8_t* pair, const uint16_t* x) {
+    float acc = 0.0f;
+#pragma unroll 1
+    for (int b = 0; b < 2; ++b) {
+        const uint8_t* blk = pair + 34 * b;
+        const float d = f16_bits_to_float(*reinterpret_cast<const uint16_t*>(blk));
+#pragma unroll 1
+        for (int j = 0; j < 32; ++j)
+            acc += f16_bits_to_float(x[32 * b + j]) * (static_cast<float>(static_cast<int8_t>(blk[2 + j])) * d);
+    }
+    return acc;
+}
+
 // Operands of a pair unpacked once and shared by every token of a row.
 struct Unpacked {
     uint32_t u[32];
@@ -50,6 +112,8 @@ struct FmtQ4 {
     static constexpr float kStart = -8.0f / 1048576.0f;   // times the block's sum of x
 
     __device__ static void load(const uint8_t* p, uint32_t (&d)[kDwords]) { load_pair(p, d); }
+
+    __device__ static float exact(const uint8_t* pair, const uint16_t* x) { return q4_0_exact_pair(pair, x); }
 
     // x of the pair (64 halves in xr) in the order the nibble operands take it.
     __device__ static void order_x(const uint32_t (&xr)[32], XPair& xv) {
@@ -146,6 +210,8 @@ struct FmtQ8 {
     static constexpr float kStart = -128.0f / 16777216.0f;  // times the block's sum of x
 
     __device__ static void load(const uint8_t* p, uint32_t (&d)[kDwords]) { load_pair_q8(p, d); }
+
+    __device__ static float exact(const uint8_t* pair, const uint16_t* x) { return q8_0_exact_pair(pair, x); }
 
     // Dword i of the pair's 64 bytes (elements 4i .. 4i + 3) takes x as
     // (x[4i], x[4i + 2]) for bytes 0 and 2 and (x[4i + 1], x[4i + 3]) for 1, 3.

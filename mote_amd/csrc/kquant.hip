@@ -94,6 +94,65 @@ __device__ __forceinline__ u32x4 load16_a2(const uint8_t* p) {
 }
 
 // ---------------------------------------------------------------------------
+// Rows whose sum is not finite.  The linears below fold a sub-block's scale
+// and min into sums over its elements (d sc sum x q - dmin m sum x); GGML's
+// definition, which the oracle follows, rounds every element's value first
+// (d1 = d sc, m1 = dmin m, then d1 q - m1 for Q4_K; (d sc)(q - 32) for
+// Q6_K) and sums x times that.  With finite scales and activations neither
+// form can overflow, so they agree to rounding; an infinite or NaN scale (or
+// a non-finite activation) makes the folded sum not finite, and then it can
+// put +-inf where the per-element values give NaN (inf * 0 for q = 0 or
+// sc = 0, products of both signs).  A wave whose reduced sum is not finite (a
+// wave-uniform test) recomputes its share of the row element by element, so
+// the NaN and infinities land where the definition puts them.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool not_finite(float v) {
+    return (__builtin_bit_cast(uint32_t, v) & 0x7F800000u) == 0x7F800000u;
+}
+
+// GGML's value of element e (0..255) of the super-block at `blk` (global
+// memory), with the oracle's f32 rounding points.
+template <Fmt F>
+__device__ inline float kq_value(const uint8_t* blk, uint32_t e) {
+    if constexpr (F == Fmt::Q4K) {
+        const uint32_t p = e >> 6, h = (e >> 5) & 1u, l = e & 31u, j = 2 * p + h;
+        const uint8_t* sb = blk + 4;
+        uint32_t sc, m;
+        if (j < 4) {
+            sc = sb[j] & 63u;
+            m = sb[j + 4] & 63u;
+        } else {
+            sc = (sb[j + 4] & 15u) | ((sb[j - 4] >> 6) << 4);
+            m = (sb[j + 4] >> 4) | ((sb[j] >> 6) << 4);
+        }
+        const float d1 = half_bits_to_float(blk[0] | (blk[1] << 8)) * static_cast<float>(sc);
+        const float m1 = half_bits_to_float(blk[2] | (blk[3] << 8)) * static_cast<float>(m);
+        const uint32_t byte = blk[16 + 32 * p + l];
+        const float prod = d1 * static_cast<float>(h ? byte >> 4 : byte & 15u);
+        return prod - m1;
+    } else {
+        const uint32_t g = e >> 7, c = (e >> 5) & 3u, l = e & 31u;
+        const uint32_t low = blk[64 * g + 32 * (c & 1u) + l] >> (4 * (c >> 1)) & 15u;
+        const uint32_t high = (blk[128 + 32 * g + l] >> (2 * c)) & 3u;
+        const float ds = half_bits_to_float(blk[208] | (blk[209] << 8)) *
+                         static_cast<float>(static_cast<int8_t>(blk[192 + e / 16]));
+        return ds * static_cast<float>(static_cast<int>(low | (high << 4)) - 32);
+    }
+}
+
+// The wave's sum of x[k] * w[k] over blocks [b_begin, b_end) of the row at
+// `row`, lanes over elements, with GGML's per-element values (rolled loop:
+// it runs only for rows holding a non-finite scale or activation).
+template <Fmt F>
+__device__ inline float kq_exact_blocks(const uint8_t* row, const uint16_t* xrow, uint32_t b_begin, uint32_t b_end) {
+    constexpr uint32_t BB = block_bytes<F>();
+    float e = 0.0f;
+    for (uint32_t k = b_begin * kSuper + (threadIdx.x & 63u); k < b_end * kSuper; k += 64u)
+        e += half_bits_to_float(xrow[k]) * kq_value<F>(row + static_cast<size_t>(k / kSuper) * BB, k % kSuper);
+    return wave_sum(e);
+}
+
+// ---------------------------------------------------------------------------
 // Decode: one thread per 16 consecutive elements of a super-block.
 // ---------------------------------------------------------------------------
 template <bool VEC>
@@ -386,7 +445,10 @@ __global__ __launch_bounds__(kGemvThreads) void kq_gemv_kernel(const uint16_t* _
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
                     if (m >= mt) break;
-                    const float s = wave_sum(acc[r][m]);
+                    float s = wave_sum(acc[r][m]);
+                    if (__builtin_expect(not_finite(s), 0))  // wave-uniform: the definition's per-element sum
+                        s = kq_exact_blocks<F>(w + static_cast<size_t>(n0 + r) * row_bytes,
+                                               x + static_cast<size_t>(m0 + m) * K, 0, K / kSuper);
                     if (lane == 0) y[static_cast<size_t>(m0 + m) * N + n0 + r] = to_out<OutT>(s);
                 }
             }
@@ -782,7 +844,12 @@ __global__ __launch_bounds__(kRingThreads) void kq_ring_kernel(const uint16_t* _
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
                 const float v = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, part_sum[m]) & keep);
-                const float tot = wave_sum(v);
+                float tot = wave_sum(v);
+                if (__builtin_expect(not_finite(tot), 0)) {  // wave-uniform: the definition's per-element sum
+                    const int mm = m < mt ? m : mt - 1;
+                    tot = kq_exact_blocks<F>(w + static_cast<size_t>(min(row_of(t), N - 1)) * row_bytes,
+                                             x + static_cast<size_t>(m0 + mm) * K, b0, b1);
+                }
                 mine[m] = lane == (t & 63u) ? tot : mine[m];
             }
             if ((t & 63u) == 63u || t + 1 == steps) {

@@ -37,9 +37,9 @@ enum class Op : int { Linear = 0, GateUp = 1, LinearQ8 = 2 };
 
 struct Key {
     uint32_t m, n, k;
-    int op, out, fast;
+    int op, out, align;  // align: align_class() of the operands
     bool operator<(const Key& o) const {
-        return std::tie(m, n, k, op, out, fast) < std::tie(o.m, o.n, o.k, o.op, o.out, o.fast);
+        return std::tie(m, n, k, op, out, align) < std::tie(o.m, o.n, o.k, o.op, o.out, o.align);
     }
 };
 
@@ -103,6 +103,19 @@ bool fast_eligible(const Problem& p) {
     return p.K % 64 == 0 && reinterpret_cast<uintptr_t>(p.w) % 4 == 0 &&
            reinterpret_cast<uintptr_t>(p.x) % 16 == 0 &&
            (p.w_up == nullptr || reinterpret_cast<uintptr_t>(p.w_up) % 4 == 0);
+}
+
+// The operands' alignment class, part of the plan key: 0 when only the
+// generic kernels run (K % 64 != 0, or weights off the 4-byte grid), 1 when
+// the kernels with dword weight loads run, 2 when the weights (both matrices
+// of a gate/up) and the activations also sit on the 16-byte grid that the
+// direct-to-LDS ring kernels load in 16-byte chunks.  A plan made for one
+// class is never reused for another.
+int align_class(const Problem& p) {
+    if (!fast_eligible(p)) return 0;
+    const bool a16 = reinterpret_cast<uintptr_t>(p.w) % 16 == 0 && reinterpret_cast<uintptr_t>(p.x) % 16 == 0 &&
+                     (p.w_up == nullptr || reinterpret_cast<uintptr_t>(p.w_up) % 16 == 0);
+    return a16 ? 2 : 1;
 }
 
 // Variants the autotuner may time: the matrix-core kernels only for M >= 64
@@ -828,8 +841,7 @@ int run(Dispatcher& d, const Problem& problem, Op op) {
             return fail(&d, hipErrorInvalidValue,
                         "forced Q4_0 variant '" + d.forced + "' cannot run this problem");
     } else {
-        const Key key{p.M, p.N, p.K, static_cast<int>(op), static_cast<int>(p.out),
-                      fast_eligible(p) ? 1 : 0};
+        const Key key{p.M, p.N, p.K, static_cast<int>(op), static_cast<int>(p.out), align_class(p)};
         auto found = d.plans.find(key);
         if (found == d.plans.end()) {
             const Variant* chosen = nullptr;
@@ -857,6 +869,10 @@ int run(Dispatcher& d, const Problem& problem, Op op) {
             found = d.plans.emplace(key, chosen).first;
         }
         v = found->second;
+        // the key's alignment class already implies this; checked again so
+        // that no launch ever runs outside its kernel's stated conditions
+        if (!supports(*v, p)) return fail(&d, hipErrorInvalidValue, std::string("cached plan ") + v->name +
+                                                                      " cannot run this problem");
     }
     const hipError_t err = v->launch(p);
     if (err != hipSuccess) return fail(&d, err, std::string("launch of ") + v->name + " failed");
@@ -876,7 +892,7 @@ int run_no_alloc(Dispatcher& d, const Problem& problem) {
         v = find_variant(d.forced);
         if (!v || !kind_matches(*v, Op::Linear) || !supports(*v, p)) return hipErrorInvalidValue;
     } else {
-        const Key key{p.M, p.N, p.K, static_cast<int>(Op::Linear), static_cast<int>(p.out), fast_eligible(p) ? 1 : 0};
+        const Key key{p.M, p.N, p.K, static_cast<int>(Op::Linear), static_cast<int>(p.out), align_class(p)};
         auto found = d.plans.find(key);
         if (found == d.plans.end()) {
             const Variant* chosen = heuristic(p, Op::Linear);
@@ -884,6 +900,7 @@ int run_no_alloc(Dispatcher& d, const Problem& problem) {
             found = d.plans.emplace(key, chosen).first;
         }
         v = found->second;
+        if (!supports(*v, p)) return hipErrorInvalidValue;  // as in run(): never outside the kernel's conditions
     }
     return static_cast<int>(v->launch(p));
 }

@@ -22,6 +22,7 @@
 // b % 8, so logical tile (b % 8) * per_xcd + b / 8 gives each XCD a contiguous
 // run of tiles, and the token chunks of one row tile share that XCD's L2.
 #include "common.hpp"
+#include "gemv_formats.hpp"
 #include "q4_0.hpp"
 
 namespace mote::q4_0 {
@@ -147,7 +148,21 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int t = 0; t < MT; ++t) sums[t * R + r] = wave_sum(acc[r][t]);
+        for (int t = 0; t < MT; ++t) {
+            float s = wave_sum(acc[r][t]);
+            // A sum that is not finite (an infinite scale or a non-finite
+            // activation): this wave's share of the row again with the
+            // reference's per-element arithmetic (gemv_formats.hpp), in the
+            // units of the dot chains.  Wave-uniform; ordinary rows skip it.
+            if (__builtin_expect(not_finite(s), 0)) {
+                float e = 0.0f;
+                for (uint32_t p = kg * kWave + lane; p < npairs; p += kWave * KSPLIT)
+                    e += q4_0_exact_pair(wrow[r] + static_cast<size_t>(p) * kPairBytes,
+                                         xrow[t] + static_cast<size_t>(p) * 64);
+                s = wave_sum(e) * (1.0f / 64.0f);
+            }
+            sums[t * R + r] = s;
+        }
 
     float mine = 0.0f;
 #pragma unroll

@@ -165,7 +165,12 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_kernel(const uint16_t* __re
         }
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            const float s = wave_sum(part[m]);
+            float s = wave_sum(part[m]);
+            if (__builtin_expect(not_finite(s), 0)) {  // wave-uniform: the reference's per-element sum
+                const uint8_t* pair = w + static_cast<size_t>(g + j * total_groups) * row_bytes + pc * F::kPairBytes;
+                const float e = keep != 0u ? F::exact(pair, x + static_cast<size_t>(m) * K + pc * 64u) : 0.0f;
+                s = wave_sum(e) * (1.0f / F::kFinal);
+            }
             mine[m] = static_cast<uint32_t>(lane) == (j & 63u) ? s : mine[m];
         }
         if ((j & 63u) == 63u || j + 1 == nrows) {
@@ -345,7 +350,13 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_split_kernel(const uint16_t
 #pragma unroll
         for (int i = 0; i < F::kDwords; ++i) raw[i] = pr[i];
         const float part = 0.0f + __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, F::dot(raw, xv)) & keep);
-        const float s = wave_sum(part);
+        float s = wave_sum(part);
+        if (__builtin_expect(not_finite(s), 0)) {  // wave-uniform: the reference's per-element sum of the slice
+            const uint32_t pi = first_pair + pc;
+            const uint8_t* pair = w + static_cast<size_t>(min(g + j * total_groups, last)) * row_bytes + pi * F::kPairBytes;
+            const float e = keep != 0u ? F::exact(pair, x + pi * 64u) : 0.0f;
+            s = wave_sum(e) * (1.0f / F::kFinal);
+        }
         mine = static_cast<uint32_t>(lane) == (j & 63u) ? s : mine;
         if ((j & 63u) == 63u) {  // uniform over the workgroup
             const uint32_t first = j - 63u;

@@ -25,6 +25,7 @@
 // Workgroup b runs on XCD b % 8; tile (b % 8) * per_xcd + b / 8 gives each XCD
 // a contiguous run of rows.
 #include "common.hpp"
+#include "gemv_formats.hpp"
 #include "q4_0.hpp"
 
 namespace mote::q4_0 {
@@ -33,12 +34,6 @@ namespace {
 constexpr int kRowsWaves = 8;
 constexpr int kRowsThreads = kRowsWaves * kWave;
 constexpr uint32_t kChunkSlot = 144;  // bytes of LDS per 128-byte pair chunk of x
-
-__device__ __forceinline__ uint32_t pick(const uint32_t* x, int a, int b) {
-    const uint32_t lo = (a & 1) ? 0x0302u : 0x0100u;
-    const uint32_t hi = (b & 1) ? 0x07060000u : 0x05040000u;
-    return __builtin_amdgcn_perm(x[b >> 1], x[a >> 1], hi | lo);
-}
 
 template <int R, int KS, typename OutT>
 __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(const uint16_t* __restrict__ x,
@@ -150,7 +145,17 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(const uint16_t*
         }
         float acc = __builtin_fmaf(d0, a0, 0.0f);
         acc = __builtin_fmaf(d1, a1, acc);
-        sums[r] = wave_sum(active ? acc : 0.0f);
+        float s = wave_sum(active ? acc : 0.0f);
+        // A sum that is not finite (an infinite scale or a non-finite
+        // activation): the wave's share of the row again with the reference's
+        // per-element arithmetic (gemv_formats.hpp).  Wave-uniform.
+        if (__builtin_expect(not_finite(s), 0)) {
+            const uint8_t* pair = w + static_cast<size_t>(min(row0 + r, N - 1)) * row_bytes +
+                                  static_cast<size_t>(pc) * kPairBytes;
+            const float e = active ? q4_0_exact_pair(pair, x + static_cast<size_t>(pc) * 64) : 0.0f;
+            s = wave_sum(e) * (1.0f / 64.0f);
+        }
+        sums[r] = s;
     }
 
     float mine = 0.0f;

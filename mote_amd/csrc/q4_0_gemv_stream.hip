@@ -178,6 +178,19 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
     float mine[MT], mine_up[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) mine[m] = mine_up[m] = 0.0f;
+    // The reference's per-element sum of this wave's share of row jj of `mat`
+    // for token m, in the units of the dot chains (a row whose factored sum
+    // is not finite; see gemv_formats.hpp).
+    auto exact_share = [&](const uint8_t* mat, uint32_t jj, int m) {
+        const uint8_t* row = mat + static_cast<size_t>(min(g + jj * total_groups, last)) * row_bytes;
+        float e = 0.0f;
+#pragma unroll  // pc and keep stay registers: no dynamic index
+        for (int i = 0; i < P; ++i)
+            if (keep[i] != 0u)
+                e += F::exact(row + static_cast<size_t>(pc[i]) * F::kPairBytes,
+                              x + static_cast<size_t>(m) * K + static_cast<size_t>(pc[i]) * 64u);
+        return wave_sum(e) * (1.0f / F::kFinal);
+    };
     uint32_t j = 0;
     do {
 #pragma unroll
@@ -215,11 +228,14 @@ __global__ __launch_bounds__(kStreamThreads) void gemv_stream_kernel(const uint1
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
                 float s = wave_sum(part[m]);
-                if constexpr (SPLIT_GU) {
-                    const float su = wave_sum(part_up[m]);
-                    mine_up[m] = mine_lane ? su : mine_up[m];
-                } else if constexpr (GU) {
-                    s = silu(F::kFinal * s) * (F::kFinal * wave_sum(part_up[m]));
+                if (__builtin_expect(not_finite(s), 0)) s = exact_share(w, jj, m);  // wave-uniform
+                if constexpr (GU) {
+                    float su = wave_sum(part_up[m]);
+                    if (__builtin_expect(not_finite(su), 0)) su = exact_share(w_up, jj, m);
+                    if constexpr (SPLIT_GU)
+                        mine_up[m] = mine_lane ? su : mine_up[m];
+                    else
+                        s = silu(F::kFinal * s) * (F::kFinal * su);
                 }
                 mine[m] = mine_lane ? s : mine[m];
             }

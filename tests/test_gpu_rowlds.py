@@ -135,3 +135,36 @@ def test_rowlds_rejects_what_it_cannot_run(stream, variant, shapes):
         w = (q8_weights if q8 else weights)(wl.seed_for(17, 2), n, k)
         with pytest.raises(HipError):
             (run_q8 if q8 else run_linear)(stream, x, w, m, n, k, dispatch=d)
+
+
+@pytest.mark.parametrize("q8", [False, True], ids=["q4_0", "q8_0"])
+def test_cached_ring_plan_is_not_reused_off_the_16_byte_grid(stream, oracle, q8):
+    """The ring kernels load weights and activations in 16-byte chunks, so
+    they run only on 16-byte-aligned operands.  One dispatch context plans
+    1 x 4096 x 14336 with aligned weights (the ring), then runs the same shape
+    with the weights 4, 8 and 12 bytes off the 16-byte grid, and aligned again:
+    the plan key carries the alignment class, so the misaligned calls get a
+    kernel of their own (dword weight loads), and every call meets the
+    oracle's tolerance.  The same sequence runs through the default entry
+    points (the library's own context)."""
+    from test_gpu_q8_0 import check as check_q8, run as run_q8, weights as q8_weights
+
+    m, n, k = 1, 14336, 4096
+    x = normal_x(wl.seed_for(18, k), m, k)
+    w = q8_weights(wl.seed_for(18, n), n, k) if q8 else weights(wl.seed_for(18, n), n, k)
+    cols = sample_columns(n, 512)
+    d = ops.Q4_0Dispatch()
+    for dispatch in (d, None):
+        for step, offset in enumerate((0, 4, 8, 12, 0)):
+            print(f"{'q8_0' if q8 else 'q4_0'} w_offset {offset} {'context' if dispatch else 'default'}", flush=True)
+            if q8:
+                y = run_q8(stream, x, w, m, n, k, dispatch=dispatch, w_offset=offset)
+                check_q8(oracle, y, x, w, m, n, k, columns=cols, what=f"q8_0 w+{offset}")
+            else:
+                y = run_linear(stream, x, w, m, n, k, dispatch=dispatch, w_offset=offset)
+                check_against_oracle(oracle, y, x, w, m, n, k, columns=cols, what=f"q4_0 w+{offset}")
+            if dispatch is not None and step < 2:
+                # the context's first plan of the shape (the lower alignment
+                # class sorts first): the ring when aligned, not after
+                plan = d.plan(m, n, k, q8_0=q8)
+                assert plan is not None and ("rowlds" in plan) == (offset == 0), (offset, plan)
