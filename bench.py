@@ -562,7 +562,162 @@ def load_probe():
     probe.mote_probe_read_u128.argtypes = [P, ctypes.c_size_t, U32, U32, U32, ctypes.c_int, P, P]
     probe.mote_probe_copy_rows.restype = ctypes.c_int
     probe.mote_probe_copy_rows.argtypes = [P, P, U32, U32, P]
+    probe.mote_probe_ring_record_words.restype = U32
+    probe.mote_probe_ring_record_words.argtypes = []
+    probe.mote_probe_ring_waves.restype = U32
+    probe.mote_probe_ring_waves.argtypes = [U32]
+    probe.mote_probe_ring_timeline.restype = ctypes.c_int
+    probe.mote_probe_ring_timeline.argtypes = [P, P, P, U32, U32, P, ctypes.c_size_t, P]
+    probe.mote_probe_ring_read.restype = ctypes.c_int
+    probe.mote_probe_ring_read.argtypes = [P, U32, U32, P, ctypes.c_size_t, P]
     return probe
+
+
+class RingTimelineCase:
+    """The shipped decode ring kernel with per-wave timestamps
+    (mote_probe_ring_timeline), or with `loads_only` the ring kernel's own
+    loads and nothing else (mote_probe_ring_read: grid, row order,
+    non-temporal 16-byte direct-to-LDS loads, 3 slots, 2 rows in flight, its
+    waits), over the rotated weight copies of a LinearCase.  With `regions`
+    launch i writes its per-wave records to region i % regions of one stamp
+    buffer; with regions = 0 nothing is recorded."""
+
+    def __init__(self, probe, case: "LinearCase", regions: int, loads_only: bool = False) -> None:
+        self.probe, self.case, self.regions, self.loads_only = probe, case, regions, loads_only
+        self.waves = probe.mote_probe_ring_waves(case.n)
+        self.words = probe.mote_probe_ring_record_words()
+        self.region_bytes = self.waves * self.words * 4
+        self.stamps = DeviceBuffer(self.region_bytes * regions) if regions else None
+
+    def launch(self, i: int, stream: Stream) -> None:
+        c = self.case
+        st = self.stamps.ptr + (i % self.regions) * self.region_bytes if self.stamps else None
+        if self.loads_only:
+            _ffi.check(self.probe.mote_probe_ring_read(c.wb[i % c.copies][0].ptr, c.n, c.k, st,
+                                                       self.region_bytes if st else 0, stream.handle),
+                       "ring read probe")
+        else:
+            _ffi.check(self.probe.mote_probe_ring_timeline(
+                c.xb.ptr, c.wb[i % c.copies][0].ptr, c.yb.ptr, c.n, c.k, st, self.region_bytes, stream.handle),
+                "ring timeline probe")
+
+    def algorithmic_bytes(self) -> int:
+        return self.case.w.nbytes if self.loads_only else self.case.algorithmic_bytes()
+
+    def records(self) -> np.ndarray:
+        return self.stamps.download(np.uint32).reshape(self.regions, self.waves, self.words)
+
+    def free(self) -> None:
+        if self.stamps:
+            self.stamps.free()
+
+
+def RingReadCase(probe, case: "LinearCase") -> RingTimelineCase:
+    """The ring kernel's loads alone, unrecorded (read-floor rows)."""
+    return RingTimelineCase(probe, case, 0, loads_only=True)
+
+
+def _pct(values, q) -> float:
+    return float(np.percentile(values, q)) if len(values) else float("nan")
+
+
+def _timeline_summary(rec: np.ndarray, row_bytes: int, has_compute: bool) -> list[dict]:
+    """Per launch: phase times in µs from the launch's first wave start (the
+    100 MHz real-time clock, 10 ns ticks)."""
+    tick_us = 0.01
+    out = []
+    launches = len(rec)
+    for L in range(launches):
+        r = rec[L]
+        base = r[:, 0].min()
+        rel = lambda a: ((a - base) & 0xFFFFFFFF) * tick_us  # noqa: E731
+        begin, ready, end, nrows = rel(r[:, 0]), rel(r[:, 1]), rel(r[:, 2]), r[:, 3]
+        active = nrows > 0
+        arr = [rel(r[w, 4:4 + int(nrows[w])]) for w in range(len(r)) if nrows[w] > 0]
+        done = [rel(r[w, 68:68 + int(nrows[w])]) for w in range(len(r)) if nrows[w] > 0]
+        landed = np.sort(np.concatenate(arr))
+        frac = lambda q: landed[min(len(landed) - 1, int(q * len(landed)))]  # noqa: E731
+        comp = np.concatenate([d - a for d, a in zip(done, arr)])
+        maxrows = int(nrows.max())
+        per_row = [(np.median([a[j] for a in arr if len(a) > j]), np.median([d[j] for d in done if len(d) > j]))
+                   for j in range(maxrows)]
+        mid = frac(0.75) - frac(0.25)
+        steady = 0.5 * len(landed) * row_bytes / (mid * 1e-6) / 1e12 if mid > 0 else float("nan")
+        gap = None
+        if L + 1 < launches:
+            gap = ((rec[L + 1][:, 0].min() - base) & 0xFFFFFFFF) * tick_us - end[active].max()
+        out.append(dict(L=L, begin_max=begin.max(),
+                        ready=(f"{_pct(ready[active], 50):.2f} / {ready[active].max():.2f}" if has_compute else "—"),
+                        first_p50=_pct([a[0] for a in arr], 50), l10=frac(0.10), l50=frac(0.50), l90=frac(0.90),
+                        l100=landed[-1], end_p50=_pct(end[active], 50), end_max=end[active].max(),
+                        comp=(f"{_pct(comp, 50):.3f}" if has_compute else "—"), steady=steady, gap=gap,
+                        per_row=per_row))
+    return out
+
+
+def run_timeline(launches: int = 8) -> int:
+    """Per-phase timeline of the shipped decode ring kernel at the headline
+    shape (M = 1, K = 4096, N = 14336) beside the same timeline of the ring's
+    loads alone: `launches` back-to-back launches of each, captured in one
+    graph (rotating weights), replayed until the device has settled, then once
+    more; the records of the last replay are summarised as markdown on
+    stdout.  Times are the 100 MHz real-time clock (10 ns ticks) relative to
+    the first wave start of each launch.  Event timings of the shipped kernel
+    and of the two stamped kernels, stamped and not (graph replays of 200
+    launches), come first."""
+    probe = load_probe()
+    stream, hip = Stream(), HipRuntime()
+    m, k, n = 1, 4096, 14336
+    case = LinearCase(m, n, k, workload=1)
+    cases = {"shipped kernel (rowlds_r3d2)": case,
+             "shipped kernel body, stamped": RingTimelineCase(probe, case, launches),
+             "ring loads only": RingTimelineCase(probe, case, 0, loads_only=True),
+             "ring loads only, stamped": RingTimelineCase(probe, case, launches, loads_only=True)}
+    timed = {}
+    for name, c in cases.items():
+        timed[name] = time_case(c, stream, hip, 200, 20)["kernel_ms_mean"] * 1e3
+        print(f"timeline: {name}: {timed[name]:.3f} us", file=sys.stderr, flush=True)
+    print("## Event timings (graph replays of 200 launches, rotated weights)\n")
+    print("| kernel | µs / launch | GB/s of its bytes |")
+    print("|---|---|---|")
+    for name, us in timed.items():
+        print(f"| {name} | {us:.3f} | {cases[name].algorithmic_bytes() / (us * 1e-6) / 1e9:.0f} |")
+    row_bytes = case.w.nbytes // n
+    for name in ("shipped kernel body, stamped", "ring loads only, stamped"):
+        tl = cases[name]
+        exe = hip.capture(stream, lambda: [tl.launch(i, stream) for i in range(launches)])
+        try:
+            t0 = time.perf_counter()
+            while time.perf_counter() - t0 < max(SETTLE_S, 0.02):
+                hip.launch_graph(exe, stream)
+                stream.synchronize()
+            hip.launch_graph(exe, stream)
+            stream.synchronize()
+        finally:
+            hip.destroy_graph(exe)
+        rows = _timeline_summary(tl.records().astype(np.int64), row_bytes, not tl.loads_only)
+        print(f"\n## {name}: phases of each launch (µs from the launch's first wave start; {tl.waves} waves, "
+              f"{n // tl.waves} rows per wave)\n")
+        print("| launch | last wave start | x staged (p50 / max) | first row landed (p50) | rows landed 10 % / 50 % / "
+              "90 % / all | last wave end (p50 / max) | row compute (p50) | TB/s landed 25-75 % | gap to next launch |")
+        print("|---|---|---|---|---|---|---|---|---|")
+        for o in rows:
+            gap = f"{o['gap']:.2f}" if o["gap"] is not None else "—"
+            print(f"| {o['L']} | {o['begin_max']:.2f} | {o['ready']} | {o['first_p50']:.2f} | {o['l10']:.2f} / "
+                  f"{o['l50']:.2f} / {o['l90']:.2f} / {o['l100']:.2f} | {o['end_p50']:.2f} / {o['end_max']:.2f} "
+                  f"| {o['comp']} | {o['steady']:.2f} | {gap} |")
+        o = rows[launches // 2]
+        print(f"\n{name}, rows of launch {o['L']} (median over waves, µs)\n")
+        print("| row j | landed | sum formed |" if not tl.loads_only else "| row j | landed |")
+        print("|---|---|---|" if not tl.loads_only else "|---|---|")
+        for j, (a, d) in enumerate(o["per_row"]):
+            print(f"| {j} | {a:.2f} | {d:.2f} |" if not tl.loads_only else f"| {j} | {a:.2f} |")
+    for c in cases.values():
+        if c is not case:
+            c.free()
+    case.free()
+    stream.close()
+    return 0
 
 
 def run_read_floor(sizes=READ_FLOOR_BYTES) -> int:
@@ -596,6 +751,21 @@ def run_read_floor(sizes=READ_FLOOR_BYTES) -> int:
         for b in bufs:
             b.free()
     sink.free()
+    # The decode ring kernel's own access pattern (mote_probe_ring_read): its
+    # grid, row order, non-temporal direct-to-LDS 16-byte loads, 3 slots and 2
+    # rows in flight, and nothing else, over the weights of the M = 1, K =
+    # 4096 linears.
+    print("\nThe decode ring kernel's own loads (weights only, K = 4096)\n")
+    print("| N | weight bytes | copies | µs / launch | GB/s | % of 8 TB/s |")
+    print("|---|---|---|---|---|---|")
+    for n in (4096, 6144, 14336):
+        case = LinearCase(1, n, 4096, workload=1)
+        ring = RingReadCase(probe, case)
+        us = time_case(ring, stream, hip, 100, 26)["kernel_ms_mean"] * 1e3
+        gbs = case.w.nbytes / (us * 1e-6) / 1e9
+        print(f"read floor ring pattern N={n}: {us:.2f} us", file=sys.stderr, flush=True)
+        print(f"| {n} | {case.w.nbytes} | {case.copies} | {us:.2f} | {gbs:.0f} | {100 * gbs / HBM_PEAK_GBS:.1f} % |")
+        case.free()
     stream.close()
     return 0
 
@@ -704,6 +874,9 @@ def main() -> int:
                     help="time pure 16-byte reads of 9.46, 14.2 and 33.1 MB (the bytes of the 1 x 4096 x "
                          "{4096, 6144, 14336} linears) in many grid shapes: the HBM floor of the GEMVs "
                          "(probe library; stdout tables, no result line)")
+    ap.add_argument("--timeline", action="store_true",
+                    help="per-wave timeline of the headline's decode ring kernel (probe library: the shipped "
+                         "kernel body with real-time stamps; stdout tables, no result line)")
     ap.add_argument("--read-bytes", default=None, metavar="B1,B2,...",
                     help="with --read-floor: these byte counts (multiples of 16) instead")
     args = ap.parse_args()
@@ -713,6 +886,8 @@ def main() -> int:
     SETTLE_S = max(args.settle_ms, 0.0) / 1e3
     if args.comparator:
         return run_comparator()
+    if args.timeline:
+        return run_timeline()
     if args.read_floor:
         sizes = tuple(int(v) for v in args.read_bytes.split(",")) if args.read_bytes else READ_FLOOR_BYTES
         return run_read_floor(sizes)
