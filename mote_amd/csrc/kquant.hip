@@ -928,9 +928,271 @@ hipError_t launch_ring_mt(const void* x, const void* w, void* y, uint32_t M, uin
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K on the matrix cores (kq4_mfma_kernel): 3 to 64 tokens, K up to
+// KS x STEPS super-blocks (4096).
+//
+// v_mfma_f32_16x16x32_f16 with the activations as the A operand (16 tokens)
+// and the weights as the B operand (16 rows), so the lane that holds output
+// (token, row) is one of the four lanes that loaded that row's block header:
+// d, dmin and the sub-block scales stay in the lane.  Wave kw of a workgroup
+// owns super-blocks kw, kw + KS, ... of every row and keeps the activations of
+// those blocks for the workgroup's 16-token tile in registers; lane group g
+// takes bytes qs[32 g .. 32 g + 31] of a block, i.e. sub-blocks 2 g (low
+// nibbles) and 2 g + 1 (high nibbles), 64 elements.  MFMA t (of 8 per block)
+// takes 8 of them: nibble h = t / 4 of bytes 8 (t % 4) .. 8 (t % 4) + 7.  The
+// weight operand is sc_j q, exact in binary16 (at most 63 x 15): q enters as
+// 1024 + q (low nibble masked into binary16 1024) or 64 + q (high nibble into
+// binary16 64, ulp 1/16), and one packed fma with (sc, -1024 sc) or
+// (sc, -64 sc) gives sc q exactly.  Each product with an activation is exact
+// in f32, so one f32 accumulator per block holds sum_j sc_j sum x q; the
+// minimum term sum_j m_j S_tj (S_tj: token t's sum over sub-block j) is a
+// second MFMA pair with S split into binary16 hi + lo (m exact), and
+//   y[t, r] += d_r C[t, r] - dmin_r C'[t, r]
+// once per block in f32.  GGML's definition rounds each element's value
+// (d1 q - m1) instead; the difference is rounding only.  The KS waves' partial
+// tiles meet in LDS and are summed in wave order (deterministic).  A result
+// that is not finite (an infinite or NaN scale, a non-finite activation) is
+// recomputed by its thread element by element with the definition's values,
+// so NaN and infinities land where the oracle puts them.
+// ---------------------------------------------------------------------------
+
+// sum over the row of x[k] w[k] with GGML's per-element values, one thread.
+__device__ inline float kq4_exact_thread(const uint8_t* row, const uint16_t* xrow, uint32_t nb) {
+    float acc = 0.0f;
+    for (uint32_t k = 0; k < nb * kSuper; ++k)
+        acc += half_bits_to_float(xrow[k]) * kq_value<Fmt::Q4K>(row + static_cast<size_t>(k / kSuper) * 144, k % kSuper);
+    return acc;
+}
+
+__device__ __forceinline__ uint32_t kq_pick(const uint32_t* x, int a, int b) {
+    const uint32_t lo = (a & 1) ? 0x0302u : 0x0100u;
+    const uint32_t hi = (b & 1) ? 0x07060000u : 0x05040000u;
+    return __builtin_amdgcn_perm(x[b >> 1], x[a >> 1], hi | lo);
+}
+
+__device__ __forceinline__ uint32_t f16x2_bits(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+template <int KS, int STEPS, typename OutT>
+__global__ __launch_bounds__(KS * 64) void kq4_mfma_kernel(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
+                                                          OutT* __restrict__ y, uint32_t M, uint32_t N, uint32_t K,
+                                                          uint32_t token_tiles, uint32_t items, uint32_t per_xcd) {
+    constexpr int kLazy = KS * 64 / 256;  // items reduced together: one output per thread
+    __shared__ float part[kLazy][KS][16][17];  // [item][wave][token][row]
+    const int tid = static_cast<int>(threadIdx.x);
+    const int kw = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+    const uint32_t nb = K / kSuper;
+    const size_t row_bytes = static_cast<size_t>(nb) * 144;
+    const uint32_t groups = gridDim.x;
+    // XCD-aware order: workgroups of one XCD take consecutive items, so the
+    // token tiles of a row tile read its weights through the same L2
+    const uint32_t first = (blockIdx.x % 8u) * per_xcd + blockIdx.x / 8u;
+    const uint32_t tok0 = (first % token_tiles) * 16u;
+
+    // The activations of this wave's blocks for the 16 tokens: the MFMA
+    // operands (permuted to the weight operands' element order) and the
+    // sub-block sums as binary16 hi + lo pairs.  Tokens past M stay zero.
+    uint32_t xa[STEPS][8][4];
+    uint32_t s_hi[STEPS], s_lo[STEPS];
+    const bool live_tok = tok0 + static_cast<uint32_t>(li) < M;
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+        const uint32_t b = static_cast<uint32_t>(kw) + KS * static_cast<uint32_t>(s);
+        uint32_t xr[32];
+        if (live_tok && b < nb) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(x + static_cast<size_t>(tok0 + li) * K +
+                                                              static_cast<size_t>(b) * kSuper + 64u * lg);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const u32x4 v = src[c];
+                xr[4 * c] = v.x; xr[4 * c + 1] = v.y; xr[4 * c + 2] = v.z; xr[4 * c + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) xr[i] = 0u;
+        }
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            s0 = dot2(xr[i], kOnePair, s0);
+            s1 = dot2(xr[16 + i], kOnePair, s1);
+        }
+        const _Float16 h0 = static_cast<_Float16>(s0), h1 = static_cast<_Float16>(s1);
+        const _Float16 l0 = static_cast<_Float16>(s0 - static_cast<float>(h0));
+        const _Float16 l1 = static_cast<_Float16>(s1 - static_cast<float>(h1));
+        s_hi[s] = f16x2_bits(f16x2{h0, h1});
+        s_lo[s] = f16x2_bits(f16x2{l0, l1});
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int e = 32 * (t >> 2) + 8 * (t & 3);
+            xa[s][t][0] = kq_pick(xr, e, e + 2);
+            xa[s][t][1] = kq_pick(xr, e + 1, e + 3);
+            xa[s][t][2] = kq_pick(xr, e + 4, e + 6);
+            xa[s][t][3] = kq_pick(xr, e + 5, e + 7);
+        }
+    }
+
+    // This lane's part of a row's block: the 16-byte header (d, dmin, the 12
+    // scale bytes) and its 32 nibble bytes.
+    struct Part {
+        u32x4 hdr, qa, qb;
+    };
+    auto load_part = [&](uint32_t item, int s, Part& pt) {
+        const uint32_t b = static_cast<uint32_t>(kw) + KS * static_cast<uint32_t>(s);
+        if (b >= nb) return;  // uniform: a step past the row's blocks
+        const uint32_t n = min((item / token_tiles) * 16u + static_cast<uint32_t>(li), N - 1);
+        const uint8_t* base = w + static_cast<size_t>(n) * row_bytes + static_cast<size_t>(b) * 144;
+        pt.hdr = *reinterpret_cast<const u32x4*>(base);
+        pt.qa = *reinterpret_cast<const u32x4*>(base + 16 + 32 * lg);
+        pt.qb = *reinterpret_cast<const u32x4*>(base + 32 + 32 * lg);
+    };
+    // One block of one item: sum_j sc_j q x on the matrix cores, the minimum
+    // term, and y += d C - dmin C' for this lane's four (token, row) outputs.
+    auto block_mfma = [&](const Part& pt, int s, f32x4 yv) {
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scale_min(pt.hdr.y, pt.hdr.z, pt.hdr.w, 2u * lg, sc0, m0);
+        q4k_scale_min(pt.hdr.y, pt.hdr.z, pt.hdr.w, 2u * lg + 1u, sc1, m1);
+        const _Float16 f0 = static_cast<_Float16>(static_cast<float>(sc0));
+        const _Float16 f1 = static_cast<_Float16>(static_cast<float>(sc1));
+        const f16x2 sc_lo = {f0, f0}, sc_hi = {f1, f1};
+        const f16x2 b_lo = {static_cast<_Float16>(-1024.0f * static_cast<float>(sc0)),
+                            static_cast<_Float16>(-1024.0f * static_cast<float>(sc0))};
+        const f16x2 b_hi = {static_cast<_Float16>(-64.0f * static_cast<float>(sc1)),
+                            static_cast<_Float16>(-64.0f * static_cast<float>(sc1))};
+        const uint32_t q[8] = {pt.qa.x, pt.qa.y, pt.qa.z, pt.qa.w, pt.qb.x, pt.qb.y, pt.qb.z, pt.qb.w};
+        f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t qa = q[2 * (t & 3)], qb = q[2 * (t & 3) + 1];
+            f16x2 v[4];
+            if (t < 4) {  // low nibbles: 1024 + q, then sc q
+                v[0] = as_h2((qa & 0x000F000Fu) | 0x64006400u);
+                v[1] = as_h2(((qa >> 8) & 0x000F000Fu) | 0x64006400u);
+                v[2] = as_h2((qb & 0x000F000Fu) | 0x64006400u);
+                v[3] = as_h2(((qb >> 8) & 0x000F000Fu) | 0x64006400u);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = __builtin_elementwise_fma(v[i], sc_lo, b_lo);
+            } else {  // high nibbles: 64 + q, then sc q
+                v[0] = as_h2((qa & 0x00F000F0u) | 0x54005400u);
+                v[1] = as_h2(((qa >> 8) & 0x00F000F0u) | 0x54005400u);
+                v[2] = as_h2((qb & 0x00F000F0u) | 0x54005400u);
+                v[3] = as_h2(((qb >> 8) & 0x00F000F0u) | 0x54005400u);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = __builtin_elementwise_fma(v[i], sc_hi, b_hi);
+            }
+            const f16x8 bw = {v[0].x, v[0].y, v[1].x, v[1].y, v[2].x, v[2].y, v[3].x, v[3].y};
+            const f16x8 ax = __builtin_bit_cast(f16x8, u32x4{xa[s][t][0], xa[s][t][1], xa[s][t][2], xa[s][t][3]});
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, bw, c, 0, 0, 0);
+        }
+        // sum_j m_j S_tj: k slots 8 g and 8 g + 1 hold sub-blocks 2 g, 2 g + 1
+        const uint32_t mw = f16x2_bits(f16x2{static_cast<_Float16>(static_cast<float>(m0)),
+                                              static_cast<_Float16>(static_cast<float>(m1))});
+        const f16x8 bm = __builtin_bit_cast(f16x8, u32x4{mw, 0u, 0u, 0u});
+        f32x4 cm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, u32x4{s_hi[s], 0u, 0u, 0u}), bm,
+                                                          f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        cm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, u32x4{s_lo[s], 0u, 0u, 0u}), bm, cm, 0, 0,
+                                                    0);
+        const float d = half_bits_to_float(pt.hdr.x & 0xffffu), dmin = half_bits_to_float(pt.hdr.x >> 16);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) yv[r] = __builtin_fmaf(-dmin, cm[r], __builtin_fmaf(d, c[r], yv[r]));
+        return yv;
+    };
+    Part cur[STEPS];
+    if (first < items) {
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) load_part(first, s, cur[s]);
+    }
+    // Items of this workgroup in chunks of kLazy: each wave streams its block
+    // of every item of the chunk with the next item's loads in flight and
+    // keeps the partial tiles in registers; the chunk's tiles then meet in
+    // LDS behind one barrier (instead of two barriers per item).
+    for (uint32_t c0 = first; c0 < items; c0 += kLazy * groups) {  // uniform per workgroup
+        f32x4 yacc[kLazy];
+#pragma unroll
+        for (int i = 0; i < kLazy; ++i) {
+            yacc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            const uint32_t item = c0 + static_cast<uint32_t>(i) * groups;
+            if (item >= items) break;  // uniform
+            const uint32_t next = item + groups;
+#pragma unroll
+            for (int s = 0; s < STEPS; ++s) {
+                const uint32_t b = static_cast<uint32_t>(kw) + KS * static_cast<uint32_t>(s);
+                if (b < nb) {  // uniform
+                    const Part pt = cur[s];
+                    if (next < items) load_part(next, s, cur[s]);  // the next item's block under this one's MFMAs
+                    yacc[i] = block_mfma(pt, s, yacc[i]);
+                }
+            }
+        }
+        // lane holds tokens 4 g .. 4 g + 3 of row li of each item; the KS
+        // partial tiles meet in LDS and are summed in wave order
+#pragma unroll
+        for (int i = 0; i < kLazy; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) part[i][kw][4 * lg + r][li] = yacc[i][r];
+        __syncthreads();
+        {
+            const int i = tid >> 8, tok = (tid >> 4) & 15, row = tid & 15;  // KS * 64 >= kLazy * 256 threads
+            const uint32_t item = c0 + static_cast<uint32_t>(i) * groups;
+            const uint32_t m = tok0 + static_cast<uint32_t>(tok);
+            const uint32_t n = (item / token_tiles) * 16u + static_cast<uint32_t>(row);
+            if (i < kLazy && item < items && m < M && n < N) {
+                float v = part[i][0][tok][row];
+#pragma unroll
+                for (int k = 1; k < KS; ++k) v += part[i][k][tok][row];
+                if (__builtin_expect(not_finite(v), 0))
+                    v = kq4_exact_thread(w + static_cast<size_t>(n) * row_bytes, x + static_cast<size_t>(m) * K, nb);
+                y[static_cast<size_t>(m) * N + n] = to_out<OutT>(v);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// The matrix-core Q4_K tile: 16-token tiles, one workgroup of 16 waves per
+// CU, one block per wave, so K <= 4096 (a wave's activations for more blocks
+// outgrow its registers: 16 waves of two blocks, or 8 of four, spill); x and
+// w 16-byte aligned.
+bool kq4_mfma_supported(const void* x, const void* w, uint32_t M, uint32_t K) {
+    const uint32_t nb = K / kSuper;
+    return M >= 3 && M <= 64 && nb >= 1 && nb <= 16 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
+           (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
+}
+
+template <int KS, int STEPS, typename OutT>
+hipError_t launch_kq4_mfma_ks(const void* x, const void* w, void* y, uint32_t M, uint32_t N, uint32_t K,
+                              hipStream_t stream) {
+    const uint32_t token_tiles = (M + 15) / 16;
+    const uint32_t row_tiles = (N + 15) / 16;
+    const uint64_t items64 = static_cast<uint64_t>(row_tiles) * token_tiles;
+    if (items64 > 0x7fffffffull) return hipErrorInvalidConfiguration;
+    const uint32_t items = static_cast<uint32_t>(items64);
+    // whole XCD rounds that are also a multiple of the token tiles, so every
+    // workgroup keeps one token tile
+    uint32_t a = 8u, b = token_tiles;
+    while (b != 0) { const uint32_t t = a % b; a = b; b = t; }
+    const uint32_t unit = 8u / a * token_tiles;
+    uint32_t groups = static_cast<uint32_t>(device_cus());
+    if (groups > items) groups = items;
+    groups = (groups + unit - 1) / unit * unit;
+    hipLaunchKernelGGL((kq4_mfma_kernel<KS, STEPS, OutT>), dim3(groups), dim3(KS * 64), 0, stream,
+                       static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), static_cast<OutT*>(y), M, N, K,
+                       token_tiles, items, groups / 8u);
+    return hipGetLastError();
+}
+
+template <typename OutT>
+hipError_t launch_kq4_mfma(const void* x, const void* w, void* y, uint32_t M, uint32_t N, uint32_t K,
+                           hipStream_t stream) {
+    return launch_kq4_mfma_ks<16, 1, OutT>(x, w, y, M, N, K, stream);
+}
+
 template <Fmt F, typename OutT>
 hipError_t launch_gemv(const void* x, const void* w, void* y, uint32_t M, uint32_t N, uint32_t K,
                        hipStream_t stream) {
+    if constexpr (F == Fmt::Q4K) {
+        if (kq4_mfma_supported(x, w, M, K)) return launch_kq4_mfma<OutT>(x, w, y, M, N, K, stream);
+    }
     if (ring_supported<F>(x, w, K)) {
         if (M == 1) return launch_ring_mt<F, 1, OutT>(x, w, y, M, N, K, stream);
         if (M == 2) return launch_ring_mt<F, 2, OutT>(x, w, y, M, N, K, stream);
