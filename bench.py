@@ -551,6 +551,20 @@ class ReadCase:
                    "read probe")
 
 
+def install_fault_report() -> None:
+    """The probe library's fatal-signal report (signal, faulting address,
+    program counter, /proc/self/maps on stderr, then the previous handler);
+    skipped when the probe library is not built."""
+    path = os.path.join(ROOT, "mote_amd", "libmote_probe.so")
+    if not os.path.exists(path):
+        return
+    probe = ctypes.CDLL(path)
+    probe.mote_probe_install_fault_report.restype = ctypes.c_int
+    probe.mote_probe_install_fault_report.argtypes = [ctypes.c_int]
+    if probe.mote_probe_install_fault_report(2) != 0:
+        print("bench.py: could not install the fault report", file=sys.stderr)
+
+
 def load_probe():
     """libmote_probe.so, the measuring kernels built beside the library."""
     path = os.path.join(ROOT, "mote_amd", "libmote_probe.so")
@@ -882,8 +896,11 @@ def main() -> int:
                     help="with --read-floor: these byte counts (multiples of 16) instead")
     args = ap.parse_args()
     # A crash inside a runtime or profiler call then names the Python line
-    # (and so the C-ABI call) it happened in.
+    # (and so the C-ABI call) it happened in, and the probe library's report
+    # (installed in front of it) prints the faulting address, the program
+    # counter and /proc/self/maps, which names the library the fault was in.
     faulthandler.enable()
+    install_fault_report()
     SETTLE_S = max(args.settle_ms, 0.0) / 1e3
     if args.comparator:
         return run_comparator()
