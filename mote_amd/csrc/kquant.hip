@@ -37,6 +37,10 @@
 // Q4_K minimum, the Q6_K -32) are applied through the staged group sums:
 //   Q4_K: sum_e x_e (d sc q_e - dmin m) = d sc 2^24 acc - dmin m S
 //   Q6_K: sum_e x_e d sc (q_e - 32)     = d sc (2^24 acc - 32 S).
+// The LDS-ring GEMV (kq_ring_kernel) streams the same arithmetic for 1-4
+// tokens per pass, and from 3 (Q4_K) or 5 (Q6_K) to 64 tokens at K <= 4096
+// the matrix-core tiles (kq4_mfma_kernel, kq6_mfma_kernel) decode each block
+// once per 16-token tile into exact binary16 operands.
 // HBM-bound: algorithmic bytes per call are |W| + 2 M K + M N |y|.
 #include "common.hpp"
 #include "q4_0.hpp"
@@ -958,10 +962,12 @@ hipError_t launch_ring_mt(const void* x, const void* w, void* y, uint32_t M, uin
 // ---------------------------------------------------------------------------
 
 // sum over the row of x[k] w[k] with GGML's per-element values, one thread.
-__device__ inline float kq4_exact_thread(const uint8_t* row, const uint16_t* xrow, uint32_t nb) {
+template <Fmt F>
+__device__ inline float kq_exact_thread(const uint8_t* row, const uint16_t* xrow, uint32_t nb) {
     float acc = 0.0f;
     for (uint32_t k = 0; k < nb * kSuper; ++k)
-        acc += half_bits_to_float(xrow[k]) * kq_value<Fmt::Q4K>(row + static_cast<size_t>(k / kSuper) * 144, k % kSuper);
+        acc += half_bits_to_float(xrow[k]) *
+               kq_value<F>(row + static_cast<size_t>(k / kSuper) * block_bytes<F>(), k % kSuper);
     return acc;
 }
 
@@ -1141,7 +1147,7 @@ __global__ __launch_bounds__(KS * 64) void kq4_mfma_kernel(const uint16_t* __res
 #pragma unroll
                 for (int k = 1; k < KS; ++k) v += part[i][k][tok][row];
                 if (__builtin_expect(not_finite(v), 0))
-                    v = kq4_exact_thread(w + static_cast<size_t>(n) * row_bytes, x + static_cast<size_t>(m) * K, nb);
+                    v = kq_exact_thread<Fmt::Q4K>(w + static_cast<size_t>(n) * row_bytes, x + static_cast<size_t>(m) * K, nb);
                 y[static_cast<size_t>(m) * N + n] = to_out<OutT>(v);
             }
         }
@@ -1149,19 +1155,230 @@ __global__ __launch_bounds__(KS * 64) void kq4_mfma_kernel(const uint16_t* __res
     }
 }
 
-// The matrix-core Q4_K tile: 16-token tiles, one workgroup of 16 waves per
-// CU, one block per wave, so K <= 4096 (a wave's activations for more blocks
-// outgrow its registers: 16 waves of two blocks, or 8 of four, spill); x and
-// w 16-byte aligned.
-bool kq4_mfma_supported(const void* x, const void* w, uint32_t M, uint32_t K) {
-    const uint32_t nb = K / kSuper;
-    return M >= 3 && M <= 64 && nb >= 1 && nb <= 16 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
-           (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
+// ---------------------------------------------------------------------------
+// Q6_K on the matrix cores (kq6_mfma_kernel), 5 to 64 tokens, K up to 4096:
+// the Q4_K tile's layout (16 tokens as the A operand, 16 weight rows as the B
+// operand, one super-block per wave, partial tiles summed in LDS in wave
+// order).
+//
+// Lane group g takes ql bytes 32 g .. 32 g + 31: half p = g / 2 of the block
+// and quarters c = g % 2 (low nibbles) and g % 2 + 2 (high nibbles), i.e.
+// elements 128 p + 32 c + l, l = 0..31, with the qh bytes 32 p + l.  MFMA
+// t = 4 h + u takes l = 8 u .. 8 u + 7 of quarter c = g % 2 + 2 h, eight
+// elements of one 16-element sub-block (scale 8 p + 2 c + u / 2), in their
+// natural order, so the activations enter the A operand as they lie in
+// memory.  The 6-bit q (nibble | two qh bits << 4) enters binary16 as
+// 1024 + q (one v_perm with 0x64 high bytes), and the weight operand
+// sc (q - 32) is split over two MFMAs: sc = 8 s + t with s = sc >> 3 in
+// [-16, 15] and t = sc & 7, so (q - 32) s (at most 512) and (q - 32) t (at
+// most 224) are exact binary16 integers, each one packed fma from 1024 + q,
+// and every product with an activation is exact in f32.  Per block
+//   y[t, r] += d_r (8 C_s[t, r] + C_t[t, r]).
+// GGML's definition rounds each element's value (d sc)(q - 32) (exact) and
+// sums x times it; the difference is rounding only.  A result that is not
+// finite is recomputed by its thread element by element, as in the Q4_K tile.
+// Blocks lie at 2-byte offsets (210-byte blocks).  Where a row is a whole
+// number of 16-byte units (K a multiple of 2048: A16), block b of every row
+// sits 2 (b mod 8) bytes past a 16-byte boundary -- the same offset for all
+// lanes of the wave that owns it -- so each 32-byte run is read as three
+// aligned 16-byte chunks and realigned by that wave-uniform offset (the chunks
+// end at most 2 bytes before the block's end).  Otherwise each 16 bytes are
+// read as five dwords from the dword boundary at or below them.  Either way
+// every read stays inside the block or the one before it (w is 16-byte
+// aligned).  The four scales come as one 8-byte read from the dword boundary
+// at or below them, d as a 16-bit word.
+// ---------------------------------------------------------------------------
+
+// The 32 bytes at p, p = 16 a + 4 o4 + sh (o4 and sh the same in every lane),
+// from the three 16-byte chunks at 16 a.
+__device__ __forceinline__ void load32_u(const uint8_t* p, uint32_t o4, uint32_t sh, u32x4& lo, u32x4& hi) {
+    const u32x4* q = reinterpret_cast<const u32x4*>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t{15});
+    const u32x4 a = q[0], b = q[1], c = q[2];
+    const uint32_t d[12] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w};
+    uint32_t o[8];
+    switch (o4) {  // uniform
+#define MOTE_Q6_REALIGN(S)                                                                      \
+    case S:                                                                                     \
+        for (int k = 0; k < 8; ++k) o[k] = __builtin_amdgcn_alignbyte(d[k + S + 1], d[k + S], sh); \
+        break;
+        MOTE_Q6_REALIGN(0)
+        MOTE_Q6_REALIGN(1)
+        MOTE_Q6_REALIGN(2)
+        default:
+        MOTE_Q6_REALIGN(3)
+#undef MOTE_Q6_REALIGN
+    }
+    lo = u32x4{o[0], o[1], o[2], o[3]};
+    hi = u32x4{o[4], o[5], o[6], o[7]};
 }
 
-template <int KS, int STEPS, typename OutT>
-hipError_t launch_kq4_mfma_ks(const void* x, const void* w, void* y, uint32_t M, uint32_t N, uint32_t K,
-                              hipStream_t stream) {
+template <int KS, bool A16, typename OutT>
+__global__ __launch_bounds__(KS * 64) void kq6_mfma_kernel(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
+                                                          OutT* __restrict__ y, uint32_t M, uint32_t N, uint32_t K,
+                                                          uint32_t token_tiles, uint32_t items, uint32_t per_xcd) {
+    constexpr int kLazy = KS * 64 / 256;  // items reduced together: one output per thread
+    __shared__ float part[kLazy][KS][16][17];  // [item][wave][token][row]
+    const int tid = static_cast<int>(threadIdx.x);
+    const int kw = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+    const uint32_t half = static_cast<uint32_t>(lg) >> 1, c0 = static_cast<uint32_t>(lg) & 1u;
+    const uint32_t nb = K / kSuper;
+    const size_t row_bytes = static_cast<size_t>(nb) * 210;
+    const uint32_t groups = gridDim.x;
+    const uint32_t b = static_cast<uint32_t>(kw);  // this wave's super-block
+    const uint32_t first = (blockIdx.x % 8u) * per_xcd + blockIdx.x / 8u;
+    const uint32_t tok0 = (first % token_tiles) * 16u;
+
+    // The activations of this wave's block for the 16 tokens (tokens past M
+    // stay zero): quarter c0 + 2 h, elements 8 u .. 8 u + 7 in xa[4 h + u].
+    uint32_t xa[8][4];
+    if (tok0 + static_cast<uint32_t>(li) < M && b < nb) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(x + static_cast<size_t>(tok0 + li) * K +
+                                                          static_cast<size_t>(b) * kSuper + 128u * half + 32u * c0);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const u32x4 v = src[8 * (t >> 2) + (t & 3)];  // + 64 elements per h
+            xa[t][0] = v.x; xa[t][1] = v.y; xa[t][2] = v.z; xa[t][3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) xa[t][0] = xa[t][1] = xa[t][2] = xa[t][3] = 0u;
+    }
+
+    // This lane's part of a row's block: 32 ql bytes, the 32 qh bytes of its
+    // half, the scales of its four sub-blocks (two 16-bit words) and d.
+    struct Part {
+        u32x4 l0, l1, h0, h1;
+        uint32_t s_lo, s_hi, d;
+    };
+    auto load_part = [&](uint32_t item, Part& pt) {
+        if (b >= nb) return;  // uniform: a wave past the row's blocks
+        const uint32_t n = min((item / token_tiles) * 16u + static_cast<uint32_t>(li), N - 1);
+        const uint8_t* base = w + static_cast<size_t>(n) * row_bytes + static_cast<size_t>(b) * 210;
+        if constexpr (A16) {
+            const uint32_t o = 2u * (b & 7u);  // base mod 16
+            load32_u(base + 32 * lg, (o + 32u * lg) % 16u / 4u, o & 3u, pt.l0, pt.l1);
+            load32_u(base + 128 + 32 * half, o / 4u, o & 3u, pt.h0, pt.h1);
+        } else {
+            pt.l0 = load16_a2(base + 32 * lg);
+            pt.l1 = load16_a2(base + 32 * lg + 16);
+            pt.h0 = load16_a2(base + 128 + 32 * half);
+            pt.h1 = load16_a2(base + 128 + 32 * half + 16);
+        }
+        // scale bytes s = 192 + 8 half + 2 c0 (+1) and s + 4 (+1): one 8-byte
+        // read from the dword boundary at or below s (s - 2 >= 190, s + 6 <= 208)
+        const uint8_t* sp = base + 192 + 8 * half + 2 * c0;
+        const uint32_t ssh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sp) & 3u);  // 0 or 2
+        typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+        const u32x2_a4 sv = *reinterpret_cast<const u32x2_a4*>(reinterpret_cast<uintptr_t>(sp) & ~uintptr_t{3});
+        pt.s_lo = __builtin_amdgcn_alignbyte(sv.y, sv.x, ssh) & 0xFFFFu;
+        pt.s_hi = (ssh ? sv.y >> 16 : sv.y) & 0xFFFFu;
+        pt.d = *reinterpret_cast<const uint16_t*>(base + 208);
+    };
+    const uint32_t sh_lo = 4u - 2u * c0, sh_hi = 2u * c0;  // qh bits 2c..2c+1 to bits 4..5
+    auto block_mfma = [&](const Part& pt, f32x4 yv) {
+        const uint32_t L[8] = {pt.l0.x, pt.l0.y, pt.l0.z, pt.l0.w, pt.l1.x, pt.l1.y, pt.l1.z, pt.l1.w};
+        const uint32_t H[8] = {pt.h0.x, pt.h0.y, pt.h0.z, pt.h0.w, pt.h1.x, pt.h1.y, pt.h1.z, pt.h1.w};
+        f32x4 cs = {0.0f, 0.0f, 0.0f, 0.0f}, ct = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {  // sub-block j of this quarter: u = 2 j, 2 j + 1
+                const int sc = static_cast<int8_t>(((h ? pt.s_hi : pt.s_lo) >> (8 * j)) & 0xFFu);
+                const _Float16 fs = static_cast<_Float16>(static_cast<float>(sc >> 3));
+                const _Float16 ft = static_cast<_Float16>(static_cast<float>(sc & 7));
+                const _Float16 gs = static_cast<_Float16>(-1056.0f * static_cast<float>(sc >> 3));
+                const _Float16 gt = static_cast<_Float16>(-1056.0f * static_cast<float>(sc & 7));
+                const f16x2 ms = {fs, fs}, as = {gs, gs}, mt = {ft, ft}, at = {gt, gt};
+#pragma unroll
+                for (int uu = 0; uu < 2; ++uu) {
+                    const int u = 2 * j + uu;
+                    uint32_t q[2];
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const uint32_t l = L[2 * u + i], hb = H[2 * u + i];
+                        q[i] = h == 0 ? (l & 0x0F0F0F0Fu) | ((hb << sh_lo) & 0x30303030u)
+                                      : ((l >> 4) & 0x0F0F0F0Fu) | ((hb >> sh_hi) & 0x30303030u);
+                    }
+                    f16x2 v[4];  // 1024 + q, elements 8 u .. 8 u + 7 in order
+                    v[0] = as_h2(__builtin_amdgcn_perm(0x64646464u, q[0], 0x04010400u));
+                    v[1] = as_h2(__builtin_amdgcn_perm(0x64646464u, q[0], 0x04030402u));
+                    v[2] = as_h2(__builtin_amdgcn_perm(0x64646464u, q[1], 0x04010400u));
+                    v[3] = as_h2(__builtin_amdgcn_perm(0x64646464u, q[1], 0x04030402u));
+                    f16x2 vs[4], vt[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        vs[i] = __builtin_elementwise_fma(v[i], ms, as);  // (q - 32) s
+                        vt[i] = __builtin_elementwise_fma(v[i], mt, at);  // (q - 32) t
+                    }
+                    const f16x8 ax =
+                        __builtin_bit_cast(f16x8, u32x4{xa[4 * h + u][0], xa[4 * h + u][1], xa[4 * h + u][2], xa[4 * h + u][3]});
+                    const f16x8 bs = {vs[0].x, vs[0].y, vs[1].x, vs[1].y, vs[2].x, vs[2].y, vs[3].x, vs[3].y};
+                    const f16x8 bt = {vt[0].x, vt[0].y, vt[1].x, vt[1].y, vt[2].x, vt[2].y, vt[3].x, vt[3].y};
+                    cs = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, bs, cs, 0, 0, 0);
+                    ct = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, bt, ct, 0, 0, 0);
+                }
+            }
+        }
+        const float d = half_bits_to_float(pt.d);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) yv[r] = __builtin_fmaf(d, __builtin_fmaf(8.0f, cs[r], ct[r]), yv[r]);
+        return yv;
+    };
+    Part cur;
+    if (first < items) load_part(first, cur);
+    for (uint32_t c0i = first; c0i < items; c0i += kLazy * groups) {  // uniform per workgroup
+        // each item's partial tile goes to LDS as soon as it is formed
+#pragma unroll
+        for (int i = 0; i < kLazy; ++i) {
+            const uint32_t item = c0i + static_cast<uint32_t>(i) * groups;
+            if (item >= items) break;  // uniform
+            const uint32_t next = item + groups;
+            f32x4 yv = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (b < nb) {  // uniform
+                const Part pt = cur;
+                if (next < items) load_part(next, cur);  // the next item's block under this one's MFMAs
+                yv = block_mfma(pt, yv);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) part[i][kw][4 * lg + r][li] = yv[r];
+        }
+        __syncthreads();
+        {
+            const int i = tid >> 8, tok = (tid >> 4) & 15, row = tid & 15;
+            const uint32_t item = c0i + static_cast<uint32_t>(i) * groups;
+            const uint32_t m = tok0 + static_cast<uint32_t>(tok);
+            const uint32_t n = (item / token_tiles) * 16u + static_cast<uint32_t>(row);
+            if (i < kLazy && item < items && m < M && n < N) {
+                float v = part[i][0][tok][row];
+#pragma unroll
+                for (int k = 1; k < KS; ++k) v += part[i][k][tok][row];
+                if (__builtin_expect(not_finite(v), 0))
+                    v = kq_exact_thread<Fmt::Q6K>(w + static_cast<size_t>(n) * row_bytes, x + static_cast<size_t>(m) * K,
+                                                  nb);
+                y[static_cast<size_t>(m) * N + n] = to_out<OutT>(v);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// The matrix-core tiles: 16-token tiles, one workgroup of 16 waves per CU,
+// one block per wave, so K <= 4096 (a Q4_K wave's activations for more
+// blocks outgrow its registers: 16 waves of two blocks, or 8 of four, spill);
+// x and w 16-byte aligned.  From 3 tokens for Q4_K and 5 for Q6_K: below
+// that the ring GEMV's single pass of four tokens is faster (4 x 4096 x
+// 14336 Q6_K: 18.5 us on the ring, 20.2 on the tile).
+template <Fmt F>
+bool kq_mfma_supported(const void* x, const void* w, uint32_t M, uint32_t K) {
+    const uint32_t nb = K / kSuper;
+    return M >= (F == Fmt::Q4K ? 3u : 5u) && M <= 64 && nb >= 1 && nb <= 16 &&
+           (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
+}
+
+template <Fmt F, typename OutT>
+hipError_t launch_kq_mfma(const void* x, const void* w, void* y, uint32_t M, uint32_t N, uint32_t K,
+                          hipStream_t stream) {
+    constexpr int KS = 16;
     const uint32_t token_tiles = (M + 15) / 16;
     const uint32_t row_tiles = (N + 15) / 16;
     const uint64_t items64 = static_cast<uint64_t>(row_tiles) * token_tiles;
@@ -1175,24 +1392,25 @@ hipError_t launch_kq4_mfma_ks(const void* x, const void* w, void* y, uint32_t M,
     uint32_t groups = static_cast<uint32_t>(device_cus());
     if (groups > items) groups = items;
     groups = (groups + unit - 1) / unit * unit;
-    hipLaunchKernelGGL((kq4_mfma_kernel<KS, STEPS, OutT>), dim3(groups), dim3(KS * 64), 0, stream,
-                       static_cast<const uint16_t*>(x), static_cast<const uint8_t*>(w), static_cast<OutT*>(y), M, N, K,
-                       token_tiles, items, groups / 8u);
+    const auto* xp = static_cast<const uint16_t*>(x);
+    const auto* wp = static_cast<const uint8_t*>(w);
+    auto* yp = static_cast<OutT*>(y);
+    if constexpr (F == Fmt::Q4K)
+        hipLaunchKernelGGL((kq4_mfma_kernel<KS, 1, OutT>), dim3(groups), dim3(KS * 64), 0, stream, xp, wp, yp, M, N, K,
+                           token_tiles, items, groups / 8u);
+    else if (K % 2048 == 0)
+        hipLaunchKernelGGL((kq6_mfma_kernel<KS, true, OutT>), dim3(groups), dim3(KS * 64), 0, stream, xp, wp, yp, M, N,
+                           K, token_tiles, items, groups / 8u);
+    else
+        hipLaunchKernelGGL((kq6_mfma_kernel<KS, false, OutT>), dim3(groups), dim3(KS * 64), 0, stream, xp, wp, yp, M, N,
+                           K, token_tiles, items, groups / 8u);
     return hipGetLastError();
-}
-
-template <typename OutT>
-hipError_t launch_kq4_mfma(const void* x, const void* w, void* y, uint32_t M, uint32_t N, uint32_t K,
-                           hipStream_t stream) {
-    return launch_kq4_mfma_ks<16, 1, OutT>(x, w, y, M, N, K, stream);
 }
 
 template <Fmt F, typename OutT>
 hipError_t launch_gemv(const void* x, const void* w, void* y, uint32_t M, uint32_t N, uint32_t K,
                        hipStream_t stream) {
-    if constexpr (F == Fmt::Q4K) {
-        if (kq4_mfma_supported(x, w, M, K)) return launch_kq4_mfma<OutT>(x, w, y, M, N, K, stream);
-    }
+    if (kq_mfma_supported<F>(x, w, M, K)) return launch_kq_mfma<F, OutT>(x, w, y, M, N, K, stream);
     if (ring_supported<F>(x, w, K)) {
         if (M == 1) return launch_ring_mt<F, 1, OutT>(x, w, y, M, N, K, stream);
         if (M == 2) return launch_ring_mt<F, 2, OutT>(x, w, y, M, N, K, stream);

@@ -301,8 +301,8 @@ KQ_MODES = ["full", "subnormal", "special", "special_x"]
 # and 8 slices and one, two and four tokens per pass (Q4_K with the
 # activations staged per workgroup at one slice), the LDS-staged fallback
 # (activations off the 16-byte grid) with one to eight tokens per group, and
-# the Q4_K matrix-core tile (3-64 tokens, K <= 4096; Q6_K takes the ring
-# there): a partial 16-token tile, one and a half tiles, ragged rows
+# the matrix-core tiles (3 or 5 to 64 tokens, K <= 4096): a partial 16-token
+# tile, one and a half tiles, ragged rows
 KQ_SHAPES = [(1, 40, 1024, 0), (2, 24, 8192, 0), (4, 20, 16384, 0), (3, 12, 32768, 0), (1, 33, 2048, 2),
              (5, 16, 4096, 2), (6, 40, 4096, 0), (24, 19, 2048, 0)]
 
