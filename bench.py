@@ -355,6 +355,72 @@ SWEEP = (
 )
 
 
+# The plan table's workloads (op: 0 linear, 1 fused gate/up; M, K, N): the
+# decode linears (1 x 4096 x 4096, the Llama-3-8B up/gate and down), the
+# reference benchmark's 11 008 shapes, the skinny sweep (2-32 tokens, K =
+# 4096, N = 4096 / 6144 / 14 336) and the prefill linears and gate/up (64,
+# 256, 512 tokens, 4096 x 14 336).
+PLAN_SHAPES = (
+    [(0, 1, 4096, 4096), (0, 1, 4096, 14336), (0, 1, 14336, 4096), (0, 1, 4096, 11008), (0, 1, 11008, 4096)]
+    + [(0, m, 4096, n) for n in (4096, 6144, 14336) for m in (2, 4, 8, 16, 32)]
+    + [(op, m, 4096, 14336) for op in (0, 1) for m in (64, 256, 512)]
+)
+
+
+class ForcedCase:
+    """A LinearCase run through a dispatch context with one variant forced."""
+
+    def __init__(self, case: LinearCase, dispatch: "ops.Q4_0Dispatch") -> None:
+        self.case, self.dispatch = case, dispatch
+
+    def launch(self, i: int, stream: Stream) -> None:
+        c, bufs = self.case, self.case.wb[i % self.case.copies]
+        if c.gate_up:
+            self.dispatch.gate_up_silu(c.xb.ptr, bufs[0].ptr, bufs[1].ptr, c.yb.ptr, c.m, c.n, c.k, stream)
+        else:
+            self.dispatch.linear(c.xb.ptr, bufs[0].ptr, c.yb.ptr, c.m, c.n, c.k, stream)
+
+    def algorithmic_bytes(self) -> int:
+        return self.case.algorithmic_bytes()
+
+
+def run_plan_table(stream: Stream, hip: HipRuntime, path: str, steps: int = 50, warmup: int = 5,
+                   samples: int = 3) -> None:
+    """Times every candidate variant of every PLAN_SHAPES workload (the median
+    of `samples` kernel means over `steps` graph-replayed calls, weights
+    rotated past the MALL) and writes the entries as the C++ initialiser list
+    that q4_0_api.hip compiles in as its plan table."""
+    d = ops.Q4_0Dispatch()
+    lines = []
+    print(f"{'op':<8}{'M':>5}{'K':>7}{'N':>7}  {'fastest':<48}{'us':>8}  this build's plan (us)", file=sys.stderr)
+    for op, m, k, n in PLAN_SHAPES:
+        case = LinearCase(m, n, k, workload=4 if m >= 64 else (2 if m > 1 else 1), gate_up=op == 1)
+        d.force(None)
+        names = d.candidates(m, n, k, gate_up=op == 1)
+        timed = []
+        for name in names:
+            d.force(name)
+            fc = ForcedCase(case, d)
+            us = sorted(time_case(fc, stream, hip, steps, warmup)["kernel_ms_mean"] * 1e3
+                        for _ in range(samples))[samples // 2]
+            timed.append((us, name))
+            lines.append(f"    {{{op}, {m}, {k}, {n}, \"{name}\", {us:.3f}}},")
+        d.force(None)
+        timed.sort()
+        by_name = {v: u for u, v in timed}
+        sel = d.select(m, n, k, gate_up=op == 1)  # the table compiled into this build, then the rules
+        print(f"{('gate/up' if op else 'linear'):<8}{m:>5}{k:>7}{n:>7}  {timed[0][1]:<48}{timed[0][0]:>8.2f}  "
+              f"{sel} ({by_name.get(sel, float('nan')):.2f})", file=sys.stderr, flush=True)
+        case.free()
+    d.close()
+    with open(path, "w") as f:
+        f.write("// The plan table: {op (0 linear, 1 gate/up), M, K, N, variant, kernel us}, every candidate of\n"
+                "// each workload, median of %d samples of %d graph-replayed calls (weights rotated past the\n"
+                "// MALL).  Generated on MI355X by: python bench.py --plan-table <this file>\n" % (samples, steps))
+        f.write("\n".join(lines) + "\n")
+    print(f"plan table: {len(lines)} entries -> {path}", file=sys.stderr, flush=True)
+
+
 class CopyRowsCase:
     """The probe library's row copy (one 256-thread workgroup per row), the
     smallest kernel of the norm's launch shape."""
@@ -889,6 +955,9 @@ def main() -> int:
                     help="time pure 16-byte reads of 9.46, 14.2 and 33.1 MB (the bytes of the 1 x 4096 x "
                          "{4096, 6144, 14336} linears) in many grid shapes: the HBM floor of the GEMVs "
                          "(probe library; stdout tables, no result line)")
+    ap.add_argument("--plan-table", default=None, metavar="PATH",
+                    help="time every candidate variant of the plan table's workloads, write the table "
+                         "(q4_0_api.hip's plan_table.inc) to PATH, and nothing else")
     ap.add_argument("--timeline", action="store_true",
                     help="per-wave timeline of the headline's decode ring kernel (probe library: the shipped "
                          "kernel body with real-time stamps; stdout tables, no result line)")
@@ -923,6 +992,9 @@ def main() -> int:
 
     stream = Stream()
     hip = HipRuntime()
+    if args.plan_table:
+        run_plan_table(stream, hip, args.plan_table)
+        return 0
     m, k, n = 1, 4096, 14336
     if args.profile_run:
         if args.profile_shape:

@@ -176,6 +176,13 @@ int mote_q4_0_dispatch_plan(void* handle, uint64_t rows, uint64_t output_feature
  * unsupported shape, hipErrorNotFound (500) when no variant fits. */
 int mote_q4_0_dispatch_select(void* handle, uint64_t rows, uint64_t output_features,
                               uint64_t input_features, int op, char* name, size_t capacity);
+/* No counterpart in the reference (for the plan-table benchmark, bench.py
+ * --plan-table): the comma-separated names of the variants the autotuner
+ * would time for a problem with 256-byte aligned operands, the rule-based
+ * heuristic's pick included.  Host only.  hipErrorInvalidValue (1) for an
+ * empty or unsupported shape or a buffer too small for the list. */
+int mote_q4_0_dispatch_candidates(void* handle, uint64_t rows, uint64_t output_features,
+                                  uint64_t input_features, int op, char* names, size_t capacity);
 int mote_q4_0_variant_count(void);
 const char* mote_q4_0_variant_name(int index);
 

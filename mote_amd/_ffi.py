@@ -70,6 +70,7 @@ SIGNATURES = {
     "mote_q4_0_dispatch_gate_up_silu": (_I, [_P, _P, _P, _P, _P, _U64, _U64, _U64, _I, _P]),
     "mote_q4_0_dispatch_plan": (_I, [_P, _U64, _U64, _U64, _I, _I, ctypes.c_char_p, _SZ]),
     "mote_q4_0_dispatch_select": (_I, [_P, _U64, _U64, _U64, _I, ctypes.c_char_p, _SZ]),
+    "mote_q4_0_dispatch_candidates": (_I, [_P, _U64, _U64, _U64, _I, ctypes.c_char_p, _SZ]),
     "mote_q4_0_variant_count": (_I, []),
     "mote_q4_0_variant_name": (ctypes.c_char_p, [_I]),
     "mote_hipblaslt_create": (_I, [ctypes.POINTER(_P)]),

@@ -422,8 +422,8 @@ const Variant* split_k_heuristic(const Problem& p, Op op) {
     return v && skinny_mfma_supports(*v, p) ? v : nullptr;
 }
 
-// Shape heuristic used when autotuning is off.
-const Variant* heuristic(const Problem& p, Op op) {
+// Rule-based shape heuristic: every shape the plan table does not list.
+const Variant* rules(const Problem& p, Op op) {
     const bool fast = fast_eligible(p);
     if (op == Op::LinearQ8) {
         // K a multiple of 256: Q8_0 rows through the per-wave LDS ring
@@ -808,6 +808,47 @@ const Variant* heuristic(const Problem& p, Op op) {
     // / 39.8 / 72.6 with two tokens per pass and 58.6 at 5 with four; 8 x
     // 3584 x 4608: 14.6 against 16.0)
     return by_name(p.M == 2 ? "gemv_r4_t2_k1" : "gemv_r4_t1_k1");
+}
+
+// Measured plans for the workloads the path is tuned on (the decode, skinny
+// and prefill linears and the fused gate/up at their benchmark shapes): every
+// candidate the autotuner would time for the shape, with its kernel time in
+// microseconds on MI355X (graph replays, weights rotated past the MALL), as
+// written by `bench.py --plan-table`.  A listed shape with operands on the
+// 16-byte grid (the class the table was measured in) runs its fastest entry
+// that supports the operands; every other shape runs the rules above.
+struct PlanEntry {
+    int op;  // Op
+    uint32_t m, k, n;
+    const char* variant;
+    double us;
+};
+constexpr PlanEntry kPlanTable[] = {
+#include "plan_table.inc"
+    {-1, 0, 0, 0, "", 0.0},  // end
+};
+
+const Variant* table_pick(const Problem& p, Op op) {
+    if (align_class(p) != 2) return nullptr;
+    const Variant* best = nullptr;
+    double best_us = 0.0;
+    for (const PlanEntry& e : kPlanTable) {
+        if (e.op != static_cast<int>(op) || e.m != p.M || e.k != p.K || e.n != p.N) continue;
+        const Variant* v = find_variant(e.variant);
+        if (!v || !kind_matches(*v, op) || !supports(*v, p)) continue;
+        if (!best || e.us < best_us) {
+            best = v;
+            best_us = e.us;
+        }
+    }
+    return best;
+}
+
+// The shape heuristic used when autotuning is off: the plan table, then the
+// rules.
+const Variant* heuristic(const Problem& p, Op op) {
+    if (const Variant* v = table_pick(p, op)) return v;
+    return rules(p, op);
 }
 
 hipError_t time_variant(const Variant& v, const Problem& p, float* ms) {
@@ -1251,6 +1292,36 @@ MOTE_EXPORT int mote_q4_0_dispatch_select(void* handle, uint64_t rows, uint64_t 
         if (!v) return hipErrorNotFound;
         std::strncpy(name, v->name, capacity - 1);
         name[capacity - 1] = '\0';
+        return 0;
+    } catch (...) {
+        return hipErrorUnknown;
+    }
+}
+
+MOTE_EXPORT int mote_q4_0_dispatch_candidates(void* handle, uint64_t rows, uint64_t output_features,
+                                             uint64_t input_features, int op, char* names, size_t capacity) noexcept {
+    auto* d = static_cast<mote::q4_0::Dispatcher*>(handle);
+    if (!d || !names || capacity == 0 || op < 0 || op > 2) return hipErrorInvalidValue;
+    names[0] = '\0';
+    if (rows == 0 || output_features == 0 || input_features == 0 || input_features % 32 != 0 ||
+        rows > UINT_MAX || output_features > UINT_MAX || input_features > 0x7fffffffull)
+        return hipErrorInvalidValue;
+    try {
+        const auto* base = reinterpret_cast<const uint8_t*>(uintptr_t{1} << 20);
+        const Problem p{base, base, op == static_cast<int>(Op::GateUp) ? base : nullptr, const_cast<uint8_t*>(base),
+                        static_cast<uint32_t>(rows), static_cast<uint32_t>(output_features),
+                        static_cast<uint32_t>(input_features), OutType::F32, nullptr};
+        std::lock_guard<std::mutex> lock(d->mutex);
+        std::vector<const Variant*> cands = candidates(p, static_cast<Op>(op));
+        const Variant* r = rules(p, static_cast<Op>(op));
+        if (r && std::find(cands.begin(), cands.end(), r) == cands.end()) cands.push_back(r);
+        std::string out;
+        for (const Variant* v : cands) {
+            if (!out.empty()) out += ',';
+            out += v->name;
+        }
+        if (out.size() + 1 > capacity) return hipErrorInvalidValue;
+        std::memcpy(names, out.c_str(), out.size() + 1);
         return 0;
     } catch (...) {
         return hipErrorUnknown;

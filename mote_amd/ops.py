@@ -174,6 +174,15 @@ class Q4_0Dispatch:
         self._check(lib().mote_q4_0_dispatch_select(self.handle, rows, n, k, op, buf, 64), "select Q4_0 variant")
         return buf.value.decode()
 
+    def candidates(self, rows, n, k, gate_up: bool = False, q8_0: bool = False) -> list[str]:
+        """The variants the autotuner would time for this shape (aligned
+        operands), the rule-based heuristic's pick included; host only."""
+        buf = ctypes.create_string_buffer(1 << 14)
+        op = 2 if q8_0 else int(gate_up)
+        self._check(lib().mote_q4_0_dispatch_candidates(self.handle, rows, n, k, op, buf, len(buf)),
+                    "list Q4_0 candidates")
+        return [v for v in buf.value.decode().split(",") if v]
+
     def close(self) -> None:
         if self.handle:
             lib().mote_q4_0_dispatch_destroy(self.handle)

@@ -2,16 +2,47 @@
 each configuration of the path plans, through mote_q4_0_dispatch_select,
 which runs the same heuristic as a call without launching.
 
-Every selected name must be a compiled variant; the decode, skinny, split-K,
-prefill, Q8_0 and fused gate/up shapes land on the kernels the measurements
-chose, including three tokens past K = 4096 (rows split over 2 or 4 waves up
-to K = 16384, the split-K tiles beyond)."""
+Every selected name must be a compiled variant.  The benchmark workloads
+(decode, skinny sweep, prefill, fused gate/up) run the fastest entry of the
+measured plan table compiled into the library (mote_amd/csrc/plan_table.inc,
+written by bench.py --plan-table); every other decode, skinny, split-K,
+prefill, Q8_0 and fused gate/up shape lands on the kernel the rules chose,
+including three tokens past K = 4096 (rows split over 2 or 4 waves up to K =
+16384, the split-K tiles beyond)."""
 
 from __future__ import annotations
+
+import os
+import re
 
 import pytest
 
 from mote_amd import HipError, ops
+
+PLAN_TABLE = os.path.join(os.path.dirname(__file__), "..", "mote_amd", "csrc", "plan_table.inc")
+
+# The benchmark workloads the plan table must list (op 0 linear, 1 gate/up;
+# M, K, N): configs 0-2 (decode, Llama-3-8B up/gate and down, the skinny
+# sweep), the reference benchmark's 11 008 shapes, and config 4's prefill
+# linear and fused gate/up.
+TABLE_SHAPES = (
+    [(0, 1, 4096, 4096), (0, 1, 4096, 14336), (0, 1, 14336, 4096), (0, 1, 4096, 11008), (0, 1, 11008, 4096)]
+    + [(0, m, 4096, n) for n in (4096, 6144, 14336) for m in (2, 4, 8, 16, 32)]
+    + [(op, m, 4096, 14336) for op in (0, 1) for m in (64, 256, 512)]
+)
+
+
+def plan_table() -> dict:
+    """{(op, M, K, N): [(us, variant), ...]} from the compiled-in table."""
+    rx = re.compile(r'\{(\d+), (\d+), (\d+), (\d+), "([^"]+)", ([0-9.]+)\}')
+    table: dict = {}
+    with open(PLAN_TABLE) as f:
+        for line in f:
+            m = rx.search(line)
+            if m:
+                op, mm, k, n = (int(v) for v in m.groups()[:4])
+                table.setdefault((op, mm, k, n), []).append((float(m.group(6)), m.group(5)))
+    return table
 
 
 @pytest.fixture(scope="module")
@@ -100,10 +131,35 @@ LINEAR = [
 ]
 
 
-@pytest.mark.parametrize("shape,want", LINEAR, ids=[f"{m}x{k}x{n}" for (m, k, n), _ in LINEAR])
+# shapes the plan table lists are decided by it (tested below), the rest by the rules
+LINEAR_RULES = [(s, v) for s, v in LINEAR if (0, *s) not in plan_table()]
+
+
+@pytest.mark.parametrize("shape,want", LINEAR_RULES, ids=[f"{m}x{k}x{n}" for (m, k, n), _ in LINEAR_RULES])
 def test_linear_plans(d, shape, want):
     m, k, n = shape
     assert d.select(m, n, k) == want
+
+
+def test_plan_table_lists_every_benchmark_workload():
+    """Every benchmark workload has measured candidates in the table, each a
+    compiled variant of the workload's kind, with positive times."""
+    table, names = plan_table(), set(ops.variant_names())
+    for shape in TABLE_SHAPES:
+        entries = table.get(shape)
+        assert entries and len(entries) >= 2, shape
+        for us, v in entries:
+            assert v in names and us > 0, (shape, v)
+            assert v.startswith("gateup_") == (shape[0] == 1), (shape, v)
+
+
+@pytest.mark.parametrize("shape", TABLE_SHAPES, ids=[f"{'gu' if o else 'lin'}-{m}x{k}x{n}" for o, m, k, n in TABLE_SHAPES])
+def test_benchmark_workloads_run_the_table_fastest_entry(d, shape):
+    """The plan of a listed workload (aligned operands) is its fastest
+    measured candidate."""
+    op, m, k, n = shape
+    fastest = min(plan_table()[shape])[1]
+    assert d.select(m, n, k, gate_up=op == 1) == fastest
 
 
 def test_every_selection_is_a_compiled_variant(d):
@@ -132,8 +188,6 @@ def test_gate_up_and_q8_plans(d):
     assert d.select(1, 14336, 4096, gate_up=True) == "gateup_stream_p1_d1_g1"
     assert d.select(2, 14336, 4096, gate_up=True) == "gateup_stream_p1_m2_d1q_g1"
     assert d.select(16, 14336, 4096, gate_up=True).startswith("gateup_skinny_")
-    assert d.select(256, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m128_n128_w1_k2"
-    assert d.select(64, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m64_n64_w2_k4"
     assert d.select(64, 28672, 8192, gate_up=True) == "gateup_mfma_x32s_m64_n128_w1_k4"
     assert d.select(32, 28672, 8192, gate_up=True) == "gateup_mfma_x32s_m64_n128_w1_k4"
     assert d.select(128, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m64_n128_w1_k4"
@@ -177,7 +231,6 @@ def test_gate_up_and_q8_plans(d):
     assert d.select(384, 14336, 4096, q8_0=True) == "q8_mfma_x32s_m128_n256_w1_k2"
     assert d.select(256, 4096, 4096, gate_up=True) == "gateup_mfma_x32s_m64_n64_w2_k4"
     assert d.select(512, 4096, 4096, gate_up=True) == "gateup_mfma_x32s_m64_n128_w1_k4"
-    assert d.select(256, 14336, 4096, gate_up=True) == "gateup_mfma_x32s_m128_n128_w1_k2"
 
 
 def test_forced_variant_and_bad_shapes(d):
