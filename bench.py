@@ -529,10 +529,14 @@ class DenseCase:
         self.ctx.close()
 
 
-def run_sweep(stream: Stream, hip: HipRuntime, steps: int, warmup: int, only: str | None = None) -> None:
+def run_sweep(stream: Stream, hip: HipRuntime, steps: int, warmup: int, only: str | None = None,
+              marker=None) -> None:
     """One line per configuration; the last column is the kernel variant the
     library's shape heuristic plans for it (the one the default entry points
-    launch).  `only`: just the linear configurations whose name contains it."""
+    launch).  `only`: just the linear configurations whose name contains it.
+    `marker`: called (and the stream synchronised) before every row and after
+    the last, so that a kernel trace can be cut into rows (--trace-markers)."""
+    mark = marker if marker is not None else (lambda: None)
     print(f"{'case':<15}{'M':>5}{'K':>7}{'N':>7}{'kernel us':>11}{'eager us':>10}{'GB/s':>9}"
           f"{'%HBM':>7}{'TFLOP/s':>9}{'%MFMA':>7}  kernel", file=sys.stderr)
     planner = ops.Q4_0Dispatch()  # no autotuning: the default entry points' heuristic
@@ -542,6 +546,7 @@ def run_sweep(stream: Stream, hip: HipRuntime, steps: int, warmup: int, only: st
         kq = kind if kind in ("q4_k", "q6_k") else None
         case = LinearCase(m, n, k, workload, x_uniform=uni, gate_up=kind is True, q8_0=kind == "q8",
                           reference_inputs=kind == "ref", kquant=kq)
+        mark()
         t = time_case(case, stream, hip, steps, warmup)
         us = t["kernel_ms_mean"] * 1e3
         w = case.wb[0]
@@ -564,9 +569,11 @@ def run_sweep(stream: Stream, hip: HipRuntime, steps: int, warmup: int, only: st
         case.free()
     planner.close()
     if only is not None:
+        mark()
         return
     for m in (64, 512):
         case = DenseCase(m, 14336, 4096)
+        mark()
         t = time_case(case, stream, hip, steps, max(warmup, 1))
         us = t["kernel_ms_mean"] * 1e3
         gbs = case.algorithmic_bytes() / (us * 1e-6) / 1e9
@@ -579,6 +586,7 @@ def run_sweep(stream: Stream, hip: HipRuntime, steps: int, warmup: int, only: st
     # bytes (32 rows of 8 KiB in and out) by one 256-thread workgroup per row.
     probe = load_probe()
     floor = CopyRowsCase(probe, NormRopeCase.TOKENS, NormRopeCase.HIDDEN * 2)
+    mark()
     t = time_case(floor, stream, hip, steps, warmup)
     us = t["kernel_ms_mean"] * 1e3
     gbs = floor.algorithmic_bytes() / (us * 1e-6) / 1e9
@@ -590,6 +598,7 @@ def run_sweep(stream: Stream, hip: HipRuntime, steps: int, warmup: int, only: st
              "rope q+k": "mote_hip_rope_qk_f16"}
     for kind in ("rmsnorm", "fused add+rmsnorm", "rope q+k"):
         case = NormRopeCase(kind)
+        mark()
         t = time_case(case, stream, hip, steps, warmup)
         us = t["kernel_ms_mean"] * 1e3
         gbs = case.algorithmic_bytes() / (us * 1e-6) / 1e9
@@ -597,6 +606,83 @@ def run_sweep(stream: Stream, hip: HipRuntime, steps: int, warmup: int, only: st
               f"{gbs:>9.0f}{100 * gbs / HBM_PEAK_GBS:>6.1f}%{0.0:>9.1f}{0.0:>6.1f}%  {entry[kind]}",
               file=sys.stderr, flush=True)
         case.free()
+    mark()
+
+
+def sweep_marker(stream: Stream):
+    """A row delimiter for kernel traces of the sweep: the probe library's row
+    copy with one 16-byte row (one workgroup; the copy-floor row copies 32 rows
+    of 8 KiB, so the two never look alike), then a synchronisation."""
+    probe = load_probe()
+    src, dst = DeviceBuffer(16), DeviceBuffer(16)
+    src.upload(np.zeros(16, dtype=np.uint8))
+
+    def mark() -> None:
+        _ffi.check(probe.mote_probe_copy_rows(src.ptr, dst.ptr, 1, 16, stream.handle), "sweep marker")
+        stream.synchronize()
+    return mark
+
+
+def trace_table(trace_csv: str, sweep_log: str) -> int:
+    """The sweep's kernel-trace table: cuts rocprofv3's kernel_trace.csv of a
+    `--sweep --trace-markers` run at the marker dispatches (one-workgroup row
+    copies), pairs each segment with the sweep row printed in the same order in
+    `sweep_log` (the run's stderr; the segment before the first marker is the
+    headline measurement), and prints per row every kernel with its grid in
+    workgroups and its average and minimum traced duration.  Runs on the CPU."""
+    import csv
+    with open(trace_csv, newline="") as f:
+        recs = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    rows, in_table = [], False
+    with open(sweep_log) as f:
+        for line in f:
+            if line.startswith("case ") and "kernel us" in line:
+                in_table = True
+                continue
+            if in_table and len(line) > 60 and line[15:].split() and line[15:].split()[0].isdigit():
+                name, rest = line[:15].strip(), line[15:].split()
+                rows.append((name, int(rest[0]), int(rest[1]), int(rest[2]), rest[-1]))
+    segments, cur = [], []
+    for r in recs:
+        groups = int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"]))
+        if "copy_rows_kernel" in r["Kernel_Name"] and groups == 1:
+            segments.append(cur)
+            cur = []
+        else:
+            cur.append(r)
+    segments.append(cur)
+    if len(segments) != len(rows) + 2:
+        print(f"trace_table: {len(segments)} segments for {len(rows)} sweep rows (+ headline, + tail)",
+              file=sys.stderr)
+        return 1
+
+    def short(name: str) -> str:
+        name = re.sub(r"^void ", "", name)
+        name = re.sub(r"^(mote::)?(q4_0::|kquant::|rope::)?(\(anonymous namespace\)::)?", "", name)
+        return re.sub(r"\(.*$", "", name)  # the parameter list
+
+    def describe(seg):
+        kernels = {}
+        for r in seg:
+            dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            groups = int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"]))
+            k = kernels.setdefault(short(r["Kernel_Name"]), {"n": 0, "sum": 0.0, "min": 1e30, "grid": groups})
+            k["n"] += 1
+            k["sum"] += dur
+            k["min"] = min(k["min"], dur)
+        main = [(k, v) for k, v in kernels.items() if "copyBuffer" not in k and "fillBuffer" not in k]
+        return (" + ".join(f"`{k}`" for k, _ in main), " + ".join(str(v["grid"]) for _, v in main),
+                " + ".join(f"{v['sum'] / v['n']:.2f}" for _, v in main),
+                " + ".join(f"{v['min']:.2f}" for _, v in main))
+
+    print("| workload | variant | kernel | grid (workgroups) | average µs | min µs |")
+    print("|---|---|---|---|---|---|")
+    k, g, a, mn = describe(segments[0])
+    print(f"| headline (bench.py default): M=1 K=4096 N=14336 | | {k} | {g} | {a} | {mn} |")
+    for (name, m, kk, n, variant), seg in zip(rows, segments[1:]):
+        k, g, a, mn = describe(seg)
+        print(f"| {name}: M={m} K={kk} N={n} | `{variant}` | {k} | {g} | {a} | {mn} |")
+    return 0
 
 
 READ_FLOOR_BYTES = (9_461_760, 14_188_544, 33_095_680)  # 1 x 4096 x {4096, 6144, 14336} linears
@@ -963,6 +1049,12 @@ def main() -> int:
                          "kernel body with real-time stamps; stdout tables, no result line)")
     ap.add_argument("--read-bytes", default=None, metavar="B1,B2,...",
                     help="with --read-floor: these byte counts (multiples of 16) instead")
+    ap.add_argument("--trace-markers", action="store_true",
+                    help="with --sweep: a one-workgroup marker kernel between rows, to cut a kernel trace "
+                         "of the run into rows (--trace-table)")
+    ap.add_argument("--trace-table", nargs=2, default=None, metavar=("KERNEL_TRACE_CSV", "SWEEP_LOG"),
+                    help="print the sweep's kernel-trace table from rocprofv3's kernel_trace.csv of a "
+                         "--sweep --trace-markers run and that run's stderr (CPU only)")
     args = ap.parse_args()
     # A crash inside a runtime or profiler call then names the Python line
     # (and so the C-ABI call) it happened in, and the probe library's report
@@ -971,6 +1063,8 @@ def main() -> int:
     faulthandler.enable()
     install_fault_report()
     SETTLE_S = max(args.settle_ms, 0.0) / 1e3
+    if args.trace_table:
+        return trace_table(*args.trace_table)
     if args.comparator:
         return run_comparator()
     if args.timeline:
@@ -1066,7 +1160,8 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     if args.sweep:
-        run_sweep(stream, hip, min(args.steps, 50), min(args.warmup, 5))
+        run_sweep(stream, hip, min(args.steps, 50), min(args.warmup, 5),
+                  marker=sweep_marker(stream) if args.trace_markers else None)
     case.free()
     stream.close()
     print(json.dumps(line), flush=True)
