@@ -1038,6 +1038,10 @@ __global__ __launch_bounds__(KS * 64) void kq4_mfma_kernel(const uint16_t* __res
         }
     }
 
+    // binary16 1024 and 64 in both halves of a VGPR, so that each
+    // mask-and-insert below is one v_and_or_b32 (a VOP3 takes no literal)
+    const DequantConsts dq = dequant_consts();
+
     // This lane's part of a row's block: the 16-byte header (d, dmin, the 12
     // scale bytes) and its 32 nibble bytes.
     struct Part {
@@ -1072,17 +1076,17 @@ __global__ __launch_bounds__(KS * 64) void kq4_mfma_kernel(const uint16_t* __res
             const uint32_t qa = q[2 * (t & 3)], qb = q[2 * (t & 3) + 1];
             f16x2 v[4];
             if (t < 4) {  // low nibbles: 1024 + q, then sc q
-                v[0] = as_h2((qa & 0x000F000Fu) | 0x64006400u);
-                v[1] = as_h2(((qa >> 8) & 0x000F000Fu) | 0x64006400u);
-                v[2] = as_h2((qb & 0x000F000Fu) | 0x64006400u);
-                v[3] = as_h2(((qb >> 8) & 0x000F000Fu) | 0x64006400u);
+                v[0] = as_h2((qa & 0x000F000Fu) | dq.c1024);
+                v[1] = as_h2(((qa >> 8) & 0x000F000Fu) | dq.c1024);
+                v[2] = as_h2((qb & 0x000F000Fu) | dq.c1024);
+                v[3] = as_h2(((qb >> 8) & 0x000F000Fu) | dq.c1024);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = __builtin_elementwise_fma(v[i], sc_lo, b_lo);
             } else {  // high nibbles: 64 + q, then sc q
-                v[0] = as_h2((qa & 0x00F000F0u) | 0x54005400u);
-                v[1] = as_h2(((qa >> 8) & 0x00F000F0u) | 0x54005400u);
-                v[2] = as_h2((qb & 0x00F000F0u) | 0x54005400u);
-                v[3] = as_h2(((qb >> 8) & 0x00F000F0u) | 0x54005400u);
+                v[0] = as_h2((qa & 0x00F000F0u) | dq.c64);
+                v[1] = as_h2(((qa >> 8) & 0x00F000F0u) | dq.c64);
+                v[2] = as_h2((qb & 0x00F000F0u) | dq.c64);
+                v[3] = as_h2(((qb >> 8) & 0x00F000F0u) | dq.c64);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = __builtin_elementwise_fma(v[i], sc_hi, b_hi);
             }
