@@ -56,6 +56,20 @@ __device__ __forceinline__ uint32_t nib_lo02(uint32_t q) { return ((q << 4) & kN
 __device__ __forceinline__ uint32_t nib_lo13(uint32_t q) { return ((q >> 4) & kNibbleField) | kOnePair; }
 __device__ __forceinline__ uint32_t nib_hi13(uint32_t q) { return ((q >> 8) & kNibbleField) | kOnePair; }
 
+// The same with binary16 (1, 1) held in a VGPR (`one`, from one_pair_reg()):
+// gfx9-family VOP3 instructions take no literal, so with the constant in a
+// register each mask-and-insert is one v_and_or_b32 instead of an AND and an
+// OR.  Bit-identical to the forms above.
+__device__ __forceinline__ uint32_t one_pair_reg() {
+    uint32_t one;
+    asm("v_mov_b32 %0, 0x3c003c00" : "=v"(one));
+    return one;
+}
+__device__ __forceinline__ uint32_t nib_hi02(uint32_t q, uint32_t one) { return (q & kNibbleField) | one; }
+__device__ __forceinline__ uint32_t nib_lo02(uint32_t q, uint32_t one) { return ((q << 4) & kNibbleField) | one; }
+__device__ __forceinline__ uint32_t nib_lo13(uint32_t q, uint32_t one) { return ((q >> 4) & kNibbleField) | one; }
+__device__ __forceinline__ uint32_t nib_hi13(uint32_t q, uint32_t one) { return ((q >> 8) & kNibbleField) | one; }
+
 __device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 
 // v_dot2_f32_f16: a.lo*b.lo + a.hi*b.hi + c with f32 accumulation.

@@ -46,6 +46,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int kg = wave % KSPLIT;
     const int rg = wave / KSPLIT;
+    const uint32_t one = one_pair_reg();  // binary16 (1, 1): one v_and_or_b32 per nibble pair
 
     const uint32_t logical = (blockIdx.x % 8u) * per_xcd + blockIdx.x / 8u;
     if (logical >= total) return;  // uniform for the workgroup, before any barrier
@@ -124,10 +125,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
             uint32_t u[32];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                u[4 * i + 0] = nib_hi02(q[i]);
-                u[4 * i + 1] = nib_lo02(q[i]);
-                u[4 * i + 2] = nib_lo13(q[i]);
-                u[4 * i + 3] = nib_hi13(q[i]);
+                u[4 * i + 0] = nib_hi02(q[i], one);
+                u[4 * i + 1] = nib_lo02(q[i], one);
+                u[4 * i + 2] = nib_lo13(q[i], one);
+                u[4 * i + 3] = nib_hi13(q[i], one);
             }
 #pragma unroll
             for (int t = 0; t < MT; ++t) {

@@ -50,6 +50,7 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(const uint16_t*
     const int lane = tid & 63;
     const int kg = wave % KS;
     const int rg = wave / KS;
+    const uint32_t one = one_pair_reg();  // binary16 (1, 1): one v_and_or_b32 per nibble pair
 
     const uint32_t tile = (blockIdx.x % 8u) * per_xcd + blockIdx.x / 8u;
     if (tile >= total) return;  // uniform for the workgroup, before any barrier
@@ -134,14 +135,14 @@ __global__ __launch_bounds__(kRowsThreads) void gemv_rows_kernel(const uint16_t*
         float a0 = c0, a1 = c1;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            a0 = dot2(nib_hi02(q[i]), xp[4 * i + 0], a0);
-            a0 = dot2(nib_lo02(q[i]), xp[4 * i + 1], a0);
-            a0 = dot2(nib_lo13(q[i]), xp[4 * i + 2], a0);
-            a0 = dot2(nib_hi13(q[i]), xp[4 * i + 3], a0);
-            a1 = dot2(nib_hi02(q[4 + i]), xp[16 + 4 * i + 0], a1);
-            a1 = dot2(nib_lo02(q[4 + i]), xp[16 + 4 * i + 1], a1);
-            a1 = dot2(nib_lo13(q[4 + i]), xp[16 + 4 * i + 2], a1);
-            a1 = dot2(nib_hi13(q[4 + i]), xp[16 + 4 * i + 3], a1);
+            a0 = dot2(nib_hi02(q[i], one), xp[4 * i + 0], a0);
+            a0 = dot2(nib_lo02(q[i], one), xp[4 * i + 1], a0);
+            a0 = dot2(nib_lo13(q[i], one), xp[4 * i + 2], a0);
+            a0 = dot2(nib_hi13(q[i], one), xp[4 * i + 3], a0);
+            a1 = dot2(nib_hi02(q[4 + i], one), xp[16 + 4 * i + 0], a1);
+            a1 = dot2(nib_lo02(q[4 + i], one), xp[16 + 4 * i + 1], a1);
+            a1 = dot2(nib_lo13(q[4 + i], one), xp[16 + 4 * i + 2], a1);
+            a1 = dot2(nib_hi13(q[4 + i], one), xp[16 + 4 * i + 3], a1);
         }
         float acc = __builtin_fmaf(d0, a0, 0.0f);
         acc = __builtin_fmaf(d1, a1, acc);
