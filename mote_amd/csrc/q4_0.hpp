@@ -74,8 +74,11 @@ hipError_t launch_zero_fill(void* y, uint64_t count, OutType out, hipStream_t st
 // scope.  Growing a buffer allocates, so the first call that needs more
 // scratch on a stream must not be under graph capture.
 hipError_t acquire_scratch(hipStream_t stream, size_t bytes, ScratchPool::Lease* lease);
-// Frees the scratch of a stream whose queued work has completed.
-hipError_t release_stream_scratch(hipStream_t stream);
+// Forgets a stream's scratch without waiting for its queued work: the buffers
+// are parked with an event recorded on the stream and freed once it has
+// completed (checked here, at later stream destroys and before the pool next
+// allocates).
+hipError_t park_stream_scratch(hipStream_t stream);
 hipError_t launch_decode_f32(const void* w, float* out, uint64_t rows, uint64_t cols,
                              hipStream_t stream);
 

@@ -998,7 +998,45 @@ int gate_up(Dispatcher* d, const void* input, const void* gate, const void* up, 
 
 namespace {
 
-int device_alloc(void** ptr, size_t bytes) { return static_cast<int>(hipMalloc(ptr, bytes)); }
+// Scratch of destroyed streams, parked until the work queued before the
+// destroy has completed: the buffers and an event recorded on the stream
+// just before it was destroyed.
+struct Parked {
+    hipEvent_t done;
+    std::vector<void*> buffers;
+};
+std::mutex g_parked_mu;
+std::vector<Parked>* g_parked = new std::vector<Parked>;  // lives until exit
+
+// Frees the parked buffers whose event has completed (a free that fails is
+// reported through the return value; its buffers are dropped either way).
+hipError_t reap_parked() {
+    std::lock_guard<std::mutex> lock(g_parked_mu);
+    hipError_t status = hipSuccess;
+    for (auto it = g_parked->begin(); it != g_parked->end();) {
+        const hipError_t q = hipEventQuery(it->done);
+        if (q == hipErrorNotReady) {
+            ++it;
+            continue;
+        }
+        for (void* p : it->buffers) {
+            const hipError_t f = hipFree(p);
+            if (status == hipSuccess) status = f;
+        }
+        (void)hipEventDestroy(it->done);
+        if (status == hipSuccess && q != hipSuccess) status = q;
+        it = g_parked->erase(it);
+    }
+    return status;
+}
+
+// Called only when the pool needs a new buffer, which never happens under
+// graph capture (an allocation there would fail anyway), so the event
+// queries of reap_parked() never run inside a capture.
+int device_alloc(void** ptr, size_t bytes) {
+    (void)reap_parked();
+    return static_cast<int>(hipMalloc(ptr, bytes));
+}
 int device_free(void* ptr) { return static_cast<int>(hipFree(ptr)); }
 
 ScratchPool& scratch_pool() {
@@ -1015,11 +1053,27 @@ hipError_t acquire_scratch(hipStream_t stream, size_t bytes, ScratchPool::Lease*
     return static_cast<hipError_t>(scratch_pool().acquire(dev, stream, bytes, lease));
 }
 
-hipError_t release_stream_scratch(hipStream_t stream) {
+hipError_t park_stream_scratch(hipStream_t stream) {
     int dev = 0;
-    const hipError_t e = hipGetDevice(&dev);
+    hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    return static_cast<hipError_t>(scratch_pool().release(dev, stream));
+    std::vector<void*> buffers = scratch_pool().detach(dev, stream);
+    if (buffers.empty()) return reap_parked();
+    hipEvent_t done = nullptr;
+    e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(done, stream);
+    if (e != hipSuccess) {
+        // no completion point to wait for: wait for the stream instead
+        if (done != nullptr) (void)hipEventDestroy(done);
+        const hipError_t sync = hipStreamSynchronize(stream);
+        const hipError_t freed = static_cast<hipError_t>(scratch_pool().free_all(buffers));
+        return sync != hipSuccess ? sync : (freed != hipSuccess ? freed : e);
+    }
+    {
+        std::lock_guard<std::mutex> lock(g_parked_mu);
+        g_parked->push_back(Parked{done, std::move(buffers)});
+    }
+    return reap_parked();
 }
 
 }  // namespace mote::q4_0

@@ -51,15 +51,17 @@ MOTE_EXPORT int mote_hip_stream_create(void** stream) noexcept {
     return static_cast<int>(status);
 }
 
-// Before the stream goes, its queued work is waited for and the split-K
-// scratch the library keeps for it is freed, so a stream created later at the
-// same address starts without it.
+// Destroys the stream without waiting for its queued work, as the reference
+// does (crates/mote-backend-hip/src/hipblaslt_shim.cpp:307).  The split-K
+// scratch the library keeps for the stream is detached first, so a stream
+// created later at the same address starts without it, and freed once the
+// work queued before the destroy has completed (an event recorded on the
+// stream marks that point).
 MOTE_EXPORT int mote_hip_stream_destroy(void* stream) noexcept {
     const auto s = static_cast<hipStream_t>(stream);
-    hipError_t status = hipStreamSynchronize(s);
-    if (status != hipSuccess) return static_cast<int>(status);
+    hipError_t status = hipSuccess;
     try {
-        status = mote::q4_0::release_stream_scratch(s);
+        status = mote::q4_0::park_stream_scratch(s);
     } catch (...) {
         status = hipErrorUnknown;
     }

@@ -13,10 +13,12 @@
 //
 // A buffer grows to the next power of two (at least 1 MiB) when a call needs
 // more.  The outgrown buffer is retired, not freed, because kernels queued
-// earlier on the stream may still read it; retired buffers are freed by
-// release(), which the caller invokes only once the stream's work has
-// completed (the library does so in mote_hip_stream_destroy, after
-// synchronising the stream).
+// earlier on the stream may still read it.  detach() forgets a stream and
+// hands back all of its buffers (current and retired) without freeing them:
+// the library's mote_hip_stream_destroy parks them with an event recorded on
+// the stream and frees them once that event has completed, so destroying a
+// stream never waits for its queued work.  release() frees them at once, for
+// a caller that knows the stream's work has completed.
 #pragma once
 
 #include <cstddef>
@@ -94,29 +96,43 @@ class ScratchPool {
         return 0;
     }
 
-    // Frees every buffer of (device, stream) and forgets the stream.  The
-    // caller guarantees the stream has no queued work left.  Returns the
-    // first failing free's status, else 0.
-    int release(int device, const void* stream) {
+    // Forgets (device, stream) and returns every buffer it held (the current
+    // one and the retired ones), which the caller now owns and frees once the
+    // stream's queued work has completed; a stream created later at the same
+    // address starts without a buffer.  Waits for a lease still held.
+    std::vector<void*> detach(int device, const void* stream) {
         std::shared_ptr<Entry> entry;
         {
             std::lock_guard<std::mutex> guard(map_mu_);
             auto found = entries_.find({device, stream});
-            if (found == entries_.end()) return 0;
+            if (found == entries_.end()) return {};
             entry = std::move(found->second);
             entries_.erase(found);
         }
         std::lock_guard<std::mutex> lock(entry->mu);  // waits for a lease still held
-        int status = 0;
-        entry->retired.push_back(entry->ptr);
-        for (void* p : entry->retired) {
-            if (p == nullptr) continue;
-            const int s = free_(p);
-            if (status == 0) status = s;
-        }
+        std::vector<void*> out;
+        for (void* p : entry->retired)
+            if (p != nullptr) out.push_back(p);
+        if (entry->ptr != nullptr) out.push_back(entry->ptr);
         entry->retired.clear();
         entry->ptr = nullptr;
         entry->size = 0;
+        return out;
+    }
+
+    // Frees every buffer of (device, stream) and forgets the stream.  The
+    // caller guarantees the stream has no queued work left.  Returns the
+    // first failing free's status, else 0.
+    int release(int device, const void* stream) { return free_all(detach(device, stream)); }
+
+    // Frees buffers handed out by detach(); returns the first failing free's
+    // status, else 0.
+    int free_all(const std::vector<void*>& buffers) {
+        int status = 0;
+        for (void* p : buffers) {
+            const int s = free_(p);
+            if (status == 0) status = s;
+        }
         return status;
     }
 

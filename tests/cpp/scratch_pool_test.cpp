@@ -174,7 +174,39 @@ void test_release_waits_for_a_held_lease() {
 
 }  // namespace
 
+
+void test_detach_hands_back_every_buffer_once() {
+    ScratchPool pool(fake_alloc, fake_free);
+    const void* stream = reinterpret_cast<const void*>(0x3000);
+    const int frees0 = g_frees;
+    {
+        ScratchPool::Lease a;
+        CHECK(pool.acquire(0, stream, 1 << 20, &a) == 0);
+    }
+    {
+        ScratchPool::Lease b;  // grows: the first buffer is retired
+        CHECK(pool.acquire(0, stream, 3 << 20, &b) == 0);
+        CHECK(b.fresh());
+    }
+    std::vector<void*> parked = pool.detach(0, stream);
+    CHECK(parked.size() == 2);
+    CHECK(g_frees == frees0);          // nothing freed yet: the caller owns them
+    CHECK(pool.streams() == 0);        // the stream is forgotten
+    CHECK(pool.detach(0, stream).empty());
+    {
+        ScratchPool::Lease c;  // a stream created later at the same address starts afresh
+        CHECK(pool.acquire(0, stream, 1 << 20, &c) == 0);
+        CHECK(c.fresh());
+        for (void* p : parked) CHECK(c.ptr() != p);
+    }
+    CHECK(pool.free_all(parked) == 0);
+    CHECK(g_frees == frees0 + 2);
+    CHECK(pool.release(0, stream) == 0);
+    CHECK(g_frees == frees0 + 3);
+}
+
 int main() {
+    test_detach_hands_back_every_buffer_once();
     test_calls_on_one_stream_stay_adjacent();
     test_streams_do_not_wait_for_each_other();
     test_growth_retires_and_release_frees_everything();

@@ -185,6 +185,55 @@ def test_scratch_growth_with_launches_in_flight(oracle):
     s.close()
 
 
+def test_stream_destroyed_with_split_k_work_queued(oracle):
+    """mote_hip_stream_destroy does not wait for the stream's work, as in the
+    reference: split-K calls (a small one, then one that grows the scratch)
+    are queued on a new stream that is destroyed at once, three times over,
+    so later streams may reuse the address while the parked scratch of the
+    earlier ones is still in use.  Every output must match the oracle, and
+    once the device is idle the next stream destroy frees every parked
+    buffer."""
+    import ctypes
+
+    from mote_amd._ffi import check, lib
+    from mote_amd.device import DeviceBuffer, Stream, memory_info
+
+    hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime the library is linked against
+    d = ops.Q4_0Dispatch()
+    d.force("skinny_mfma_k8_s1_t2_d1_g1_r1_tr_l8_c_w_sk")  # 14 parts of 2048 at K = 28672
+    k, n_max = 28672, 8192
+    w = q4_weights(wl.seed_for(46, 1), n_max, k)
+    wb = DeviceBuffer.from_array(w)
+    rounds = []
+    for r in range(3):
+        calls = []
+        for m, n in [(16, 4096), (64, 8192)]:  # 4 MB of partial tiles, then 32 MB
+            x = normal_x(wl.seed_for(46, 10 * r + m), m, k)
+            calls.append((m, n, x, DeviceBuffer.from_array(x), DeviceBuffer(m * n * 4)))
+        rounds.append(calls)
+    check(hip.hipDeviceSynchronize(), "device synchronize")
+    free_before = memory_info()[0]
+    for calls in rounds:
+        s = Stream()
+        for m, n, _, xb, yb in calls:
+            d.linear(xb.ptr, wb.ptr, yb.ptr, m, n, k, s)
+        check(lib().mote_hip_stream_destroy(s.handle), "destroy stream")
+        s.handle = 0
+    check(hip.hipDeviceSynchronize(), "device synchronize")
+    idle = Stream()
+    check(lib().mote_hip_stream_destroy(idle.handle), "destroy stream")  # frees what is parked
+    idle.handle = 0
+    free_after = memory_info()[0]
+    assert free_after >= free_before - (8 << 20), f"parked scratch not freed: {free_before - free_after} bytes held"
+    row_bytes = wl.q4_0_row_bytes(k)
+    for r, calls in enumerate(rounds):
+        for m, n, x, _, yb in calls:
+            y = yb.download(np.float32).reshape(m, n)
+            check_against_oracle(oracle, y, x, w[: n * row_bytes], m, n, k, columns=sample_columns(n, 48),
+                                 what=f"destroyed stream {r}: {m}x{n}x{k}")
+    d.close()
+
+
 @pytest.mark.parametrize("m,k,n,kind", [(4, 5120, 5120, "linear"), (32, 3072, 8192, "linear"), (64, 5120, 1024, "linear"),
                                         (8, 3072, 8192, "gate_up"), (24, 2048, 5632, "gate_up"),
                                         (4, 5120, 5120, "q8"), (40, 3072, 3072, "q8")])
