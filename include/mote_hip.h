@@ -44,8 +44,11 @@ int mote_hip_mem_get_info(size_t* free_bytes, size_t* total_bytes);
  * rows of K/32 blocks of 18 bytes), f32 accumulation, one f16 rounding.
  * Status: null pointer or K % 32 != 0 -> 1 (hipErrorInvalidValue);
  * rows == 0 or N == 0 -> 0, nothing launched; rows * N > UINT_MAX -> 9
- * (hipErrorInvalidConfiguration); K == 0 launches and writes zeros; K >
- * 2^31 - 1 -> 9; else the launch status.  Output must not alias the inputs. */
+ * (hipErrorInvalidConfiguration); K == 0 launches and writes zeros; else the
+ * launch status.  K above 2^31 - 1 (64-bit sizes, as in the reference) runs
+ * per-element products over K parts of each output, added in part order, with
+ * the partials in the stream's split-K scratch.  Output must not alias the
+ * inputs. */
 int mote_hip_quantized_linear_q4_0_f16(const void* input, const void* weights, void* output,
                                        uint64_t rows, uint64_t output_features,
                                        uint64_t input_features, void* stream);
@@ -66,7 +69,8 @@ int mote_hip_quantized_linear_q4_0_f32(const void* input, const void* weights, v
  * array, and it keeps the last call's contents: calls that overlap in time on
  * one GPU (several streams or threads) race.  A problem whose partial tiles
  * need more than 16 MiB (M x N x K-parts x 4 bytes) returns 2
- * (hipErrorOutOfMemory) before any launch. */
+ * (hipErrorOutOfMemory) before any launch; K above 2^31 - 1 keeps its K-part
+ * partials there too. */
 int mote_hip_quantized_linear_q4_0_f32_no_alloc(const void* input, const void* weights, void* output,
                                                 uint64_t rows, uint64_t output_features,
                                                 uint64_t input_features, void* stream);
@@ -171,9 +175,10 @@ int mote_q4_0_dispatch_plan(void* handle, uint64_t rows, uint64_t output_feature
                             char* name, size_t capacity);
 /* The variant the context would plan for a problem with 256-byte aligned
  * operands (op: 0 linear, 1 gate/up, 2 Q8_0 linear): the forced variant, else
- * the shape heuristic's choice.  Host only: nothing is launched or cached,
- * and no device is needed.  hipErrorInvalidValue (1) for an empty or
- * unsupported shape, hipErrorNotFound (500) when no variant fits. */
+ * the shape heuristic's choice ("wide_k" for K above 2^31 - 1, which a forced
+ * variant cannot run).  Host only: nothing is launched or cached, and no
+ * device is needed.  hipErrorInvalidValue (1) for an empty or unsupported
+ * shape, hipErrorNotFound (500) when no variant fits. */
 int mote_q4_0_dispatch_select(void* handle, uint64_t rows, uint64_t output_features,
                               uint64_t input_features, int op, char* name, size_t capacity);
 /* No counterpart in the reference (for the plan-table benchmark, bench.py

@@ -67,6 +67,10 @@ bool skinny_mfma_supports(const Variant& v, const Problem& p);
 bool prefill_supports(const Variant& v, const Problem& p);
 
 hipError_t launch_zero_fill(void* y, uint64_t count, OutType out, hipStream_t stream);
+// K above 2^31 - 1 (p.K unused; the fused gate/up when p.w_up is set): 64-bit
+// per-element products over K parts of each output, then the parts added in
+// part order.  The partials use the split-K scratch (p.scratch when set).
+hipError_t launch_wide_k(const Problem& p, uint64_t k, bool q8);
 
 // Split-K scratch owned by the library, one buffer per (device, stream)
 // (scratch_pool.hpp): the lease holds the stream's scratch lock, so a caller

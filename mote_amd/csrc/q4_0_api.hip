@@ -967,8 +967,20 @@ int check_linear(const void* input, const void* weights, const void* output, uin
     if (k % 32 != 0) return hipErrorInvalidValue;
     if (rows == 0 || n == 0) return hipSuccess;
     if (rows > UINT_MAX || n > UINT_MAX || rows > UINT_MAX / n) return hipErrorInvalidConfiguration;
-    if (k > 0x7fffffffull) return hipErrorInvalidConfiguration;
     return -1;
+}
+
+// The largest K of the tiled kernels (32-bit K and element offsets); larger K
+// runs the 64-bit path of q4_0_wide_k.hip, outside the plans.
+constexpr uint64_t kMaxTiledK = 0x7fffffffull;
+
+int wide(Dispatcher* d, const Problem& problem, uint64_t k, bool q8) {
+    Dispatcher& disp = d ? *d : default_dispatcher();
+    std::lock_guard<std::mutex> lock(disp.mutex);
+    if (!disp.forced.empty())
+        return fail(d, hipErrorInvalidValue, "forced Q4_0 variant '" + disp.forced + "' cannot run K > 2^31 - 1");
+    const hipError_t e = launch_wide_k(problem, k, q8);
+    return e == hipSuccess ? 0 : fail(d, e, "wide-K launch failed");
 }
 
 int linear(Dispatcher* d, const void* input, const void* weights, void* output, uint64_t rows,
@@ -977,6 +989,10 @@ int linear(Dispatcher* d, const void* input, const void* weights, void* output, 
     if (pre >= 0) return pre == 0 ? 0 : fail(d, static_cast<hipError_t>(pre), "invalid quantized linear arguments");
     const auto s = static_cast<hipStream_t>(stream);
     if (k == 0) return static_cast<int>(launch_zero_fill(output, rows * n, out, s));
+    if (k > kMaxTiledK)
+        return wide(d, Problem{input, weights, nullptr, output, static_cast<uint32_t>(rows), static_cast<uint32_t>(n),
+                               0, out, s},
+                    k, op == Op::LinearQ8);
     const Problem p{input, weights, nullptr, output, static_cast<uint32_t>(rows),
                     static_cast<uint32_t>(n), static_cast<uint32_t>(k), out, s};
     return run(d ? *d : default_dispatcher(), p, op);
@@ -989,6 +1005,9 @@ int gate_up(Dispatcher* d, const void* input, const void* gate, const void* up, 
     const auto s = static_cast<hipStream_t>(stream);
     if (k == 0) return static_cast<int>(launch_zero_fill(output, rows * n, out, s));
     if (up == nullptr) up = static_cast<const uint8_t*>(gate) + n * (k / 32) * 18;
+    if (k > kMaxTiledK)
+        return wide(d, Problem{input, gate, up, output, static_cast<uint32_t>(rows), static_cast<uint32_t>(n), 0, out, s},
+                    k, false);
     const Problem p{input, gate, up, output, static_cast<uint32_t>(rows), static_cast<uint32_t>(n),
                     static_cast<uint32_t>(k), out, s};
     return run(d ? *d : default_dispatcher(), p, Op::GateUp);
@@ -1157,9 +1176,15 @@ MOTE_EXPORT int mote_hip_quantized_linear_q4_0_f32_no_alloc(const void* input, c
         const hipError_t e = no_alloc_scratch(&buf);
         if (e != hipSuccess) return static_cast<int>(e);
         Problem p{input, weights, nullptr, output, static_cast<uint32_t>(rows), static_cast<uint32_t>(output_features),
-                  static_cast<uint32_t>(input_features), OutType::F32, s};
+                  input_features > kMaxTiledK ? 0u : static_cast<uint32_t>(input_features), OutType::F32, s};
         p.scratch = static_cast<float*>(buf);
         p.scratch_bytes = kNoAllocScratchBytes;
+        if (input_features > kMaxTiledK) {
+            Dispatcher& d = default_dispatcher();
+            std::lock_guard<std::mutex> lock(d.mutex);
+            if (!d.forced.empty()) return hipErrorInvalidValue;
+            return static_cast<int>(launch_wide_k(p, input_features, false));
+        }
         return run_no_alloc(default_dispatcher(), p);
     } catch (...) {
         return hipErrorUnknown;
@@ -1332,9 +1357,16 @@ MOTE_EXPORT int mote_q4_0_dispatch_select(void* handle, uint64_t rows, uint64_t 
     if (!d || !name || capacity == 0 || op < 0 || op > 2) return hipErrorInvalidValue;
     name[0] = '\0';
     if (rows == 0 || output_features == 0 || input_features == 0 || input_features % 32 != 0 ||
-        rows > UINT_MAX || output_features > UINT_MAX || input_features > 0x7fffffffull)
+        rows > UINT_MAX || output_features > UINT_MAX)
         return hipErrorInvalidValue;
     try {
+        if (input_features > kMaxTiledK) {  // the 64-bit path, which no variant name forces
+            std::lock_guard<std::mutex> lock(d->mutex);
+            if (!d->forced.empty()) return hipErrorNotFound;
+            std::strncpy(name, "wide_k", capacity - 1);
+            name[capacity - 1] = '\0';
+            return 0;
+        }
         // Stand-in operands at the library's 256-byte allocation alignment;
         // nothing is dereferenced or launched.
         const auto* base = reinterpret_cast<const uint8_t*>(uintptr_t{1} << 20);

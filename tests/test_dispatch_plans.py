@@ -244,6 +244,22 @@ def test_forced_variant_and_bad_shapes(d):
             d.select(*shape)
 
 
+def test_k_past_the_tiled_kernels_plans_the_64_bit_path(d):
+    """K above 2^31 - 1 (the reference takes 64-bit sizes) runs the 64-bit
+    K-part path for every op; a forced variant cannot run it."""
+    assert d.select(1, 4096, (1 << 31) - 32) != "wide_k"
+    for k in (1 << 31, (1 << 31) + 32, 1 << 40):
+        assert d.select(1, 3, k) == "wide_k"
+        assert d.select(5, 7, k, gate_up=True) == "wide_k"
+        assert d.select(2, 3, k, q8_0=True) == "wide_k"
+    d.force("stream_d1q_g1")
+    try:
+        with pytest.raises(HipError):
+            d.select(1, 3, 1 << 31)
+    finally:
+        d.force(None)
+
+
 def test_plans_below_k_4096_and_past_16384(d):
     """Gate/up: three tokens at 2048 < K < 4096 on the stream with rows split
     2 ways (K = 4096 keeps the one-slice skinny tiles), 49-64 tokens below K =
