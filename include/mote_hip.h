@@ -25,7 +25,10 @@ extern "C" {
 /* ---- HIP runtime wrappers ------------------------------------------------ */
 /* [reference] crates/mote-backend-hip/src/hipblaslt_shim.cpp:259-324, bound at
  * crates/mote-backend-hip/src/ffi.rs:42-61.  Raw hipError_t; -1 for a null
- * out-parameter. */
+ * out-parameter.  mote_hip_stream_create also allocates the stream's 64 MiB
+ * split-K scratch (so split-K linears on it allocate nothing up to that
+ * size); mote_hip_stream_destroy does not wait for the stream, and frees that
+ * scratch once the work queued before it has completed. */
 int mote_hip_get_device_count(int* count);
 int mote_hip_set_device(int ordinal);
 int mote_hip_malloc(void** pointer, size_t bytes);

@@ -75,9 +75,15 @@ hipError_t launch_wide_k(const Problem& p, uint64_t k, bool q8);
 // Split-K scratch owned by the library, one buffer per (device, stream)
 // (scratch_pool.hpp): the lease holds the stream's scratch lock, so a caller
 // queues every kernel that uses the buffer before the lease goes out of
-// scope.  Growing a buffer allocates, so the first call that needs more
-// scratch on a stream must not be under graph capture.
+// scope.  Growing a buffer allocates, which a stream under graph capture may
+// not do: there an acquire beyond the buffer's size returns
+// hipErrorStreamCaptureUnsupported and allocates nothing.
 hipError_t acquire_scratch(hipStream_t stream, size_t bytes, ScratchPool::Lease* lease);
+// Sizes a stream's scratch to at least `bytes` ahead of its first split-K
+// call (a new buffer gets its tile counters cleared on the stream).
+hipError_t reserve_stream_scratch(hipStream_t stream, size_t bytes);
+// Frees the parked scratch of destroyed streams whose work has completed.
+hipError_t reap_parked_scratch();
 // Forgets a stream's scratch without waiting for its queued work: the buffers
 // are parked with an event recorded on the stream and freed once it has
 // completed (checked here, at later stream destroys and before the pool next

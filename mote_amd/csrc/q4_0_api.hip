@@ -422,8 +422,19 @@ const Variant* split_k_heuristic(const Problem& p, Op op) {
     return v && skinny_mfma_supports(*v, p) ? v : nullptr;
 }
 
+bool splits_k(const Variant& v) {
+    const size_t n = std::strlen(v.name);
+    return n > 3 && std::strcmp(v.name + n - 3, "_sk") == 0;
+}
+
+const Variant* split_k(const Problem& p, Op op, bool split_ok) {
+    return split_ok ? split_k_heuristic(p, op) : nullptr;
+}
+
 // Rule-based shape heuristic: every shape the plan table does not list.
-const Variant* rules(const Problem& p, Op op) {
+// split_ok false leaves out the split-K tiles (which need scratch): the
+// choice of a call under graph capture whose stream has too little.
+const Variant* rules(const Problem& p, Op op, bool split_ok) {
     const bool fast = fast_eligible(p);
     if (op == Op::LinearQ8) {
         // K a multiple of 256: Q8_0 rows through the per-wave LDS ring
@@ -498,7 +509,7 @@ const Variant* rules(const Problem& p, Op op) {
         }
         if (fast && p.M <= 64) {
             if (const Variant* v = skinny_q8_heuristic(p)) return v;
-            if (const Variant* v = split_k_heuristic(p, op)) return v;
+            if (const Variant* v = split_k(p, op, split_ok)) return v;
         }
         if (fast && p.M >= 64) {
             // The prefill tiles with 68-byte pairs: the largest 32 x 32 MFMA
@@ -578,7 +589,7 @@ const Variant* rules(const Problem& p, Op op) {
         }
         if (fast && p.M <= 64) {
             if (const Variant* v = skinny_gate_up_heuristic(p)) return v;
-            if (const Variant* v = split_k_heuristic(p, op)) return v;
+            if (const Variant* v = split_k(p, op, split_ok)) return v;
         }
         if (fast && p.M > 32) {
             // 32 x 32 MFMA tiles with staging waves once 128 x 128 tiles give
@@ -639,7 +650,7 @@ const Variant* rules(const Problem& p, Op op) {
     if (p.M == 64) {
         // 64 tokens still run as a skinny GEMM (faster than the prefill tiles).
         const Variant* v = skinny_heuristic(p);
-        if (!v) v = split_k_heuristic(p, op);
+        if (!v) v = split_k(p, op, split_ok);
         if (v) return v;
     }
     if (p.M >= 64) {
@@ -791,7 +802,7 @@ const Variant* rules(const Problem& p, Op op) {
         if (v && gemv_stream_supports(*v, p)) return v;
     }
     if (const Variant* v = skinny_heuristic(p)) return v;
-    if (const Variant* v = split_k_heuristic(p, op)) return v;
+    if (const Variant* v = split_k(p, op, split_ok)) return v;
     // one K slice of 2048 or 1024 (K that no split fits)
     for (const char* name : {"skinny_mfma_k8_s1_t1_d1_g1_r1", "skinny_mfma_k4_s1_t1_d1_g1_r1"}) {
         const Variant* v = by_name(name);
@@ -828,14 +839,14 @@ constexpr PlanEntry kPlanTable[] = {
     {-1, 0, 0, 0, "", 0.0},  // end
 };
 
-const Variant* table_pick(const Problem& p, Op op) {
+const Variant* table_pick(const Problem& p, Op op, bool split_ok) {
     if (align_class(p) != 2) return nullptr;
     const Variant* best = nullptr;
     double best_us = 0.0;
     for (const PlanEntry& e : kPlanTable) {
         if (e.op != static_cast<int>(op) || e.m != p.M || e.k != p.K || e.n != p.N) continue;
         const Variant* v = find_variant(e.variant);
-        if (!v || !kind_matches(*v, op) || !supports(*v, p)) continue;
+        if (!v || !kind_matches(*v, op) || !supports(*v, p) || (!split_ok && splits_k(*v))) continue;
         if (!best || e.us < best_us) {
             best = v;
             best_us = e.us;
@@ -846,9 +857,9 @@ const Variant* table_pick(const Problem& p, Op op) {
 
 // The shape heuristic used when autotuning is off: the plan table, then the
 // rules.
-const Variant* heuristic(const Problem& p, Op op) {
-    if (const Variant* v = table_pick(p, op)) return v;
-    return rules(p, op);
+const Variant* heuristic(const Problem& p, Op op, bool split_ok = true) {
+    if (const Variant* v = table_pick(p, op, split_ok)) return v;
+    return rules(p, op, split_ok);
 }
 
 hipError_t time_variant(const Variant& v, const Problem& p, float* ms) {
@@ -915,7 +926,18 @@ int run(Dispatcher& d, const Problem& problem, Op op) {
         if (!supports(*v, p)) return fail(&d, hipErrorInvalidValue, std::string("cached plan ") + v->name +
                                                                       " cannot run this problem");
     }
-    const hipError_t err = v->launch(p);
+    hipError_t err = v->launch(p);
+    if (err == hipErrorStreamCaptureUnsupported && splits_k(*v) && d.forced.empty()) {
+        // Under graph capture the stream's split-K scratch was too small (a
+        // capture may not allocate) and nothing was queued: this call runs
+        // the best plan without split K instead (the cached plan stays for
+        // eager calls, which size the scratch).
+        const Variant* f = heuristic(p, op, false);
+        if (f && supports(*f, p)) {
+            v = f;
+            err = f->launch(p);
+        }
+    }
     if (err != hipSuccess) return fail(&d, err, std::string("launch of ") + v->name + " failed");
     d.last_error.clear();
     return 0;
@@ -1067,10 +1089,29 @@ ScratchPool& scratch_pool() {
 
 hipError_t acquire_scratch(hipStream_t stream, size_t bytes, ScratchPool::Lease* lease) {
     int dev = 0;
-    const hipError_t e = hipGetDevice(&dev);
+    hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    return static_cast<hipError_t>(scratch_pool().acquire(dev, stream, bytes, lease));
+    // A stream under graph capture must not allocate: its buffer is used if
+    // it is large enough, else hipErrorStreamCaptureUnsupported before any
+    // launch.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &capture);
+    if (e != hipSuccess) return e;
+    const int status = scratch_pool().acquire(dev, stream, bytes, lease, capture == hipStreamCaptureStatusNone);
+    if (status == ScratchPool::kWouldAllocate) return hipErrorStreamCaptureUnsupported;
+    return static_cast<hipError_t>(status);
 }
+
+hipError_t reserve_stream_scratch(hipStream_t stream, size_t bytes) {
+    ScratchPool::Lease lease;
+    const hipError_t e = acquire_scratch(stream, bytes, &lease);
+    if (e != hipSuccess) return e;
+    if (!lease.fresh()) return hipSuccess;
+    // a new buffer: its split-K tile counters start at zero
+    return launch_zero_fill(lease.ptr(), kSplitKCounterBytes / 4, OutType::F32, stream);
+}
+
+hipError_t reap_parked_scratch() { return reap_parked(); }
 
 hipError_t park_stream_scratch(hipStream_t stream) {
     int dev = 0;
@@ -1399,7 +1440,7 @@ MOTE_EXPORT int mote_q4_0_dispatch_candidates(void* handle, uint64_t rows, uint6
                         static_cast<uint32_t>(input_features), OutType::F32, nullptr};
         std::lock_guard<std::mutex> lock(d->mutex);
         std::vector<const Variant*> cands = candidates(p, static_cast<Op>(op));
-        const Variant* r = rules(p, static_cast<Op>(op));
+        const Variant* r = rules(p, static_cast<Op>(op), true);
         if (r && std::find(cands.begin(), cands.end(), r) == cands.end()) cands.push_back(r);
         std::string out;
         for (const Variant* v : cands) {

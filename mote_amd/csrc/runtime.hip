@@ -42,13 +42,36 @@ MOTE_EXPORT int mote_hip_memcpy_device_to_host(void* destination, const void* so
     return static_cast<int>(hipMemcpy(destination, source, bytes, hipMemcpyDeviceToHost));
 }
 
+// Split-K scratch each stream created here gets up front: the partial tiles
+// of every split-K shape up to 64 tokens of a 70B-class MLP (64 x 28 672 x
+// 8192 fused gate/up: 58.7 MB), so split-K calls on the stream allocate
+// nothing up to that size, under graph capture too.
+constexpr std::size_t kStreamScratchBytes = std::size_t{64} << 20;
+
+// As in the reference (crates/mote-backend-hip/src/hipblaslt_shim.cpp:296-305),
+// plus the stream's split-K scratch; a stream whose scratch cannot be
+// allocated is destroyed again and the error returned.
 MOTE_EXPORT int mote_hip_stream_create(void** stream) noexcept {
     if (stream == nullptr) return kInvalidArgument;
     *stream = nullptr;
     hipStream_t native = nullptr;
-    const hipError_t status = hipStreamCreate(&native);
+    hipError_t status = hipStreamCreate(&native);
+    if (status != hipSuccess) return static_cast<int>(status);
+    try {
+        status = mote::q4_0::reserve_stream_scratch(native, kStreamScratchBytes);
+    } catch (...) {
+        status = hipErrorUnknown;
+    }
+    if (status != hipSuccess) {
+        try {
+            (void)mote::q4_0::park_stream_scratch(native);
+        } catch (...) {
+        }
+        (void)hipStreamDestroy(native);
+        return static_cast<int>(status);
+    }
     *stream = native;
-    return static_cast<int>(status);
+    return 0;
 }
 
 // Destroys the stream without waiting for its queued work, as the reference
@@ -69,8 +92,17 @@ MOTE_EXPORT int mote_hip_stream_destroy(void* stream) noexcept {
     return static_cast<int>(status != hipSuccess ? status : destroyed);
 }
 
+// As in the reference; afterwards the parked scratch of destroyed streams
+// whose work has completed is freed.
 MOTE_EXPORT int mote_hip_stream_synchronize(void* stream) noexcept {
-    return static_cast<int>(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    const hipError_t status = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    if (status == hipSuccess) {
+        try {
+            (void)mote::q4_0::reap_parked_scratch();
+        } catch (...) {
+        }
+    }
+    return static_cast<int>(status);
 }
 
 MOTE_EXPORT int mote_hip_mem_get_info(std::size_t* free_bytes, std::size_t* total_bytes) noexcept {

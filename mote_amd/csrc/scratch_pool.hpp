@@ -13,7 +13,9 @@
 //
 // A buffer grows to the next power of two (at least 1 MiB) when a call needs
 // more.  The outgrown buffer is retired, not freed, because kernels queued
-// earlier on the stream may still read it.  detach() forgets a stream and
+// earlier on the stream may still read it.  A caller that must not allocate
+// (a stream under graph capture) acquires with may_allocate false and gets
+// kWouldAllocate instead of a growth.  detach() forgets a stream and
 // hands back all of its buffers (current and retired) without freeing them:
 // the library's mote_hip_stream_destroy parks them with an event recorded on
 // the stream and frees them once that event has completed, so destroying a
@@ -67,9 +69,13 @@ class ScratchPool {
         bool fresh_ = false;
     };
 
+    // Status of an acquire that would have to allocate but may not.
+    static constexpr int kWouldAllocate = -2;
+
     // Blocks while another lease of the same (device, stream) is held.
-    // Returns 0, or the allocator's status (the lease is then not held).
-    int acquire(int device, const void* stream, std::size_t bytes, Lease* lease) {
+    // Returns 0, kWouldAllocate, or the allocator's status (the lease is then
+    // not held).
+    int acquire(int device, const void* stream, std::size_t bytes, Lease* lease, bool may_allocate = true) {
         std::shared_ptr<Entry> entry;
         {
             std::lock_guard<std::mutex> guard(map_mu_);
@@ -80,6 +86,7 @@ class ScratchPool {
         std::unique_lock<std::mutex> lock(entry->mu);
         lease->fresh_ = false;
         if (entry->size < bytes) {
+            if (!may_allocate) return kWouldAllocate;
             std::size_t want = std::size_t{1} << 20;
             while (want < bytes) want <<= 1;
             void* fresh = nullptr;

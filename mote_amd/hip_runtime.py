@@ -34,7 +34,19 @@ class HipRuntime:
         h.hipGraphExecDestroy.argtypes = [P]
         h.hipGraphDestroy.argtypes = [P]
         h.hipMemcpy.argtypes = [P, P, ctypes.c_size_t, ctypes.c_int]
+        h.hipStreamCreate.argtypes = [ctypes.POINTER(P)]
+        h.hipDeviceSynchronize.argtypes = []
         self.h = h
+
+    def foreign_stream(self) -> "ForeignStream":
+        """A stream made by hipStreamCreate directly, as a caller's own
+        stream would be (the library has reserved no scratch for it)."""
+        s = ctypes.c_void_p()
+        _ffi.check(self.h.hipStreamCreate(ctypes.byref(s)), "create stream")
+        return ForeignStream(s.value)
+
+    def device_synchronize(self) -> None:
+        _ffi.check(self.h.hipDeviceSynchronize(), "device synchronize")
 
     def create(self) -> int:
         e = ctypes.c_void_p()
@@ -77,3 +89,20 @@ class HipRuntime:
 
     def copy_device_to_device(self, dst: int, src: int, nbytes: int) -> None:
         _ffi.check(self.h.hipMemcpy(dst, src, nbytes, self.DEVICE_TO_DEVICE), "device-to-device copy")
+
+
+class ForeignStream:
+    """A HIP stream the library did not create; close() hands it to
+    mote_hip_stream_destroy, which also parks the scratch the library kept
+    for it."""
+
+    def __init__(self, handle: int) -> None:
+        self.handle = handle
+
+    def synchronize(self) -> None:
+        _ffi.check(_ffi.lib().mote_hip_stream_synchronize(self.handle), "synchronize stream")
+
+    def close(self) -> None:
+        if self.handle:
+            _ffi.check(_ffi.lib().mote_hip_stream_destroy(self.handle), "destroy stream")
+            self.handle = 0

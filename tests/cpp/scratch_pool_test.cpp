@@ -205,8 +205,44 @@ void test_detach_hands_back_every_buffer_once() {
     CHECK(g_frees == frees0 + 3);
 }
 
+void test_acquire_that_may_not_allocate() {
+    ScratchPool pool(fake_alloc, fake_free);
+    const void* stream = reinterpret_cast<const void*>(0x5000);
+    const int allocs0 = g_allocs;
+    {
+        ScratchPool::Lease a;  // no buffer yet: refused, nothing allocated, no lease held
+        CHECK(pool.acquire(0, stream, 64, &a, false) == ScratchPool::kWouldAllocate);
+        CHECK(!a.held());
+        CHECK(g_allocs == allocs0);
+    }
+    void* first = nullptr;
+    {
+        ScratchPool::Lease b;  // an allocating acquire sizes the buffer (1 MiB)
+        CHECK(pool.acquire(0, stream, 64, &b) == 0);
+        first = b.ptr();
+    }
+    {
+        ScratchPool::Lease c;  // fits: the same buffer, no allocation
+        CHECK(pool.acquire(0, stream, 1 << 20, &c, false) == 0);
+        CHECK(c.held() && c.ptr() == first && !c.fresh());
+    }
+    {
+        ScratchPool::Lease d;  // would grow: refused, the buffer kept
+        CHECK(pool.acquire(0, stream, (1 << 20) + 1, &d, false) == ScratchPool::kWouldAllocate);
+        CHECK(!d.held());
+    }
+    CHECK(g_allocs == allocs0 + 1);
+    {
+        ScratchPool::Lease e;  // the refusal left the stream usable
+        CHECK(pool.acquire(0, stream, 1 << 20, &e) == 0);
+        CHECK(e.ptr() == first);
+    }
+    CHECK(pool.release(0, stream) == 0);
+}
+
 int main() {
     test_detach_hands_back_every_buffer_once();
+    test_acquire_that_may_not_allocate();
     test_calls_on_one_stream_stay_adjacent();
     test_streams_do_not_wait_for_each_other();
     test_growth_retires_and_release_frees_everything();

@@ -107,3 +107,61 @@ def test_decoder_step_graph_replays_match_eager(stream):
         hip.destroy_graph(exe)
         for b in bufs.values():
             b.free()
+
+
+def test_first_split_k_call_under_capture(oracle):
+    """A split-K call (16 tokens of the Llama-3-8B down projection, K = 14336)
+    captured before any eager call on its stream.  On a stream the library
+    created, the scratch reserved at creation holds the partial tiles, so the
+    graph runs the split-K tiles: bit for bit the eager result.  On the
+    caller's own stream the library has no scratch yet and a capture may not
+    allocate, so the captured call runs the best plan without split K (to the
+    oracle's tolerance); the next eager call sizes the scratch and runs the
+    split-K tiles again."""
+    from mote_amd.device import Stream
+    from test_gpu_q4_0 import check_against_oracle, sample_columns
+
+    m, n, k = 16, 4096, 14336
+    assert ops.Q4_0Dispatch().select(m, n, k).endswith("_sk")  # the shape plans the split-K tiles
+    hip = HipRuntime()
+    x, w = wl.normal_f16(52, m * k), wl.q4_0_weights(53, n, k)
+    xb, wb = DeviceBuffer.from_array(x), DeviceBuffer.from_array(w)
+    ys = {name: DeviceBuffer(m * n * 4) for name in ("eager", "graph", "foreign_graph", "foreign_eager")}
+    cols = sample_columns(n, 96)
+
+    def call(out, s):
+        return lambda: ops.quantized_linear_q4_0_f32(xb.ptr, wb.ptr, ys[out].ptr, m, n, k, s)
+
+    def result(out, s):
+        s.synchronize()
+        return ys[out].download(np.float32).reshape(m, n)
+
+    own, foreign = Stream(), hip.foreign_stream()
+    try:
+        for out in ys:
+            ys[out].upload(np.full(m * n * 4, 0xA5, dtype=np.uint8))
+        exe = hip.capture(own, call("graph", own))
+        try:
+            hip.launch_graph(exe, own)
+            graph = result("graph", own)
+        finally:
+            hip.destroy_graph(exe)
+        call("eager", own)()
+        eager = result("eager", own)
+        check_against_oracle(oracle, eager, x, w, m, n, k, columns=cols, what="eager split K")
+        assert np.array_equal(graph, eager), "the captured call on the library's stream is not the split-K result"
+
+        exe = hip.capture(foreign, call("foreign_graph", foreign))
+        try:
+            hip.launch_graph(exe, foreign)
+            captured = result("foreign_graph", foreign)
+        finally:
+            hip.destroy_graph(exe)
+        check_against_oracle(oracle, captured, x, w, m, n, k, columns=cols, what="captured without split K")
+        call("foreign_eager", foreign)()
+        assert np.array_equal(result("foreign_eager", foreign), eager), "the eager call after capture is not split K"
+    finally:
+        foreign.close()
+        own.close()
+        for b in [xb, wb, *ys.values()]:
+            b.free()

@@ -159,11 +159,14 @@ def test_llama_70b_gate_up_through_the_default_entry_point(stream, oracle, m):
 def test_scratch_growth_with_launches_in_flight(oracle):
     """Split-K calls on a new stream at growing sizes (then a small one),
     issued back to back with no synchronisation between them: the partial-tile
-    buffer grows from 128 KB to 32 MB while earlier launches may still read
-    the buffer they were given, and every output must match the oracle."""
-    from mote_amd.device import DeviceBuffer, Stream
+    buffer grows from 1 MiB to 32 MiB while earlier launches may still read
+    the buffer they were given, and every output must match the oracle.  The
+    stream is the caller's own (hipStreamCreate), so the library reserved no
+    scratch for it."""
+    from mote_amd.device import DeviceBuffer
+    from mote_amd.hip_runtime import HipRuntime
 
-    s = Stream()
+    s = HipRuntime().foreign_stream()
     d = ops.Q4_0Dispatch()
     d.force("skinny_mfma_k8_s1_t2_d1_g1_r1_tr_l8_c_w_sk")  # 14 parts of 2048 at K = 28672
     k, n_max = 28672, 8192
@@ -193,12 +196,11 @@ def test_stream_destroyed_with_split_k_work_queued(oracle):
     earlier ones is still in use.  Every output must match the oracle, and
     once the device is idle the next stream destroy frees every parked
     buffer."""
-    import ctypes
-
     from mote_amd._ffi import check, lib
     from mote_amd.device import DeviceBuffer, Stream, memory_info
+    from mote_amd.hip_runtime import HipRuntime
 
-    hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime the library is linked against
+    hip = HipRuntime()
     d = ops.Q4_0Dispatch()
     d.force("skinny_mfma_k8_s1_t2_d1_g1_r1_tr_l8_c_w_sk")  # 14 parts of 2048 at K = 28672
     k, n_max = 28672, 8192
@@ -211,19 +213,19 @@ def test_stream_destroyed_with_split_k_work_queued(oracle):
             x = normal_x(wl.seed_for(46, 10 * r + m), m, k)
             calls.append((m, n, x, DeviceBuffer.from_array(x), DeviceBuffer(m * n * 4)))
         rounds.append(calls)
-    check(hip.hipDeviceSynchronize(), "device synchronize")
+    idle = Stream()
+    hip.device_synchronize()
     free_before = memory_info()[0]
     for calls in rounds:
-        s = Stream()
+        s = Stream()  # 64 MiB of scratch reserved, 3 x 64 MiB parked by the three destroys
         for m, n, _, xb, yb in calls:
             d.linear(xb.ptr, wb.ptr, yb.ptr, m, n, k, s)
         check(lib().mote_hip_stream_destroy(s.handle), "destroy stream")
         s.handle = 0
-    check(hip.hipDeviceSynchronize(), "device synchronize")
-    idle = Stream()
-    check(lib().mote_hip_stream_destroy(idle.handle), "destroy stream")  # frees what is parked
-    idle.handle = 0
+    hip.device_synchronize()
+    idle.synchronize()  # frees the parked scratch whose work has completed
     free_after = memory_info()[0]
+    idle.close()
     assert free_after >= free_before - (8 << 20), f"parked scratch not freed: {free_before - free_after} bytes held"
     row_bytes = wl.q4_0_row_bytes(k)
     for r, calls in enumerate(rounds):

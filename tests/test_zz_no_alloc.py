@@ -74,22 +74,24 @@ def test_partial_tiles_beyond_the_array_are_rejected_before_launch(stream):
 
 
 def test_split_k_calls_allocate_nothing(stream, oracle):
-    """On a fresh stream that no allocating call has used, the no-allocation
-    entry point's split-K calls (64 x 14336 x 4096: 7 K parts, 7.3 MB of
-    partial tiles) leave the device's free memory unchanged; the per-stream
-    pool of the allocating entry point would allocate that buffer on the
-    stream's first split-K call.  The same call through the allocating entry
-    point on another stream loads every kernel first, and one decode call
-    (no scratch) pays any per-stream cost of the runtime before the
+    """On a fresh stream of the caller's own (hipStreamCreate: the library
+    has reserved no scratch for it) that no allocating call has used, the
+    no-allocation entry point's split-K calls (64 x 14336 x 4096: 7 K parts,
+    7.3 MB of partial tiles) leave the device's free memory unchanged; the
+    per-stream pool of the allocating entry point would allocate that buffer
+    on the stream's first split-K call.  The same call through the allocating
+    entry point on another stream loads every kernel first, and one decode
+    call (no scratch) pays any per-stream cost of the runtime before the
     measurement."""
-    from mote_amd.device import Stream, memory_info
+    from mote_amd.device import memory_info
+    from mote_amd.hip_runtime import HipRuntime
 
     m, k, n = 64, 14336, 4096
     assert ops.Q4_0Dispatch().select(m, n, k).endswith("_sk")
     x = wl.normal_f16(wl.seed_for(33, m), m * k)
     w = wl.q4_0_weights(wl.seed_for(33, n), n, k)
     want = _run(stream, ops.quantized_linear_q4_0_f32, x, w, m, n, k)
-    fresh = Stream()
+    fresh = HipRuntime().foreign_stream()
     try:
         xb, wb, yb = DeviceBuffer.from_array(x), DeviceBuffer.from_array(w), DeviceBuffer(m * n * 4)
         ops.quantized_linear_q4_0_f32_no_alloc(xb.ptr, wb.ptr, yb.ptr, 1, n, k, fresh)
