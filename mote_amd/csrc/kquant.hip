@@ -979,12 +979,65 @@ __device__ __forceinline__ uint32_t kq_pick(const uint32_t* x, int a, int b) {
 
 __device__ __forceinline__ uint32_t f16x2_bits(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 
+// Activations of one super-block (512 bytes per token) for the 16 tokens of a
+// token tile, loaded whole cache lines per instruction and handed out through
+// a wave-private LDS region.  Load instruction c covers tokens 2c and 2c + 1
+// (lanes 0-31 and 32-63, 16 bytes each), so each instruction reads 8 whole
+// 128-byte lines once; loaded per lane instead (each lane its own 128 bytes of
+// one token), every instruction touched 64 lines and the 16 waves' lines
+// outgrew the vector L1, which fetched them again.  Round r then passes tokens
+// 4r .. 4r + 3 through the region: every lane writes what it loaded for them,
+// and the lanes of those tokens (li = token) read the eight 16-byte chunks at
+// byte offsets off(0..7) of their token's slice (a wave's LDS operations
+// complete in order).  Tokens past M read row M - 1 (lines the wave already
+// holds in L1; loads skipped per instruction compiled to a chain of waits):
+// a token only feeds its own output row of the MFMA, and those rows are never
+// stored.  Rounds whose tokens all lie past M are skipped (uniform), and the
+// lanes of such tokens keep zeros.
+constexpr int kXRowBytes = 512 + 16;  // a token's slice plus padding, per LDS row
+constexpr int kXRoundTokens = 4;
+constexpr int kXStageBytes = kXRoundTokens * kXRowBytes;  // per wave
+
+template <typename Off>
+__device__ __forceinline__ void stage_block_x(const uint16_t* __restrict__ x, uint32_t K, uint32_t M, uint32_t tok0,
+                                              uint32_t b, int lane, uint8_t* xs, Off off, uint32_t (&xr)[32]) {
+    const int li = lane & 15;
+    u32x4 g[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const uint32_t m = min(tok0 + 2u * c + static_cast<uint32_t>(lane >> 5), M - 1);
+        g[c] = *reinterpret_cast<const u32x4*>(x + static_cast<size_t>(m) * K + static_cast<size_t>(b) * kSuper +
+                                               static_cast<uint32_t>(lane & 31) * 8u);
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) xr[i] = 0u;
+#pragma unroll
+    for (int r = 0; r < 16 / kXRoundTokens; ++r) {
+        if (tok0 + static_cast<uint32_t>(r * kXRoundTokens) < M) {  // uniform
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int tr = 2 * j + (lane >> 5);  // token within the round
+                *reinterpret_cast<u32x4*>(xs + tr * kXRowBytes + (lane & 31) * 16) = g[2 * r + j];
+            }
+            if (li / kXRoundTokens == r) {
+                const uint8_t* row = xs + (li % kXRoundTokens) * kXRowBytes;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const u32x4 v = *reinterpret_cast<const u32x4*>(row + off(c));
+                    xr[4 * c] = v.x; xr[4 * c + 1] = v.y; xr[4 * c + 2] = v.z; xr[4 * c + 3] = v.w;
+                }
+            }
+        }
+    }
+}
+
 template <int KS, int STEPS, typename OutT>
 __global__ __launch_bounds__(KS * 64) void kq4_mfma_kernel(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
                                                           OutT* __restrict__ y, uint32_t M, uint32_t N, uint32_t K,
                                                           uint32_t token_tiles, uint32_t items, uint32_t per_xcd) {
     constexpr int kLazy = KS * 64 / 256;  // items reduced together: one output per thread
     __shared__ float part[kLazy][KS][16][17];  // [item][wave][token][row]
+    __shared__ __attribute__((aligned(16))) uint8_t xstage[KS][kXStageBytes];
     const int tid = static_cast<int>(threadIdx.x);
     const int kw = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
     const uint32_t nb = K / kSuper;
@@ -1000,19 +1053,13 @@ __global__ __launch_bounds__(KS * 64) void kq4_mfma_kernel(const uint16_t* __res
     // sub-block sums as binary16 hi + lo pairs.  Tokens past M stay zero.
     uint32_t xa[STEPS][8][4];
     uint32_t s_hi[STEPS], s_lo[STEPS];
-    const bool live_tok = tok0 + static_cast<uint32_t>(li) < M;
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
         const uint32_t b = static_cast<uint32_t>(kw) + KS * static_cast<uint32_t>(s);
         uint32_t xr[32];
-        if (live_tok && b < nb) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(x + static_cast<size_t>(tok0 + li) * K +
-                                                              static_cast<size_t>(b) * kSuper + 64u * lg);
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const u32x4 v = src[c];
-                xr[4 * c] = v.x; xr[4 * c + 1] = v.y; xr[4 * c + 2] = v.z; xr[4 * c + 3] = v.w;
-            }
+        if (b < nb) {  // uniform
+            // lane (li, lg): elements 64 lg .. 64 lg + 63 of token li
+            stage_block_x(x, K, M, tok0, b, lane, xstage[kw], [&](int c) { return 128 * lg + 16 * c; }, xr);
         } else {
 #pragma unroll
             for (int i = 0; i < 32; ++i) xr[i] = 0u;
