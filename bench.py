@@ -350,7 +350,7 @@ SWEEP = (
     # K-quant GEMV (Q4_K, Q6_K): the decode-shaped linears
     + [(f"{f} {what}", m, k, n, 6, False, f) for f in ("q4_k", "q6_k")
        for what, m, k, n in (("decode", 1, 4096, 4096), ("up/gate", 1, 4096, 14336), ("down", 1, 14336, 4096),
-                             ("4 tok", 4, 4096, 14336), ("8 tok", 8, 4096, 14336), ("16 tok", 16, 4096, 14336),
+                             ("2 tok", 2, 4096, 14336), ("3 tok", 3, 4096, 14336), ("4 tok", 4, 4096, 14336), ("8 tok", 8, 4096, 14336), ("16 tok", 16, 4096, 14336),
                              ("32 tok", 32, 4096, 14336), ("64 tok", 64, 4096, 14336))]
 )
 

@@ -38,7 +38,7 @@
 //   Q4_K: sum_e x_e (d sc q_e - dmin m) = d sc 2^24 acc - dmin m S
 //   Q6_K: sum_e x_e d sc (q_e - 32)     = d sc (2^24 acc - 32 S).
 // The LDS-ring GEMV (kq_ring_kernel) streams the same arithmetic for 1-4
-// tokens per pass, and from 3 (Q4_K) or 5 (Q6_K) to 64 tokens at K <= 4096
+// tokens per pass, and from 2 (Q4_K) or 5 (Q6_K) to 64 tokens at K <= 4096
 // the matrix-core tiles (kq4_mfma_kernel, kq6_mfma_kernel) decode each block
 // once per 16-token tile into exact binary16 operands.
 // HBM-bound: algorithmic bytes per call are |W| + 2 M K + M N |y|.
@@ -1269,6 +1269,7 @@ __global__ __launch_bounds__(KS * 64) void kq6_mfma_kernel(const uint16_t* __res
                                                           uint32_t token_tiles, uint32_t items, uint32_t per_xcd) {
     constexpr int kLazy = KS * 64 / 256;  // items reduced together: one output per thread
     __shared__ float part[kLazy][KS][16][17];  // [item][wave][token][row]
+    __shared__ __attribute__((aligned(16))) uint8_t xstage[KS][kXStageBytes];
     const int tid = static_cast<int>(threadIdx.x);
     const int kw = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
     const uint32_t half = static_cast<uint32_t>(lg) >> 1, c0 = static_cast<uint32_t>(lg) & 1u;
@@ -1279,20 +1280,23 @@ __global__ __launch_bounds__(KS * 64) void kq6_mfma_kernel(const uint16_t* __res
     const uint32_t first = (blockIdx.x % 8u) * per_xcd + blockIdx.x / 8u;
     const uint32_t tok0 = (first % token_tiles) * 16u;
 
-    // The activations of this wave's block for the 16 tokens (tokens past M
-    // stay zero): quarter c0 + 2 h, elements 8 u .. 8 u + 7 in xa[4 h + u].
+    // The activations of this wave's block for the 16 tokens: quarter c0 + 2 h,
+    // elements 8 u .. 8 u + 7 in xa[4 h + u] (byte 256 half + 64 c0 + 128 h +
+    // 16 u of the token's slice).
     uint32_t xa[8][4];
-    if (tok0 + static_cast<uint32_t>(li) < M && b < nb) {
-        const u32x4* src = reinterpret_cast<const u32x4*>(x + static_cast<size_t>(tok0 + li) * K +
-                                                          static_cast<size_t>(b) * kSuper + 128u * half + 32u * c0);
+    {
+        uint32_t xr[32];
+        if (b < nb) {  // uniform
+            stage_block_x(x, K, M, tok0, b, lane, xstage[kw],
+                          [&](int t) { return 256 * half + 64 * c0 + 128 * (t >> 2) + 16 * (t & 3); }, xr);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) xr[i] = 0u;
+        }
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const u32x4 v = src[8 * (t >> 2) + (t & 3)];  // + 64 elements per h
-            xa[t][0] = v.x; xa[t][1] = v.y; xa[t][2] = v.z; xa[t][3] = v.w;
+            xa[t][0] = xr[4 * t]; xa[t][1] = xr[4 * t + 1]; xa[t][2] = xr[4 * t + 2]; xa[t][3] = xr[4 * t + 3];
         }
-    } else {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) xa[t][0] = xa[t][1] = xa[t][2] = xa[t][3] = 0u;
     }
 
     // This lane's part of a row's block: 32 ql bytes, the 32 qh bytes of its
@@ -1416,13 +1420,14 @@ __global__ __launch_bounds__(KS * 64) void kq6_mfma_kernel(const uint16_t* __res
 // The matrix-core tiles: 16-token tiles, one workgroup of 16 waves per CU,
 // one block per wave, so K <= 4096 (a Q4_K wave's activations for more
 // blocks outgrow its registers: 16 waves of two blocks, or 8 of four, spill);
-// x and w 16-byte aligned.  From 3 tokens for Q4_K and 5 for Q6_K: below
-// that the ring GEMV's single pass of four tokens is faster (4 x 4096 x
-// 14336 Q6_K: 18.5 us on the ring, 20.2 on the tile).
+// x and w 16-byte aligned.  From 2 tokens for Q4_K (2 x 4096 x 14336: 10.5 us
+// on the tile, 11.1 on the ring) and 5 for Q6_K: below that the ring GEMV's
+// single pass of up to four tokens is faster (3 / 4 x 4096 x 14336 Q6_K: 18.9
+// / 19.2 us on the ring, 19.7 on the tile).
 template <Fmt F>
 bool kq_mfma_supported(const void* x, const void* w, uint32_t M, uint32_t K) {
     const uint32_t nb = K / kSuper;
-    return M >= (F == Fmt::Q4K ? 3u : 5u) && M <= 64 && nb >= 1 && nb <= 16 &&
+    return M >= (F == Fmt::Q4K ? 2u : 5u) && M <= 64 && nb >= 1 && nb <= 16 &&
            (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
 }
 

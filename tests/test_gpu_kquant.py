@@ -153,7 +153,7 @@ SHAPES = [
     (1, 18, 28672),
     (4, 1000, 4096),
     (5, 12, 6144),
-    # the matrix-core tiles (3 for Q4_K, 5 for Q6_K, to 64 tokens, K <=
+    # the matrix-core tiles (2 for Q4_K, 5 for Q6_K, to 64 tokens, K <=
     # 4096): four full 16-token tiles, and two and a bit over odd-block rows
     # (Q6_K rows at 2 mod 4: the five-dword reads)
     (64, 40, 4096),
