@@ -705,16 +705,24 @@ __device__ __forceinline__ void ring_part_dot(uint32_t slot, uint32_t blk_off, u
             d * static_cast<float>(static_cast<int8_t>(sc[1] & 0xffu)),
             d * static_cast<float>(static_cast<int8_t>((sc[1] >> 8) & 0xffu)),
         };
-        const uint32_t sh_lo = 2 * c, sh_hi = 4 + 2 * c;
+        // The binary16-subnormal pairs straight from the bytes: quarter c's
+        // q = nibble | 2 qh bits << 4 in bits 0-5 of each half (q 2^-24), and
+        // quarter c + 2's in bits 4-9 (16 q 2^-24: its nibble masked in
+        // place, its qh bits shifted to 8-9; 16 q <= 1008 stays subnormal), so
+        // each pair is one mask and one v_and_or_b32 and the second quarter's
+        // sums carry 2^20 instead of 2^24.  qh bits 2c, 2c + 1 (quarter c) and
+        // 2c + 4, 2c + 5 (quarter c + 2) of bytes 0 and 2 reach bits 4-5 and
+        // 8-9 shifted left by 4 - 2c; those of bytes 1 and 3 shifted right by
+        // 4 + 2c.
+        const uint32_t sh02 = 4 - 2 * c, sh13 = 4 + 2 * c;
         uint32_t v02[2][8], v13[2][8];
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
-            const uint32_t vlo = (ql[w] & 0x0F0F0F0Fu) | (((qh[w] >> sh_lo) & 0x03030303u) << 4);
-            const uint32_t vhi = ((ql[w] >> 4) & 0x0F0F0F0Fu) | (((qh[w] >> sh_hi) & 0x03030303u) << 4);
-            v02[0][w] = vlo & 0x00FF00FFu;
-            v13[0][w] = (vlo >> 8) & 0x00FF00FFu;
-            v02[1][w] = vhi & 0x00FF00FFu;
-            v13[1][w] = (vhi >> 8) & 0x00FF00FFu;
+            const uint32_t l8 = ql[w] >> 8, h02 = qh[w] << sh02, h13 = qh[w] >> sh13;
+            v02[0][w] = (ql[w] & 0x000F000Fu) | (h02 & 0x00300030u);
+            v13[0][w] = (l8 & 0x000F000Fu) | (h13 & 0x00300030u);
+            v02[1][w] = (ql[w] & 0x00F000F0u) | (h02 & 0x03000300u);
+            v13[1][w] = (l8 & 0x00F000F0u) | (h13 & 0x03000300u);
         }
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
@@ -730,7 +738,7 @@ __device__ __forceinline__ void ring_part_dot(uint32_t slot, uint32_t blk_off, u
                         a = dot2(v13[r][w], lx.xr[m][16 * r + 2 * w + 1], a);
                     }
                     const float dsg = ds[2 * r + gi];
-                    v = __builtin_fmaf(dsg * 16777216.0f, a, v);
+                    v = __builtin_fmaf(dsg * (r ? 1048576.0f : 16777216.0f), a, v);
                     v = __builtin_fmaf(-32.0f * dsg, lx.sum[m][2 * r + gi], v);
                 }
             }
