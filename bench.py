@@ -737,6 +737,12 @@ def load_probe():
     probe.mote_probe_ring_timeline.argtypes = [P, P, P, U32, U32, P, ctypes.c_size_t, P]
     probe.mote_probe_ring_read.restype = ctypes.c_int
     probe.mote_probe_ring_read.argtypes = [P, U32, U32, P, ctypes.c_size_t, P]
+    probe.mote_probe_skinny_record_words.restype = U32
+    probe.mote_probe_skinny_record_words.argtypes = []
+    probe.mote_probe_skinny_waves.restype = U32
+    probe.mote_probe_skinny_waves.argtypes = [U32, U32]
+    probe.mote_probe_skinny_timeline.restype = ctypes.c_int
+    probe.mote_probe_skinny_timeline.argtypes = [P, P, P, U32, U32, U32, P, ctypes.c_size_t, P]
     return probe
 
 
@@ -883,6 +889,109 @@ def run_timeline(launches: int = 8) -> int:
         if c is not case:
             c.free()
     case.free()
+    stream.close()
+    return 0
+
+
+class SkinnyTimelineCase:
+    """The shipped skinny matrix-core kernel of 4-32 tokens at K = 4096
+    (skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w) with per-wave timestamps
+    (mote_probe_skinny_timeline), over the rotated weight copies of a
+    LinearCase; launch i writes its records to region i % regions."""
+
+    def __init__(self, probe, case: "LinearCase", regions: int) -> None:
+        self.probe, self.case, self.regions = probe, case, regions
+        self.waves = probe.mote_probe_skinny_waves(case.m, case.n)
+        self.words = probe.mote_probe_skinny_record_words()
+        self.region_bytes = self.waves * self.words * 4
+        self.stamps = DeviceBuffer(self.region_bytes * regions)
+
+    def launch(self, i: int, stream: Stream) -> None:
+        c = self.case
+        _ffi.check(self.probe.mote_probe_skinny_timeline(
+            c.xb.ptr, c.wb[i % c.copies][0].ptr, c.yb.ptr, c.m, c.n, c.k,
+            self.stamps.ptr + (i % self.regions) * self.region_bytes, self.region_bytes, stream.handle),
+            "skinny timeline probe")
+
+    def algorithmic_bytes(self) -> int:
+        return self.case.algorithmic_bytes()
+
+    def records(self) -> np.ndarray:
+        return self.stamps.download(np.uint32).reshape(self.regions, self.waves, self.words)
+
+    def free(self) -> None:
+        self.stamps.free()
+
+
+SKINNY_TIMELINE_VARIANT = "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w"
+
+
+def run_skinny_timeline(launches: int = 8, shapes=((4, 4096, 4096), (16, 4096, 4096), (32, 4096, 4096),
+                                                    (16, 4096, 6144), (16, 4096, 14336))) -> int:
+    """Per-phase timeline of the skinny matrix-core kernel the library plans
+    for the skinny sweep (M x 4096 x N): for each shape, event timings of the
+    library's planned call, of the variant forced, and of the probe's stamped
+    instantiation (graph replays of 200 launches), then the records of
+    `launches` back-to-back stamped launches (one graph, rotating weights,
+    replayed until the device has settled, then once more), summarised per
+    launch as markdown on stdout.  Times are the 100 MHz real-time clock (10 ns
+    ticks) relative to the first wave start of each launch; each workgroup's
+    16 waves share its items."""
+    probe = load_probe()
+    stream, hip = Stream(), HipRuntime()
+    d = ops.Q4_0Dispatch()
+    tick_us = 0.01
+    for m, k, n in shapes:
+        case = LinearCase(m, n, k, workload=2)
+        plan = d.select(m, n, k)
+        d.force(SKINNY_TIMELINE_VARIANT)
+        forced = ForcedCase(case, d)
+        tl = SkinnyTimelineCase(probe, case, launches)
+        timed = {f"planned call (`{plan}`)": time_case(case, stream, hip, 200, 20)["kernel_ms_mean"] * 1e3,
+                 f"`{SKINNY_TIMELINE_VARIANT}` forced": time_case(forced, stream, hip, 200, 20)["kernel_ms_mean"] * 1e3,
+                 "the same kernel, stamped (probe)": time_case(tl, stream, hip, 200, 20)["kernel_ms_mean"] * 1e3}
+        d.force(None)
+        exe = hip.capture(stream, lambda: [tl.launch(i, stream) for i in range(launches)])
+        try:
+            t0 = time.perf_counter()
+            while time.perf_counter() - t0 < max(SETTLE_S, 0.02):
+                hip.launch_graph(exe, stream)
+                stream.synchronize()
+            hip.launch_graph(exe, stream)
+            stream.synchronize()
+        finally:
+            hip.destroy_graph(exe)
+        rec = tl.records().astype(np.int64)
+        items = rec[0][:, 4]
+        groups = tl.waves // 16
+        print(f"\n## {m} × {k} × {n} ({groups} workgroups of 16 waves, {int(items.max())} item(s) of 16 rows "
+              f"per workgroup at most)\n")
+        print("| kernel | µs / launch | GB/s of the call's bytes |")
+        print("|---|---|---|")
+        for name, us in timed.items():
+            print(f"| {name} | {us:.3f} | {case.algorithmic_bytes() / (us * 1e-6) / 1e9:.0f} |")
+            print(f"timeline-skinny {m}x{k}x{n}: {name}: {us:.3f} us", file=sys.stderr, flush=True)
+        print("\nPhases of each launch (µs from the launch's first wave start; p10 / p50 / p90 / max over the "
+              "waves that own an item):\n")
+        print("| launch | last wave start | x converted | item 1 weights landed | item 1 MFMAs issued | "
+              "last item MFMAs issued | reduced and stored | wave end | gap to next launch |")
+        print("|---|---|---|---|---|---|---|---|---|")
+        for L in range(launches):
+            r = rec[L]
+            live = r[:, 4] > 0
+            base = r[:, 0].min()
+            rel = lambda a: ((a - base) & 0xFFFFFFFF) * tick_us  # noqa: E731
+            q = lambda a: " / ".join(f"{_pct(a, p):.2f}" for p in (10, 50, 90)) + f" / {a.max():.2f}"  # noqa: E731
+            last_issue = np.array([rel(r[w, 5 + 4 + int(r[w, 4]) - 1]) for w in np.nonzero(live)[0]])
+            end = rel(r[:, 3])
+            gap = "—"
+            if L + 1 < launches:
+                gap = f"{((rec[L + 1][:, 0].min() - base) & 0xFFFFFFFF) * tick_us - end.max():.2f}"
+            print(f"| {L} | {rel(r[:, 0]).max():.2f} | {q(rel(r[live, 1]))} | {q(rel(r[live, 5]))} | "
+                  f"{q(rel(r[live, 9]))} | {q(last_issue)} | {q(rel(r[live, 2]))} | {q(end[live])} | {gap} |")
+        tl.free()
+        case.free()
+    d.close()
     stream.close()
     return 0
 
@@ -1044,6 +1153,9 @@ def main() -> int:
     ap.add_argument("--plan-table", default=None, metavar="PATH",
                     help="time every candidate variant of the plan table's workloads, write the table "
                          "(q4_0_api.hip's plan_table.inc) to PATH, and nothing else")
+    ap.add_argument("--timeline-skinny", action="store_true",
+                    help="per-wave timeline of the skinny matrix-core kernel at the skinny sweep's K = 4096 shapes "
+                         "(probe library: the shipped kernel with timestamps), as markdown on stdout, and nothing else")
     ap.add_argument("--timeline", action="store_true",
                     help="per-wave timeline of the headline's decode ring kernel (probe library: the shipped "
                          "kernel body with real-time stamps; stdout tables, no result line)")
@@ -1069,6 +1181,8 @@ def main() -> int:
         return run_comparator()
     if args.timeline:
         return run_timeline()
+    if args.timeline_skinny:
+        return run_skinny_timeline()
     if args.read_floor:
         sizes = tuple(int(v) for v in args.read_bytes.split(",")) if args.read_bytes else READ_FLOOR_BYTES
         return run_read_floor(sizes)
