@@ -216,6 +216,21 @@ def test_read_probe_is_a_separate_library(lib):
     assert copy(FAKE, FAKE, 1, 24, STREAM) == 1  # row bytes not a multiple of 16
     assert copy(FAKE + 8, FAKE, 1, 16, STREAM) == 1  # misaligned
     assert copy(FAKE, FAKE, 0, 16, STREAM) == 0  # nothing to copy
+    # the skinny kernel's timeline instantiation (bench.py --timeline-skinny):
+    # 16 words per wave; only its form's K, 1-64 tokens, aligned x and w
+    words = probe.mote_probe_skinny_record_words
+    words.restype, words.argtypes = U32, []
+    assert words() == 16
+    tl = probe.mote_probe_skinny_timeline
+    tl.restype = ctypes.c_int
+    tl.argtypes = [P, P, P, U32, U32, U32, P, ctypes.c_size_t, P]
+    assert tl(None, FAKE, FAKE, 16, 4096, 4096, FAKE, 1 << 20, STREAM) == 1
+    assert tl(FAKE, FAKE, FAKE, 16, 4096, 4096, None, 1 << 20, STREAM) == 1
+    assert tl(FAKE, FAKE, FAKE, 16, 4096, 2048, FAKE, 1 << 20, STREAM) == 1  # not the form's K
+    assert tl(FAKE, FAKE, FAKE, 0, 4096, 4096, FAKE, 1 << 20, STREAM) == 1
+    assert tl(FAKE, FAKE, FAKE, 65, 4096, 4096, FAKE, 1 << 20, STREAM) == 1
+    assert tl(FAKE + 8, FAKE, FAKE, 16, 4096, 4096, FAKE, 1 << 20, STREAM) == 1  # x not 16-byte aligned
+    assert tl(FAKE, FAKE + 2, FAKE, 16, 4096, 4096, FAKE, 1 << 20, STREAM) == 1  # w not 4-byte aligned
 
 
 def test_python_wrappers_raise_hip_error(lib):
