@@ -953,8 +953,8 @@ hipError_t launch_ring_mt(const void* x, const void* w, void* y, uint32_t M, uin
 }
 
 // ---------------------------------------------------------------------------
-// Q4_K on the matrix cores (kq4_mfma_kernel): 3 to 64 tokens, K up to
-// KS x STEPS super-blocks (4096).
+// Q4_K on the matrix cores (kq4_mfma_kernel): 2 to 64 tokens, K parts of up
+// to KS x STEPS super-blocks (4096).
 //
 // v_mfma_f32_16x16x32_f16 with the activations as the A operand (16 tokens)
 // and the weights as the B operand (16 rows), so the lane that holds output
@@ -978,7 +978,10 @@ hipError_t launch_ring_mt(const void* x, const void* w, void* y, uint32_t M, uin
 // tiles meet in LDS and are summed in wave order (deterministic).  A result
 // that is not finite (an infinite or NaN scale, a non-finite activation) is
 // recomputed by its thread element by element with the definition's values,
-// so NaN and infinities land where the oracle puts them.
+// so NaN and infinities land where the oracle puts them.  Split K (K past
+// 4096): each workgroup keeps one K part of 16 super-blocks and writes that
+// part's f32 plane of the partial tiles (recomputing a non-finite part over
+// the part's elements); kq_splitk_reduce_kernel adds the planes in part order.
 // ---------------------------------------------------------------------------
 
 // sum over the row of x[k] w[k] with GGML's per-element values, one thread.
@@ -1051,10 +1054,11 @@ __device__ __forceinline__ void stage_block_x(const uint16_t* __restrict__ x, ui
     }
 }
 
-template <int KS, int STEPS, typename OutT>
+template <int KS, int STEPS, typename OutT, bool SK = false>
 __global__ __launch_bounds__(KS * 64) void kq4_mfma_kernel(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
                                                           OutT* __restrict__ y, uint32_t M, uint32_t N, uint32_t K,
-                                                          uint32_t token_tiles, uint32_t items, uint32_t per_xcd) {
+                                                          uint32_t token_tiles, uint32_t items, uint32_t per_xcd,
+                                                          uint32_t kparts, float* __restrict__ partial) {
     constexpr int kLazy = KS * 64 / 256;  // items reduced together: one output per thread
     __shared__ float part[kLazy][KS][16][17];  // [item][wave][token][row]
     __shared__ __attribute__((aligned(16))) uint8_t xstage[KS][kXStageBytes];
@@ -1064,9 +1068,14 @@ __global__ __launch_bounds__(KS * 64) void kq4_mfma_kernel(const uint16_t* __res
     const size_t row_bytes = static_cast<size_t>(nb) * 144;
     const uint32_t groups = gridDim.x;
     // XCD-aware order: workgroups of one XCD take consecutive items, so the
-    // token tiles of a row tile read its weights through the same L2
+    // token tiles of a row tile read its weights through the same L2.  Items
+    // are (row tile, token tile, K part); the grid is a multiple of the
+    // combos, so a workgroup keeps one token tile and one K part (SK: KS x
+    // STEPS super-blocks from b0; without split K, all of K).
     const uint32_t first = (blockIdx.x % 8u) * per_xcd + blockIdx.x / 8u;
+    const uint32_t combos = SK ? token_tiles * kparts : token_tiles;
     const uint32_t tok0 = (first % token_tiles) * 16u;
+    const uint32_t b0 = SK ? (first % combos) / token_tiles * (KS * STEPS) : 0u;
 
     // The activations of this wave's blocks for the 16 tokens: the MFMA
     // operands (permuted to the weight operands' element order) and the
@@ -1075,7 +1084,7 @@ __global__ __launch_bounds__(KS * 64) void kq4_mfma_kernel(const uint16_t* __res
     uint32_t s_hi[STEPS], s_lo[STEPS];
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
-        const uint32_t b = static_cast<uint32_t>(kw) + KS * static_cast<uint32_t>(s);
+        const uint32_t b = b0 + static_cast<uint32_t>(kw) + KS * static_cast<uint32_t>(s);
         uint32_t xr[32];
         if (b < nb) {  // uniform
             // lane (li, lg): elements 64 lg .. 64 lg + 63 of token li
@@ -1115,9 +1124,9 @@ __global__ __launch_bounds__(KS * 64) void kq4_mfma_kernel(const uint16_t* __res
         u32x4 hdr, qa, qb;
     };
     auto load_part = [&](uint32_t item, int s, Part& pt) {
-        const uint32_t b = static_cast<uint32_t>(kw) + KS * static_cast<uint32_t>(s);
+        const uint32_t b = b0 + static_cast<uint32_t>(kw) + KS * static_cast<uint32_t>(s);
         if (b >= nb) return;  // uniform: a step past the row's blocks
-        const uint32_t n = min((item / token_tiles) * 16u + static_cast<uint32_t>(li), N - 1);
+        const uint32_t n = min((item / combos) * 16u + static_cast<uint32_t>(li), N - 1);
         const uint8_t* base = w + static_cast<size_t>(n) * row_bytes + static_cast<size_t>(b) * 144;
         pt.hdr = *reinterpret_cast<const u32x4*>(base);
         pt.qa = *reinterpret_cast<const u32x4*>(base + 16 + 32 * lg);
@@ -1193,7 +1202,7 @@ __global__ __launch_bounds__(KS * 64) void kq4_mfma_kernel(const uint16_t* __res
             const uint32_t next = item + groups;
 #pragma unroll
             for (int s = 0; s < STEPS; ++s) {
-                const uint32_t b = static_cast<uint32_t>(kw) + KS * static_cast<uint32_t>(s);
+                const uint32_t b = b0 + static_cast<uint32_t>(kw) + KS * static_cast<uint32_t>(s);
                 if (b < nb) {  // uniform
                     const Part pt = cur[s];
                     if (next < items) load_part(next, s, cur[s]);  // the next item's block under this one's MFMAs
@@ -1212,14 +1221,20 @@ __global__ __launch_bounds__(KS * 64) void kq4_mfma_kernel(const uint16_t* __res
             const int i = tid >> 8, tok = (tid >> 4) & 15, row = tid & 15;  // KS * 64 >= kLazy * 256 threads
             const uint32_t item = c0 + static_cast<uint32_t>(i) * groups;
             const uint32_t m = tok0 + static_cast<uint32_t>(tok);
-            const uint32_t n = (item / token_tiles) * 16u + static_cast<uint32_t>(row);
+            const uint32_t n = (item / combos) * 16u + static_cast<uint32_t>(row);
             if (i < kLazy && item < items && m < M && n < N) {
                 float v = part[i][0][tok][row];
 #pragma unroll
                 for (int k = 1; k < KS; ++k) v += part[i][k][tok][row];
+                // not finite: the definition's per-element sum over this K part
                 if (__builtin_expect(not_finite(v), 0))
-                    v = kq_exact_thread<Fmt::Q4K>(w + static_cast<size_t>(n) * row_bytes, x + static_cast<size_t>(m) * K, nb);
-                y[static_cast<size_t>(m) * N + n] = to_out<OutT>(v);
+                    v = kq_exact_thread<Fmt::Q4K>(w + static_cast<size_t>(n) * row_bytes + static_cast<size_t>(b0) * 144,
+                                                  x + static_cast<size_t>(m) * K + static_cast<size_t>(b0) * kSuper,
+                                                  SK ? min(static_cast<uint32_t>(KS * STEPS), nb - b0) : nb);
+                if constexpr (SK)  // this K part's plane of the partial sums
+                    partial[(static_cast<size_t>(b0 / (KS * STEPS)) * M + m) * N + n] = v;
+                else
+                    y[static_cast<size_t>(m) * N + n] = to_out<OutT>(v);
             }
         }
         __syncthreads();
@@ -1227,7 +1242,8 @@ __global__ __launch_bounds__(KS * 64) void kq4_mfma_kernel(const uint16_t* __res
 }
 
 // ---------------------------------------------------------------------------
-// Q6_K on the matrix cores (kq6_mfma_kernel), 5 to 64 tokens, K up to 4096:
+// Q6_K on the matrix cores (kq6_mfma_kernel), 5 to 64 tokens, K parts of up
+// to KS super-blocks (4096):
 // the Q4_K tile's layout (16 tokens as the A operand, 16 weight rows as the B
 // operand, one super-block per wave, partial tiles summed in LDS in wave
 // order).
@@ -1283,10 +1299,11 @@ __device__ __forceinline__ void load32_u(const uint8_t* p, uint32_t o4, uint32_t
     hi = u32x4{o[4], o[5], o[6], o[7]};
 }
 
-template <int KS, bool A16, typename OutT>
+template <int KS, bool A16, typename OutT, bool SK = false>
 __global__ __launch_bounds__(KS * 64) void kq6_mfma_kernel(const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
                                                           OutT* __restrict__ y, uint32_t M, uint32_t N, uint32_t K,
-                                                          uint32_t token_tiles, uint32_t items, uint32_t per_xcd) {
+                                                          uint32_t token_tiles, uint32_t items, uint32_t per_xcd,
+                                                          uint32_t kparts, float* __restrict__ partial) {
     constexpr int kLazy = KS * 64 / 256;  // items reduced together: one output per thread
     __shared__ float part[kLazy][KS][16][17];  // [item][wave][token][row]
     __shared__ __attribute__((aligned(16))) uint8_t xstage[KS][kXStageBytes];
@@ -1296,9 +1313,12 @@ __global__ __launch_bounds__(KS * 64) void kq6_mfma_kernel(const uint16_t* __res
     const uint32_t nb = K / kSuper;
     const size_t row_bytes = static_cast<size_t>(nb) * 210;
     const uint32_t groups = gridDim.x;
-    const uint32_t b = static_cast<uint32_t>(kw);  // this wave's super-block
+    // items and K parts as in the Q4_K tile (SK: KS super-blocks from b0)
     const uint32_t first = (blockIdx.x % 8u) * per_xcd + blockIdx.x / 8u;
+    const uint32_t combos = SK ? token_tiles * kparts : token_tiles;
     const uint32_t tok0 = (first % token_tiles) * 16u;
+    const uint32_t b0 = SK ? (first % combos) / token_tiles * KS : 0u;
+    const uint32_t b = b0 + static_cast<uint32_t>(kw);  // this wave's super-block
 
     // The activations of this wave's block for the 16 tokens: quarter c0 + 2 h,
     // elements 8 u .. 8 u + 7 in xa[4 h + u] (byte 256 half + 64 c0 + 128 h +
@@ -1327,7 +1347,7 @@ __global__ __launch_bounds__(KS * 64) void kq6_mfma_kernel(const uint16_t* __res
     };
     auto load_part = [&](uint32_t item, Part& pt) {
         if (b >= nb) return;  // uniform: a wave past the row's blocks
-        const uint32_t n = min((item / token_tiles) * 16u + static_cast<uint32_t>(li), N - 1);
+        const uint32_t n = min((item / combos) * 16u + static_cast<uint32_t>(li), N - 1);
         const uint8_t* base = w + static_cast<size_t>(n) * row_bytes + static_cast<size_t>(b) * 210;
         if constexpr (A16) {
             const uint32_t o = 2u * (b & 7u);  // base mod 16
@@ -1422,15 +1442,20 @@ __global__ __launch_bounds__(KS * 64) void kq6_mfma_kernel(const uint16_t* __res
             const int i = tid >> 8, tok = (tid >> 4) & 15, row = tid & 15;
             const uint32_t item = c0i + static_cast<uint32_t>(i) * groups;
             const uint32_t m = tok0 + static_cast<uint32_t>(tok);
-            const uint32_t n = (item / token_tiles) * 16u + static_cast<uint32_t>(row);
+            const uint32_t n = (item / combos) * 16u + static_cast<uint32_t>(row);
             if (i < kLazy && item < items && m < M && n < N) {
                 float v = part[i][0][tok][row];
 #pragma unroll
                 for (int k = 1; k < KS; ++k) v += part[i][k][tok][row];
+                // not finite: the definition's per-element sum over this K part
                 if (__builtin_expect(not_finite(v), 0))
-                    v = kq_exact_thread<Fmt::Q6K>(w + static_cast<size_t>(n) * row_bytes, x + static_cast<size_t>(m) * K,
-                                                  nb);
-                y[static_cast<size_t>(m) * N + n] = to_out<OutT>(v);
+                    v = kq_exact_thread<Fmt::Q6K>(w + static_cast<size_t>(n) * row_bytes + static_cast<size_t>(b0) * 210,
+                                                  x + static_cast<size_t>(m) * K + static_cast<size_t>(b0) * kSuper,
+                                                  SK ? min(static_cast<uint32_t>(KS), nb - b0) : nb);
+                if constexpr (SK)  // this K part's plane of the partial sums
+                    partial[(static_cast<size_t>(b0 / KS) * M + m) * N + n] = v;
+                else
+                    y[static_cast<size_t>(m) * N + n] = to_out<OutT>(v);
             }
         }
         __syncthreads();
@@ -1438,55 +1463,115 @@ __global__ __launch_bounds__(KS * 64) void kq6_mfma_kernel(const uint16_t* __res
 }
 
 // The matrix-core tiles: 16-token tiles, one workgroup of 16 waves per CU,
-// one block per wave, so K <= 4096 (a Q4_K wave's activations for more
-// blocks outgrow its registers: 16 waves of two blocks, or 8 of four, spill);
-// x and w 16-byte aligned.  From 2 tokens for Q4_K (2 x 4096 x 14336: 10.5 us
-// on the tile, 11.1 on the ring) and 5 for Q6_K: below that the ring GEMV's
-// single pass of up to four tokens is faster (3 / 4 x 4096 x 14336 Q6_K: 18.9
-// / 19.2 us on the ring, 19.7 on the tile).
+// one block per wave: K <= 4096 in one pass (a Q4_K wave's activations for
+// more blocks outgrow its registers: 16 waves of two blocks, or 8 of four,
+// spill), longer K in parts of 16 super-blocks whose partial tiles a second
+// kernel adds in part order (split K; the last part may be short); x and w
+// 16-byte aligned.  From 2 tokens for Q4_K in one pass (2 x 4096 x 14336:
+// 10.5 us on the tile, 11.1 on the ring), 3 with split K (2 x 14336 x 4096:
+// 13.2 us on the tiles and the part sum, 12.8 on the ring; 3 tokens: 13.3
+// against 21.0), and 5 for Q6_K: below that the ring GEMV's single pass of up
+// to four tokens is faster (3 / 4 x 4096 x 14336: 18.9 / 19.2 us on the ring,
+// 19.7 on the tile; 4 x 14336 x 4096: 20.6 on the ring, 22.5 on the split
+// tiles at 5 tokens).
 template <Fmt F>
 bool kq_mfma_supported(const void* x, const void* w, uint32_t M, uint32_t K) {
     const uint32_t nb = K / kSuper;
-    return M >= (F == Fmt::Q4K ? 2u : 5u) && M <= 64 && nb >= 1 && nb <= 16 &&
+    const uint32_t min_m = F == Fmt::Q4K ? (nb <= 16 ? 2u : 3u) : 5u;
+    return M >= min_m && M <= 64 && nb >= 1 &&
            (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
 }
 
+// y[i] = the sum of the K parts' planes at i, in part order, converted.
+template <typename OutT>
+__global__ __launch_bounds__(256) void kq_splitk_reduce_kernel(const float* __restrict__ partial, uint32_t kparts,
+                                                               uint64_t count, OutT* __restrict__ y) {
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < count;
+         i += static_cast<uint64_t>(gridDim.x) * 256) {
+        float v = partial[i];
+        for (uint32_t k = 1; k < kparts; ++k) v += partial[static_cast<uint64_t>(k) * count + i];
+        y[i] = to_out<OutT>(v);
+    }
+}
+
+// Returns hipErrorStreamCaptureUnsupported, with nothing queued, when split K
+// needs more scratch than a stream under graph capture holds (the caller then
+// runs the ring GEMV).
 template <Fmt F, typename OutT>
 hipError_t launch_kq_mfma(const void* x, const void* w, void* y, uint32_t M, uint32_t N, uint32_t K,
                           hipStream_t stream) {
     constexpr int KS = 16;
+    const uint32_t nb = K / kSuper;
+    const uint32_t kparts = (nb + KS - 1) / KS;
     const uint32_t token_tiles = (M + 15) / 16;
     const uint32_t row_tiles = (N + 15) / 16;
-    const uint64_t items64 = static_cast<uint64_t>(row_tiles) * token_tiles;
+    const uint64_t items64 = static_cast<uint64_t>(row_tiles) * token_tiles * kparts;
     if (items64 > 0x7fffffffull) return hipErrorInvalidConfiguration;
     const uint32_t items = static_cast<uint32_t>(items64);
-    // whole XCD rounds that are also a multiple of the token tiles, so every
-    // workgroup keeps one token tile
-    uint32_t a = 8u, b = token_tiles;
+    // whole XCD rounds that are also a multiple of the (token tile, K part)
+    // combos, so every workgroup keeps one token tile and K part
+    const uint32_t combos = token_tiles * kparts;
+    uint32_t a = 8u, b = combos;
     while (b != 0) { const uint32_t t = a % b; a = b; b = t; }
-    const uint32_t unit = 8u / a * token_tiles;
+    const uint32_t unit = 8u / a * combos;
     uint32_t groups = static_cast<uint32_t>(device_cus());
     if (groups > items) groups = items;
     groups = (groups + unit - 1) / unit * unit;
     const auto* xp = static_cast<const uint16_t*>(x);
     const auto* wp = static_cast<const uint8_t*>(w);
     auto* yp = static_cast<OutT*>(y);
+    if (kparts == 1) {
+        if constexpr (F == Fmt::Q4K)
+            hipLaunchKernelGGL((kq4_mfma_kernel<KS, 1, OutT>), dim3(groups), dim3(KS * 64), 0, stream, xp, wp, yp, M, N,
+                               K, token_tiles, items, groups / 8u, 1u, nullptr);
+        else if (K % 2048 == 0)
+            hipLaunchKernelGGL((kq6_mfma_kernel<KS, true, OutT>), dim3(groups), dim3(KS * 64), 0, stream, xp, wp, yp, M,
+                               N, K, token_tiles, items, groups / 8u, 1u, nullptr);
+        else
+            hipLaunchKernelGGL((kq6_mfma_kernel<KS, false, OutT>), dim3(groups), dim3(KS * 64), 0, stream, xp, wp, yp,
+                               M, N, K, token_tiles, items, groups / 8u, 1u, nullptr);
+        return hipGetLastError();
+    }
+    // Split K: the stream's scratch is held until both kernels are queued
+    // (the lease goes out of scope at return).  Its layout is the Q4_0 split
+    // K's: the tile arrival counters first (cleared when the buffer is new,
+    // since the Q4_0 folded epilogue expects them zero), then the partial
+    // tiles, [kparts][M][N] f32.
+    const uint64_t count = static_cast<uint64_t>(M) * N;
+    q4_0::ScratchPool::Lease lease;
+    const hipError_t se =
+        q4_0::acquire_scratch(stream, q4_0::kSplitKCounterBytes + count * kparts * sizeof(float), &lease);
+    if (se != hipSuccess) return se;
+    auto* base = static_cast<uint8_t*>(lease.ptr());
+    if (lease.fresh()) {
+        const hipError_t z = q4_0::launch_zero_fill(base, q4_0::kSplitKCounterBytes / 4, q4_0::OutType::F32, stream);
+        if (z != hipSuccess) return z;
+    }
+    auto* part = reinterpret_cast<float*>(base + q4_0::kSplitKCounterBytes);
     if constexpr (F == Fmt::Q4K)
-        hipLaunchKernelGGL((kq4_mfma_kernel<KS, 1, OutT>), dim3(groups), dim3(KS * 64), 0, stream, xp, wp, yp, M, N, K,
-                           token_tiles, items, groups / 8u);
+        hipLaunchKernelGGL((kq4_mfma_kernel<KS, 1, OutT, true>), dim3(groups), dim3(KS * 64), 0, stream, xp, wp, yp, M,
+                           N, K, token_tiles, items, groups / 8u, kparts, part);
     else if (K % 2048 == 0)
-        hipLaunchKernelGGL((kq6_mfma_kernel<KS, true, OutT>), dim3(groups), dim3(KS * 64), 0, stream, xp, wp, yp, M, N,
-                           K, token_tiles, items, groups / 8u);
+        hipLaunchKernelGGL((kq6_mfma_kernel<KS, true, OutT, true>), dim3(groups), dim3(KS * 64), 0, stream, xp, wp, yp,
+                           M, N, K, token_tiles, items, groups / 8u, kparts, part);
     else
-        hipLaunchKernelGGL((kq6_mfma_kernel<KS, false, OutT>), dim3(groups), dim3(KS * 64), 0, stream, xp, wp, yp, M, N,
-                           K, token_tiles, items, groups / 8u);
+        hipLaunchKernelGGL((kq6_mfma_kernel<KS, false, OutT, true>), dim3(groups), dim3(KS * 64), 0, stream, xp, wp,
+                           yp, M, N, K, token_tiles, items, groups / 8u, kparts, part);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint64_t blocks = (count + 255) / 256;
+    hipLaunchKernelGGL((kq_splitk_reduce_kernel<OutT>), dim3(static_cast<uint32_t>(blocks < 2048 ? blocks : 2048)),
+                       dim3(256), 0, stream, part, kparts, count, yp);
     return hipGetLastError();
 }
 
 template <Fmt F, typename OutT>
 hipError_t launch_gemv(const void* x, const void* w, void* y, uint32_t M, uint32_t N, uint32_t K,
                        hipStream_t stream) {
-    if (kq_mfma_supported<F>(x, w, M, K)) return launch_kq_mfma<F, OutT>(x, w, y, M, N, K, stream);
+    if (kq_mfma_supported<F>(x, w, M, K)) {
+        const hipError_t e = launch_kq_mfma<F, OutT>(x, w, y, M, N, K, stream);
+        if (e != hipErrorStreamCaptureUnsupported) return e;  // else: split K under capture without scratch
+    }
     if (ring_supported<F>(x, w, K)) {
         if (M == 1) return launch_ring_mt<F, 1, OutT>(x, w, y, M, N, K, stream);
         if (M == 2) return launch_ring_mt<F, 2, OutT>(x, w, y, M, N, K, stream);

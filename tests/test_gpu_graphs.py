@@ -165,3 +165,68 @@ def test_first_split_k_call_under_capture(oracle):
         own.close()
         for b in [xb, wb, *ys.values()]:
             b.free()
+
+
+@pytest.mark.parametrize("name", ["q4_k", "q6_k"])
+def test_k_quant_split_k_under_capture(oracle, name):
+    """The K-quant split-K tiles (16 tokens, K = 14336: four K parts) under
+    capture.  On a stream the library created, its reserved scratch holds the
+    partial planes: the graph, replayed three times with the output reset to
+    a sentinel between replays, gives the eager result bit for bit.  On the
+    caller's own stream the library has no scratch yet and a capture may not
+    allocate, so the captured call runs the ring GEMV (to the oracle's
+    tolerance); the next eager call sizes the scratch and gives the split-K
+    result again."""
+    from mote_amd.device import Stream
+    from test_gpu_kquant import FORMATS, _check, _judge
+
+    m, n, k = 16, 1024, 14336
+    hip = HipRuntime()
+    w = (wl.q4_k_weights if name == "q4_k" else wl.q6_k_weights)(54, n, k)
+    x = wl.normal_f16(55, m * k)
+    y64, max_w, max_x = _judge(oracle, name, x, w, m, n, k)
+    xb, wb = DeviceBuffer.from_array(x), DeviceBuffer.from_array(w)
+    ys = {out: DeviceBuffer(m * n * 4) for out in ("eager", "graph", "foreign_graph", "foreign_eager")}
+    linear = FORMATS[name][2]
+
+    def call(out, s):
+        return lambda: linear(xb.ptr, wb.ptr, ys[out].ptr, m, n, k, s)
+
+    def result(out, s):
+        s.synchronize()
+        return ys[out].download(np.float32).reshape(m, n).astype(np.float64)
+
+    own, foreign = Stream(), hip.foreign_stream()
+    try:
+        for out in ys:
+            ys[out].upload(np.full(m * n * 4, 0xA5, dtype=np.uint8))
+        exe = hip.capture(own, call("graph", own))
+        try:
+            graphs = []
+            for _ in range(3):
+                ys["graph"].upload(np.full(m * n * 4, 0xA5, dtype=np.uint8))
+                own.synchronize()
+                hip.launch_graph(exe, own)
+                graphs.append(result("graph", own))
+        finally:
+            hip.destroy_graph(exe)
+        call("eager", own)()
+        eager = result("eager", own)
+        _check(eager, y64, k, max_w, max_x, what=f"{name} eager split K")
+        for i, g in enumerate(graphs):
+            assert np.array_equal(g, eager), f"{name}: replay {i} on the library's stream is not the split-K result"
+
+        exe = hip.capture(foreign, call("foreign_graph", foreign))
+        try:
+            hip.launch_graph(exe, foreign)
+            captured = result("foreign_graph", foreign)
+        finally:
+            hip.destroy_graph(exe)
+        _check(captured, y64, k, max_w, max_x, what=f"{name} captured without scratch (ring)")
+        call("foreign_eager", foreign)()
+        assert np.array_equal(result("foreign_eager", foreign), eager), f"{name}: the eager call after capture is not split K"
+    finally:
+        foreign.close()
+        own.close()
+        for b in [xb, wb, *ys.values()]:
+            b.free()

@@ -153,11 +153,18 @@ SHAPES = [
     (1, 18, 28672),
     (4, 1000, 4096),
     (5, 12, 6144),
-    # the matrix-core tiles (2 for Q4_K, 5 for Q6_K, to 64 tokens, K <=
-    # 4096): four full 16-token tiles, and two and a bit over odd-block rows
-    # (Q6_K rows at 2 mod 4: the five-dword reads)
+    # the matrix-core tiles (2 for Q4_K, 3 past K = 4096, 5 for Q6_K, to 64
+    # tokens):
+    # four full 16-token tiles, and two and a bit over odd-block rows (Q6_K
+    # rows at 2 mod 4: the five-dword reads)
     (64, 40, 4096),
     (33, 50, 2304),
+    # split K (parts of 16 super-blocks): four parts, a short last part of one
+    # block over odd-block rows, and nine parts (Q6_K rows of whole 16-byte
+    # units at K % 2048 == 0, five-dword reads otherwise)
+    (64, 40, 14336),
+    (21, 30, 8448),
+    (16, 20, 36864),
 ]
 
 
@@ -188,15 +195,45 @@ def test_linear_unaligned_activations(stream, oracle, name, m, n, k):
 
 
 @pytest.mark.parametrize("name", list(FORMATS))
-def test_linear_every_finite_scale(stream, oracle, name):
+@pytest.mark.parametrize("m,k", [(3, 1536), (20, 8192)])
+def test_linear_every_finite_scale(stream, oracle, name, m, k):
     """Scales over every finite binary16 magnitude, subnormal to 65504 (the
-    kernel computes in f32: no binary16 product can overflow)."""
-    m, n, k = 3, 40, 1536
-    w = _blocks(name, 610, n * k // SUPER)
+    kernel computes in f32: no binary16 product can overflow), also through
+    the split-K tiles."""
+    n = 40
+    w = _blocks(name, 610 + k, n * k // SUPER)
     x = wl.normal_f16(wl.seed_for(32, 1), m * k)
     y64, max_w, max_x = _judge(oracle, name, x, w, m, n, k)
     assert np.isfinite(y64).all()
     _check(_run(stream, name, x, w, m, n, k), y64, k, max_w, max_x, what=f"{name} wide scales")
+
+
+@pytest.mark.parametrize("name", list(FORMATS))
+@pytest.mark.parametrize("m", [2, 6, 20])
+def test_linear_non_finite_activations(stream, oracle, name, m):
+    """inf, -inf and NaN activations in different K parts of different tokens
+    (K = 12288: three parts on the split-K tiles; the ring for Q6_K at 2
+    tokens): those tokens' outputs are what the f64 definition gives (+-inf
+    where one infinity meets nonzero weights, NaN where it meets a zero weight
+    or a NaN), every other output is judged as usual."""
+    n, k = 24, 12288
+    w = (wl.q4_k_weights if name == "q4_k" else wl.q6_k_weights)(620 + m, n, k)
+    x = wl.normal_f16(wl.seed_for(35, m), m * k).copy()
+    x[5000] = 0x7C00  # token 0, part 1: +inf
+    x[(m - 1) * k + 9000] = 0xFC00  # the last token, part 2: -inf
+    if m > 2:
+        x[k + 100] = 0x7E00  # token 1, part 0: NaN
+    y64 = oracle.kquant_linear_f64(bits_to_f32(x), w, _fmt(oracle, name), m, n, k)
+    finite_x = bits_to_f32(x)[np.isfinite(bits_to_f32(x))]
+    max_w = float(np.abs(oracle.dequantize_kquant_row(w, _fmt(oracle, name), n * k)).max())
+    for f16_out in (False, True):
+        y = _run(stream, name, x, w, m, n, k, f16_out=f16_out)
+        for cls in (np.isnan, np.isposinf, np.isneginf):
+            assert np.array_equal(cls(y), cls(y64)), f"{name} {m} tokens: {cls.__name__} positions differ"
+        assert not np.isfinite(y64[0]).any() and not np.isfinite(y64[m - 1]).any()
+        ok = np.isfinite(y64)
+        _check(y[ok], y64[ok], k, max_w, float(np.abs(finite_x).max()), 2.0 ** -11 if f16_out else 0.0,
+               what=f"{name} {m} tokens, finite outputs")
 
 
 def test_q6_k_weights_at_two_byte_offset(stream, oracle):
