@@ -153,7 +153,7 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_split_kernel(const uint16_t
     const uint32_t xsteps = (K + 4095u) / 4096u;
     uint8_t* xs = ring_lds + kWaves * R * slot_bytes;
     for (uint32_t i = 0; i < xsteps; ++i) {
-        const uint32_t c = min(512u * i + static_cast<uint32_t>(tid), K / 8u - 1u);
+        const uint32_t c = min(swizzled_chunk(512u * i + static_cast<uint32_t>(tid)), K / 8u - 1u);
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(x) + 16u * c,
                                          (lds_ptr)(xs + 8192u * i + 1024u * static_cast<uint32_t>(wave)), 16, 0, 0);
     }
@@ -169,10 +169,11 @@ __global__ __launch_bounds__(kThreads) void gemv_lds_split_kernel(const uint16_t
     XPair xv;
     {
         uint32_t xr[32];
-        const uint8_t* xslot = xs + (first_pair + pc) * 128u;
+        const uint32_t xp = first_pair + pc;
+        const uint8_t* xslot = xs + xp * 128u;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const u32x4 v = *reinterpret_cast<const u32x4*>(xslot + i * 16);
+            const u32x4 v = *reinterpret_cast<const u32x4*>(xslot + ((static_cast<uint32_t>(i) + xp) & 7u) * 16u);
             xr[4 * i + 0] = v.x; xr[4 * i + 1] = v.y; xr[4 * i + 2] = v.z; xr[4 * i + 3] = v.w;
         }
         float s0 = 0.0f, s1 = 0.0f;
