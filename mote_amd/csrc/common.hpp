@@ -144,6 +144,17 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t q, f16x2 d, uint32_t c1024, u
 // 68 bytes (17 dwords), dword aligned whenever the row is.
 constexpr uint32_t kQ8PairBytes = 68;
 
+// Swizzled x stages in LDS: the 16-byte chunk 8 a + i of an activation row
+// (bytes 16 i .. 16 i + 15 of its a-th 128) sits at position 8 a + ((i + a) &
+// 7), so lanes reading their own 128 (or 64) contiguous bytes of x, chunk by
+// chunk, spread over the banks instead of all hitting one bank row.
+// swizzled_chunk(q): the chunk at position q; swizzled_position(c): the
+// position of chunk c (its inverse).
+__host__ __device__ constexpr uint32_t swizzled_chunk(uint32_t q) { return (q & ~7u) + (((q & 7u) - (q >> 3)) & 7u); }
+__host__ __device__ constexpr uint32_t swizzled_position(uint32_t c) {
+    return (c & ~7u) + (((c & 7u) + (c >> 3)) & 7u);
+}
+
 // Loads the seventeen dwords of the Q8_0 pair that starts at `p`.
 __device__ __forceinline__ void load_pair_q8(const uint8_t* p, uint32_t (&d)[17]) {
 #pragma unroll

@@ -33,11 +33,6 @@ typedef __attribute__((address_space(3))) void* lds_ptr;
 // outstanding (vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt not waited).
 constexpr int vm_wait(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x0F70; }
 
-// The x chunk (16 bytes) held at LDS position q of a swizzled x stage: chunk
-// 8 a + i (pair a, bytes 16 i .. 16 i + 15 of its 128) sits at position
-// 8 a + ((i + a) & 7), so a lane reading pair a's i-th chunk at 128 a +
-// 16 ((i + a) & 7) and its seven neighbours cover all banks of a 128-byte row.
-__host__ __device__ constexpr uint32_t swizzled_chunk(uint32_t q) { return (q & ~7u) + (((q & 7u) - (q >> 3)) & 7u); }
 
 // F: the weight format (FmtQ4: 36-byte Q4_0 block pairs, FmtQ8: 68-byte Q8_0
 // pairs); MT: tokens, every row read once for all of them (the pair's

@@ -805,7 +805,12 @@ __global__ __launch_bounds__(kRingThreads) void kq_ring_kernel(const uint16_t* _
                 const int mm = m < mt ? m : mt - 1;  // tokens past the group re-read the last one
                 const uint8_t* src = reinterpret_cast<const uint8_t*>(x + static_cast<size_t>(m0 + mm) * K);
                 for (uint32_t i = 0; i < xsteps; ++i) {
-                    const uint32_t c = min(512u * i + threadIdx.x, K / 8u - 1u);
+                    // Q4_K: swizzled as the decode ring's x (chunk 8 a + i at 8 a + ((i + a) &
+                    // 7)), since each lane reads 128 contiguous bytes below (1 x 4096 x 14336
+                    // 8.36 -> 8.03 us, 1 x 4096 x 4096 4.92 -> 4.55); Q6_K's two 64-byte runs
+                    // per lane measured level either way and stay unswizzled
+                    const uint32_t q = 512u * i + threadIdx.x;
+                    const uint32_t c = min(F == Fmt::Q4K ? swizzled_chunk(q) : q, K / 8u - 1u);
                     __builtin_amdgcn_global_load_lds(
                         src + 16u * c, (lds_ptr)(x_lds + m * xstride + 8192u * i + 1024u * static_cast<uint32_t>(wave)),
                         16, 0, 0);
@@ -829,10 +834,12 @@ __global__ __launch_bounds__(kRingThreads) void kq_ring_kernel(const uint16_t* _
             for (int m = 0; m < MT; ++m) {
 #pragma unroll
                 for (int r = 0; r < 2; ++r) {
-                    const uint8_t* run = x_lds + m * xstride + 2u * (elem0 + (r ? e1 : e0));
+                    const uint32_t c0 = (elem0 + (r ? e1 : e0)) / 8u;  // the run's first chunk
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const u32x4 v = *reinterpret_cast<const u32x4*>(run + 16 * i);
+                        const uint32_t c = c0 + static_cast<uint32_t>(i);
+                        const u32x4 v = *reinterpret_cast<const u32x4*>(
+                            x_lds + m * xstride + 16u * (F == Fmt::Q4K ? swizzled_position(c) : c));
                         raw[m][16 * r + 4 * i + 0] = v.x; raw[m][16 * r + 4 * i + 1] = v.y;
                         raw[m][16 * r + 4 * i + 2] = v.z; raw[m][16 * r + 4 * i + 3] = v.w;
                     }
