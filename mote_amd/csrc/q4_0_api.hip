@@ -683,13 +683,15 @@ const Variant* rules(const Problem& p, Op op, bool split_ok) {
     }
     if (p.M == 1) {
         // K a multiple of 256 up to 4096: rows through the per-wave LDS ring
-        // with coalesced non-temporal loads (q4_0_gemv_lds.hip), two rows in
-        // flight from three rows per wave, one below (measured on MI355X at K
-        // = 4096: N = 14336 7.27 us, 6144 4.62 us, 4096 3.90 us, 1024 3.12 us,
-        // against 7.62, 5.14, 4.22 and 3.51 us for the pair-load GEMV).
+        // with coalesced non-temporal loads (q4_0_gemv_lds.hip), one row in
+        // flight beside the one computed (measured on MI355X at K = 4096: N =
+        // 14336 7.12-7.27 us, 6144 4.34, 4096 3.73, 1024 3.12, against 7.62,
+        // 5.14, 4.22 and 3.51 us for the pair-load GEMV; with x's stage
+        // swizzled, two rows in flight measured level or slower at every N:
+        // 7.28-7.40, 4.63, 4.17 us, and 5.24 against 5.08 at 8192, 11.82
+        // against 11.53 at 28672).
         {
-            const uint64_t rows_per_wave = p.N / (static_cast<uint64_t>(device_cus()) * 8u);
-            const Variant* v = by_name(rows_per_wave >= 3 ? "rowlds_r3d2" : "rowlds_r2d1");
+            const Variant* v = by_name("rowlds_r2d1");
             if (v && gemv_lds_supports(*v, p)) return v;
         }
         // K past 4096: rows split over S waves through the LDS ring where
@@ -772,6 +774,14 @@ const Variant* rules(const Problem& p, Op op, bool split_ok) {
         // vector-ALU GEMV).
         uint32_t split = 1;
         while (split < 8 && p.K > 4096u * split) split *= 2;
+        if (split == 1 && p.M == 2) {
+            // Two tokens at K <= 4096 (K % 256 == 0, 16-byte aligned): the LDS
+            // ring reading each row once for both tokens (2 x 4096 x 4096 /
+            // 6144 / 14336: 4.25 / 5.11 / 8.37 us, against 4.94 / 6.40 /
+            // 9.2 us on the streaming GEMV below).
+            const Variant* ring = by_name("rowlds_m2_r2d1");
+            if (ring && gemv_lds_supports(*ring, p)) return ring;
+        }
         char name[32];
         if (split == 1 && p.M > 2)
             std::snprintf(name, sizeof name, "%s", p.M == 3 ? "stream_m3_d1_g1" : "stream_m4_d1_g1");

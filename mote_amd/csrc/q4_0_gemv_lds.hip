@@ -332,6 +332,10 @@ const Variant kLds[] = {
     Variant{"rowlds_r2d1", Kind::GemvLds, 2, 1, 0, &launch_gemv_lds<FmtQ4, 1, 2, 1>},
     Variant{"rowlds_r3d1", Kind::GemvLds, 3, 1, 0, &launch_gemv_lds<FmtQ4, 1, 3, 1>},
     Variant{"rowlds_r3d2", Kind::GemvLds, 3, 2, 0, &launch_gemv_lds<FmtQ4, 1, 3, 2>},
+    // two tokens, each row read once for both (2 x 4096 x 4096 / 6144 / 14336
+    // in 4.25 / 5.11 / 8.37 us against 4.94 on the streaming GEMV and 6.22 /
+    // 8.97 on the skinny tiles; three tokens measured slower at N = 14336)
+    Variant{"rowlds_m2_r2d1", Kind::GemvLds, 2, 1, 0, &launch_gemv_lds<FmtQ4, 2, 2, 1>, 2},
 #define MOTE_LDS_Q8(MT, R, D)                                                          \
     Variant{MT == 1 ? "q8_rowlds_r" #R "d" #D : "q8_rowlds_m" #MT "_r" #R "d" #D, Kind::Q8Lds, R, D, 0,     \
             &launch_gemv_lds<FmtQ8, MT, R, D>, MT}

@@ -54,9 +54,9 @@ def d():
 
 LINEAR = [
     # (M, K, N) -> variant
-    ((1, 4096, 14336), "rowlds_r3d2"),
+    ((1, 4096, 14336), "rowlds_r2d1"),
     ((1, 4096, 4096), "rowlds_r2d1"),
-    ((1, 4096, 6144), "rowlds_r3d2"),
+    ((1, 4096, 6144), "rowlds_r2d1"),
     ((1, 1024, 4096), "rowlds_r2d1"),
     ((1, 4160, 4096), "stream_s2_d1_g2"),
     ((1, 14336, 4096), "rowlds_s4_r3d2_g1"),
@@ -66,9 +66,12 @@ LINEAR = [
     ((1, 14336, 1024), "stream_s4_d1q_g1"),
     ((1, 8192, 8192), "stream_s2_d1_g2"),
     ((1, 11008, 4096), "stream_s4_d1q_g2"),
-    ((1, 4096, 11008), "rowlds_r3d2"),
+    ((1, 4096, 11008), "rowlds_r2d1"),
     ((1, 28672, 8192), "rowlds_s8_r3d2_g1"),
-    ((2, 4096, 14336), "stream_m2_d1q_g1"),
+    ((2, 4096, 14336), "rowlds_m2_r2d1"),
+    ((2, 4096, 8192), "rowlds_m2_r2d1"),
+    ((2, 1024, 4096), "rowlds_m2_r2d1"),
+    ((2, 4032, 4096), "stream_m2_d1q_g1"),  # K % 256 != 0: no ring
     ((2, 14336, 4096), "stream_s4_m2_d1q_g1"),
     ((3, 8192, 8192), "stream_s2_m3_d1q_g1"),
     ((3, 14336, 4096), "stream_s4_m3_d1q_g1"),

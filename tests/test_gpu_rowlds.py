@@ -43,6 +43,8 @@ SPLIT_SHAPES = {
     8: [(1, 2048), (3, 6400), (257, 10240), (130, 13824), (4099, 28672), (1000, 32768), (40001, 2304)],
 }
 REFERENCE = {1: "stream_d1_g2", 2: "stream_s2_d1_g1", 4: "stream_s4_d1q_g1", 8: "stream_s8_d1_g1"}
+# the streaming GEMV reading each row once for every token (Q4_0 rings of 2 tokens)
+TOKENS_REFERENCE = {2: "stream_m2_d1q_g1"}
 # the Q8_0 streaming GEMV reading each row once for every token, or with rows
 # split over S waves
 Q8_REFERENCE = {1: "q8_stream_d1_g1", 2: "q8_stream_m2_d1q_g1", 4: "q8_stream_m4_d1q_g1"}
@@ -61,22 +63,24 @@ def _tokens(variant: str) -> int:
 
 @pytest.mark.parametrize("variant", [v for v in ops.variant_names() if v.startswith("rowlds_")])
 def test_every_rowlds_variant(stream, oracle, variant):
-    split = _split(variant)
+    """Q4_0 rings of two tokens (rowlds_m2_*) read each row once for both and
+    must equal the two-token streaming GEMV bit for bit."""
+    split, tokens = _split(variant), _tokens(variant)
     d = ops.Q4_0Dispatch()
     d.force(variant)
     ref = ops.Q4_0Dispatch()
-    ref.force(REFERENCE[split])
+    ref.force(REFERENCE[split] if tokens == 1 else TOKENS_REFERENCE[tokens])
     for n, k in SHAPES if split == 1 else SPLIT_SHAPES[split]:
-        print(f"{variant} 1x{n}x{k}", flush=True)
-        x = normal_x(wl.seed_for(17, k), 1, k)
+        print(f"{variant} {tokens}x{n}x{k}", flush=True)
+        x = normal_x(wl.seed_for(17, k), tokens, k)
         w = weights(wl.seed_for(17, 100 + n), n, k)
         cols = None if n < 5000 else sample_columns(n, 512)
         for f16_out in (False, True):
-            y = run_linear(stream, x, w, 1, n, k, dispatch=d, f16_out=f16_out)
-            want = run_linear(stream, x, w, 1, n, k, dispatch=ref, f16_out=f16_out)
+            y = run_linear(stream, x, w, tokens, n, k, dispatch=d, f16_out=f16_out)
+            want = run_linear(stream, x, w, tokens, n, k, dispatch=ref, f16_out=f16_out)
             assert np.array_equal(y.view(np.uint32), want.view(np.uint32)), (variant, n, k, f16_out)
-            check_against_oracle(oracle, y, x, w, 1, n, k, columns=cols, f16_out=f16_out,
-                                 what=f"{variant} 1x{n}x{k}{' f16' if f16_out else ''}")
+            check_against_oracle(oracle, y, x, w, tokens, n, k, columns=cols, f16_out=f16_out,
+                                 what=f"{variant} {tokens}x{n}x{k}{' f16' if f16_out else ''}")
 
 
 @pytest.mark.parametrize("variant", [v for v in ops.variant_names() if v.startswith("q8_rowlds_")])
