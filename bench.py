@@ -750,7 +750,7 @@ class RingTimelineCase:
     """The shipped decode ring kernel with per-wave timestamps
     (mote_probe_ring_timeline), or with `loads_only` the ring kernel's own
     loads and nothing else (mote_probe_ring_read: grid, row order,
-    non-temporal 16-byte direct-to-LDS loads, 3 slots, 2 rows in flight, its
+    non-temporal 16-byte direct-to-LDS loads, 2 slots, 1 row in flight, its
     waits), over the rotated weight copies of a LinearCase.  With `regions`
     launch i writes its per-wave records to region i % regions of one stamp
     buffer; with regions = 0 nothing is recorded."""
@@ -842,7 +842,7 @@ def run_timeline(launches: int = 8) -> int:
     stream, hip = Stream(), HipRuntime()
     m, k, n = 1, 4096, 14336
     case = LinearCase(m, n, k, workload=1)
-    cases = {"shipped kernel (rowlds_r3d2)": case,
+    cases = {"shipped kernel (rowlds_r2d1)": case,
              "shipped kernel body, stamped": RingTimelineCase(probe, case, launches),
              "ring loads only": RingTimelineCase(probe, case, 0, loads_only=True),
              "ring loads only, stamped": RingTimelineCase(probe, case, launches, loads_only=True)}
@@ -1028,8 +1028,8 @@ def run_read_floor(sizes=READ_FLOOR_BYTES) -> int:
             b.free()
     sink.free()
     # The decode ring kernel's own access pattern (mote_probe_ring_read): its
-    # grid, row order, non-temporal direct-to-LDS 16-byte loads, 3 slots and 2
-    # rows in flight, and nothing else, over the weights of the M = 1, K =
+    # grid, row order, non-temporal direct-to-LDS 16-byte loads, 2 slots and 1
+    # row in flight, and nothing else, over the weights of the M = 1, K =
     # 4096 linears.
     print("\nThe decode ring kernel's own loads (weights only, K = 4096)\n")
     print("| N | weight bytes | copies | µs / launch | GB/s | % of 8 TB/s |")

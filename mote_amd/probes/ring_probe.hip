@@ -3,7 +3,7 @@
 // loads (bench.py --timeline, --read-floor).
 //
 //  * mote_probe_ring_timeline: the shipped kernel body (gemv_lds_body of
-//    gemv_lds.hpp, Q4_0, one token, 3 ring slots, 2 rows in flight, f32 out)
+//    gemv_lds.hpp, Q4_0, one token, 2 ring slots, 1 row in flight, f32 out)
 //    instantiated with a timeline policy: every wave records the 100 MHz
 //    real-time clock at its start, once x is staged and its first rows are
 //    issued, when each of its rows has landed in the ring, when each row's sum
@@ -12,7 +12,7 @@
 //    written by vector stores after the wave's last y store, so the loop runs
 //    the shipped instruction stream plus one clock read per hook.
 //  * mote_probe_ring_read: the ring's loads and nothing else -- the same grid,
-//    row order, non-temporal 16-byte direct-to-LDS loads, 3 slots and 2 rows in
+//    row order, non-temporal 16-byte direct-to-LDS loads, 2 slots and 1 row in
 //    flight, and the same waits, with no LDS reads, arithmetic or stores: the
 //    read floor of this kernel's own access pattern.
 #include <hip/hip_runtime.h>
@@ -30,6 +30,9 @@ namespace {
 using q4_0::FmtQ4;
 using q4_0::kThreads;
 using q4_0::kWaves;
+
+// The shipped headline kernel's ring: slots per wave and rows in flight.
+constexpr uint32_t kSlots = 2, kDepth = 1;
 
 // Words of one wave's record: begin, ready, end, rows, then 64 arrival and 64
 // computed stamps (rows past 64 are not recorded).
@@ -77,15 +80,15 @@ __global__ __launch_bounds__(kThreads) void ring_timeline_kernel(const uint16_t*
                                                                  uint32_t N, uint32_t K, uint32_t total,
                                                                  uint32_t* __restrict__ stamps) {
     WaveTimeline tl{stamps};
-    q4_0::gemv_lds_body<FmtQ4, 1, 3, 2, LOADS, float>(x, w, y, N, K, total, tl);
+    q4_0::gemv_lds_body<FmtQ4, 1, kSlots, kDepth, LOADS, float>(x, w, y, N, K, total, tl);
 }
 
-// The ring's loads alone (see the file comment): R = 3 slots, D = 2 rows in
-// flight, as the shipped headline kernel.
+// The ring's loads alone (see the file comment), with the shipped headline
+// kernel's slots and rows in flight.
 template <int LOADS, bool STAMPS>
 __global__ __launch_bounds__(kThreads) void ring_read_kernel(const uint8_t* __restrict__ w, uint32_t N, uint32_t K,
                                                              uint32_t total, uint32_t* __restrict__ stamps) {
-    constexpr uint32_t R = 3, D = 2;
+    constexpr uint32_t R = kSlots, D = kDepth;
     extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t row_bytes = (K >> 6) * FmtQ4::kPairBytes, chunks = row_bytes >> 4;
@@ -178,7 +181,7 @@ MOTE_EXPORT int mote_probe_ring_timeline(const void* x, const void* w, void* y, 
     if (stamps_bytes < static_cast<size_t>(groups) * mote::q4_0::kWaves * kRecordWords * 4) return hipErrorInvalidValue;
     const uint32_t row_bytes = k / 64 * mote::kPairBytes;
     const uint32_t loads = (row_bytes / 16 + 63) / 64;
-    const size_t lds = static_cast<size_t>(mote::q4_0::kWaves) * 3 * row_bytes;
+    const size_t lds = static_cast<size_t>(mote::q4_0::kWaves) * kSlots * row_bytes;
     const uint32_t total = groups * mote::q4_0::kWaves;
     const auto s = static_cast<hipStream_t>(stream);
     const auto* xp = static_cast<const uint16_t*>(x);
@@ -207,7 +210,7 @@ MOTE_EXPORT int mote_probe_ring_read(const void* w, uint32_t n, uint32_t k, void
         return hipErrorInvalidValue;
     const uint32_t row_bytes = k / 64 * mote::kPairBytes;
     const uint32_t loads = (row_bytes / 16 + 63) / 64;
-    const size_t lds = static_cast<size_t>(mote::q4_0::kWaves) * 3 * row_bytes;
+    const size_t lds = static_cast<size_t>(mote::q4_0::kWaves) * kSlots * row_bytes;
     const uint32_t total = groups * mote::q4_0::kWaves;
     const auto s = static_cast<hipStream_t>(stream);
     const auto* wp = static_cast<const uint8_t*>(w);
