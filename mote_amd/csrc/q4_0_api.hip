@@ -755,6 +755,16 @@ const Variant* rules(const Problem& p, Op op, bool split_ok) {
     // (4096 x 14336: 9.2 us against 11.9 us on the matrix cores).  From 3
     // tokens: the skinny GEMM of skinny_heuristic, then any skinny variant
     // whose K slicing fits, then the vector-ALU GEMV.
+    if (p.K == 4096 && ((p.M == 3 && p.N <= 6144) || (p.M == 4 && p.N <= 2048))) {
+        // Three tokens up to three rows per wave, four up to one: the LDS ring
+        // reading each row once for every token (3 x 4096 x 1024 / 2048 /
+        // 6144: 4.06 / 4.11 / 6.13 us against 4.81 / 4.90 / 6.28 on the
+        // skinny tiles, 4096 level at 5.2; 4 x 4096 x 1024 / 2048: 4.51 /
+        // 4.69 against 4.89 / 5.04; more rows per wave favour the tiles, 3 x
+        // 4096 x 8192 7.24 against 6.62, 4 x 4096 x 4096 5.81 against 5.35).
+        const Variant* ring = by_name(p.M == 3 ? "rowlds_m3_r2d1" : "rowlds_m4_r2d1");
+        if (ring && gemv_lds_supports(*ring, p)) return ring;
+    }
     const bool mid_k = (p.M == 3 || p.M == 4) && p.K > 2048 && p.K < 4096;
     if (p.M == 2 || (p.M == 3 && p.K > 4096 && p.K <= 16384) ||
         (p.M == 4 && p.K > 4096 && p.K <= 16384 && p.K % 1024 != 0) || mid_k) {
@@ -774,12 +784,16 @@ const Variant* rules(const Problem& p, Op op, bool split_ok) {
         // vector-ALU GEMV).
         uint32_t split = 1;
         while (split < 8 && p.K > 4096u * split) split *= 2;
-        if (split == 1 && p.M == 2) {
+        if (split == 1 && (p.M == 2 || p.N <= 10240)) {
             // Two tokens at K <= 4096 (K % 256 == 0, 16-byte aligned): the LDS
             // ring reading each row once for both tokens (2 x 4096 x 4096 /
             // 6144 / 14336: 4.25 / 5.11 / 8.37 us, against 4.94 / 6.40 /
-            // 9.2 us on the streaming GEMV below).
-            const Variant* ring = by_name("rowlds_m2_r2d1");
+            // 9.2 us on the streaming GEMV below).  Three or four tokens at
+            // 2048 < K < 4096 up to five rows per wave, bit for bit the
+            // streaming GEMV (3 / 4 x 2560 x 10240: 8.17 / 9.48 us against
+            // 9.03 / 10.64; 3072 x 8192: 7.14 / 8.30 against 7.38 / 8.53;
+            // at 3584 x 18944 the ring is 2-3 % slower).
+            const Variant* ring = by_name(p.M == 2 ? "rowlds_m2_r2d1" : p.M == 3 ? "rowlds_m3_r2d1" : "rowlds_m4_r2d1");
             if (ring && gemv_lds_supports(*ring, p)) return ring;
         }
         char name[32];

@@ -336,6 +336,8 @@ const Variant kLds[] = {
     // in 4.25 / 5.11 / 8.37 us against 4.94 on the streaming GEMV and 6.22 /
     // 8.97 on the skinny tiles; three tokens measured slower at N = 14336)
     Variant{"rowlds_m2_r2d1", Kind::GemvLds, 2, 1, 0, &launch_gemv_lds<FmtQ4, 2, 2, 1>, 2},
+    Variant{"rowlds_m3_r2d1", Kind::GemvLds, 2, 1, 0, &launch_gemv_lds<FmtQ4, 3, 2, 1>, 3},
+    Variant{"rowlds_m4_r2d1", Kind::GemvLds, 2, 1, 0, &launch_gemv_lds<FmtQ4, 4, 2, 1>, 4},
 #define MOTE_LDS_Q8(MT, R, D)                                                          \
     Variant{MT == 1 ? "q8_rowlds_r" #R "d" #D : "q8_rowlds_m" #MT "_r" #R "d" #D, Kind::Q8Lds, R, D, 0,     \
             &launch_gemv_lds<FmtQ8, MT, R, D>, MT}

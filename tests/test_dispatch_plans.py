@@ -72,6 +72,10 @@ LINEAR = [
     ((2, 4096, 8192), "rowlds_m2_r2d1"),
     ((2, 1024, 4096), "rowlds_m2_r2d1"),
     ((2, 4032, 4096), "stream_m2_d1q_g1"),  # K % 256 != 0: no ring
+    ((3, 4096, 4096), "rowlds_m3_r2d1"),
+    ((3, 4096, 6144), "rowlds_m3_r2d1"),
+    ((3, 4096, 8192), "skinny_mfma_k16_s1_t1_d1_g1_r1_tr_l4_c_w"),
+    ((4, 4096, 2048), "rowlds_m4_r2d1"),
     ((2, 14336, 4096), "stream_s4_m2_d1q_g1"),
     ((3, 8192, 8192), "stream_s2_m3_d1q_g1"),
     ((3, 14336, 4096), "stream_s4_m3_d1q_g1"),
@@ -108,8 +112,11 @@ LINEAR = [
     ((256, 14336, 4096), "mfma_x32s_m64_n64_w2_k4"),
     ((512, 4096, 14336), "mfma_x32s_m128_n256_w1_k2"),
     ((256, 4160, 14336), "mfma_x32s_m128_n128_w1"),  # 65 block pairs: one pair per step
-    # 3-4 tokens at 2048 < K < 4096: each row read once for all tokens
-    ((3, 3072, 8192), "stream_m3_d1_g1"),
+    # 3-4 tokens at 2048 < K < 4096: each row read once for all tokens, through
+    # the LDS ring up to five rows per wave
+    ((3, 3072, 8192), "rowlds_m3_r2d1"),
+    ((4, 2560, 10240), "rowlds_m4_r2d1"),
+    ((3, 3584, 18944), "stream_m3_d1_g1"),
     ((4, 3584, 18944), "stream_m4_d1_g1"),
     # 5-11 tokens at K = 3584 (no K slicing): passes of four tokens on wide N,
     # the one-token-per-pass vector-ALU GEMV on narrow N and past K = 16384

@@ -44,7 +44,7 @@ SPLIT_SHAPES = {
 }
 REFERENCE = {1: "stream_d1_g2", 2: "stream_s2_d1_g1", 4: "stream_s4_d1q_g1", 8: "stream_s8_d1_g1"}
 # the streaming GEMV reading each row once for every token (Q4_0 rings of 2 tokens)
-TOKENS_REFERENCE = {2: "stream_m2_d1q_g1"}
+TOKENS_REFERENCE = {2: "stream_m2_d1q_g1", 3: "stream_m3_d1_g1", 4: "stream_m4_d1_g1"}
 # the Q8_0 streaming GEMV reading each row once for every token, or with rows
 # split over S waves
 Q8_REFERENCE = {1: "q8_stream_d1_g1", 2: "q8_stream_m2_d1q_g1", 4: "q8_stream_m4_d1q_g1"}
